@@ -1,0 +1,82 @@
+/*
+ * peregrine_oracle.h — TEST INFRASTRUCTURE, not product code.
+ *
+ * A scalar C restatement of the reference's Metal shader semantics for the
+ * Qwen3.5-9B 4-bit decode path (XiaoConstantine/peregrine, shaders/ and
+ * src/model/). It is the parity checker for the HIP kernels in
+ * peregrine_amd/csrc and the CPU baseline timed by bench.py. Only tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it.
+ *
+ * Every function cites the reference file:line it restates and reproduces
+ * each bf16 rounding point written there (RNE f32 -> bf16). Reductions that
+ * the reference leaves to hardware (Metal simd_sum over 32 lanes, threadgroup
+ * trees) are restated as butterfly / strided trees in the order noted at each
+ * function; the hardware's own order is not observable here, so last-ulp
+ * agreement with Apple GPUs is "parity unpinned" (see DESIGN.md).
+ *
+ * Parallelism: only across independent output rows (pthreads), so results do
+ * not depend on the thread count (orc_set_threads).
+ *
+ * Layouts match the reference: Q4 weight u32 [N, K/8] (nibble j of word c is
+ * column 8c+j), scales/biases bf16 [N, K/64]; bf16 values are uint16_t bits.
+ */
+#ifndef PEREGRINE_ORACLE_H
+#define PEREGRINE_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+void orc_set_threads(int n);
+int orc_get_threads(void);
+
+/* bf16 helpers */
+float orc_bf2f(uint16_t b);
+uint16_t orc_f2bf(float f);
+
+/* A1: w = bf16(s*q + b). shaders/linear.metal:422-444 */
+void orc_q4_dequantize_bf16(const uint32_t *w, const uint16_t *s, const uint16_t *b,
+                            uint16_t *out, uint32_t N, uint32_t K);
+
+/* A2: raw fp32 dot of M activation rows against every weight row, in the
+ * reference's lane structure (shaders/linear_decode.metal:13-74 /
+ * shaders/linear.metal:65-126): 32 lanes x 16 values per 512-wide K step,
+ * per-lane s*sum(q*x) + b*sum(x) accumulation, then a 32-lane butterfly sum.
+ * dots: f32 [M, N]. */
+void orc_q4_dots(const uint16_t *x, uint32_t M, const uint32_t *w, const uint16_t *s,
+                 const uint16_t *b, float *dots, uint32_t N, uint32_t K);
+
+/* A3: y = bf16(dot).  shaders/linear.metal:128-193 */
+void orc_q4_gemv_bf16(const uint16_t *x, const uint32_t *w, const uint16_t *s,
+                      const uint16_t *b, uint16_t *y, uint32_t M, uint32_t N, uint32_t K);
+
+/* A4/A6: out = bf16(float(bf16(dot)) + float(res)).
+ * shaders/linear_decode.metal:161-192 (M=1), :233-271 (M=2) */
+void orc_q4_gemv_residual_add_bf16(const uint16_t *x, const uint32_t *w, const uint16_t *s,
+                                   const uint16_t *b, const uint16_t *res, uint16_t *out,
+                                   uint32_t M, uint32_t N, uint32_t K);
+
+/* A5/A6: out = bf16(silu(bf16(g)) * bf16(u)), silu(g) = g/(1+exp(-g)).
+ * shaders/linear_decode.metal:311-356 (M=1), :484-541 (M=2) */
+void orc_q4_gemv_silu_gate_bf16(const uint16_t *x, const uint32_t *gw, const uint16_t *gs,
+                                const uint16_t *gb, const uint32_t *uw, const uint16_t *us,
+                                const uint16_t *ub, uint16_t *out, uint32_t M, uint32_t N,
+                                uint32_t K);
+
+/* A7/A6: per 8 rows the first strict max of bf16-rounded logits.
+ * shaders/linear.metal:195-255 (M=1), :342-420 (M=2). pval/pidx: [M, N/8] */
+void orc_q4_gemv_argmax_partial_bf16(const uint16_t *x, const uint32_t *w, const uint16_t *s,
+                                     const uint16_t *b, float *pval, uint32_t *pidx,
+                                     uint32_t M, uint32_t N, uint32_t K);
+
+/* A7: 256-thread strided scan + tree, exactly. shaders/argmax.metal:6-43 */
+uint32_t orc_argmax_pairs_f32_u32(const float *values, const uint32_t *indices, uint32_t n);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,119 @@
+// Shared device/host helpers for the gfx950 decode-path kernels.
+//
+// Numeric conventions (every kernel follows them):
+//   * activations, norm weights, Q4 scales/biases are bf16 stored as uint16_t;
+//   * accumulation is fp32;
+//   * f32 -> bf16 is round-to-nearest-even (NaN stays NaN, quieted).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "peregrine_hip.h"
+
+namespace prg {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------- bf16 -------
+__host__ __device__ inline float bf2f(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+__host__ __device__ inline uint16_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+// Round an f32 to the nearest bf16 value and return it as f32.
+__host__ __device__ inline float round_bf(float f) { return bf2f(f2bf(f)); }
+
+// Low / high bf16 of a packed pair, widened to f32.
+__device__ inline float bf_lo(uint32_t p) { return __uint_as_float(p << 16); }
+__device__ inline float bf_hi(uint32_t p) { return __uint_as_float(p & 0xffff0000u); }
+
+// ------------------------------------------------------------ wave ops -------
+constexpr int kWave = 64;
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+// Sum over aligned groups of `W` lanes (W a power of two <= 64).
+template <int W>
+__device__ inline float group_sum(float v) {
+#pragma unroll
+  for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+__device__ inline float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+template <int W>
+__device__ inline float group_max(float v) {
+#pragma unroll
+  for (int o = W / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+// Block-wide sum for a block of NT threads (NT multiple of 64). `red` must hold
+// NT/64 floats of shared memory. Every thread gets the total. The combination
+// order is fixed (wave sums, then wave 0..n-1 in order), so every block that
+// runs this on the same data produces the same bits.
+template <int NT>
+__device__ inline float block_sum(float v, float* red) {
+  constexpr int NW = NT / kWave;
+  v = wave_sum(v);
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wid = threadIdx.x / kWave;
+  __syncthreads();
+  if (lane == 0) red[wid] = v;
+  __syncthreads();
+  float t = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) t += red[i];
+  return t;
+}
+
+__device__ inline float silu(float g) { return g / (1.0f + expf(-g)); }
+__device__ inline float sigmoid(float g) { return 1.0f / (1.0f + expf(-g)); }
+
+}  // namespace prg
+
+// ------------------------------------------------------------- host side -----
+namespace prg {
+
+// Records a message for prg_last_error() and returns `code`.
+int set_error(int code, const char* fmt, ...);
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+}  // namespace prg
+
+#define PRG_CHECK_ARG(cond, ...)                                      \
+  do {                                                                \
+    if (!(cond)) return ::prg::set_error(PRG_ERR_INVALID_ARG, __VA_ARGS__); \
+  } while (0)
+
+#define PRG_CHECK_LAUNCH(name)                                                    \
+  do {                                                                            \
+    hipError_t e__ = hipGetLastError();                                           \
+    if (e__ != hipSuccess)                                                        \
+      return ::prg::set_error(PRG_ERR_HIP, "%s: launch failed: %s", name,         \
+                              hipGetErrorString(e__));                            \
+  } while (0)
+
+#define PRG_HIP(call)                                                             \
+  do {                                                                            \
+    hipError_t e__ = (call);                                                      \
+    if (e__ != hipSuccess)                                                        \
+      return ::prg::set_error(PRG_ERR_HIP, "%s: %s", #call, hipGetErrorString(e__)); \
+  } while (0)

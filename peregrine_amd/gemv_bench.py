@@ -1,0 +1,103 @@
+"""Q4 GEMV sweep on one GPU with MALL-defeating rotation.
+
+Each shape is timed over a ring of distinct weight copies totalling >= 512 MiB
+(MI355X's Infinity Cache is 256 MiB), so every launch streams its weights from
+HBM. Per-launch kernel time comes from a HIP event pair around each launch;
+the median over >= 50 rotated launches is reported together with the
+algorithmic bytes (weights + scales + biases + x + outputs) and GB/s.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from .device import DeviceArray, Event, synchronize
+from .ops import Q4Linear, argmax_pairs, gate_up_silu
+from .synth import random_bf16, random_q4
+
+HBM_PEAK_GBS = 8000.0
+ROTATE_BYTES = 512 * 1024 * 1024
+
+
+def q4_bytes(N: int, K: int) -> int:
+    return N * K // 2 + N * K // 16  # nibbles + bf16 scale + bf16 bias
+
+
+def _ring(rng, N: int, K: int, **kw) -> list[Q4Linear]:
+    one = random_q4(rng, N, K, **kw)
+    copies = max(2, -(-ROTATE_BYTES // one.nbytes))
+    ring = [Q4Linear.upload(one)]
+    for _ in range(copies - 1):
+        # distinct allocations holding the same bits: the cache cannot tell
+        ring.append(Q4Linear.upload(one))
+    return ring
+
+
+def time_launches(fn, ring, iters: int = 60, warmup: int = 5) -> float:
+    """Median per-launch milliseconds of fn(lin) over the rotated ring."""
+    evs = [(Event(), Event()) for _ in range(iters)]
+    for i in range(warmup):
+        fn(ring[i % len(ring)])
+    synchronize()
+    for i, (a, b) in enumerate(evs):
+        a.record()
+        fn(ring[i % len(ring)])
+        b.record()
+    synchronize()
+    ms = [a.elapsed_ms(b) for a, b in evs]
+    for a, b in evs:
+        a.close()
+        b.close()
+    return float(np.median(ms))
+
+
+def sweep(shapes=None, Ms=(1, 2), seed: int = 0, iters: int = 60) -> list[dict]:
+    rng = np.random.default_rng(seed)
+    shapes = shapes or [(12288, 4096), (4096, 12288), (4096, 4096), (248320, 4096)]
+    rows = []
+    for N, K in shapes:
+        lm_head = N == 248320
+        ring = _ring(rng, N, K, zero_mean=lm_head)
+        for M in Ms:
+            x = [DeviceArray.from_numpy(random_bf16(rng, (1, K))) for _ in range(M)]
+            if lm_head:
+                P = N // 8
+                pv = [DeviceArray((P,), np.float32) for _ in range(M)]
+                pi = [DeviceArray((P,), np.uint32) for _ in range(M)]
+                if M == 1:
+                    fn = lambda lin: lin.encode_bf16_argmax_partial(x[0], pv[0], pi[0])
+                else:
+                    fn = lambda lin: lin.encode_bf16_argmax_partial2(x[0], x[1], pv[0], pi[0], pv[1], pi[1])
+                out_bytes = M * P * 8
+            else:
+                y = DeviceArray((M, N), np.uint16)
+                xx = DeviceArray.from_numpy(random_bf16(rng, (M, K)))
+                fn = lambda lin: lin.encode_bf16_fast(xx, y, token_count=M)
+                out_bytes = M * N * 2
+            ms = time_launches(fn, ring, iters=iters)
+            algo = q4_bytes(N, K) + M * K * 2 + out_bytes
+            gbs = algo / (ms * 1e-3) / 1e9
+            rows.append({"kernel": "lm_head_argmax" if lm_head else "q4_gemv", "N": N, "K": K, "M": M,
+                         "us": ms * 1e3, "algo_bytes": algo, "GBps": gbs, "frac_peak": gbs / HBM_PEAK_GBS})
+            if lm_head:
+                o = DeviceArray((1,), np.uint32)
+                argmax_pairs(pv[0], pi[0], o, N // 8)
+                synchronize()
+        for lin in ring:
+            for a in (lin.weight, lin.scales, lin.biases):
+                a.close()
+    return rows
+
+
+def silu_sweep(seed: int = 1, iters: int = 60) -> dict:
+    rng = np.random.default_rng(seed)
+    N, K = 12288, 4096
+    one_g, one_u = random_q4(rng, N, K), random_q4(rng, N, K)
+    copies = max(2, -(-ROTATE_BYTES // (2 * one_g.nbytes)))
+    ring = [(Q4Linear.upload(one_g), Q4Linear.upload(one_u)) for _ in range(copies)]
+    x = DeviceArray.from_numpy(random_bf16(rng, (1, K)))
+    out = DeviceArray((1, N), np.uint16)
+    ms = time_launches(lambda gu: gate_up_silu(gu[0], gu[1], x, out), ring, iters=iters)
+    algo = 2 * q4_bytes(N, K) + K * 2 + N * 2
+    gbs = algo / (ms * 1e-3) / 1e9
+    return {"kernel": "q4_gemv_silu_gate", "N": N, "K": K, "M": 1, "us": ms * 1e3, "algo_bytes": algo,
+            "GBps": gbs, "frac_peak": gbs / HBM_PEAK_GBS}

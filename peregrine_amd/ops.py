@@ -1,0 +1,85 @@
+"""Python mirror of the reference's op layer over the C ABI.
+
+`Q4Linear` mirrors the reference's Q4Linear (src/model/linear_q4.zig:17-253):
+a resident MLX affine Q4 weight whose encode* methods launch the GEMV family.
+Every call goes straight to libperegrine_hip.so; there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from ._lib import call
+from .device import DeviceArray, ptr
+from .synth import Q4Weight
+
+QMV_FAST_RESULTS_PER_THREADGROUP = 8  # linear_q4.zig:11 (partial = 8 rows)
+
+
+def _s(stream):
+    return C.c_void_p(stream) if stream else None
+
+
+class Q4Linear:
+    """Device-resident Q4 weight. Mirrors Q4Linear (linear_q4.zig:17-63)."""
+
+    def __init__(self, w: DeviceArray, s: DeviceArray, b: DeviceArray) -> None:
+        self.weight, self.scales, self.biases = w, s, b
+        self.out_dim = w.shape[0]
+        self.in_dim = w.shape[1] * 8
+
+    @classmethod
+    def upload(cls, q: Q4Weight) -> "Q4Linear":
+        return cls(DeviceArray.from_numpy(q.w), DeviceArray.from_numpy(q.s), DeviceArray.from_numpy(q.b))
+
+    @property
+    def nbytes(self) -> int:
+        return self.weight.nbytes + self.scales.nbytes + self.biases.nbytes
+
+    def _wsb(self):
+        return ptr(self.weight), ptr(self.scales), ptr(self.biases)
+
+    # linear_q4.zig:77-95
+    def encode_bf16_fast(self, x, y, token_count: int = 1, stream=None) -> None:
+        call("prg_q4_gemv_bf16", _s(stream), ptr(x), *self._wsb(), ptr(y), token_count,
+             self.out_dim, self.in_dim)
+
+    # linear_q4.zig:149-168
+    def encode_bf16_fast_residual_add(self, x, residual, out, token_count: int = 1, stream=None) -> None:
+        call("prg_q4_gemv_residual_add_bf16", _s(stream), ptr(x), *self._wsb(), ptr(residual), ptr(out),
+             token_count, self.out_dim, self.in_dim)
+
+    # linear_q4.zig:170-194
+    def encode_bf16_fast_residual_add2(self, x0, x1, r0, r1, o0, o1, stream=None) -> None:
+        call("prg_q4_gemv2_residual_add_bf16", _s(stream), ptr(x0), ptr(x1), *self._wsb(), ptr(r0), ptr(r1),
+             ptr(o0), ptr(o1), self.out_dim, self.in_dim)
+
+    # linear_q4.zig:97-118
+    def encode_bf16_argmax_partial(self, x, pval, pidx, stream=None) -> None:
+        call("prg_q4_gemv_argmax_partial_bf16", _s(stream), ptr(x), *self._wsb(), ptr(pval), ptr(pidx),
+             self.out_dim, self.in_dim)
+
+    # linear_q4.zig:120-146
+    def encode_bf16_argmax_partial2(self, x0, x1, pv0, pi0, pv1, pi1, stream=None) -> None:
+        call("prg_q4_gemv_argmax2_partial_bf16", _s(stream), ptr(x0), ptr(x1), *self._wsb(),
+             ptr(pv0), ptr(pi0), ptr(pv1), ptr(pi1), self.out_dim, self.in_dim)
+
+    def dequantize(self, out, stream=None) -> None:
+        call("prg_q4_dequantize_bf16", _s(stream), *self._wsb(), ptr(out), self.out_dim, self.in_dim)
+
+
+# block_mlp.zig:313-345 / :347-383
+def gate_up_silu(gate: Q4Linear, up: Q4Linear, x, out, stream=None) -> None:
+    call("prg_q4_gemv_silu_gate_bf16", _s(stream), ptr(x), *gate._wsb(), *up._wsb(), ptr(out),
+         gate.out_dim, gate.in_dim)
+
+
+def gate_up_silu2(gate: Q4Linear, up: Q4Linear, x0, x1, o0, o1, stream=None) -> None:
+    call("prg_q4_gemv_silu_gate2_bf16", _s(stream), ptr(x0), ptr(x1), *gate._wsb(), *up._wsb(), ptr(o0),
+         ptr(o1), gate.out_dim, gate.in_dim)
+
+
+# argmax.zig:14-35
+def argmax_pairs(pval, pidx, out_index, pair_count: int, stream=None) -> None:
+    call("prg_argmax_pairs_f32_u32", _s(stream), ptr(pval), ptr(pidx), ptr(out_index), pair_count)
