@@ -163,6 +163,104 @@ int prg_q4_dequantize_bf16(void *stream, const uint32_t *w, const uint16_t *scal
                            const uint16_t *biases, uint16_t *out, uint32_t out_dim,
                            uint32_t in_dim);
 
+/* ======================================================================
+ * Norms and embedding
+ * ====================================================================== */
+
+/* out = bf16(x * rsqrt(mean(x^2) + eps) * w) per row of `hidden` values.
+ * Replaces rmsnorm_bf16 (shaders/rmsnorm.metal:80-116,222-245), host
+ * DecoderLayer.encodeRmsNormBf16 (src/model/decoder_layer.zig:419-437). */
+int prg_rmsnorm_bf16(void *stream, const uint16_t *x, const uint16_t *weight, uint16_t *out,
+                     uint32_t hidden, uint32_t rows, float eps);
+
+/* residual_out = bf16(lhs + rhs); norm_out = rmsnorm(residual_out) (the norm of
+ * the ROUNDED sum). Replaces add_rmsnorm_bf16 (shaders/rmsnorm.metal:178-220,
+ * 280-307), host encodeAddRmsNormBf16 (decoder_layer.zig:439-459). */
+int prg_add_rmsnorm_bf16(void *stream, const uint16_t *lhs, const uint16_t *rhs,
+                         const uint16_t *weight, uint16_t *residual_out, uint16_t *norm_out,
+                         uint32_t hidden, uint32_t rows, float eps);
+
+/* out[h] = bf16(s*q + b) for row `token` of the Q4 embedding table
+ * [vocab, hidden/8]. token >= vocab -> PRG_ERR_INVALID_TOKEN (model.zig:806).
+ * Replaces q4_embedding_gather_bf16 (shaders/embedding.metal:55-71). */
+int prg_q4_embedding_gather_bf16(void *stream, const uint32_t *weight, const uint16_t *scales,
+                                 const uint16_t *biases, uint16_t *out, uint32_t token,
+                                 uint32_t hidden, uint32_t vocab);
+
+/* Batched gather of `tokens` rows (token_ids: device u32 [tokens]).
+ * Replaces q4_embedding_gather_many_bf16 (shaders/embedding.metal:73-96). */
+int prg_q4_embedding_gather_many_bf16(void *stream, const uint32_t *weight, const uint16_t *scales,
+                                      const uint16_t *biases, uint16_t *out,
+                                      const uint32_t *token_ids, uint32_t tokens, uint32_t hidden);
+
+/* ======================================================================
+ * Gated DeltaNet (linear attention) decode. Shape fixed by the model:
+ * Hk=16, Hv=32, Dk=Dv=128, conv_dim=8192, conv kernel 4
+ * (src/model/block_linear.zig:19-30).
+ * ====================================================================== */
+
+/* Depthwise causal conv + SiLU for one token, rolling the f32 state
+ * [3, conv_dim] in place. Replaces conv1d_silu_decode_bf16
+ * (shaders/conv1d.metal:40-62), host block_linear.zig:236-240. */
+int prg_conv1d_silu_decode_bf16(void *stream, float *state, const uint16_t *qkv,
+                                const uint16_t *weight, uint16_t *out, uint32_t conv_dim,
+                                uint32_t kernel_size);
+
+/* Delta-rule recurrence with inline q/k L2 norms and gates; state f32
+ * [Hv, Dv, Dk] updated in place; y bf16 [Hv*Dv]. has_previous_state == 0
+ * treats the state as zero. Replaces gated_delta_decode_h128_fused_bf16
+ * (shaders/gated_delta.metal:147-261), host block_linear.zig:242-258. */
+int prg_gated_delta_decode_bf16(void *stream, float *state, const uint16_t *conv_out,
+                                const uint16_t *a, const uint16_t *b, const float *A_log,
+                                const uint16_t *dt_bias, uint16_t *y, uint32_t Hk, uint32_t Hv,
+                                uint32_t Dk, uint32_t Dv, uint32_t conv_dim,
+                                uint32_t has_previous_state);
+
+/* The recurrence fused with the gated RMSNorm of each head:
+ * out = bf16(y * rsqrt(mean(y^2)+eps) * norm_weight * silu(z)). One dispatch for
+ * the reference's gated_delta_decode + rmsnorm_gated pair
+ * (block_linear.zig:242-262). */
+int prg_gated_delta_decode_norm_bf16(void *stream, float *state, const uint16_t *conv_out,
+                                     const uint16_t *a, const uint16_t *b, const float *A_log,
+                                     const uint16_t *dt_bias, const uint16_t *norm_weight,
+                                     const uint16_t *z, uint16_t *out, float eps,
+                                     uint32_t has_previous_state);
+
+/* Gated RMSNorm per row of `dim` (<= 128) values. Replaces rmsnorm_gated_bf16
+ * (shaders/gated_norm.metal:163-189), host block_linear.zig:471-489. */
+int prg_rmsnorm_gated_bf16(void *stream, const uint16_t *x, const uint16_t *weight,
+                           const uint16_t *gate, uint16_t *out, uint32_t dim, float eps,
+                           uint32_t rows);
+
+/* ======================================================================
+ * GQA decode attention. Shape fixed by the model: 16 q heads, 4 kv heads,
+ * head_dim 256, partial RoPE on 64 dims, theta 1e7 (block_attn.zig:21-28).
+ * Caches: K bf16 [4, stride, 256], V bf16 [4, 256, stride] (value-dim-major,
+ * src/model/state.zig:41-48); stride % 64 == 0.
+ * ====================================================================== */
+
+/* Split packed q [16, 512] into q and gate, RMSNorm q/k with q_weight/k_weight,
+ * RoPE at position_offset, append k and v to the caches at dst_token_index.
+ * Replaces qwen35_q_gate_prepare_kv_append_pair_head_major_value_dim_major_bf16
+ * (shaders/attention.metal:327-421), host block_attn.zig:321-326. */
+int prg_attn_decode_prepare_bf16(void *stream, const uint16_t *packed_q, const uint16_t *q_weight,
+                                 uint16_t *q_output, uint16_t *gate, const uint16_t *k_input,
+                                 const uint16_t *v_input, const uint16_t *k_weight,
+                                 uint16_t *key_cache, uint16_t *value_cache,
+                                 uint32_t cache_stride_tokens, uint32_t dst_token_index,
+                                 uint32_t position_offset);
+
+/* out = bf16(softmax(scale * q.K^T) V * sigmoid(gate)) over the first seq_len
+ * cache slots, as split-context partials + merge. partials: device f32 of
+ * prg_attn_decode_partials_bytes(stride) bytes. Replaces the pair
+ * sdpa_decode_prefix_flash_partials_bf16 + ..._reduce_gated_bf16
+ * (shaders/attention_decode.metal:24-243), host block_attn.zig:328-358. */
+int prg_attn_decode_bf16(void *stream, const uint16_t *q, const uint16_t *key_cache,
+                         const uint16_t *value_cache, const uint16_t *gate, uint16_t *out,
+                         float *partials, uint32_t cache_stride_tokens, uint32_t seq_len,
+                         float scale);
+size_t prg_attn_decode_partials_bytes(uint32_t cache_stride_tokens);
+
 #ifdef __cplusplus
 }
 #endif

@@ -39,6 +39,17 @@ class Oracle:
         d.orc_q4_gemv_argmax_partial_bf16.argtypes = [_u16p, _u32p, _u16p, _u16p, _f32p, _u32p, _u32, _u32, _u32]
         d.orc_argmax_pairs_f32_u32.argtypes = [_f32p, _u32p, _u32]
         d.orc_argmax_pairs_f32_u32.restype = C.c_uint32
+        _f = C.c_float
+        d.orc_rmsnorm_bf16.argtypes = [_u16p, _u16p, _u16p, _u32, _u32, _f]
+        d.orc_add_rmsnorm_bf16.argtypes = [_u16p, _u16p, _u16p, _u16p, _u16p, _u32, _u32, _f]
+        d.orc_q4_embedding_gather_bf16.argtypes = [_u32p, _u16p, _u16p, _u16p, _u32, _u32]
+        d.orc_conv1d_silu_decode_bf16.argtypes = [_f32p, _u16p, _u16p, _u16p, _u32, _u32]
+        d.orc_gated_delta_decode_bf16.argtypes = [_f32p, _u16p, _u16p, _u16p, _f32p, _u16p, _u16p,
+                                                  _u32, _u32, _u32, _u32, _u32]
+        d.orc_rmsnorm_gated_bf16.argtypes = [_u16p, _u16p, _u16p, _u16p, _u32, _f, _u32]
+        d.orc_attn_decode_prepare_bf16.argtypes = [_u16p, _u16p, _u16p, _u16p, _u16p, _u16p, _u16p, _u16p,
+                                                   _u16p, _u32, _u32, _u32, _u32, _u32, _f, _u32, _u32]
+        d.orc_attn_decode_bf16.argtypes = [_u16p, _u16p, _u16p, _u16p, _u16p, _u32, _u32, _u32, _u32, _f]
 
     # ------------------------------------------------------------------ misc
     def set_threads(self, n: int) -> None:
@@ -106,6 +117,71 @@ class Oracle:
         v = _c(values, np.float32)
         i = _c(indices, np.uint32)
         return int(self.d.orc_argmax_pairs_f32_u32(v, i, v.size))
+
+    # ------------------------------------------------------ norms / embed
+    def rmsnorm(self, x, w, eps=1e-6) -> np.ndarray:
+        x = _c(np.atleast_2d(x), np.uint16)
+        out = np.empty_like(x)
+        self.d.orc_rmsnorm_bf16(x, _c(w, np.uint16), out, x.shape[1], x.shape[0], eps)
+        return out
+
+    def add_rmsnorm(self, a, b, w, eps=1e-6):
+        a = _c(np.atleast_2d(a), np.uint16)
+        b = _c(np.atleast_2d(b), np.uint16)
+        r = np.empty_like(a)
+        n = np.empty_like(a)
+        self.d.orc_add_rmsnorm_bf16(a, b, _c(w, np.uint16), r, n, a.shape[1], a.shape[0], eps)
+        return r, n
+
+    def embedding(self, wt, token: int) -> np.ndarray:
+        V, H = wt.shape
+        out = np.empty(H, np.uint16)
+        self.d.orc_q4_embedding_gather_bf16(_c(wt.w, np.uint32), _c(wt.s, np.uint16), _c(wt.b, np.uint16), out,
+                                            int(token), H)
+        return out
+
+    # ---------------------------------------------------------------- GDN
+    def conv1d_decode(self, state, qkv, w):
+        """Returns (out, new_state); state is not modified."""
+        st = np.array(state, np.float32, copy=True, order="C")
+        qkv = _c(qkv, np.uint16)
+        out = np.empty_like(qkv)
+        self.d.orc_conv1d_silu_decode_bf16(st, qkv, _c(w, np.uint16), out, qkv.size, 4)
+        return out, st
+
+    def gated_delta_decode(self, state, conv_out, a, b, A_log, dt_bias, has_prev=True,
+                           Hk=16, Hv=32, Dk=128, Dv=128):
+        st = np.array(state, np.float32, copy=True, order="C")
+        y = np.empty(Hv * Dv, np.uint16)
+        self.d.orc_gated_delta_decode_bf16(st, _c(conv_out, np.uint16), _c(a, np.uint16), _c(b, np.uint16),
+                                           _c(A_log, np.float32), _c(dt_bias, np.uint16), y, Hk, Hv, Dk, Dv,
+                                           int(bool(has_prev)))
+        return y, st
+
+    def rmsnorm_gated(self, x, w, gate, dim, eps=1e-6):
+        x = _c(x, np.uint16)
+        out = np.empty_like(x)
+        self.d.orc_rmsnorm_gated_bf16(x, _c(w, np.uint16), _c(gate, np.uint16), out, dim, eps, x.size // dim)
+        return out
+
+    # ---------------------------------------------------------- attention
+    def attn_prepare(self, packed_q, q_w, k_in, v_in, k_w, key_cache, value_cache, stride, dst, pos,
+                     theta=1.0e7):
+        """Returns (q_out, gate, key_cache', value_cache') — caches are copied."""
+        kc = np.array(key_cache, np.uint16, copy=True, order="C")
+        vc = np.array(value_cache, np.uint16, copy=True, order="C")
+        q_out = np.empty(16 * 256, np.uint16)
+        gate = np.empty(16 * 256, np.uint16)
+        self.d.orc_attn_decode_prepare_bf16(_c(packed_q, np.uint16), _c(q_w, np.uint16), q_out, gate,
+                                            _c(k_in, np.uint16), _c(v_in, np.uint16), _c(k_w, np.uint16), kc, vc,
+                                            16, 4, 256, 64, int(pos), theta, int(stride), int(dst))
+        return q_out, gate, kc, vc
+
+    def attn_decode(self, q, key_cache, value_cache, gate, stride, seq_len, scale=1.0 / 16.0):
+        out = np.empty(16 * 256, np.uint16)
+        self.d.orc_attn_decode_bf16(_c(q, np.uint16), _c(key_cache, np.uint16), _c(value_cache, np.uint16),
+                                    _c(gate, np.uint16), out, 16, 4, int(stride), int(seq_len), scale)
+        return out
 
 
 _singleton: Oracle | None = None

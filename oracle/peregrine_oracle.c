@@ -267,3 +267,358 @@ uint32_t orc_argmax_pairs_f32_u32(const float *values, const uint32_t *indices, 
       }
   return bi[0];
 }
+
+/* ---------------------------------------------------------- A16 norms ---- */
+/* rmsnorm_threadgroup_impl (shaders/rmsnorm.metal:80-116) with the host's
+ * 512 threads (src/model/dims.zig:6): thread t sums col = t, t+512, ...;
+ * tree over partial_sums with stride 256..1; scale = rsqrt(sum/hidden + eps);
+ * out = T(float(x) * scale * float(w)). rsqrt restated as 1/sqrtf. */
+#define ORC_NORM_THREADS 512
+static float tree_sum(float *partial, int n) {
+  for (int stride = n >> 1; stride > 0; stride >>= 1)
+    for (int t = 0; t < stride; ++t) partial[t] += partial[t + stride];
+  return partial[0];
+}
+
+static float rms_scale_ref(const float *v, uint32_t hidden, float eps) {
+  float partial[ORC_NORM_THREADS];
+  for (int t = 0; t < ORC_NORM_THREADS; ++t) {
+    float sum = 0.0f;
+    for (uint32_t col = (uint32_t)t; col < hidden; col += ORC_NORM_THREADS) sum += v[col] * v[col];
+    partial[t] = sum;
+  }
+  const float total = tree_sum(partial, ORC_NORM_THREADS);
+  return 1.0f / sqrtf(total / (float)hidden + eps);
+}
+
+void orc_rmsnorm_bf16(const uint16_t *x, const uint16_t *w, uint16_t *out, uint32_t hidden,
+                      uint32_t rows, float eps) {
+  float *v = (float *)malloc(sizeof(float) * hidden);
+  for (uint32_t r = 0; r < rows; ++r) {
+    const uint16_t *xr = x + (size_t)r * hidden;
+    for (uint32_t i = 0; i < hidden; ++i) v[i] = orc_bf2f(xr[i]);
+    const float scale = rms_scale_ref(v, hidden, eps);
+    for (uint32_t i = 0; i < hidden; ++i) out[(size_t)r * hidden + i] = orc_f2bf(v[i] * scale * orc_bf2f(w[i]));
+  }
+  free(v);
+}
+
+/* add_rmsnorm_threadgroup_impl (shaders/rmsnorm.metal:178-220): the residual
+ * is rounded to bf16 first and the rounded value is normalised. */
+void orc_add_rmsnorm_bf16(const uint16_t *lhs, const uint16_t *rhs, const uint16_t *w,
+                          uint16_t *residual_out, uint16_t *norm_out, uint32_t hidden,
+                          uint32_t rows, float eps) {
+  float *v = (float *)malloc(sizeof(float) * hidden);
+  for (uint32_t r = 0; r < rows; ++r) {
+    const size_t o = (size_t)r * hidden;
+    for (uint32_t i = 0; i < hidden; ++i) {
+      residual_out[o + i] = orc_f2bf(orc_bf2f(lhs[o + i]) + orc_bf2f(rhs[o + i]));
+      v[i] = orc_bf2f(residual_out[o + i]);
+    }
+    const float scale = rms_scale_ref(v, hidden, eps);
+    for (uint32_t i = 0; i < hidden; ++i) norm_out[o + i] = orc_f2bf(v[i] * scale * orc_bf2f(w[i]));
+  }
+  free(v);
+}
+
+/* ------------------------------------------------------ A18 embedding ---- */
+/* q4_embedding_gather_bf16 (shaders/embedding.metal:55-71) */
+void orc_q4_embedding_gather_bf16(const uint32_t *w, const uint16_t *s, const uint16_t *b,
+                                  uint16_t *out, uint32_t token, uint32_t hidden) {
+  const size_t words = hidden / 8, groups = hidden / 64;
+  for (uint32_t h = 0; h < hidden; ++h) {
+    const uint32_t q = (w[(size_t)token * words + (h >> 3)] >> ((h & 7) * 4)) & 0xF;
+    const uint32_t g = h >> 6;
+    out[h] = orc_f2bf(orc_bf2f(s[(size_t)token * groups + g]) * (float)q + orc_bf2f(b[(size_t)token * groups + g]));
+  }
+}
+
+/* ---------------------------------------------------------- A8 conv ------ */
+/* conv1d_silu_decode_bf16 (shaders/conv1d.metal:40-62); state f32 [K-1, C]. */
+void orc_conv1d_silu_decode_bf16(float *state, const uint16_t *qkv, const uint16_t *w,
+                                 uint16_t *out, uint32_t conv_dim, uint32_t kernel_size) {
+  const uint32_t km1 = kernel_size - 1;
+  for (uint32_t c = 0; c < conv_dim; ++c) {
+    const float xnew = orc_bf2f(qkv[c]);
+    float acc = 0.0f;
+    for (uint32_t j = 0; j < km1; ++j) acc += orc_bf2f(w[c * kernel_size + j]) * state[j * conv_dim + c];
+    acc += orc_bf2f(w[c * kernel_size + km1]) * xnew;
+    out[c] = orc_f2bf(acc / (1.0f + expf(-acc)));
+    for (uint32_t j = 0; j + 1 < km1; ++j) state[j * conv_dim + c] = state[(j + 1) * conv_dim + c];
+    if (km1 > 0) state[(km1 - 1) * conv_dim + c] = xnew;
+  }
+}
+
+/* ------------------------------------------------------------ A9 GDN ----- */
+/* gated_delta_decode_h128_fused_bf16 (shaders/gated_delta.metal:147-261):
+ * lane L holds dk = L + 32*chunk (chunk 0..3); per-lane sums over chunks in
+ * order, then simd_sum. Dk must be 128. */
+void orc_gated_delta_decode_bf16(float *state, const uint16_t *conv_out, const uint16_t *a,
+                                 const uint16_t *b, const float *A_log, const uint16_t *dt_bias,
+                                 uint16_t *y, uint32_t Hk, uint32_t Hv, uint32_t Dk, uint32_t Dv,
+                                 uint32_t has_previous_state) {
+  const uint32_t key_dim = Hk * Dk;
+  for (uint32_t hv = 0; hv < Hv; ++hv) {
+    const uint32_t hk = hv / (Hv / Hk);
+    const float gate_x = orc_bf2f(a[hv]) + orc_bf2f(dt_bias[hv]);
+    const float softplus = fmaxf(gate_x, 0.0f) + logf(1.0f + expf(-fabsf(gate_x)));
+    const float decay = expf(-expf(A_log[hv]) * softplus);
+    const float beta = 1.0f / (1.0f + expf(-orc_bf2f(b[hv])));
+    float qraw[32][4], kraw[32][4], qss[32], kss[32];
+    for (int l = 0; l < 32; ++l) {
+      qss[l] = kss[l] = 0.0f;
+      for (int ch = 0; ch < 4; ++ch) {
+        const uint32_t dk = l + ch * 32;
+        qraw[l][ch] = orc_bf2f(conv_out[hk * Dk + dk]);
+        kraw[l][ch] = orc_bf2f(conv_out[key_dim + hk * Dk + dk]);
+        qss[l] += qraw[l][ch] * qraw[l][ch];
+        kss[l] += kraw[l][ch] * kraw[l][ch];
+      }
+    }
+    const float q_inv = (1.0f / sqrtf(simd_sum32(qss) + 1.0e-6f)) * (1.0f / sqrtf((float)Dk));
+    const float k_inv = 1.0f / sqrtf(simd_sum32(kss) + 1.0e-6f);
+    float key[32][4], query[32][4], kql[32];
+    for (int l = 0; l < 32; ++l) {
+      kql[l] = 0.0f;
+      for (int ch = 0; ch < 4; ++ch) {
+        query[l][ch] = qraw[l][ch] * q_inv;
+        key[l][ch] = kraw[l][ch] * k_inv;
+        kql[l] += key[l][ch] * query[l][ch];
+      }
+    }
+    const float kq = simd_sum32(kql);
+    for (uint32_t dv = 0; dv < Dv; ++dv) {
+      float *row = state + ((size_t)hv * Dv + dv) * Dk;
+      float dec[32][4], kvl[32], obl[32];
+      for (int l = 0; l < 32; ++l) {
+        kvl[l] = obl[l] = 0.0f;
+        for (int ch = 0; ch < 4; ++ch) {
+          const float s = has_previous_state ? row[l + ch * 32] : 0.0f;
+          dec[l][ch] = s * decay;
+          kvl[l] += dec[l][ch] * key[l][ch];
+          obl[l] += dec[l][ch] * query[l][ch];
+        }
+      }
+      const float kv_mem = simd_sum32(kvl);
+      const float ob = simd_sum32(obl);
+      const float delta = (orc_bf2f(conv_out[2 * key_dim + hv * Dv + dv]) - kv_mem) * beta;
+      for (int l = 0; l < 32; ++l)
+        for (int ch = 0; ch < 4; ++ch) row[l + ch * 32] = dec[l][ch] + key[l][ch] * delta;
+      y[hv * Dv + dv] = orc_f2bf(ob + delta * kq);
+    }
+  }
+}
+
+/* ----------------------------------------------------- A10 gated norm ---- */
+/* rmsnorm_gated_bf16 (shaders/gated_norm.metal:163-189): one serial thread per
+ * row. */
+void orc_rmsnorm_gated_bf16(const uint16_t *x, const uint16_t *w, const uint16_t *gate,
+                            uint16_t *out, uint32_t dim, float eps, uint32_t rows) {
+  for (uint32_t r = 0; r < rows; ++r) {
+    const uint16_t *xr = x + (size_t)r * dim, *gr = gate + (size_t)r * dim;
+    float ss = 0.0f;
+    for (uint32_t i = 0; i < dim; ++i) {
+      const float v = orc_bf2f(xr[i]);
+      ss += v * v;
+    }
+    const float scale = 1.0f / sqrtf(ss / (float)dim + eps);
+    for (uint32_t i = 0; i < dim; ++i) {
+      const float n = orc_bf2f(xr[i]) * scale * orc_bf2f(w[i]);
+      const float gg = orc_bf2f(gr[i]);
+      out[(size_t)r * dim + i] = orc_f2bf(n * (gg / (1.0f + expf(-gg))));
+    }
+  }
+}
+
+/* -------------------------------------------------- A12 attn prepare ----- */
+/* qwen35_q_gate_prepare_kv_append_pair_head_major_value_dim_major_bf16
+ * (shaders/attention.metal:327-421), threads_per_threadgroup = 256
+ * (block_attn.zig:35), one value per thread, tree over 256. */
+void orc_attn_decode_prepare_bf16(const uint16_t *packed_q, const uint16_t *q_weight,
+                                  uint16_t *q_out, uint16_t *gate, const uint16_t *k_in,
+                                  const uint16_t *v_in, const uint16_t *k_weight,
+                                  uint16_t *key_dst, uint16_t *value_dst, uint32_t num_heads,
+                                  uint32_t num_kv_heads, uint32_t head_dim, uint32_t rotary_dim,
+                                  uint32_t position_offset, float theta, uint32_t stride,
+                                  uint32_t dst) {
+  float partial[256];
+  for (uint32_t tg = 0; tg < num_heads + num_kv_heads; ++tg) {
+    const int use_q = tg < num_heads;
+    const uint32_t head = use_q ? tg : tg - num_heads;
+    const size_t row_base = (size_t)head * head_dim, packed_base = (size_t)head * 2 * head_dim;
+    const uint16_t *w = use_q ? q_weight : k_weight;
+    for (uint32_t t = 0; t < 256; ++t) {
+      float sum = 0.0f;
+      for (uint32_t col = t; col < head_dim; col += 256) {
+        const float v = orc_bf2f(use_q ? packed_q[packed_base + col] : k_in[row_base + col]);
+        sum += v * v;
+        if (use_q) gate[row_base + col] = packed_q[packed_base + head_dim + col];
+        else value_dst[(row_base + col) * stride + dst] = v_in[row_base + col];
+      }
+      partial[t] = sum;
+    }
+    const float inv_rms = 1.0f / sqrtf(tree_sum(partial, 256) / (float)head_dim + 1.0e-6f);
+    const uint32_t half = rotary_dim / 2;
+    for (uint32_t p = 0; p < half; ++p) {
+      const float s1 = orc_bf2f(use_q ? packed_q[packed_base + p] : k_in[row_base + p]);
+      const float s2 = orc_bf2f(use_q ? packed_q[packed_base + p + half] : k_in[row_base + p + half]);
+      const float x1 = rbf(s1 * inv_rms * orc_bf2f(w[p]));
+      const float x2 = rbf(s2 * inv_rms * orc_bf2f(w[p + half]));
+      const float inv_freq = powf(theta, -(2.0f * (float)p) / (float)rotary_dim);
+      const float angle = (float)position_offset * inv_freq;
+      const float c = cosf(angle), s = sinf(angle);
+      const uint16_t r1 = orc_f2bf(x1 * c - x2 * s), r2 = orc_f2bf(x2 * c + x1 * s);
+      if (use_q) {
+        q_out[row_base + p] = r1;
+        q_out[row_base + p + half] = r2;
+      } else {
+        const size_t kb = ((size_t)head * stride + dst) * head_dim;
+        key_dst[kb + p] = r1;
+        key_dst[kb + p + half] = r2;
+      }
+    }
+    for (uint32_t col = rotary_dim; col < head_dim; ++col) {
+      const float sv = orc_bf2f(use_q ? packed_q[packed_base + col] : k_in[row_base + col]);
+      const uint16_t nv = orc_f2bf(sv * inv_rms * orc_bf2f(w[col]));
+      if (use_q) q_out[row_base + col] = nv;
+      else key_dst[((size_t)head * stride + dst) * head_dim + col] = nv;
+    }
+  }
+}
+
+/* -------------------------------------------- A13/A14 attention decode --- */
+/* sdpa_decode_prefix_flash_partials_bf16 (shaders/attention_decode.metal:24-210)
+ * with the non-prefix binding (prefix = local cache, prefix_len = 0,
+ * block_attn.zig:340-343), then ..._reduce_gated_bf16 (:215-243).
+ * 1024-token chunks per kv head; 8 simdgroups take 64-token tiles sg, sg+8..;
+ * lane L holds dims 4L..4L+3 and 128+4L..; online softmax per tile; the
+ * simdgroup partials are merged in order, then the chunk partials. */
+#define ATT_D 256
+#define ATT_G 4
+typedef struct {
+  const uint16_t *q, *K, *V, *gate;
+  uint16_t *out;
+  uint32_t num_q, num_kv, stride, seq_len, chunk_count;
+  float scale;
+  float *partials;
+} att_ctx;
+
+static void att_partial_one(const att_ctx *c, uint32_t kvh, uint32_t chunk) {
+  const uint32_t t_begin = chunk * 1024, t_end = (t_begin + 1024 < c->seq_len) ? t_begin + 1024 : c->seq_len;
+  float q[ATT_G][ATT_D];
+  for (int g = 0; g < ATT_G; ++g)
+    for (int d = 0; d < ATT_D; ++d) q[g][d] = orc_bf2f(c->q[(size_t)(kvh * ATT_G + g) * ATT_D + d]);
+  const uint16_t *kb = c->K + (size_t)kvh * c->stride * ATT_D;
+  const uint16_t *vb = c->V + (size_t)kvh * ATT_D * c->stride;
+  float sg_m[8][ATT_G], sg_den[8][ATT_G];
+  static __thread float sg_acc[8][ATT_G][ATT_D];
+  for (int sg = 0; sg < 8; ++sg) {
+    float m[ATT_G], den[ATT_G];
+    for (int g = 0; g < ATT_G; ++g) {
+      m[g] = -INFINITY;
+      den[g] = 0.0f;
+      for (int d = 0; d < ATT_D; ++d) sg_acc[sg][g][d] = 0.0f;
+    }
+    for (uint32_t tile = (uint32_t)sg; tile < 16; tile += 8) {
+      const uint32_t tile_base = t_begin + tile * 64;
+      if (tile_base >= t_end) break;
+      const uint32_t valid = (t_end - tile_base < 64) ? t_end - tile_base : 64;
+      float s[64][ATT_G];
+      for (uint32_t tt = 0; tt < 64; ++tt) {
+        for (int g = 0; g < ATT_G; ++g) s[tt][g] = -INFINITY;
+        if (tt >= valid) continue;
+        const uint16_t *kt = kb + (size_t)(tile_base + tt) * ATT_D;
+        for (int g = 0; g < ATT_G; ++g) {
+          float lanev[32];
+          for (int l = 0; l < 32; ++l) {
+            float p[4];
+            for (int i = 0; i < 4; ++i)
+              p[i] = q[g][4 * l + i] * orc_bf2f(kt[4 * l + i]) + q[g][128 + 4 * l + i] * orc_bf2f(kt[128 + 4 * l + i]);
+            lanev[l] = p[0] + p[1] + p[2] + p[3];
+          }
+          s[tt][g] = simd_sum32(lanev) * c->scale;
+        }
+      }
+      float w_t[64][ATT_G];
+      for (int g = 0; g < ATT_G; ++g) {
+        float tile_max = -INFINITY;
+        for (int l = 0; l < 32; ++l) {
+          const float a = s[l][g], b2 = s[32 + l][g];
+          tile_max = fmaxf(tile_max, fmaxf(a, b2));
+        }
+        const float m_new = fmaxf(m[g], tile_max);
+        const float corr = (m[g] == -INFINITY) ? 0.0f : expf(m[g] - m_new);
+        float lw[32];
+        for (int l = 0; l < 32; ++l) {
+          const float wa = (s[l][g] == -INFINITY) ? 0.0f : expf(s[l][g] - m_new);
+          const float wb = (s[32 + l][g] == -INFINITY) ? 0.0f : expf(s[32 + l][g] - m_new);
+          w_t[l][g] = wa;
+          w_t[32 + l][g] = wb;
+          lw[l] = wa + wb;
+        }
+        den[g] = den[g] * corr + simd_sum32(lw);
+        m[g] = m_new;
+        for (int d = 0; d < ATT_D; ++d) sg_acc[sg][g][d] *= corr;
+      }
+      for (int d = 0; d < ATT_D; ++d) {
+        const uint16_t *vrow = vb + (size_t)d * c->stride + tile_base;
+        float sum_g[ATT_G] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (uint32_t tt = 0; tt < valid; ++tt) {
+          const float vv = orc_bf2f(vrow[tt]);
+          for (int g = 0; g < ATT_G; ++g) sum_g[g] += w_t[tt][g] * vv;
+        }
+        for (int g = 0; g < ATT_G; ++g) sg_acc[sg][g][d] += sum_g[g];
+      }
+    }
+    for (int g = 0; g < ATT_G; ++g) {
+      sg_m[sg][g] = m[g];
+      sg_den[sg][g] = den[g];
+    }
+  }
+  for (int g = 0; g < ATT_G; ++g) {
+    float m_all = -INFINITY;
+    for (int i = 0; i < 8; ++i) m_all = fmaxf(m_all, sg_m[i][g]);
+    float den_all = 0.0f, outv[ATT_D];
+    for (int d = 0; d < ATT_D; ++d) outv[d] = 0.0f;
+    for (int i = 0; i < 8; ++i) {
+      const float w = (sg_m[i][g] == -INFINITY) ? 0.0f : expf(sg_m[i][g] - m_all);
+      den_all += sg_den[i][g] * w;
+      for (int d = 0; d < ATT_D; ++d) outv[d] += sg_acc[i][g][d] * w;
+    }
+    float *dst = c->partials + ((size_t)(kvh * ATT_G + g) * c->chunk_count + chunk) * (ATT_D + 2);
+    dst[0] = m_all;
+    dst[1] = den_all;
+    for (int d = 0; d < ATT_D; ++d) dst[2 + d] = outv[d];
+  }
+}
+
+static void att_range(void *ctx, size_t b, size_t e) {
+  const att_ctx *c = (const att_ctx *)ctx;
+  for (size_t i = b; i < e; ++i) att_partial_one(c, (uint32_t)(i / c->chunk_count), (uint32_t)(i % c->chunk_count));
+}
+
+void orc_attn_decode_bf16(const uint16_t *q, const uint16_t *K, const uint16_t *V,
+                          const uint16_t *gate, uint16_t *out, uint32_t num_q_heads,
+                          uint32_t num_kv_heads, uint32_t stride, uint32_t seq_len, float scale) {
+  const uint32_t chunk_count = (seq_len + 1023) / 1024;
+  float *partials = (float *)malloc(sizeof(float) * num_q_heads * chunk_count * (ATT_D + 2));
+  att_ctx c = {q, K, V, gate, out, num_q_heads, num_kv_heads, stride, seq_len, chunk_count, scale, partials};
+  parallel_for((size_t)num_kv_heads * chunk_count, att_range, &c);
+  for (uint32_t h = 0; h < num_q_heads; ++h)
+    for (uint32_t d = 0; d < ATT_D; ++d) {
+      const float *base = partials + (size_t)h * chunk_count * (ATT_D + 2);
+      float m_all = -INFINITY;
+      for (uint32_t ch = 0; ch < chunk_count; ++ch) m_all = fmaxf(m_all, base[ch * (ATT_D + 2)]);
+      float den = 0.0f, acc = 0.0f;
+      for (uint32_t ch = 0; ch < chunk_count; ++ch) {
+        const float *pc = base + ch * (ATT_D + 2);
+        const float w = (pc[0] == -INFINITY) ? 0.0f : expf(pc[0] - m_all);
+        den += pc[1] * w;
+        acc += pc[2 + d] * w;
+      }
+      const size_t i = (size_t)h * ATT_D + d;
+      const float sig = 1.0f / (1.0f + expf(-orc_bf2f(gate[i])));
+      out[i] = orc_f2bf((acc / den) * sig);
+    }
+  free(partials);
+}

@@ -75,6 +75,40 @@ void orc_q4_gemv_argmax_partial_bf16(const uint16_t *x, const uint32_t *w, const
 /* A7: 256-thread strided scan + tree, exactly. shaders/argmax.metal:6-43 */
 uint32_t orc_argmax_pairs_f32_u32(const float *values, const uint32_t *indices, uint32_t n);
 
+/* A16: shaders/rmsnorm.metal:80-116 (512 threads, tree reduction) */
+void orc_rmsnorm_bf16(const uint16_t *x, const uint16_t *w, uint16_t *out, uint32_t hidden,
+                      uint32_t rows, float eps);
+/* A17: shaders/rmsnorm.metal:178-220 */
+void orc_add_rmsnorm_bf16(const uint16_t *lhs, const uint16_t *rhs, const uint16_t *w,
+                          uint16_t *residual_out, uint16_t *norm_out, uint32_t hidden,
+                          uint32_t rows, float eps);
+/* A18: shaders/embedding.metal:55-71 */
+void orc_q4_embedding_gather_bf16(const uint32_t *w, const uint16_t *s, const uint16_t *b,
+                                  uint16_t *out, uint32_t token, uint32_t hidden);
+/* A8: shaders/conv1d.metal:40-62 */
+void orc_conv1d_silu_decode_bf16(float *state, const uint16_t *qkv, const uint16_t *w,
+                                 uint16_t *out, uint32_t conv_dim, uint32_t kernel_size);
+/* A9: shaders/gated_delta.metal:147-261 */
+void orc_gated_delta_decode_bf16(float *state, const uint16_t *conv_out, const uint16_t *a,
+                                 const uint16_t *b, const float *A_log, const uint16_t *dt_bias,
+                                 uint16_t *y, uint32_t Hk, uint32_t Hv, uint32_t Dk, uint32_t Dv,
+                                 uint32_t has_previous_state);
+/* A10: shaders/gated_norm.metal:163-189 */
+void orc_rmsnorm_gated_bf16(const uint16_t *x, const uint16_t *w, const uint16_t *gate,
+                            uint16_t *out, uint32_t dim, float eps, uint32_t rows);
+/* A12: shaders/attention.metal:327-421 */
+void orc_attn_decode_prepare_bf16(const uint16_t *packed_q, const uint16_t *q_weight,
+                                  uint16_t *q_out, uint16_t *gate, const uint16_t *k_in,
+                                  const uint16_t *v_in, const uint16_t *k_weight,
+                                  uint16_t *key_dst, uint16_t *value_dst, uint32_t num_heads,
+                                  uint32_t num_kv_heads, uint32_t head_dim, uint32_t rotary_dim,
+                                  uint32_t position_offset, float theta, uint32_t stride,
+                                  uint32_t dst);
+/* A13+A14: shaders/attention_decode.metal:24-243 */
+void orc_attn_decode_bf16(const uint16_t *q, const uint16_t *K, const uint16_t *V,
+                          const uint16_t *gate, uint16_t *out, uint32_t num_q_heads,
+                          uint32_t num_kv_heads, uint32_t stride, uint32_t seq_len, float scale);
+
 #ifdef __cplusplus
 }
 #endif

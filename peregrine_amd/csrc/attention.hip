@@ -1,0 +1,334 @@
+// GQA decode attention: prepare (q/gate split, q/k RMSNorm + RoPE, KV append),
+// split-context flash-decode partials, and the merge + sigmoid-gate reduce.
+//
+// Reference semantics:
+//   prepare   qwen35_q_gate_prepare_kv_append_pair_head_major_value_dim_major_bf16
+//             shaders/attention.metal:327-421 (params :50-60 = block_attn.zig:43-53)
+//   partials  sdpa_decode_prefix_flash_partials_bf16 shaders/attention_decode.metal:24-210
+//   reduce    sdpa_decode_prefix_flash_reduce_gated_bf16 shaders/attention_decode.metal:215-243
+//   compose   FullAttentionBlock.decodeStepBf16 src/model/block_attn.zig:261-359
+//
+// Cache layout (the reference's, src/model/state.zig:41-48): K [kv, stride, 256]
+// token-major, V [kv, 256, stride] value-dim-major.
+//
+// gfx950 partials design: the 4 q heads of a kv head share every K/V byte.
+// Each block owns a contiguous token range of one kv head; the number of
+// ranges is fixed per cache (graph-stable) and sized to put >= 256 blocks on
+// the chip at long context.
+//   phase 1  16 lanes per token (one DPP row), 16 dims per lane as two dwordx4
+//            loads; q.k for 4 heads with v_dot2c_f32_bf16; row-local DPP sum.
+//   phase 2  wave g takes head g: max, exp, sum over the range (scores in LDS).
+//   phase 3  P.V: 8 lanes x 16 B cover 64 consecutive tokens of one V row
+//            (128 B, coalesced); 8 rows per wave load; fp32 FMA with p from
+//            LDS; 8-lane DPP sum at the end.
+#include "attention.hpp"
+
+namespace {
+
+using namespace prg;
+
+constexpr int kAttnThreads = 256;
+
+template <int CTRL>
+__device__ inline float dpp_add(float v) {
+  return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+// Sum over each aligned group of 16 lanes; all 16 lanes get the same bits.
+__device__ inline float row16_sum(float v) {
+  v = dpp_add<0xB1>(v);   // quad_perm [1,0,3,2]
+  v = dpp_add<0x4E>(v);   // quad_perm [2,3,0,1]
+  v = dpp_add<0x141>(v);  // row_half_mirror
+  v = dpp_add<0x140>(v);  // row_mirror
+  return v;
+}
+// Sum over each aligned group of 8 lanes.
+__device__ inline float row8_sum(float v) {
+  v = dpp_add<0xB1>(v);
+  v = dpp_add<0x4E>(v);
+  v = dpp_add<0x141>(v);
+  return v;
+}
+
+__device__ inline float dot2(uint32_t a, uint32_t b, float c) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
+// ------------------------------------------------------------------ prepare --
+__global__ __launch_bounds__(kAttnThreads) void attn_prepare_kernel(const AttnPrepareArgs a) {
+  __shared__ float red[kAttnThreads / kWave];
+  const uint32_t tg = blockIdx.x;
+  const bool use_q = tg < kAttnQHeads;
+  const uint32_t head = use_q ? tg : tg - kAttnQHeads;
+  const uint32_t col = threadIdx.x;  // 256 threads == head_dim
+  const size_t row_base = static_cast<size_t>(head) * kAttnHeadDim;
+  const size_t packed_base = static_cast<size_t>(head) * 2 * kAttnHeadDim;
+  const uint32_t cache_pos = a.step ? a.step->cache_pos : a.cache_pos_host;
+  const uint32_t rope_pos = a.step ? a.step->rope_pos : a.rope_pos_host;
+  const uint16_t* w = use_q ? a.q_norm : a.k_norm;
+
+  const float v = bf2f(use_q ? a.packed_q[packed_base + col] : a.k_in[row_base + col]);
+  if (use_q)
+    a.gate_out[row_base + col] = a.packed_q[packed_base + kAttnHeadDim + col];
+  else
+    a.value_cache[(row_base + col) * a.stride + cache_pos] = a.v_in[row_base + col];
+  const float ss = block_sum<kAttnThreads>(v * v, red);
+  const float inv_rms = rsqrtf(ss / static_cast<float>(kAttnHeadDim) + kAttnEps);
+
+  constexpr uint32_t half = kAttnRotary / 2;
+  uint16_t* dst = use_q ? a.q_out + row_base
+                        : a.key_cache + (static_cast<size_t>(head) * a.stride + cache_pos) * kAttnHeadDim;
+  if (col < half) {
+    // partial NeoX RoPE on dims [0, 64): pairs (i, i + 32); normed values are
+    // rounded to bf16 before rotation (attention.metal:391-392).
+    const float v2 = bf2f(use_q ? a.packed_q[packed_base + col + half] : a.k_in[row_base + col + half]);
+    const float x1 = round_bf(v * inv_rms * bf2f(w[col]));
+    const float x2 = round_bf(v2 * inv_rms * bf2f(w[col + half]));
+    const float inv_freq = powf(kAttnTheta, -(2.0f * static_cast<float>(col)) / static_cast<float>(kAttnRotary));
+    const float angle = static_cast<float>(rope_pos) * inv_freq;
+    const float c = cosf(angle), s = sinf(angle);
+    dst[col] = f2bf(x1 * c - x2 * s);
+    dst[col + half] = f2bf(x2 * c + x1 * s);
+  } else if (col >= kAttnRotary) {
+    dst[col] = f2bf(v * inv_rms * bf2f(w[col]));
+  }
+}
+
+// ----------------------------------------------------------------- partials --
+__global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnDecodeArgs a) {
+  extern __shared__ float sc[];  // [4][split_tokens] scores, then probabilities
+  __shared__ float mh[kAttnGroup], lh[kAttnGroup];
+
+  const uint32_t kvh = blockIdx.y;
+  const uint32_t split = blockIdx.x;
+  const uint32_t L = a.step ? a.step->seq_len : a.seq_len_host;
+  uint32_t chunk = (L + a.nsplit - 1) / a.nsplit;
+  chunk = (chunk + 63u) & ~63u;
+  const uint32_t t0 = split * chunk;
+  const uint32_t t1 = min(t0 + chunk, L);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  float* part = a.partials + (static_cast<size_t>(kvh) * kAttnGroup * a.nsplit + split) * kAttnPartialStride;
+  const size_t head_stride = static_cast<size_t>(a.nsplit) * kAttnPartialStride;
+
+  if (t0 >= t1) {  // empty range: neutral partial
+    for (uint32_t i = threadIdx.x; i < kAttnGroup * kAttnPartialStride; i += kAttnThreads) {
+      const uint32_t g = i / kAttnPartialStride, k = i % kAttnPartialStride;
+      part[g * head_stride + k] = (k == 0) ? -INFINITY : 0.0f;
+    }
+    return;
+  }
+  const uint32_t T = t1 - t0;
+  const uint32_t ld = a.split_tokens;
+
+  // ---- phase 1: scores. lane -> (token row r = lane/16, dims 16*jd .. +16)
+  const int jd = lane & 15, r = lane >> 4;
+  uint32_t qd[kAttnGroup][8];
+#pragma unroll
+  for (int g = 0; g < static_cast<int>(kAttnGroup); ++g) {
+    const uint4* qp = reinterpret_cast<const uint4*>(a.q + (static_cast<size_t>(kvh) * kAttnGroup + g) * kAttnHeadDim + 16 * jd);
+    const uint4 q0 = qp[0], q1 = qp[1];
+    qd[g][0] = q0.x; qd[g][1] = q0.y; qd[g][2] = q0.z; qd[g][3] = q0.w;
+    qd[g][4] = q1.x; qd[g][5] = q1.y; qd[g][6] = q1.z; qd[g][7] = q1.w;
+  }
+  const uint16_t* kbase = a.key_cache + static_cast<size_t>(kvh) * a.stride * kAttnHeadDim + 16 * jd;
+  for (uint32_t tt = 4 * w + r; tt < T; tt += 16) {
+    const uint4* kp = reinterpret_cast<const uint4*>(kbase + static_cast<size_t>(t0 + tt) * kAttnHeadDim);
+    const uint4 k0 = kp[0], k1 = kp[1];
+    const uint32_t kd[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+    float s[kAttnGroup];
+#pragma unroll
+    for (int g = 0; g < static_cast<int>(kAttnGroup); ++g) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc = dot2(qd[g][i], kd[i], acc);
+      s[g] = row16_sum(acc);
+    }
+    if (jd == 0) {
+#pragma unroll
+      for (int g = 0; g < static_cast<int>(kAttnGroup); ++g) sc[g * ld + tt] = s[g] * a.scale;
+    }
+  }
+  __syncthreads();
+
+  // ---- phase 2: softmax statistics, wave g owns head g.
+  {
+    const int g = w;
+    float m = -INFINITY;
+    for (uint32_t t = lane; t < T; t += 64) m = fmaxf(m, sc[g * ld + t]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    float l = 0.0f;
+    for (uint32_t t = lane; t < T; t += 64) {
+      const float s = sc[g * ld + t];
+      const float p = (s == -INFINITY) ? 0.0f : expf(s - m);
+      sc[g * ld + t] = p;
+      l += p;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, 64);
+    if (lane == 0) {
+      mh[g] = m;
+      lh[g] = l;
+    }
+  }
+  __syncthreads();
+
+  // ---- phase 3: P.V. wave w owns dims [64w, 64w+64): 8 passes x 8 rows.
+  const int rr = lane >> 3, ts = lane & 7;
+  float acc[8][kAttnGroup];
+#pragma unroll
+  for (int p = 0; p < 8; ++p)
+#pragma unroll
+    for (int g = 0; g < static_cast<int>(kAttnGroup); ++g) acc[p][g] = 0.0f;
+  const uint16_t* vbase = a.value_cache + (static_cast<size_t>(kvh) * kAttnHeadDim + 64 * w + rr) * a.stride;
+  for (uint32_t tb = 0; tb < T; tb += 64) {
+    const uint32_t tl = tb + 8 * ts;  // first of this lane's 8 tokens (block-local)
+    if (tl >= T) continue;
+    const uint32_t nvalid = min(8u, T - tl);
+    float pv[kAttnGroup][8];
+#pragma unroll
+    for (int g = 0; g < static_cast<int>(kAttnGroup); ++g)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) pv[g][i] = (static_cast<uint32_t>(i) < nvalid) ? sc[g * ld + tl + i] : 0.0f;
+    uint4 vv[8];
+#pragma unroll
+    for (int p = 0; p < 8; ++p)
+      vv[p] = *reinterpret_cast<const uint4*>(vbase + static_cast<size_t>(8 * p) * a.stride + t0 + tl);
+#pragma unroll
+    for (int p = 0; p < 8; ++p) {
+      const uint32_t vd[4] = {vv[p].x, vv[p].y, vv[p].z, vv[p].w};
+      float v8[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        v8[2 * i] = bf_lo(vd[i]);
+        v8[2 * i + 1] = bf_hi(vd[i]);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (static_cast<uint32_t>(i) >= nvalid) v8[i] = 0.0f;  // slots past seq_len may hold anything
+#pragma unroll
+      for (int g = 0; g < static_cast<int>(kAttnGroup); ++g)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[p][g] += pv[g][i] * v8[i];
+    }
+  }
+#pragma unroll
+  for (int p = 0; p < 8; ++p)
+#pragma unroll
+    for (int g = 0; g < static_cast<int>(kAttnGroup); ++g) acc[p][g] = row8_sum(acc[p][g]);
+  if (ts == 0) {
+#pragma unroll
+    for (int p = 0; p < 8; ++p) {
+      const uint32_t d = 64 * w + 8 * p + rr;
+#pragma unroll
+      for (int g = 0; g < static_cast<int>(kAttnGroup); ++g) part[g * head_stride + 2 + d] = acc[p][g];
+    }
+  }
+  if (threadIdx.x < kAttnGroup) {
+    part[threadIdx.x * head_stride + 0] = mh[threadIdx.x];
+    part[threadIdx.x * head_stride + 1] = lh[threadIdx.x];
+  }
+}
+
+// ------------------------------------------------------------------- reduce --
+__global__ __launch_bounds__(kAttnThreads) void attn_reduce_kernel(const AttnDecodeArgs a) {
+  const uint32_t h = blockIdx.x;  // q head
+  const uint32_t d = threadIdx.x;
+  const float* base = a.partials + static_cast<size_t>(h) * a.nsplit * kAttnPartialStride;
+  float m_all = -INFINITY;
+  for (uint32_t c = 0; c < a.nsplit; ++c) m_all = fmaxf(m_all, base[c * kAttnPartialStride]);
+  float den = 0.0f, acc = 0.0f;
+  for (uint32_t c = 0; c < a.nsplit; ++c) {
+    const float* pc = base + c * kAttnPartialStride;
+    const float wgt = (pc[0] == -INFINITY) ? 0.0f : expf(pc[0] - m_all);
+    den += pc[1] * wgt;
+    acc += pc[2 + d] * wgt;
+  }
+  const size_t i = static_cast<size_t>(h) * kAttnHeadDim + d;
+  const float sig = 1.0f / (1.0f + expf(-bf2f(a.gate[i])));
+  a.out[i] = f2bf((acc / den) * sig);
+}
+
+}  // namespace
+
+namespace prg {
+
+uint32_t attn_num_splits(uint32_t capacity) {
+  // >= 64 splits per kv head (256 blocks) and <= 1024 tokens per split.
+  uint32_t n = 64;
+  while ((capacity + n - 1) / n > 1024) n *= 2;
+  return n;
+}
+
+uint32_t attn_split_tokens(uint32_t capacity, uint32_t nsplit) {
+  const uint32_t c = (capacity + nsplit - 1) / nsplit;
+  return (c + 63u) & ~63u;
+}
+
+int launch_attn_prepare(hipStream_t s, const AttnPrepareArgs& a) {
+  hipLaunchKernelGGL(attn_prepare_kernel, dim3(kAttnQHeads + kAttnKvHeads), dim3(kAttnThreads), 0, s, a);
+  PRG_CHECK_LAUNCH("attn_prepare");
+  return PRG_OK;
+}
+
+int launch_attn_decode(hipStream_t s, const AttnDecodeArgs& a) {
+  const size_t lds = static_cast<size_t>(kAttnGroup) * a.split_tokens * sizeof(float);
+  hipLaunchKernelGGL(attn_partials_kernel, dim3(a.nsplit, kAttnKvHeads), dim3(kAttnThreads), lds, s, a);
+  PRG_CHECK_LAUNCH("attn_partials");
+  hipLaunchKernelGGL(attn_reduce_kernel, dim3(kAttnQHeads), dim3(kAttnHeadDim), 0, s, a);
+  PRG_CHECK_LAUNCH("attn_reduce");
+  return PRG_OK;
+}
+
+}  // namespace prg
+
+extern "C" {
+
+int prg_attn_decode_prepare_bf16(void* stream, const uint16_t* packed_q, const uint16_t* q_weight,
+                                 uint16_t* q_output, uint16_t* gate, const uint16_t* k_input,
+                                 const uint16_t* v_input, const uint16_t* k_weight,
+                                 uint16_t* key_cache, uint16_t* value_cache,
+                                 uint32_t cache_stride_tokens, uint32_t dst_token_index,
+                                 uint32_t position_offset) {
+  PRG_CHECK_ARG(packed_q && q_weight && q_output && gate && k_input && v_input && k_weight && key_cache && value_cache,
+                "prg_attn_decode_prepare_bf16: null pointer");
+  if (dst_token_index >= cache_stride_tokens)
+    return prg::set_error(PRG_ERR_SEQUENCE_TOO_LONG, "prg_attn_decode_prepare_bf16: dst %u >= stride %u",
+                          dst_token_index, cache_stride_tokens);
+  prg::AttnPrepareArgs a{packed_q, q_weight, k_input, v_input, k_weight, q_output, gate, key_cache, value_cache,
+                         cache_stride_tokens, dst_token_index, position_offset, nullptr};
+  return prg::launch_attn_prepare(prg::as_stream(stream), a);
+}
+
+int prg_attn_decode_bf16(void* stream, const uint16_t* q, const uint16_t* key_cache,
+                         const uint16_t* value_cache, const uint16_t* gate, uint16_t* out,
+                         float* partials, uint32_t cache_stride_tokens, uint32_t seq_len,
+                         float scale) {
+  PRG_CHECK_ARG(q && key_cache && value_cache && gate && out && partials, "prg_attn_decode_bf16: null pointer");
+  PRG_CHECK_ARG(cache_stride_tokens % 64 == 0, "prg_attn_decode_bf16: stride %u must be a multiple of 64",
+                cache_stride_tokens);
+  if (seq_len == 0 || seq_len > cache_stride_tokens)
+    return prg::set_error(PRG_ERR_SEQUENCE_TOO_LONG, "prg_attn_decode_bf16: seq_len %u outside (0, %u]", seq_len,
+                          cache_stride_tokens);
+  prg::AttnDecodeArgs a{};
+  a.q = q;
+  a.key_cache = key_cache;
+  a.value_cache = value_cache;
+  a.gate = gate;
+  a.out = out;
+  a.partials = partials;
+  a.stride = cache_stride_tokens;
+  a.nsplit = prg::attn_num_splits(cache_stride_tokens);
+  a.split_tokens = prg::attn_split_tokens(cache_stride_tokens, a.nsplit);
+  a.seq_len_host = seq_len;
+  a.step = nullptr;
+  a.scale = scale;
+  return prg::launch_attn_decode(prg::as_stream(stream), a);
+}
+
+size_t prg_attn_decode_partials_bytes(uint32_t cache_stride_tokens) {
+  const uint32_t n = prg::attn_num_splits(cache_stride_tokens);
+  return static_cast<size_t>(prg::kAttnQHeads) * n * prg::kAttnPartialStride * sizeof(float);
+}
+
+}  // extern "C"

@@ -1,0 +1,61 @@
+// GQA decode attention for the Qwen3.5 full-attention layers — declarations.
+#pragma once
+
+#include "common.hpp"
+
+namespace prg {
+
+// reference src/model/block_attn.zig:21-28, shaders/attention.metal:43-48
+constexpr uint32_t kAttnQHeads = 16;
+constexpr uint32_t kAttnKvHeads = 4;
+constexpr uint32_t kAttnGroup = kAttnQHeads / kAttnKvHeads;  // 4
+constexpr uint32_t kAttnHeadDim = 256;
+constexpr uint32_t kAttnRotary = 64;
+constexpr float kAttnTheta = 1.0e7f;
+constexpr float kAttnEps = 1.0e-6f;
+constexpr float kAttnScale = 1.0f / 16.0f;
+constexpr uint32_t kAttnPartialStride = kAttnHeadDim + 2;  // [m, denom, acc[256]]
+
+// Split-context count for a cache of `capacity` tokens: every kv head is split
+// into this many contiguous token ranges (one block each), fixed per cache so a
+// captured graph stays valid as seq_len grows.
+uint32_t attn_num_splits(uint32_t capacity);
+// Largest per-split token range (rounded to 64) for a cache of `capacity`.
+uint32_t attn_split_tokens(uint32_t capacity, uint32_t nsplit);
+
+struct AttnPrepareArgs {
+  const uint16_t* packed_q;  // [16, 512] = q(256) | gate(256) per head
+  const uint16_t* q_norm;    // [256]
+  const uint16_t* k_in;      // [4, 256]
+  const uint16_t* v_in;      // [4, 256]
+  const uint16_t* k_norm;    // [256]
+  uint16_t* q_out;           // [16, 256]
+  uint16_t* gate_out;        // [16, 256]
+  uint16_t* key_cache;       // [4, stride, 256]
+  uint16_t* value_cache;     // [4, 256, stride]
+  uint32_t stride;           // cache capacity in tokens
+  uint32_t cache_pos_host;   // used when step == nullptr
+  uint32_t rope_pos_host;
+  const StepScalars* step;   // device scalars (graph replay) or nullptr
+};
+
+int launch_attn_prepare(hipStream_t s, const AttnPrepareArgs& a);
+
+struct AttnDecodeArgs {
+  const uint16_t* q;          // [16, 256] prepared queries
+  const uint16_t* key_cache;  // [4, stride, 256]
+  const uint16_t* value_cache;  // [4, 256, stride]
+  const uint16_t* gate;       // [16, 256]
+  uint16_t* out;              // [16, 256]
+  float* partials;            // [16, nsplit, 258]
+  uint32_t stride;
+  uint32_t nsplit;
+  uint32_t split_tokens;      // LDS sizing bound (>= ceil(seq_len/nsplit) rounded to 64)
+  uint32_t seq_len_host;      // used when step == nullptr
+  const StepScalars* step;
+  float scale;
+};
+
+int launch_attn_decode(hipStream_t s, const AttnDecodeArgs& a);
+
+}  // namespace prg

@@ -15,6 +15,16 @@ namespace prg {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+// Per-decode-step scalars. The decode graph keeps them in device memory so one
+// captured graph serves every position; kernels read them at run time.
+// (Names follow DeviceModel.forwardNextToken's arguments, model.zig:1564-1575.)
+struct StepScalars {
+  uint32_t token;      // input token id
+  uint32_t cache_pos;  // KV slot written this step
+  uint32_t rope_pos;   // RoPE position; GDN state is used iff rope_pos != 0
+  uint32_t seq_len;    // tokens attended (cache_pos + 1 without a prefix)
+};
+
 // ---------------------------------------------------------------- bf16 -------
 __host__ __device__ inline float bf2f(uint16_t b) {
   return __uint_as_float(static_cast<uint32_t>(b) << 16);

@@ -24,6 +24,8 @@
 #pragma once
 
 #include "common.hpp"
+#include "norm.hpp"
+#include "gdn.hpp"
 
 namespace prg {
 
@@ -48,6 +50,13 @@ struct GemvSeg {
   const uint16_t* res[2];     // per activation row m (residual epilogue)
   float* pval[2];             // per activation row m (argmax epilogue)
   uint32_t* pidx[2];
+  // Optional conv1d+SiLU epilogue (plain epilogue, M == 1): the bf16 GEMV
+  // output x of row c feeds the depthwise causal conv of channel c, whose f32
+  // state [3, conv_dim] is rolled in place; out receives the conv output.
+  // This fuses in_proj_qkv with conv1d_silu_decode_bf16 (block_linear.zig:230-240).
+  float* conv_state;
+  const uint16_t* conv_w;     // bf16 [conv_dim, 4]
+  uint32_t conv_dim;
   uint32_t rows;              // output rows of this segment
   uint32_t block_begin;       // first block index of this segment
 };
@@ -107,34 +116,11 @@ __device__ inline void gemv_stage_x(const GemvParams& p, uint32_t* xs, float* re
     const uint4* src = reinterpret_cast<const uint4*>(p.x[m]);
     uint4* dst = reinterpret_cast<uint4*>(xs + m * (p.K / 2));
     if constexpr (NORM) {
-      float ss = 0.0f;
-      for (uint32_t g = threadIdx.x; g < n8; g += kGemvThreads) {
-        const uint4 v = src[g];
-        const uint32_t d[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float a = bf_lo(d[i]), b = bf_hi(d[i]);
-          ss += a * a;
-          ss += b * b;
-        }
-      }
-      const float total = block_sum<kGemvThreads>(ss, red);
-      const float scale = 1.0f / sqrtf(total / static_cast<float>(p.K) + p.eps);
+      static_assert(kGemvThreads == kNormThreads, "fused norm shares the standalone reduction");
+      const float scale = rms_scale(src, n8, p.K, p.eps, red);
       const uint4* wsrc = reinterpret_cast<const uint4*>(p.norm_w);
-      for (uint32_t g = threadIdx.x; g < n8; g += kGemvThreads) {
-        const uint4 v = src[g];
-        const uint4 w = wsrc[g];
-        const uint32_t d[4] = {v.x, v.y, v.z, v.w};
-        const uint32_t e[4] = {w.x, w.y, w.z, w.w};
-        uint32_t o[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const uint32_t lo = f2bf(bf_lo(d[i]) * scale * bf_lo(e[i]));
-          const uint32_t hi = f2bf(bf_hi(d[i]) * scale * bf_hi(e[i]));
-          o[i] = lo | (hi << 16);
-        }
-        dst[g] = permute_pairs(make_uint4(o[0], o[1], o[2], o[3]));
-      }
+      for (uint32_t g = threadIdx.x; g < n8; g += kGemvThreads)
+        dst[g] = permute_pairs(rms_apply(src[g], wsrc[g], scale));
     } else {
       for (uint32_t g = threadIdx.x; g < n8; g += kGemvThreads) dst[g] = permute_pairs(src[g]);
     }
@@ -294,7 +280,10 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(const GemvParams 
       for (int m = 0; m < M; ++m) {
         uint16_t o;
         if constexpr (EPI == kEpiPlain) {
-          o = f2bf(tot[0][r][m]);
+          if (M == 1 && sg.conv_state != nullptr)
+            o = conv1d_silu_step(sg.conv_state, sg.conv_w, sg.conv_dim, row, round_bf(tot[0][r][m]));
+          else
+            o = f2bf(tot[0][r][m]);
         } else if constexpr (EPI == kEpiResidual) {
           o = f2bf(round_bf(tot[0][r][m]) + bf2f(sg.res[m][row]));
         } else {

@@ -83,3 +83,59 @@ def gate_up_silu2(gate: Q4Linear, up: Q4Linear, x0, x1, o0, o1, stream=None) -> 
 # argmax.zig:14-35
 def argmax_pairs(pval, pidx, out_index, pair_count: int, stream=None) -> None:
     call("prg_argmax_pairs_f32_u32", _s(stream), ptr(pval), ptr(pidx), ptr(out_index), pair_count)
+
+
+# ------------------------------------------------------------ norms / embed
+def rmsnorm(x, w, out, hidden: int, rows: int = 1, eps: float = 1e-6, stream=None) -> None:
+    call("prg_rmsnorm_bf16", _s(stream), ptr(x), ptr(w), ptr(out), hidden, rows, eps)
+
+
+def add_rmsnorm(a, b, w, residual_out, norm_out, hidden: int, rows: int = 1, eps: float = 1e-6,
+                stream=None) -> None:
+    call("prg_add_rmsnorm_bf16", _s(stream), ptr(a), ptr(b), ptr(w), ptr(residual_out), ptr(norm_out), hidden,
+         rows, eps)
+
+
+def embedding_gather(table: Q4Linear, token: int, out, stream=None) -> None:
+    call("prg_q4_embedding_gather_bf16", _s(stream), *table._wsb(), ptr(out), int(token), table.in_dim,
+         table.out_dim)
+
+
+# ----------------------------------------------------------------- GDN ops
+def conv1d_silu_decode(state, qkv, w, out, conv_dim: int = 8192, stream=None) -> None:
+    call("prg_conv1d_silu_decode_bf16", _s(stream), ptr(state), ptr(qkv), ptr(w), ptr(out), conv_dim, 4)
+
+
+def gated_delta_decode(state, conv_out, a, b, A_log, dt_bias, y, has_previous_state: bool = True,
+                       stream=None) -> None:
+    call("prg_gated_delta_decode_bf16", _s(stream), ptr(state), ptr(conv_out), ptr(a), ptr(b), ptr(A_log),
+         ptr(dt_bias), ptr(y), 16, 32, 128, 128, 8192, int(bool(has_previous_state)))
+
+
+def gated_delta_decode_norm(state, conv_out, a, b, A_log, dt_bias, norm_w, z, out, eps: float = 1e-6,
+                            has_previous_state: bool = True, stream=None) -> None:
+    call("prg_gated_delta_decode_norm_bf16", _s(stream), ptr(state), ptr(conv_out), ptr(a), ptr(b), ptr(A_log),
+         ptr(dt_bias), ptr(norm_w), ptr(z), ptr(out), eps, int(bool(has_previous_state)))
+
+
+def rmsnorm_gated(x, w, gate, out, dim: int = 128, rows: int = 32, eps: float = 1e-6, stream=None) -> None:
+    call("prg_rmsnorm_gated_bf16", _s(stream), ptr(x), ptr(w), ptr(gate), ptr(out), dim, eps, rows)
+
+
+# ----------------------------------------------------------- attention ops
+def attn_decode_prepare(packed_q, q_w, q_out, gate, k_in, v_in, k_w, key_cache, value_cache, stride: int,
+                        dst: int, pos: int, stream=None) -> None:
+    call("prg_attn_decode_prepare_bf16", _s(stream), ptr(packed_q), ptr(q_w), ptr(q_out), ptr(gate), ptr(k_in),
+         ptr(v_in), ptr(k_w), ptr(key_cache), ptr(value_cache), stride, dst, pos)
+
+
+def attn_partials_bytes(stride: int) -> int:
+    from ._lib import lib
+
+    return int(lib.prg_attn_decode_partials_bytes(stride))
+
+
+def attn_decode(q, key_cache, value_cache, gate, out, partials, stride: int, seq_len: int,
+                scale: float = 1.0 / 16.0, stream=None) -> None:
+    call("prg_attn_decode_bf16", _s(stream), ptr(q), ptr(key_cache), ptr(value_cache), ptr(gate), ptr(out),
+         ptr(partials), stride, seq_len, scale)
