@@ -129,6 +129,21 @@ int prg_q4_gemv_silu_gate2_bf16(void *stream, const uint16_t *x0, const uint16_t
                                 uint16_t *out0, uint16_t *out1, uint32_t out_dim,
                                 uint32_t in_dim);
 
+/* RMSNorm fused into the GEMV prologue: y = bf16(W . bf16(x * rsqrt(mean(x^2)
+ * + eps) * norm_w)) for one activation row; several blocks' norms become one
+ * dispatch with their projection (decoder_layer.zig:419-437 + linear_q4.zig:77-95). */
+int prg_q4_gemv_norm_bf16(void *stream, const uint16_t *x, const uint16_t *norm_weight, float eps,
+                          const uint32_t *w, const uint16_t *scales, const uint16_t *biases,
+                          uint16_t *y, uint32_t out_dim, uint32_t in_dim);
+
+/* post_attention_layernorm fused with the gate/up SiLU GEMV
+ * (decoder_layer.zig:756-781 + block_mlp.zig:313-345). */
+int prg_q4_gemv_silu_gate_norm_bf16(void *stream, const uint16_t *x, const uint16_t *norm_weight,
+                                    float eps, const uint32_t *gate_w, const uint16_t *gate_s,
+                                    const uint16_t *gate_b, const uint32_t *up_w,
+                                    const uint16_t *up_s, const uint16_t *up_b, uint16_t *out,
+                                    uint32_t out_dim, uint32_t in_dim);
+
 /* lm_head partial argmax: logits are bf16-rounded dots; partial p covers rows
  * [8p, 8p+8) and holds the first strict maximum in row order.
  * partial_values f32 [out_dim/8], partial_indices u32 [out_dim/8].

@@ -1,0 +1,120 @@
+/*
+ * peregrine_model.h — C ABI of the decode model layer in libperegrine_hip.so.
+ *
+ * Replaces the reference's Zig model composition for the single-stream Q4
+ * token loop:
+ *   DeviceModel            src/model/model.zig:538-790, 1326-1460, 1564-1662
+ *   ModelState             src/model/state.zig:45-180
+ *   DecoderLayer           src/model/decoder_layer.zig:461-566, 756-819
+ *   LinearAttentionBlock   src/model/block_linear.zig:199-263
+ *   FullAttentionBlock     src/model/block_attn.zig:261-359
+ *   MlpBlock               src/model/block_mlp.zig:260-311
+ *   decodeFromPrefixCache  src/server/decode_loop.zig:96-160 (no prefix)
+ * The checkpoint loader is out of scope: models are random-initialised on the
+ * GPU from a seed, in the reference's tensor layout and names.
+ * All functions return 0 or a PRG_ERR_* code (see peregrine_hip.h).
+ */
+#ifndef PEREGRINE_MODEL_H
+#define PEREGRINE_MODEL_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct PrgModel PrgModel;
+typedef struct PrgModelState PrgModelState;
+
+/* Model shape. The attention / GDN head geometry is fixed by the kernels
+ * (16 q / 4 kv heads x 256; GDN 16 k / 32 v heads x 128, conv 4). */
+typedef struct PrgModelConfig {
+  uint32_t num_layers;              /* 32 */
+  uint32_t hidden;                  /* 4096, multiple of 512 */
+  uint32_t intermediate;            /* 12288, multiple of 512 */
+  uint32_t vocab;                   /* 248320, multiple of 8 */
+  uint32_t full_attention_interval; /* 4: layer i is full attention iff (i+1) % 4 == 0 */
+  float rms_eps;                    /* 1e-6 */
+} PrgModelConfig;
+
+/* Qwen3.5-9B shape (src/model/config.zig:58-72, dims.zig:3-7). */
+void prg_model_default_config(PrgModelConfig *cfg);
+
+/* Allocate and randomly initialise a model on the current device.
+ * Q4 weights: nibbles uniform 0..15, scales ~U(0.002, 0.02), biases
+ * -7.5*scale + N(0, 0.01) (zero-mean dequantised weights); norm weights
+ * 1 + N(0, 0.1); conv weights N(0, 0.5); A_log, dt_bias N(0, 0.5).
+ * Replaces DeviceModel.upload (model.zig:580-658). */
+int prg_model_create_random(const PrgModelConfig *cfg, uint64_t seed, PrgModel **out);
+void prg_model_destroy(PrgModel *model);
+/* Total bytes of device weights. */
+size_t prg_model_weight_bytes(const PrgModel *model);
+/* Device pointer and byte size of a named tensor, e.g.
+ * "language_model.model.layers.3.self_attn.q_proj.weight" (names as the
+ * reference's checkpoint, decoder_layer.zig:376-412). */
+int prg_model_tensor(const PrgModel *model, const char *name, void **ptr, size_t *bytes);
+
+/* Per-sequence state for up to max_seq tokens: GDN conv f32 [3, 8192] and
+ * recurrent f32 [32, 128, 128] per linear layer, bf16 K [4, stride, 256] and
+ * V [4, 256, stride] per full-attention layer (stride = max_seq aligned to 256,
+ * or 64 when max_seq >= 16000, state.zig:25-32), plus the decode workspace.
+ * Replaces ModelState.initBf16FullCaches (state.zig:52-90). */
+int prg_model_state_create(PrgModel *model, uint32_t max_seq, PrgModelState **out);
+void prg_model_state_destroy(PrgModelState *state);
+/* Zero the GDN states (ModelState.resetForNewSequence, state.zig:110-118). */
+int prg_model_state_reset(PrgModelState *state);
+/* Device pointer of a state tensor: "layers.<i>.conv", "layers.<i>.recur",
+ * "layers.<i>.cache_k", "layers.<i>.cache_v"; or of a workspace buffer. */
+int prg_model_state_tensor(const PrgModelState *state, const char *name, void **ptr, size_t *bytes);
+uint32_t prg_model_state_stride(const PrgModelState *state);
+
+/* One token through the whole stack and the greedy argmax tail, synchronous.
+ * cache_pos: KV slot written; rope_pos: RoPE position (GDN state is used iff
+ * rope_pos != 0); seq_len: tokens attended (must be cache_pos + 1: prefix
+ * caches are not supported). Errors: SEQUENCE_TOO_LONG, INVALID_TOKEN.
+ * Replaces DeviceModel.forwardNextTokenBf16WithPrefix (model.zig:1564-1578). */
+int prg_model_forward_next_token(PrgModel *model, PrgModelState *state, uint32_t token,
+                                 uint32_t cache_pos, uint32_t rope_pos, uint32_t seq_len,
+                                 uint32_t *next_token);
+
+/* Reset the state and ingest prompt[0..prompt_len) at positions 0.. (the lm_head
+ * runs only on the last prompt token). *next_token receives the greedy token
+ * that follows the prompt; the state is then positioned to decode it.
+ * Replaces the prompt half of the serving path (prefill + first token,
+ * model.zig:1201-1238) with per-token steps. */
+int prg_model_prefill(PrgModel *model, PrgModelState *state, const uint32_t *prompt,
+                      uint32_t prompt_len, uint32_t *next_token);
+
+/* Continue the greedy loop for n_steps tokens from the current state,
+ * device-resident (graph replay, no host sync between tokens). tokens_out (host,
+ * n_steps) receives the greedy token produced by each step; gpu_ms (optional)
+ * the GPU time of the n_steps steps from HIP events on the decode stream.
+ * Replaces decode_loop.decodeFromPrefixCache (decode_loop.zig:96-160). */
+int prg_model_decode(PrgModel *model, PrgModelState *state, uint32_t n_steps, uint32_t *tokens_out,
+                     float *gpu_ms);
+
+/* Greedy generation from an empty state, the whole loop device-resident (one
+ * captured HIP graph per token, no host sync between tokens). Step n consumes
+ * the token at position n.
+ *   teacher_force == 0: steps n = 0 .. prompt_len + n_new - 2. The inputs are
+ *     prompt[n] while n < prompt_len, then the previous step's greedy token.
+ *     Steps before prompt_len - 1 skip the lm_head (prompt ingestion).
+ *     predictions (host, prompt_len - 1 + n_new entries) receives the greedy
+ *     token after position n for every step that ran the lm_head (others are
+ *     0xFFFFFFFF); the generated tokens are predictions[prompt_len - 1 ..].
+ *   teacher_force != 0: n_new must be 0; steps n = 0 .. prompt_len - 1 all take
+ *     prompt[n] as input and all run the lm_head (predictions: prompt_len).
+ * decode_ms (optional): GPU time of the steps that ran the lm_head after the
+ * prompt (the n_new generation steps), from HIP events on the decode stream.
+ * Replaces decode_loop.decodeFromPrefixCache (decode_loop.zig:96-160) for an
+ * empty prefix. */
+int prg_model_generate(PrgModel *model, PrgModelState *state, const uint32_t *prompt,
+                       uint32_t prompt_len, uint32_t n_new, int teacher_force,
+                       uint32_t *predictions, float *decode_ms);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,129 @@
+"""TEST INFRASTRUCTURE: CPU restatement of the reference's decode composition.
+
+Orchestrates the C oracle primitives exactly as the reference's Zig host code
+dispatches its kernels for one token, without any of the GPU build's fusions:
+  DecoderLayer.decodeStepBf16          src/model/decoder_layer.zig:461-566, 756-781
+  LinearAttentionBlock.decodeStepBf16  src/model/block_linear.zig:199-263
+  FullAttentionBlock.decodeStepBf16    src/model/block_attn.zig:261-359
+  MlpBlock.decodeResidualBf16          src/model/block_mlp.zig:260-277
+  encodeStackBf16 + argmax tail        src/model/model.zig:686-717, 1346-1388
+  decodeFromPrefixCache (no prefix)    src/server/decode_loop.zig:96-160
+Weights are read back from the GPU model (same bits on both sides).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from peregrine_amd.synth import Q4Weight, bf16_to_f32
+
+from .binding import oracle
+
+ROOT = "language_model.model"
+
+
+def _q4(model, base: str, out_dim: int, in_dim: int) -> Q4Weight:
+    w = model.read(base + ".weight", np.uint32).reshape(out_dim, in_dim // 8)
+    s = model.read(base + ".scales", np.uint16).reshape(out_dim, in_dim // 64)
+    b = model.read(base + ".biases", np.uint16).reshape(out_dim, in_dim // 64)
+    return Q4Weight(w, s, b)
+
+
+class OracleModel:
+    def __init__(self, model, max_seq: int) -> None:
+        """model: peregrine_amd.model.DeviceModel (weights are copied to host)."""
+        c = model.cfg
+        self.cfg = c
+        self.o = oracle()
+        self.embed = _q4(model, ROOT + ".embed_tokens", c.vocab, c.hidden)
+        self.layers = []
+        for i in range(c.num_layers):
+            p = f"{ROOT}.layers.{i}"
+            L = {"linear": c.is_linear(i),
+                 "input_norm": model.read(p + ".input_layernorm.weight", np.uint16),
+                 "post_norm": model.read(p + ".post_attention_layernorm.weight", np.uint16),
+                 "gate": _q4(model, p + ".mlp.gate_proj", c.intermediate, c.hidden),
+                 "up": _q4(model, p + ".mlp.up_proj", c.intermediate, c.hidden),
+                 "down": _q4(model, p + ".mlp.down_proj", c.hidden, c.intermediate)}
+            if L["linear"]:
+                a = p + ".linear_attn"
+                L.update(qkv=_q4(model, a + ".in_proj_qkv", 8192, c.hidden),
+                         z=_q4(model, a + ".in_proj_z", 4096, c.hidden),
+                         a=_q4(model, a + ".in_proj_a", 32, c.hidden),
+                         b=_q4(model, a + ".in_proj_b", 32, c.hidden),
+                         out=_q4(model, a + ".out_proj", c.hidden, 4096),
+                         conv_w=model.read(a + ".conv1d.weight", np.uint16).reshape(8192, 4),
+                         A_log=model.read(a + ".A_log", np.float32),
+                         dt_bias=model.read(a + ".dt_bias", np.uint16),
+                         norm_w=model.read(a + ".norm.weight", np.uint16))
+            else:
+                a = p + ".self_attn"
+                L.update(q=_q4(model, a + ".q_proj", 8192, c.hidden),
+                         k=_q4(model, a + ".k_proj", 1024, c.hidden),
+                         v=_q4(model, a + ".v_proj", 1024, c.hidden),
+                         o=_q4(model, a + ".o_proj", c.hidden, 4096),
+                         q_norm=model.read(a + ".q_norm.weight", np.uint16),
+                         k_norm=model.read(a + ".k_norm.weight", np.uint16))
+            self.layers.append(L)
+        self.final_norm = model.read(ROOT + ".norm.weight", np.uint16)
+        self.lm_head = _q4(model, "language_model.lm_head", c.vocab, c.hidden)
+        a = 64 if max_seq >= 16000 else 256
+        self.stride = (max_seq + a - 1) // a * a  # state.zig:25-32
+        self.reset()
+
+    def reset(self) -> None:  # state.zig:52-90 (zeroed), resetForNewSequence
+        self.state = []
+        for L in self.layers:
+            if L["linear"]:
+                self.state.append({"conv": np.zeros((3, 8192), np.float32),
+                                   "recur": np.zeros((32, 128, 128), np.float32)})
+            else:
+                self.state.append({"k": np.zeros((4, self.stride, 256), np.uint16),
+                                   "v": np.zeros((4, 256, self.stride), np.uint16)})
+
+    def _layer(self, i: int, h: np.ndarray, pos: int) -> np.ndarray:
+        o, L, S, eps = self.o, self.layers[i], self.state[i], self.cfg.rms_eps
+        normed = o.rmsnorm(h, L["input_norm"], eps)[0]            # decoder_layer.zig:531
+        if L["linear"]:                                            # block_linear.zig:222-262
+            qkv = o.q4_gemv(normed, L["qkv"])[0]
+            z = o.q4_gemv(normed, L["z"])[0]
+            a = o.q4_gemv(normed, L["a"])[0]
+            b = o.q4_gemv(normed, L["b"])[0]
+            conv_out, S["conv"] = o.conv1d_decode(S["conv"], qkv, L["conv_w"])
+            y, S["recur"] = o.gated_delta_decode(S["recur"], conv_out, a, b, L["A_log"], L["dt_bias"],
+                                                 has_prev=pos != 0)  # decoder_layer.zig:564
+            gated = o.rmsnorm_gated(y, L["norm_w"], z, 128, eps)
+            attn = o.q4_gemv(gated, L["out"])[0]
+        else:                                                      # block_attn.zig:312-358
+            qp = o.q4_gemv(normed, L["q"])[0]
+            k = o.q4_gemv(normed, L["k"])[0]
+            v = o.q4_gemv(normed, L["v"])[0]
+            q, gate, S["k"], S["v"] = o.attn_prepare(qp, L["q_norm"], k, v, L["k_norm"], S["k"], S["v"],
+                                                     self.stride, dst=pos, pos=pos)
+            ctx = o.attn_decode(q, S["k"], S["v"], gate, self.stride, pos + 1)
+            attn = o.q4_gemv(ctx, L["o"])[0]
+        r, normed2 = o.add_rmsnorm(h, attn, L["post_norm"], eps)   # decoder_layer.zig:772
+        inter = o.q4_gemv_silu_gate(normed2, L["gate"], L["up"])   # block_mlp.zig:272
+        return o.q4_gemv_residual_add(inter, L["down"], r)[0]      # block_mlp.zig:276
+
+    def step(self, token: int, pos: int, want_logits: bool = False):
+        """One decode step at position pos; returns (next_token, logits|None)."""
+        o = self.o
+        h = o.embedding(self.embed, token)                          # model.zig:700
+        for i in range(len(self.layers)):
+            h = self._layer(i, h, pos)
+        normed = o.rmsnorm(h, self.final_norm, self.cfg.rms_eps)[0]  # model.zig:1355
+        pv, pi = o.q4_argmax_partial(normed, self.lm_head)          # model.zig:1386
+        tok = o.argmax_pairs(pv[0], pi[0])                          # model.zig:1387
+        logits = None
+        if want_logits:
+            logits = bf16_to_f32(o.q4_gemv(normed, self.lm_head)[0])
+        return tok, logits
+
+    def teacher_forced(self, tokens, want_logits: bool = False):
+        self.reset()
+        preds, logits = [], []
+        for pos, t in enumerate(tokens):
+            tok, lg = self.step(int(t), pos, want_logits)
+            preds.append(tok)
+            logits.append(lg)
+        return np.array(preds, np.uint32), logits

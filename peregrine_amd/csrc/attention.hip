@@ -66,6 +66,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_prepare_kernel(const AttnPr
   const uint32_t cache_pos = a.step ? a.step->cache_pos : a.cache_pos_host;
   const uint32_t rope_pos = a.step ? a.step->rope_pos : a.rope_pos_host;
   const uint16_t* w = use_q ? a.q_norm : a.k_norm;
+  if (cache_pos >= a.stride) return;  // never write outside the cache (host checks first)
 
   const float v = bf2f(use_q ? a.packed_q[packed_base + col] : a.k_in[row_base + col]);
   if (use_q)
@@ -101,7 +102,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnD
 
   const uint32_t kvh = blockIdx.y;
   const uint32_t split = blockIdx.x;
-  const uint32_t L = a.step ? a.step->seq_len : a.seq_len_host;
+  const uint32_t L = min(a.step ? a.step->seq_len : a.seq_len_host, a.stride);
   uint32_t chunk = (L + a.nsplit - 1) / a.nsplit;
   chunk = (chunk + 63u) & ~63u;
   const uint32_t t0 = split * chunk;

@@ -25,6 +25,19 @@ struct StepScalars {
   uint32_t seq_len;    // tokens attended (cache_pos + 1 without a prefix)
 };
 
+// Device-resident control block of the token loop (decode_loop.zig:96-160
+// without a prefix): step n consumes tokens[n] at position n and records the
+// greedy prediction for position n+1 in predictions[n]. While n+1 < prompt_len
+// the next input is forced to prompt[n+1] (prompt ingestion / teacher forcing),
+// afterwards it is the prediction itself.
+struct DecodeCtl {
+  StepScalars s;
+  uint32_t n;
+  uint32_t prompt_len;
+  uint32_t capacity;  // KV cache slots; positions never advance past it
+  uint32_t overflow;  // set when a step would have exceeded capacity
+};
+
 // ---------------------------------------------------------------- bf16 -------
 __host__ __device__ inline float bf2f(uint16_t b) {
   return __uint_as_float(static_cast<uint32_t>(b) << 16);

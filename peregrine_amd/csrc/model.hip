@@ -1,0 +1,732 @@
+// Decode model layer: weights, per-sequence state, the per-token kernel
+// sequence, and the device-resident greedy token loop.
+//
+// Mirrors the reference's composition (file:line in the reference tree):
+//   DeviceModel.encodeStackBf16 / encodeNextTokenBf16     src/model/model.zig:686-809
+//   DecoderLayer.decodeStepBf16                           src/model/decoder_layer.zig:461-566, 756-781
+//   LinearAttentionBlock.decodeStepBf16                   src/model/block_linear.zig:199-263
+//   FullAttentionBlock.decodeStepBf16                     src/model/block_attn.zig:261-359
+//   MlpBlock.decodeResidualBf16                           src/model/block_mlp.zig:260-277
+//   encodeArgmaxFromHiddenBf16 (final norm, lm_head, argmax) src/model/model.zig:1346-1388
+//   ModelState (GDN conv/recurrent state, bf16 KV caches)  src/model/state.zig:11-118
+//   decodeFromPrefixCache                                 src/server/decode_loop.zig:96-160
+//
+// Where the reference runs a separate dispatch for a norm, a residual add or
+// the conv, this layer fuses it into the neighbouring kernel with the same
+// rounding points:
+//   input_layernorm / post_attention_layernorm / final norm -> GEMV prologue
+//   conv1d_silu_decode -> in_proj_qkv GEMV epilogue
+//   add_rmsnorm's add (bf16(x + bf16(attn))) -> out_proj / o_proj residual epilogue
+//   rmsnorm_gated -> gated-delta kernel
+// giving 5 launches per GDN layer, 7 per attention layer and 3 for embed + tail.
+// One token's launches are captured once into a HIP graph; the token, positions
+// and sequence length live in device memory (DecodeCtl) and are advanced by the
+// argmax kernel, so replaying the graph runs the greedy loop with no host sync.
+#include <stdio.h>
+#include <string.h>
+
+#include <map>
+#include <string>
+#include <vector>
+
+#include "attention.hpp"
+#include "gdn.hpp"
+#include "norm.hpp"
+#include "peregrine_model.h"
+#include "q4_gemv.hpp"
+
+namespace prg {
+namespace {
+
+// ------------------------------------------------------------------ RNG ----
+__device__ __host__ inline uint64_t mix64(uint64_t z) {
+  z += 0x9e3779b97f4a7c15ull;
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+  return z ^ (z >> 31);
+}
+__device__ inline float u01(uint64_t h) { return static_cast<float>(h >> 40) * (1.0f / 16777216.0f); }
+__device__ inline float normal01(uint64_t key, uint64_t i) {
+  const float u1 = fmaxf(u01(mix64(key ^ (2 * i))), 1.0e-7f);
+  const float u2 = u01(mix64(key ^ (2 * i + 1)));
+  return sqrtf(-2.0f * logf(u1)) * cospif(2.0f * u2);
+}
+
+enum FillKind : int { kFillBits = 0, kFillUniform = 1, kFillNormal = 2, kFillQ4Bias = 3 };
+
+// Fill `n` elements. bits: u32 words; uniform/normal: bf16 (or f32 when f32);
+// q4 bias: bf16(-7.5 * scale[i] + N(0, std)).
+__global__ void fill_kernel(void* dst, size_t n, uint64_t key, int kind, float a, float b, int f32,
+                            const uint16_t* scale) {
+  const size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  if (kind == kFillBits) {
+    static_cast<uint32_t*>(dst)[i] = static_cast<uint32_t>(mix64(key ^ i));
+    return;
+  }
+  float v;
+  if (kind == kFillUniform)
+    v = a + (b - a) * u01(mix64(key ^ i));
+  else if (kind == kFillNormal)
+    v = a + b * normal01(key, i);
+  else
+    v = -7.5f * bf2f(scale[i]) + b * normal01(key, i);
+  if (f32)
+    static_cast<float*>(dst)[i] = v;
+  else
+    static_cast<uint16_t*>(dst)[i] = f2bf(v);
+}
+
+constexpr size_t kAlign = 256;
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+}  // namespace
+
+// ------------------------------------------------------------ structures ---
+struct Q4Linear {  // linear_q4.zig:17-25
+  uint32_t* weight = nullptr;
+  uint16_t* scales = nullptr;
+  uint16_t* biases = nullptr;
+  uint32_t out_dim = 0, in_dim = 0;
+};
+
+struct LinearAttentionBlock {  // block_linear.zig:143-184
+  Q4Linear in_qkv, in_z, in_a, in_b, out_proj;
+  uint16_t* conv_weight = nullptr;  // bf16 [8192, 4]
+  float* a_log = nullptr;           // f32 [32]
+  uint16_t* dt_bias = nullptr;      // bf16 [32]
+  uint16_t* norm_weight = nullptr;  // bf16 [128]
+};
+
+struct FullAttentionBlock {  // block_attn.zig:227-255
+  Q4Linear q_proj, k_proj, v_proj, o_proj;
+  uint16_t* q_norm = nullptr;  // bf16 [256]
+  uint16_t* k_norm = nullptr;
+};
+
+struct MlpBlock {  // block_mlp.zig:110-130
+  Q4Linear gate_proj, up_proj, down_proj;
+};
+
+struct DecoderLayer {  // decoder_layer.zig:360-412
+  bool linear = true;
+  uint16_t* input_norm = nullptr;
+  uint16_t* post_norm = nullptr;
+  LinearAttentionBlock lin;
+  FullAttentionBlock full;
+  MlpBlock mlp;
+};
+
+struct TensorRef {
+  void* ptr;
+  size_t bytes;
+};
+
+}  // namespace prg
+
+struct PrgModel {
+  PrgModelConfig cfg{};
+  uint8_t* arena = nullptr;
+  size_t arena_bytes = 0;
+  std::map<std::string, prg::TensorRef> tensors;
+  prg::Q4Linear embed;
+  std::vector<prg::DecoderLayer> layers;
+  uint16_t* final_norm = nullptr;
+  prg::Q4Linear lm_head;
+};
+
+namespace prg {
+namespace {
+
+struct LayerState {
+  float* conv = nullptr;       // f32 [3, 8192]
+  float* recur = nullptr;      // f32 [32, 128, 128]
+  uint16_t* cache_k = nullptr; // bf16 [4, stride, 256]
+  uint16_t* cache_v = nullptr; // bf16 [4, 256, stride]
+};
+
+}  // namespace
+}  // namespace prg
+
+struct PrgModelState {
+  PrgModel* model = nullptr;
+  uint32_t max_seq = 0, stride = 0;
+  uint8_t* arena = nullptr;
+  size_t arena_bytes = 0;
+  std::map<std::string, prg::TensorRef> tensors;
+  std::vector<prg::LayerState> layers;
+  // workspace
+  uint16_t *hA = nullptr, *hB = nullptr;
+  uint16_t *conv_out = nullptr, *zbuf = nullptr, *abuf = nullptr, *bbuf = nullptr, *gated = nullptr;
+  uint16_t *qp = nullptr, *kbuf = nullptr, *vbuf = nullptr, *qbuf = nullptr, *gatebuf = nullptr, *ctx = nullptr;
+  float* partials = nullptr;
+  uint16_t* inter = nullptr;
+  float* pval = nullptr;
+  uint32_t* pidx = nullptr;
+  prg::DecodeCtl* ctl = nullptr;
+  uint32_t* prompt = nullptr;
+  uint32_t* predictions = nullptr;
+  uint32_t nsplit = 0, split_tokens = 0;
+  // execution
+  hipStream_t stream = nullptr;
+  hipGraphExec_t graph_decode = nullptr;  // layers + lm_head argmax + advance
+  hipGraphExec_t graph_prompt = nullptr;  // layers + forced advance
+  hipEvent_t ev0 = nullptr, ev1 = nullptr;
+};
+
+namespace prg {
+namespace {
+
+// ------------------------------------------------------------ builders -----
+struct Builder {
+  PrgModel* m;
+  uint64_t seed;
+  uint64_t tensor_id = 0;
+  size_t offset = 0;
+  bool sizing = true;
+  struct Fill {
+    void* dst;
+    size_t n;
+    int kind;
+    float a, b;
+    int f32;
+    const uint16_t* scale;
+    uint64_t key;
+  };
+  std::vector<Fill> fills;
+
+  void* take(const std::string& name, size_t bytes) {
+    const size_t off = offset;
+    offset = align_up(offset + bytes, kAlign);
+    if (sizing) return nullptr;
+    void* p = m->arena + off;
+    m->tensors[name] = TensorRef{p, bytes};
+    return p;
+  }
+  uint64_t next_key() { return mix64(seed ^ mix64(++tensor_id * 0x632be59bd9b4e019ull)); }
+
+  Q4Linear q4(const std::string& base, uint32_t out_dim, uint32_t in_dim) {
+    Q4Linear l;
+    l.out_dim = out_dim;
+    l.in_dim = in_dim;
+    const size_t nw = static_cast<size_t>(out_dim) * in_dim / 8, ng = static_cast<size_t>(out_dim) * in_dim / 64;
+    l.weight = static_cast<uint32_t*>(take(base + ".weight", nw * 4));
+    l.scales = static_cast<uint16_t*>(take(base + ".scales", ng * 2));
+    l.biases = static_cast<uint16_t*>(take(base + ".biases", ng * 2));
+    const uint64_t k0 = next_key(), k1 = next_key(), k2 = next_key();
+    if (!sizing) {
+      fills.push_back({l.weight, nw, kFillBits, 0, 0, 0, nullptr, k0});
+      fills.push_back({l.scales, ng, kFillUniform, 0.002f, 0.02f, 0, nullptr, k1});
+      fills.push_back({l.biases, ng, kFillQ4Bias, 0.0f, 0.01f, 0, l.scales, k2});
+    }
+    return l;
+  }
+  uint16_t* bf16(const std::string& name, size_t n, float mean, float stddev) {
+    auto* p = static_cast<uint16_t*>(take(name, n * 2));
+    const uint64_t k = next_key();
+    if (!sizing) fills.push_back({p, n, kFillNormal, mean, stddev, 0, nullptr, k});
+    return p;
+  }
+  float* f32(const std::string& name, size_t n, float mean, float stddev) {
+    auto* p = static_cast<float*>(take(name, n * 4));
+    const uint64_t k = next_key();
+    if (!sizing) fills.push_back({p, n, kFillNormal, mean, stddev, 1, nullptr, k});
+    return p;
+  }
+};
+
+bool is_linear_layer(const PrgModelConfig& c, uint32_t i) {  // decoder_layer.zig:29-31
+  return (i + 1) % c.full_attention_interval != 0;
+}
+
+void build_model(Builder& b) {
+  PrgModel* m = b.m;
+  const PrgModelConfig& c = m->cfg;
+  const std::string root = "language_model.model";
+  m->embed = b.q4(root + ".embed_tokens", c.vocab, c.hidden);
+  m->layers.assign(c.num_layers, DecoderLayer{});
+  for (uint32_t i = 0; i < c.num_layers; ++i) {
+    DecoderLayer& L = m->layers[i];
+    const std::string p = root + ".layers." + std::to_string(i);
+    L.linear = is_linear_layer(c, i);
+    L.input_norm = b.bf16(p + ".input_layernorm.weight", c.hidden, 1.0f, 0.1f);
+    L.post_norm = b.bf16(p + ".post_attention_layernorm.weight", c.hidden, 1.0f, 0.1f);
+    if (L.linear) {
+      const std::string a = p + ".linear_attn";
+      L.lin.in_qkv = b.q4(a + ".in_proj_qkv", kGdnConvDim, c.hidden);
+      L.lin.in_z = b.q4(a + ".in_proj_z", kGdnValDim, c.hidden);
+      L.lin.in_a = b.q4(a + ".in_proj_a", kGdnHv, c.hidden);
+      L.lin.in_b = b.q4(a + ".in_proj_b", kGdnHv, c.hidden);
+      L.lin.out_proj = b.q4(a + ".out_proj", c.hidden, kGdnValDim);
+      L.lin.conv_weight = b.bf16(a + ".conv1d.weight", static_cast<size_t>(kGdnConvDim) * kGdnConvK, 0.0f, 0.5f);
+      L.lin.a_log = b.f32(a + ".A_log", kGdnHv, 0.0f, 0.5f);
+      L.lin.dt_bias = b.bf16(a + ".dt_bias", kGdnHv, 0.0f, 0.5f);
+      L.lin.norm_weight = b.bf16(a + ".norm.weight", kGdnDv, 1.0f, 0.1f);
+    } else {
+      const std::string a = p + ".self_attn";
+      L.full.q_proj = b.q4(a + ".q_proj", 2 * kAttnQHeads * kAttnHeadDim, c.hidden);
+      L.full.k_proj = b.q4(a + ".k_proj", kAttnKvHeads * kAttnHeadDim, c.hidden);
+      L.full.v_proj = b.q4(a + ".v_proj", kAttnKvHeads * kAttnHeadDim, c.hidden);
+      L.full.o_proj = b.q4(a + ".o_proj", c.hidden, kAttnQHeads * kAttnHeadDim);
+      L.full.q_norm = b.bf16(a + ".q_norm.weight", kAttnHeadDim, 1.0f, 0.1f);
+      L.full.k_norm = b.bf16(a + ".k_norm.weight", kAttnHeadDim, 1.0f, 0.1f);
+    }
+    const std::string mp = p + ".mlp";
+    L.mlp.gate_proj = b.q4(mp + ".gate_proj", c.intermediate, c.hidden);
+    L.mlp.up_proj = b.q4(mp + ".up_proj", c.intermediate, c.hidden);
+    L.mlp.down_proj = b.q4(mp + ".down_proj", c.hidden, c.intermediate);
+  }
+  m->final_norm = b.bf16(root + ".norm.weight", c.hidden, 1.0f, 0.1f);
+  m->lm_head = b.q4("language_model.lm_head", c.vocab, c.hidden);
+}
+
+int validate_config(const PrgModelConfig& c) {
+  PRG_CHECK_ARG(c.num_layers >= 1 && c.num_layers <= 256, "config: num_layers %u", c.num_layers);
+  PRG_CHECK_ARG(c.hidden >= 512 && c.hidden % 512 == 0 && c.hidden <= 16384, "config: hidden %u", c.hidden);
+  PRG_CHECK_ARG(c.intermediate >= 512 && c.intermediate % 512 == 0 && c.intermediate <= 16384,
+                "config: intermediate %u", c.intermediate);
+  PRG_CHECK_ARG(c.vocab >= 8 && c.vocab % 8 == 0, "config: vocab %u must be a multiple of 8", c.vocab);
+  PRG_CHECK_ARG(c.full_attention_interval >= 1, "config: full_attention_interval 0");
+  PRG_CHECK_ARG(c.rms_eps > 0.0f, "config: rms_eps");
+  return PRG_OK;
+}
+
+// ------------------------------------------------------- per-token chain ---
+GemvParams gemv_params(const uint16_t* x, uint32_t K) {
+  GemvParams p{};
+  p.x[0] = x;
+  p.K = K;
+  return p;
+}
+
+void add_seg(GemvParams& p, const Q4Linear& l, uint16_t* out) {
+  GemvSeg& s = p.seg[p.nseg++];
+  s.w[0] = l.weight;
+  s.s[0] = l.scales;
+  s.b[0] = l.biases;
+  s.out[0] = out;
+  s.rows = l.out_dim;
+}
+
+uint32_t total_rows(const GemvParams& p) {
+  uint32_t r = 0;
+  for (uint32_t i = 0; i < p.nseg; ++i) r += p.seg[i].rows;
+  return r;
+}
+
+int run_gemv(hipStream_t s, GemvParams& p, int epi, bool norm, const char* name) {
+  const int rows = gemv_rows_per_wave(total_rows(p), p.K, epi, 1);
+  return launch_q4_gemv(s, p, 1, rows, epi, norm, name);
+}
+
+// GDN layer: norm+in_proj(+conv) -> recurrence+gated norm -> out_proj + residual.
+int encode_linear_attention(PrgModel* m, PrgModelState* st, const DecoderLayer& L, LayerState& ls) {
+  const LinearAttentionBlock& b = L.lin;
+  const PrgModelConfig& c = m->cfg;
+  hipStream_t s = st->stream;
+  GemvParams p = gemv_params(st->hA, c.hidden);
+  p.norm_w = L.input_norm;
+  p.eps = c.rms_eps;
+  add_seg(p, b.in_qkv, st->conv_out);
+  p.seg[0].conv_state = ls.conv;
+  p.seg[0].conv_w = b.conv_weight;
+  p.seg[0].conv_dim = kGdnConvDim;
+  add_seg(p, b.in_z, st->zbuf);
+  add_seg(p, b.in_a, st->abuf);
+  add_seg(p, b.in_b, st->bbuf);
+  if (int rc = run_gemv(s, p, kEpiPlain, true, "linear_attn.in_proj")) return rc;
+  if (int rc = launch_gdn_decode(s, ls.recur, st->conv_out, st->abuf, st->bbuf, b.a_log, b.dt_bias, st->gated,
+                                 &st->ctl->s, 0, b.norm_weight, st->zbuf, c.rms_eps))
+    return rc;
+  GemvParams o = gemv_params(st->gated, kGdnValDim);
+  add_seg(o, b.out_proj, st->hB);
+  o.seg[0].res[0] = st->hA;
+  return run_gemv(s, o, kEpiResidual, false, "linear_attn.out_proj");
+}
+
+// Attention layer: norm+q/k/v -> prepare/append -> flash decode -> o_proj + residual.
+int encode_full_attention(PrgModel* m, PrgModelState* st, const DecoderLayer& L, LayerState& ls) {
+  const FullAttentionBlock& b = L.full;
+  const PrgModelConfig& c = m->cfg;
+  hipStream_t s = st->stream;
+  GemvParams p = gemv_params(st->hA, c.hidden);
+  p.norm_w = L.input_norm;
+  p.eps = c.rms_eps;
+  add_seg(p, b.q_proj, st->qp);
+  add_seg(p, b.k_proj, st->kbuf);
+  add_seg(p, b.v_proj, st->vbuf);
+  if (int rc = run_gemv(s, p, kEpiPlain, true, "self_attn.qkv_proj")) return rc;
+  AttnPrepareArgs pa{st->qp, b.q_norm, st->kbuf, st->vbuf, b.k_norm, st->qbuf, st->gatebuf, ls.cache_k, ls.cache_v,
+                     st->stride, 0, 0, &st->ctl->s};
+  if (int rc = launch_attn_prepare(s, pa)) return rc;
+  AttnDecodeArgs da{};
+  da.q = st->qbuf;
+  da.key_cache = ls.cache_k;
+  da.value_cache = ls.cache_v;
+  da.gate = st->gatebuf;
+  da.out = st->ctx;
+  da.partials = st->partials;
+  da.stride = st->stride;
+  da.nsplit = st->nsplit;
+  da.split_tokens = st->split_tokens;
+  da.step = &st->ctl->s;
+  da.scale = kAttnScale;
+  if (int rc = launch_attn_decode(s, da)) return rc;
+  GemvParams o = gemv_params(st->ctx, kAttnQHeads * kAttnHeadDim);
+  add_seg(o, b.o_proj, st->hB);
+  o.seg[0].res[0] = st->hA;
+  return run_gemv(s, o, kEpiResidual, false, "self_attn.o_proj");
+}
+
+// MLP: post_attention_layernorm + gate/up SiLU -> down + residual (into hA).
+int encode_mlp(PrgModel* m, PrgModelState* st, const DecoderLayer& L) {
+  const PrgModelConfig& c = m->cfg;
+  hipStream_t s = st->stream;
+  GemvParams p = gemv_params(st->hB, c.hidden);
+  p.norm_w = L.post_norm;
+  p.eps = c.rms_eps;
+  add_seg(p, L.mlp.gate_proj, st->inter);
+  p.seg[0].w[1] = L.mlp.up_proj.weight;
+  p.seg[0].s[1] = L.mlp.up_proj.scales;
+  p.seg[0].b[1] = L.mlp.up_proj.biases;
+  if (int rc = run_gemv(s, p, kEpiSiluGate, true, "mlp.gate_up")) return rc;
+  GemvParams d = gemv_params(st->inter, c.intermediate);
+  add_seg(d, L.mlp.down_proj, st->hA);
+  d.seg[0].res[0] = st->hB;
+  return run_gemv(s, d, kEpiResidual, false, "mlp.down_proj");
+}
+
+// One token: embed(ctl.token) -> layers -> (lm_head argmax | forced) + advance.
+int encode_token(PrgModel* m, PrgModelState* st, bool with_head) {
+  hipStream_t s = st->stream;
+  if (int rc = launch_embedding(s, m->embed.weight, m->embed.scales, m->embed.biases, st->hA, &st->ctl->s.token, 0,
+                                1, m->cfg.hidden))
+    return rc;
+  for (size_t i = 0; i < m->layers.size(); ++i) {
+    const DecoderLayer& L = m->layers[i];
+    int rc = L.linear ? encode_linear_attention(m, st, L, st->layers[i])
+                      : encode_full_attention(m, st, L, st->layers[i]);
+    if (rc) return rc;
+    if ((rc = encode_mlp(m, st, L))) return rc;
+  }
+  if (!with_head) return launch_advance_forced(s, st->ctl, st->prompt);
+  GemvParams p = gemv_params(st->hA, m->cfg.hidden);
+  p.norm_w = m->final_norm;
+  p.eps = m->cfg.rms_eps;
+  add_seg(p, m->lm_head, nullptr);
+  p.seg[0].pval[0] = st->pval;
+  p.seg[0].pidx[0] = st->pidx;
+  if (int rc = launch_q4_gemv(s, p, 1, 8, kEpiArgmax, true, "lm_head.argmax")) return rc;
+  return launch_argmax_advance(s, st->pval, st->pidx, m->cfg.vocab / 8, st->ctl, st->prompt, st->predictions);
+}
+
+int capture(PrgModel* m, PrgModelState* st, bool with_head, hipGraphExec_t* out) {
+  hipGraph_t g = nullptr;
+  PRG_HIP(hipStreamBeginCapture(st->stream, hipStreamCaptureModeThreadLocal));
+  const int rc = encode_token(m, st, with_head);
+  hipError_t e = hipStreamEndCapture(st->stream, &g);
+  if (rc) {
+    if (g) hipGraphDestroy(g);
+    return rc;
+  }
+  if (e != hipSuccess) return set_error(PRG_ERR_HIP, "hipStreamEndCapture: %s", hipGetErrorString(e));
+  e = hipGraphInstantiate(out, g, nullptr, nullptr, 0);
+  hipGraphDestroy(g);
+  if (e != hipSuccess) return set_error(PRG_ERR_HIP, "hipGraphInstantiate: %s", hipGetErrorString(e));
+  return PRG_OK;
+}
+
+int ensure_graphs(PrgModelState* st) {
+  if (!st->graph_decode)
+    if (int rc = capture(st->model, st, true, &st->graph_decode)) return rc;
+  if (!st->graph_prompt)
+    if (int rc = capture(st->model, st, false, &st->graph_prompt)) return rc;
+  return PRG_OK;
+}
+
+uint32_t cache_stride_for(uint32_t max_seq) {  // state.zig:25-32
+  const uint32_t a = max_seq >= 16000 ? 64u : 256u;
+  return (max_seq + a - 1) / a * a;
+}
+
+}  // namespace
+}  // namespace prg
+
+using namespace prg;
+
+extern "C" {
+
+void prg_model_default_config(PrgModelConfig* cfg) {
+  if (!cfg) return;
+  cfg->num_layers = 32;
+  cfg->hidden = 4096;
+  cfg->intermediate = 12288;
+  cfg->vocab = 248320;
+  cfg->full_attention_interval = 4;
+  cfg->rms_eps = 1e-6f;
+}
+
+int prg_model_create_random(const PrgModelConfig* cfg, uint64_t seed, PrgModel** out) {
+  PRG_CHECK_ARG(cfg && out, "prg_model_create_random: null argument");
+  *out = nullptr;
+  if (int rc = validate_config(*cfg)) return rc;
+  auto* m = new PrgModel();
+  m->cfg = *cfg;
+  Builder sizing{m, seed};
+  build_model(sizing);
+  m->arena_bytes = sizing.offset;
+  hipError_t e = hipMalloc(reinterpret_cast<void**>(&m->arena), m->arena_bytes);
+  if (e != hipSuccess) {
+    delete m;
+    return set_error(PRG_ERR_OOM, "model weights: hipMalloc(%zu): %s", sizing.offset, hipGetErrorString(e));
+  }
+  Builder b{m, seed};
+  b.sizing = false;
+  build_model(b);
+  for (const auto& f : b.fills) {
+    const uint32_t blocks = static_cast<uint32_t>((f.n + 255) / 256);
+    hipLaunchKernelGGL(fill_kernel, dim3(blocks), dim3(256), 0, nullptr, f.dst, f.n, f.key, f.kind, f.a, f.b,
+                       f.f32, f.scale);
+  }
+  e = hipDeviceSynchronize();
+  if (e != hipSuccess) {
+    hipFree(m->arena);
+    delete m;
+    return set_error(PRG_ERR_HIP, "model init: %s", hipGetErrorString(e));
+  }
+  *out = m;
+  return PRG_OK;
+}
+
+void prg_model_destroy(PrgModel* model) {
+  if (!model) return;
+  hipFree(model->arena);
+  delete model;
+}
+
+size_t prg_model_weight_bytes(const PrgModel* model) { return model ? model->arena_bytes : 0; }
+
+int prg_model_tensor(const PrgModel* model, const char* name, void** ptr, size_t* bytes) {
+  PRG_CHECK_ARG(model && name && ptr && bytes, "prg_model_tensor: null argument");
+  auto it = model->tensors.find(name);
+  if (it == model->tensors.end()) return set_error(PRG_ERR_INVALID_ARG, "prg_model_tensor: no tensor '%s'", name);
+  *ptr = it->second.ptr;
+  *bytes = it->second.bytes;
+  return PRG_OK;
+}
+
+int prg_model_state_create(PrgModel* model, uint32_t max_seq, PrgModelState** out) {
+  PRG_CHECK_ARG(model && out, "prg_model_state_create: null argument");
+  PRG_CHECK_ARG(max_seq >= 1 && max_seq <= 65536, "prg_model_state_create: max_seq %u outside [1, 65536]", max_seq);
+  *out = nullptr;
+  auto* st = new PrgModelState();
+  st->model = model;
+  st->max_seq = max_seq;
+  st->stride = cache_stride_for(max_seq);
+  st->nsplit = attn_num_splits(st->stride);
+  st->split_tokens = attn_split_tokens(st->stride, st->nsplit);
+  const PrgModelConfig& c = model->cfg;
+
+  // Two passes over the same layout: size, then carve the arena.
+  struct Item {
+    std::string name;
+    size_t bytes;
+    void** slot;
+  };
+  std::vector<Item> items;
+  st->layers.assign(c.num_layers, LayerState{});
+  for (uint32_t i = 0; i < c.num_layers; ++i) {
+    const std::string p = "layers." + std::to_string(i);
+    if (model->layers[i].linear) {
+      items.push_back({p + ".conv", sizeof(float) * (kGdnConvK - 1) * kGdnConvDim, reinterpret_cast<void**>(&st->layers[i].conv)});
+      items.push_back({p + ".recur", sizeof(float) * kGdnHv * kGdnDv * kGdnDk, reinterpret_cast<void**>(&st->layers[i].recur)});
+    } else {
+      const size_t kv = sizeof(uint16_t) * kAttnKvHeads * static_cast<size_t>(st->stride) * kAttnHeadDim;
+      items.push_back({p + ".cache_k", kv, reinterpret_cast<void**>(&st->layers[i].cache_k)});
+      items.push_back({p + ".cache_v", kv, reinterpret_cast<void**>(&st->layers[i].cache_v)});
+    }
+  }
+  const size_t bf = sizeof(uint16_t);
+  const size_t state_items = items.size();
+  items.push_back({"ws.hA", bf * c.hidden, reinterpret_cast<void**>(&st->hA)});
+  items.push_back({"ws.hB", bf * c.hidden, reinterpret_cast<void**>(&st->hB)});
+  items.push_back({"ws.conv_out", bf * kGdnConvDim, reinterpret_cast<void**>(&st->conv_out)});
+  items.push_back({"ws.z", bf * kGdnValDim, reinterpret_cast<void**>(&st->zbuf)});
+  items.push_back({"ws.a", bf * kGdnHv, reinterpret_cast<void**>(&st->abuf)});
+  items.push_back({"ws.b", bf * kGdnHv, reinterpret_cast<void**>(&st->bbuf)});
+  items.push_back({"ws.gated", bf * kGdnValDim, reinterpret_cast<void**>(&st->gated)});
+  items.push_back({"ws.qp", bf * 2 * kAttnQHeads * kAttnHeadDim, reinterpret_cast<void**>(&st->qp)});
+  items.push_back({"ws.k", bf * kAttnKvHeads * kAttnHeadDim, reinterpret_cast<void**>(&st->kbuf)});
+  items.push_back({"ws.v", bf * kAttnKvHeads * kAttnHeadDim, reinterpret_cast<void**>(&st->vbuf)});
+  items.push_back({"ws.q", bf * kAttnQHeads * kAttnHeadDim, reinterpret_cast<void**>(&st->qbuf)});
+  items.push_back({"ws.gate", bf * kAttnQHeads * kAttnHeadDim, reinterpret_cast<void**>(&st->gatebuf)});
+  items.push_back({"ws.ctx", bf * kAttnQHeads * kAttnHeadDim, reinterpret_cast<void**>(&st->ctx)});
+  items.push_back({"ws.partials", sizeof(float) * kAttnQHeads * st->nsplit * kAttnPartialStride,
+                   reinterpret_cast<void**>(&st->partials)});
+  items.push_back({"ws.inter", bf * c.intermediate, reinterpret_cast<void**>(&st->inter)});
+  items.push_back({"ws.pval", sizeof(float) * (c.vocab / 8), reinterpret_cast<void**>(&st->pval)});
+  items.push_back({"ws.pidx", sizeof(uint32_t) * (c.vocab / 8), reinterpret_cast<void**>(&st->pidx)});
+  items.push_back({"ws.ctl", sizeof(DecodeCtl), reinterpret_cast<void**>(&st->ctl)});
+  items.push_back({"ws.prompt", sizeof(uint32_t) * st->stride, reinterpret_cast<void**>(&st->prompt)});
+  items.push_back({"ws.predictions", sizeof(uint32_t) * st->stride, reinterpret_cast<void**>(&st->predictions)});
+  size_t total = 0;
+  for (auto& it : items) total = align_up(total + it.bytes, kAlign);
+  hipError_t e = hipMalloc(reinterpret_cast<void**>(&st->arena), total);
+  if (e != hipSuccess) {
+    delete st;
+    return set_error(PRG_ERR_OOM, "model state: hipMalloc(%zu): %s", total, hipGetErrorString(e));
+  }
+  st->arena_bytes = total;
+  size_t off = 0;
+  for (auto& it : items) {
+    *it.slot = st->arena + off;
+    st->tensors[it.name] = TensorRef{st->arena + off, it.bytes};
+    off = align_up(off + it.bytes, kAlign);
+  }
+  (void)state_items;
+  // Everything starts at zero (GDN states, caches, workspace).
+  if ((e = hipMemset(st->arena, 0, total)) != hipSuccess ||
+      (e = hipStreamCreateWithFlags(&st->stream, hipStreamNonBlocking)) != hipSuccess ||
+      (e = hipEventCreate(&st->ev0)) != hipSuccess || (e = hipEventCreate(&st->ev1)) != hipSuccess ||
+      (e = hipDeviceSynchronize()) != hipSuccess) {
+    prg_model_state_destroy(st);
+    return set_error(PRG_ERR_HIP, "model state init: %s", hipGetErrorString(e));
+  }
+  *out = st;
+  return PRG_OK;
+}
+
+void prg_model_state_destroy(PrgModelState* st) {
+  if (!st) return;
+  if (st->graph_decode) hipGraphExecDestroy(st->graph_decode);
+  if (st->graph_prompt) hipGraphExecDestroy(st->graph_prompt);
+  if (st->ev0) hipEventDestroy(st->ev0);
+  if (st->ev1) hipEventDestroy(st->ev1);
+  if (st->stream) hipStreamDestroy(st->stream);
+  hipFree(st->arena);
+  delete st;
+}
+
+int prg_model_state_reset(PrgModelState* st) {
+  PRG_CHECK_ARG(st, "prg_model_state_reset: null state");
+  for (auto& l : st->layers) {
+    if (l.conv) PRG_HIP(hipMemsetAsync(l.conv, 0, sizeof(float) * (kGdnConvK - 1) * kGdnConvDim, st->stream));
+    if (l.recur) PRG_HIP(hipMemsetAsync(l.recur, 0, sizeof(float) * kGdnHv * kGdnDv * kGdnDk, st->stream));
+  }
+  PRG_HIP(hipStreamSynchronize(st->stream));
+  return PRG_OK;
+}
+
+int prg_model_state_tensor(const PrgModelState* st, const char* name, void** ptr, size_t* bytes) {
+  PRG_CHECK_ARG(st && name && ptr && bytes, "prg_model_state_tensor: null argument");
+  auto it = st->tensors.find(name);
+  if (it == st->tensors.end()) return set_error(PRG_ERR_INVALID_ARG, "prg_model_state_tensor: no tensor '%s'", name);
+  *ptr = it->second.ptr;
+  *bytes = it->second.bytes;
+  return PRG_OK;
+}
+
+uint32_t prg_model_state_stride(const PrgModelState* st) { return st ? st->stride : 0; }
+
+int prg_model_forward_next_token(PrgModel* model, PrgModelState* st, uint32_t token, uint32_t cache_pos,
+                                 uint32_t rope_pos, uint32_t seq_len, uint32_t* next_token) {
+  PRG_CHECK_ARG(model && st && next_token && st->model == model, "prg_model_forward_next_token: bad argument");
+  if (cache_pos >= st->max_seq)  // model.zig:805
+    return set_error(PRG_ERR_SEQUENCE_TOO_LONG, "cache_pos %u >= max_seq %u", cache_pos, st->max_seq);
+  if (token >= model->cfg.vocab)  // model.zig:806
+    return set_error(PRG_ERR_INVALID_TOKEN, "token %u >= vocab %u", token, model->cfg.vocab);
+  if (seq_len != cache_pos + 1)
+    return set_error(PRG_ERR_INVALID_ARG, "seq_len %u != cache_pos + 1 (prefix caches are not supported)", seq_len);
+  if (int rc = ensure_graphs(st)) return rc;
+  DecodeCtl ctl{};
+  ctl.s = StepScalars{token, cache_pos, rope_pos, seq_len};
+  ctl.n = 0;
+  ctl.prompt_len = 0;
+  ctl.capacity = st->max_seq;
+  PRG_HIP(hipMemcpyAsync(st->ctl, &ctl, sizeof(ctl), hipMemcpyHostToDevice, st->stream));
+  PRG_HIP(hipGraphLaunch(st->graph_decode, st->stream));
+  PRG_HIP(hipMemcpyAsync(next_token, st->predictions, sizeof(uint32_t), hipMemcpyDeviceToHost, st->stream));
+  PRG_HIP(hipStreamSynchronize(st->stream));
+  return PRG_OK;
+}
+
+int prg_model_prefill(PrgModel* model, PrgModelState* st, const uint32_t* prompt, uint32_t prompt_len,
+                      uint32_t* next_token) {
+  PRG_CHECK_ARG(model && st && prompt && next_token && st->model == model, "prg_model_prefill: bad argument");
+  PRG_CHECK_ARG(prompt_len >= 1, "prg_model_prefill: empty prompt");
+  if (prompt_len > st->max_seq)
+    return set_error(PRG_ERR_SEQUENCE_TOO_LONG, "prompt of %u tokens exceeds max_seq %u", prompt_len, st->max_seq);
+  for (uint32_t i = 0; i < prompt_len; ++i)
+    if (prompt[i] >= model->cfg.vocab)
+      return set_error(PRG_ERR_INVALID_TOKEN, "prompt[%u] = %u >= vocab %u", i, prompt[i], model->cfg.vocab);
+  if (int rc = ensure_graphs(st)) return rc;
+  if (int rc = prg_model_state_reset(st)) return rc;
+  DecodeCtl ctl{};
+  ctl.s = StepScalars{prompt[0], 0, 0, 1};
+  ctl.prompt_len = prompt_len;
+  ctl.capacity = st->max_seq;
+  PRG_HIP(hipMemcpyAsync(st->prompt, prompt, sizeof(uint32_t) * prompt_len, hipMemcpyHostToDevice, st->stream));
+  PRG_HIP(hipMemcpyAsync(st->ctl, &ctl, sizeof(ctl), hipMemcpyHostToDevice, st->stream));
+  for (uint32_t n = 0; n + 1 < prompt_len; ++n) PRG_HIP(hipGraphLaunch(st->graph_prompt, st->stream));
+  PRG_HIP(hipGraphLaunch(st->graph_decode, st->stream));
+  PRG_HIP(hipMemcpyAsync(next_token, st->predictions + (prompt_len - 1), sizeof(uint32_t), hipMemcpyDeviceToHost,
+                         st->stream));
+  PRG_HIP(hipStreamSynchronize(st->stream));
+  return PRG_OK;
+}
+
+int prg_model_decode(PrgModel* model, PrgModelState* st, uint32_t n_steps, uint32_t* tokens_out, float* gpu_ms) {
+  PRG_CHECK_ARG(model && st && tokens_out && st->model == model, "prg_model_decode: bad argument");
+  PRG_CHECK_ARG(n_steps >= 1, "prg_model_decode: n_steps == 0");
+  if (int rc = ensure_graphs(st)) return rc;
+  DecodeCtl ctl{};
+  PRG_HIP(hipMemcpyAsync(&ctl, st->ctl, sizeof(ctl), hipMemcpyDeviceToHost, st->stream));
+  PRG_HIP(hipStreamSynchronize(st->stream));
+  if (ctl.n + n_steps > st->max_seq)
+    return set_error(PRG_ERR_SEQUENCE_TOO_LONG, "position %u + %u steps exceeds max_seq %u", ctl.n, n_steps,
+                     st->max_seq);
+  PRG_HIP(hipEventRecord(st->ev0, st->stream));
+  for (uint32_t i = 0; i < n_steps; ++i) PRG_HIP(hipGraphLaunch(st->graph_decode, st->stream));
+  PRG_HIP(hipEventRecord(st->ev1, st->stream));
+  PRG_HIP(hipMemcpyAsync(tokens_out, st->predictions + ctl.n, sizeof(uint32_t) * n_steps, hipMemcpyDeviceToHost,
+                         st->stream));
+  PRG_HIP(hipStreamSynchronize(st->stream));
+  if (gpu_ms) PRG_HIP(hipEventElapsedTime(gpu_ms, st->ev0, st->ev1));
+  return PRG_OK;
+}
+
+int prg_model_generate(PrgModel* model, PrgModelState* st, const uint32_t* prompt, uint32_t prompt_len,
+                       uint32_t n_new, int teacher_force, uint32_t* predictions, float* decode_ms) {
+  PRG_CHECK_ARG(model && st && prompt && predictions && st->model == model, "prg_model_generate: bad argument");
+  PRG_CHECK_ARG(prompt_len >= 1, "prg_model_generate: empty prompt");
+  if (teacher_force) PRG_CHECK_ARG(n_new == 0, "prg_model_generate: teacher forcing takes n_new == 0");
+  else PRG_CHECK_ARG(n_new >= 1, "prg_model_generate: n_new == 0");
+  const uint32_t steps = teacher_force ? prompt_len : prompt_len - 1 + n_new;
+  if (steps > st->max_seq)
+    return set_error(PRG_ERR_SEQUENCE_TOO_LONG, "%u steps exceed max_seq %u", steps, st->max_seq);
+  for (uint32_t i = 0; i < prompt_len; ++i)
+    if (prompt[i] >= model->cfg.vocab)
+      return set_error(PRG_ERR_INVALID_TOKEN, "prompt[%u] = %u >= vocab %u", i, prompt[i], model->cfg.vocab);
+  if (int rc = ensure_graphs(st)) return rc;
+  if (int rc = prg_model_state_reset(st)) return rc;
+
+  DecodeCtl ctl{};
+  ctl.s = StepScalars{prompt[0], 0, 0, 1};
+  ctl.n = 0;
+  ctl.prompt_len = prompt_len;
+  ctl.capacity = st->max_seq;
+  PRG_HIP(hipMemcpyAsync(st->prompt, prompt, sizeof(uint32_t) * prompt_len, hipMemcpyHostToDevice, st->stream));
+  PRG_HIP(hipMemsetAsync(st->predictions, 0xFF, sizeof(uint32_t) * st->stride, st->stream));
+  PRG_HIP(hipMemcpyAsync(st->ctl, &ctl, sizeof(ctl), hipMemcpyHostToDevice, st->stream));
+  const uint32_t head_from = teacher_force ? 0 : prompt_len - 1;
+  for (uint32_t n = 0; n < head_from; ++n) PRG_HIP(hipGraphLaunch(st->graph_prompt, st->stream));
+  PRG_HIP(hipEventRecord(st->ev0, st->stream));
+  for (uint32_t n = head_from; n < steps; ++n) PRG_HIP(hipGraphLaunch(st->graph_decode, st->stream));
+  PRG_HIP(hipEventRecord(st->ev1, st->stream));
+  PRG_HIP(hipMemcpyAsync(predictions, st->predictions, sizeof(uint32_t) * steps, hipMemcpyDeviceToHost, st->stream));
+  PRG_HIP(hipStreamSynchronize(st->stream));
+  if (decode_ms) PRG_HIP(hipEventElapsedTime(decode_ms, st->ev0, st->ev1));
+  return PRG_OK;
+}
+
+}  // extern "C"

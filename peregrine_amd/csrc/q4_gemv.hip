@@ -114,6 +114,12 @@ int launch_q4_gemv(hipStream_t stream, GemvParams& p, int M, int rows, int epi, 
 }  // namespace prg
 
 // ================================================================ kernels ====
+namespace prg {
+int launch_argmax_advance(hipStream_t s, const float* values, const uint32_t* indices, uint32_t n,
+                          DecodeCtl* ctl, const uint32_t* prompt, uint32_t* predictions);
+int launch_advance_forced(hipStream_t s, DecodeCtl* ctl, const uint32_t* prompt);
+}  // namespace prg
+
 namespace {
 
 // Final argmax over partials with the reference's effective tie order.
@@ -140,9 +146,30 @@ __device__ inline bool argmax_better(float v, uint32_t p, float bv, uint32_t bp)
   return argmax_tie_key(p) < argmax_tie_key(bp);
 }
 
+// Advance the token loop by one step (see DecodeCtl). `pred` is ignored when
+// the step has no argmax (prompt ingestion).
+__device__ inline void advance_ctl(prg::DecodeCtl* ctl, const uint32_t* prompt, uint32_t* predictions,
+                                   bool has_pred, uint32_t pred) {
+  const uint32_t n = ctl->n;
+  if (has_pred && predictions) predictions[n] = pred;
+  const uint32_t n1 = n + 1;
+  if (n1 >= ctl->capacity) {  // never step past the cache
+    ctl->overflow = 1;
+    return;
+  }
+  const uint32_t next = (n1 < ctl->prompt_len || !has_pred) ? prompt[n1] : pred;
+  ctl->s.token = next;
+  ctl->s.cache_pos = n1;
+  ctl->s.rope_pos = n1;
+  ctl->s.seq_len = n1 + 1;
+  ctl->n = n1;
+}
+
+template <bool ADVANCE>
 __global__ __launch_bounds__(kArgmaxThreads) void argmax_pairs_kernel(
     const float* __restrict__ values, const uint32_t* __restrict__ indices,
-    uint32_t* __restrict__ out, uint32_t n) {
+    uint32_t* __restrict__ out, uint32_t n, prg::DecodeCtl* ctl, const uint32_t* prompt,
+    uint32_t* predictions) {
   __shared__ float sv[kArgmaxThreads / 64];
   __shared__ uint32_t sp[kArgmaxThreads / 64];
   float bv = -INFINITY;
@@ -175,8 +202,14 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_pairs_kernel(
         bv = sv[i];
         bp = sp[i];
       }
-    out[0] = (bp == 0xffffffffu) ? 0u : indices[bp];
+    const uint32_t winner = (bp == 0xffffffffu) ? 0u : indices[bp];
+    if (out) out[0] = winner;
+    if constexpr (ADVANCE) advance_ctl(ctl, prompt, predictions, true, winner);
   }
+}
+
+__global__ void advance_forced_kernel(prg::DecodeCtl* ctl, const uint32_t* prompt) {
+  if (threadIdx.x == 0) advance_ctl(ctl, prompt, nullptr, false, 0);
 }
 
 __global__ void q4_dequantize_kernel(const uint32_t* __restrict__ w, const uint16_t* __restrict__ s,
@@ -226,6 +259,21 @@ prg::GemvParams one_seg(const uint32_t* w, const uint16_t* s, const uint16_t* b,
 }  // namespace
 
 using prg::launch_q4_gemv;
+
+namespace prg {
+int launch_argmax_advance(hipStream_t s, const float* values, const uint32_t* indices, uint32_t n,
+                          DecodeCtl* ctl, const uint32_t* prompt, uint32_t* predictions) {
+  hipLaunchKernelGGL(argmax_pairs_kernel<true>, dim3(1), dim3(kArgmaxThreads), 0, s, values, indices,
+                     nullptr, n, ctl, prompt, predictions);
+  PRG_CHECK_LAUNCH("argmax_advance");
+  return PRG_OK;
+}
+int launch_advance_forced(hipStream_t s, DecodeCtl* ctl, const uint32_t* prompt) {
+  hipLaunchKernelGGL(advance_forced_kernel, dim3(1), dim3(64), 0, s, ctl, prompt);
+  PRG_CHECK_LAUNCH("advance_forced");
+  return PRG_OK;
+}
+}  // namespace prg
 
 extern "C" {
 
@@ -330,6 +378,40 @@ int prg_q4_gemv_silu_gate2_bf16(void* stream, const uint16_t* x0, const uint16_t
   return launch_q4_gemv(prg::as_stream(stream), p, 2, rows, prg::kEpiSiluGate, false, name);
 }
 
+int prg_q4_gemv_norm_bf16(void* stream, const uint16_t* x, const uint16_t* norm_weight, float eps,
+                          const uint32_t* w, const uint16_t* scales, const uint16_t* biases, uint16_t* y,
+                          uint32_t out_dim, uint32_t in_dim) {
+  const char* name = "prg_q4_gemv_norm_bf16";
+  if (int rc = check_q4(name, x, w, scales, biases, out_dim, in_dim)) return rc;
+  PRG_CHECK_ARG(norm_weight && y, "%s: null pointer", name);
+  prg::GemvParams p = one_seg(w, scales, biases, out_dim, in_dim);
+  p.x[0] = x;
+  p.norm_w = norm_weight;
+  p.eps = eps;
+  p.seg[0].out[0] = y;
+  const int rows = prg::gemv_rows_per_wave(out_dim, in_dim, prg::kEpiPlain, 1);
+  return launch_q4_gemv(prg::as_stream(stream), p, 1, rows, prg::kEpiPlain, true, name);
+}
+
+int prg_q4_gemv_silu_gate_norm_bf16(void* stream, const uint16_t* x, const uint16_t* norm_weight, float eps,
+                                    const uint32_t* gate_w, const uint16_t* gate_s, const uint16_t* gate_b,
+                                    const uint32_t* up_w, const uint16_t* up_s, const uint16_t* up_b,
+                                    uint16_t* out, uint32_t out_dim, uint32_t in_dim) {
+  const char* name = "prg_q4_gemv_silu_gate_norm_bf16";
+  if (int rc = check_q4(name, x, gate_w, gate_s, gate_b, out_dim, in_dim)) return rc;
+  PRG_CHECK_ARG(norm_weight && up_w && up_s && up_b && out, "%s: null pointer", name);
+  prg::GemvParams p = one_seg(gate_w, gate_s, gate_b, out_dim, in_dim);
+  p.seg[0].w[1] = up_w;
+  p.seg[0].s[1] = up_s;
+  p.seg[0].b[1] = up_b;
+  p.x[0] = x;
+  p.norm_w = norm_weight;
+  p.eps = eps;
+  p.seg[0].out[0] = out;
+  const int rows = prg::gemv_rows_per_wave(out_dim, in_dim, prg::kEpiSiluGate, 1);
+  return launch_q4_gemv(prg::as_stream(stream), p, 1, rows, prg::kEpiSiluGate, true, name);
+}
+
 int prg_q4_gemv_argmax_partial_bf16(void* stream, const uint16_t* x, const uint32_t* w,
                                     const uint16_t* scales, const uint16_t* biases,
                                     float* partial_values, uint32_t* partial_indices,
@@ -369,8 +451,8 @@ int prg_argmax_pairs_f32_u32(void* stream, const float* values, const uint32_t* 
   const char* name = "prg_argmax_pairs_f32_u32";
   PRG_CHECK_ARG(values && indices && out_index, "%s: null pointer", name);
   PRG_CHECK_ARG(pair_count > 0, "%s: pair_count == 0", name);
-  hipLaunchKernelGGL(argmax_pairs_kernel, dim3(1), dim3(kArgmaxThreads), 0, prg::as_stream(stream),
-                     values, indices, out_index, pair_count);
+  hipLaunchKernelGGL(argmax_pairs_kernel<false>, dim3(1), dim3(kArgmaxThreads), 0, prg::as_stream(stream),
+                     values, indices, out_index, pair_count, nullptr, nullptr, nullptr);
   PRG_CHECK_LAUNCH(name);
   return PRG_OK;
 }

@@ -306,4 +306,10 @@ int launch_q4_gemv(hipStream_t stream, GemvParams& p, int M, int rows_per_wave, 
 // Rows per wave picked for a launch of `total_rows` rows at in_dim K.
 int gemv_rows_per_wave(uint32_t total_rows, uint32_t K, int epi, int M);
 
+// Final argmax over partials + advance of the device token loop.
+int launch_argmax_advance(hipStream_t s, const float* values, const uint32_t* indices, uint32_t n,
+                          DecodeCtl* ctl, const uint32_t* prompt, uint32_t* predictions);
+// Advance with the next token forced from prompt (no lm_head this step).
+int launch_advance_forced(hipStream_t s, DecodeCtl* ctl, const uint32_t* prompt);
+
 }  // namespace prg

@@ -1,0 +1,151 @@
+"""Python handle on the C++ decode model (include/peregrine_model.h).
+
+Mirrors the reference's DeviceModel / ModelState surface
+(src/model/model.zig:538-1662, src/model/state.zig:45-180) for tests and the
+benchmark. All compute runs in libperegrine_hip.so.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import numpy as np
+
+from ._lib import call, lib
+from .device import init
+
+
+class PrgModelConfig(C.Structure):
+    _fields_ = [("num_layers", C.c_uint32), ("hidden", C.c_uint32), ("intermediate", C.c_uint32),
+                ("vocab", C.c_uint32), ("full_attention_interval", C.c_uint32), ("rms_eps", C.c_float)]
+
+
+@dataclass
+class ModelConfig:
+    num_layers: int = 32
+    hidden: int = 4096
+    intermediate: int = 12288
+    vocab: int = 248320
+    full_attention_interval: int = 4
+    rms_eps: float = 1e-6
+
+    def c(self) -> PrgModelConfig:
+        return PrgModelConfig(self.num_layers, self.hidden, self.intermediate, self.vocab,
+                              self.full_attention_interval, self.rms_eps)
+
+    def is_linear(self, i: int) -> bool:  # decoder_layer.zig:29-31
+        return (i + 1) % self.full_attention_interval != 0
+
+
+QWEN35_9B = ModelConfig()
+
+
+def _tensor(getter, handle, name: str, dtype) -> tuple[int, int]:
+    p = C.c_void_p(0)
+    n = C.c_size_t(0)
+    call(getter, handle, name.encode(), C.byref(p), C.byref(n))
+    return p.value, n.value
+
+
+def _d2h(ptr: int, nbytes: int, dtype) -> np.ndarray:
+    out = np.empty(nbytes // np.dtype(dtype).itemsize, dtype)
+    call("prg_hip_memcpy", out.ctypes.data_as(C.c_void_p), C.c_void_p(ptr), C.c_size_t(nbytes), 1, None, 1)
+    return out
+
+
+class DeviceModel:
+    """Random-initialised Qwen3.5-shaped Q4 decoder resident on the GPU."""
+
+    def __init__(self, cfg: ModelConfig = QWEN35_9B, seed: int = 0) -> None:
+        init()
+        self.cfg = cfg
+        h = C.c_void_p(0)
+        call("prg_model_create_random", C.byref(cfg.c()), C.c_uint64(seed), C.byref(h))
+        self.handle = h
+
+    @property
+    def weight_bytes(self) -> int:
+        return int(lib.prg_model_weight_bytes(self.handle))
+
+    def tensor_ptr(self, name: str) -> tuple[int, int]:
+        return _tensor("prg_model_tensor", self.handle, name, None)
+
+    def read(self, name: str, dtype) -> np.ndarray:
+        p, n = self.tensor_ptr(name)
+        return _d2h(p, n, dtype)
+
+    def close(self) -> None:
+        if self.handle:
+            lib.prg_model_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self) -> None:
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class ModelState:
+    """KV caches + GDN states + decode workspace for one sequence."""
+
+    def __init__(self, model: DeviceModel, max_seq: int) -> None:
+        self.model = model
+        h = C.c_void_p(0)
+        call("prg_model_state_create", model.handle, max_seq, C.byref(h))
+        self.handle = h
+        self.max_seq = max_seq
+        self.stride = int(lib.prg_model_state_stride(h))
+
+    def reset(self) -> None:  # state.zig:110-118
+        call("prg_model_state_reset", self.handle)
+
+    def read(self, name: str, dtype) -> np.ndarray:
+        p, n = _tensor("prg_model_state_tensor", self.handle, name, None)
+        return _d2h(p, n, dtype)
+
+    # model.zig:1564-1578
+    def forward_next_token(self, token: int, cache_pos: int, rope_pos: int | None = None,
+                           seq_len: int | None = None) -> int:
+        rope_pos = cache_pos if rope_pos is None else rope_pos
+        seq_len = cache_pos + 1 if seq_len is None else seq_len
+        out = C.c_uint32(0)
+        call("prg_model_forward_next_token", self.model.handle, self.handle, token, cache_pos, rope_pos, seq_len,
+             C.byref(out))
+        return int(out.value)
+
+    def prefill(self, prompt) -> int:
+        prompt = np.ascontiguousarray(prompt, np.uint32)
+        out = C.c_uint32(0)
+        call("prg_model_prefill", self.model.handle, self.handle, prompt.ctypes.data_as(C.c_void_p), len(prompt),
+             C.byref(out))
+        return int(out.value)
+
+    def decode(self, n_steps: int) -> tuple[np.ndarray, float]:
+        toks = np.empty(n_steps, np.uint32)
+        ms = C.c_float(0.0)
+        call("prg_model_decode", self.model.handle, self.handle, n_steps, toks.ctypes.data_as(C.c_void_p),
+             C.byref(ms))
+        return toks, float(ms.value)
+
+    # decode_loop.zig:96-160 (empty prefix)
+    def generate(self, prompt, n_new: int, teacher_force: bool = False) -> tuple[np.ndarray, float]:
+        prompt = np.ascontiguousarray(prompt, np.uint32)
+        steps = len(prompt) if teacher_force else len(prompt) - 1 + n_new
+        preds = np.empty(steps, np.uint32)
+        ms = C.c_float(0.0)
+        call("prg_model_generate", self.model.handle, self.handle, prompt.ctypes.data_as(C.c_void_p), len(prompt),
+             0 if teacher_force else n_new, 1 if teacher_force else 0, preds.ctypes.data_as(C.c_void_p),
+             C.byref(ms))
+        return preds, float(ms.value)
+
+    def close(self) -> None:
+        if self.handle:
+            lib.prg_model_state_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self) -> None:
+        try:
+            self.close()
+        except Exception:
+            pass
