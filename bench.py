@@ -121,16 +121,37 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=32)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--sweep", action="store_true", help="also run the Q4 GEMV sweep (configs[1])")
+    ap.add_argument("--eager", action="store_true",
+                    help="launch each token's kernels directly instead of replaying the HIP graph "
+                         "(for kernel tracers; slower)")
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="only the dominant-kernel loop and a 256 MiB copy-kernel reference (for PMC runs)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(json.dumps({"error": "this build runs on exactly one GPU (no multi-GPU path); use --gpus 1"}))
         return 2
 
+    if a.eager:
+        os.environ["PEREGRINE_EAGER"] = "1"
     from peregrine_amd import device
     from peregrine_amd.model import QWEN35_9B, DeviceModel, ModelState
 
     device.init(0)
     log("[bench]", device.device_name())
+    if a.roofline_only:
+        import ctypes as C
+
+        from peregrine_amd._lib import call
+        from peregrine_amd.device import DeviceArray
+
+        nbytes = 256 * 1024 * 1024
+        src, dst = DeviceArray((nbytes,), np.uint8), DeviceArray((nbytes,), np.uint8)
+        for _ in range(4):
+            call("prg_hip_copy_kernel", C.c_void_p(dst.ptr), C.c_void_p(src.ptr), C.c_size_t(nbytes), None)
+        device.synchronize()
+        roof = dominant_kernel_roofline(iters=20)
+        print(json.dumps({"copy_bytes": nbytes, "roofline": roof}), flush=True)
+        return 0
     t0 = time.time()
     model = DeviceModel(QWEN35_9B, seed=0)
     log(f"[bench] model init {time.time() - t0:.1f}s, {model.weight_bytes / 1e9:.2f} GB weights")
@@ -169,7 +190,8 @@ def main() -> int:
                    "layers": QWEN35_9B.num_layers, "gdn_layers": 24, "attention_layers": 8,
                    "hidden": QWEN35_9B.hidden, "ffn": QWEN35_9B.intermediate, "vocab": QWEN35_9B.vocab,
                    "prompt_tokens": PROMPT_TOKENS, "context_at_end": int(max_seq), "batch": 1,
-                   "weight_bytes": int(model.weight_bytes), "parallelism": "single GPU"},
+                   "weight_bytes": int(model.weight_bytes), "parallelism": "single GPU",
+                   "execution": "eager launches" if a.eager else "one HIP graph replay per token"},
         "roofline": roof,
         "cpu_baseline": cpu,
         **extra,

@@ -74,6 +74,9 @@ int prg_hip_event_create(void **event);
 int prg_hip_event_destroy(void *event);
 int prg_hip_event_record(void *event, void *stream);
 int prg_hip_event_elapsed_ms(void *start, void *stop, float *ms);
+/* Plain device-to-device copy kernel (bytes % 16 == 0); the reference dispatch
+ * for calibrating HBM byte counters. */
+int prg_hip_copy_kernel(void *dst, const void *src, size_t bytes, void *stream);
 
 /* ======================================================================
  * Q4 linear ops — MLX affine 4-bit, group 64, bf16 scale + bias.

@@ -23,6 +23,7 @@
 // and sequence length live in device memory (DecodeCtl) and are advanced by the
 // argmax kernel, so replaying the graph runs the greedy loop with no host sync.
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <map>
@@ -172,6 +173,10 @@ struct PrgModelState {
   hipGraphExec_t graph_decode = nullptr;  // layers + lm_head argmax + advance
   hipGraphExec_t graph_prompt = nullptr;  // layers + forced advance
   hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  // PEREGRINE_EAGER=1: launch each token's kernels directly instead of
+  // replaying the captured graph (same kernels and arguments; for tools such as
+  // kernel tracers that do not follow graph launches).
+  bool eager = false;
 };
 
 namespace prg {
@@ -437,10 +442,18 @@ int capture(PrgModel* m, PrgModelState* st, bool with_head, hipGraphExec_t* out)
 }
 
 int ensure_graphs(PrgModelState* st) {
+  if (st->eager) return PRG_OK;
   if (!st->graph_decode)
     if (int rc = capture(st->model, st, true, &st->graph_decode)) return rc;
   if (!st->graph_prompt)
     if (int rc = capture(st->model, st, false, &st->graph_prompt)) return rc;
+  return PRG_OK;
+}
+
+// One token step: graph replay, or the same launches issued eagerly.
+int run_step(PrgModelState* st, bool with_head) {
+  if (st->eager) return encode_token(st->model, st, with_head);
+  PRG_HIP(hipGraphLaunch(with_head ? st->graph_decode : st->graph_prompt, st->stream));
   return PRG_OK;
 }
 
@@ -525,6 +538,7 @@ int prg_model_state_create(PrgModel* model, uint32_t max_seq, PrgModelState** ou
   st->stride = cache_stride_for(max_seq);
   st->nsplit = attn_num_splits(st->stride);
   st->split_tokens = attn_split_tokens(st->stride, st->nsplit);
+  if (const char* e = getenv("PEREGRINE_EAGER")) st->eager = (e[0] == '1');
   const PrgModelConfig& c = model->cfg;
 
   // Two passes over the same layout: size, then carve the arena.
@@ -644,7 +658,7 @@ int prg_model_forward_next_token(PrgModel* model, PrgModelState* st, uint32_t to
   ctl.prompt_len = 0;
   ctl.capacity = st->max_seq;
   PRG_HIP(hipMemcpyAsync(st->ctl, &ctl, sizeof(ctl), hipMemcpyHostToDevice, st->stream));
-  PRG_HIP(hipGraphLaunch(st->graph_decode, st->stream));
+  if (int rc = run_step(st, true)) return rc;
   PRG_HIP(hipMemcpyAsync(next_token, st->predictions, sizeof(uint32_t), hipMemcpyDeviceToHost, st->stream));
   PRG_HIP(hipStreamSynchronize(st->stream));
   return PRG_OK;
@@ -667,8 +681,9 @@ int prg_model_prefill(PrgModel* model, PrgModelState* st, const uint32_t* prompt
   ctl.capacity = st->max_seq;
   PRG_HIP(hipMemcpyAsync(st->prompt, prompt, sizeof(uint32_t) * prompt_len, hipMemcpyHostToDevice, st->stream));
   PRG_HIP(hipMemcpyAsync(st->ctl, &ctl, sizeof(ctl), hipMemcpyHostToDevice, st->stream));
-  for (uint32_t n = 0; n + 1 < prompt_len; ++n) PRG_HIP(hipGraphLaunch(st->graph_prompt, st->stream));
-  PRG_HIP(hipGraphLaunch(st->graph_decode, st->stream));
+  for (uint32_t n = 0; n + 1 < prompt_len; ++n)
+    if (int rc = run_step(st, false)) return rc;
+  if (int rc = run_step(st, true)) return rc;
   PRG_HIP(hipMemcpyAsync(next_token, st->predictions + (prompt_len - 1), sizeof(uint32_t), hipMemcpyDeviceToHost,
                          st->stream));
   PRG_HIP(hipStreamSynchronize(st->stream));
@@ -686,7 +701,8 @@ int prg_model_decode(PrgModel* model, PrgModelState* st, uint32_t n_steps, uint3
     return set_error(PRG_ERR_SEQUENCE_TOO_LONG, "position %u + %u steps exceeds max_seq %u", ctl.n, n_steps,
                      st->max_seq);
   PRG_HIP(hipEventRecord(st->ev0, st->stream));
-  for (uint32_t i = 0; i < n_steps; ++i) PRG_HIP(hipGraphLaunch(st->graph_decode, st->stream));
+  for (uint32_t i = 0; i < n_steps; ++i)
+    if (int rc = run_step(st, true)) return rc;
   PRG_HIP(hipEventRecord(st->ev1, st->stream));
   PRG_HIP(hipMemcpyAsync(tokens_out, st->predictions + ctl.n, sizeof(uint32_t) * n_steps, hipMemcpyDeviceToHost,
                          st->stream));
@@ -719,9 +735,11 @@ int prg_model_generate(PrgModel* model, PrgModelState* st, const uint32_t* promp
   PRG_HIP(hipMemsetAsync(st->predictions, 0xFF, sizeof(uint32_t) * st->stride, st->stream));
   PRG_HIP(hipMemcpyAsync(st->ctl, &ctl, sizeof(ctl), hipMemcpyHostToDevice, st->stream));
   const uint32_t head_from = teacher_force ? 0 : prompt_len - 1;
-  for (uint32_t n = 0; n < head_from; ++n) PRG_HIP(hipGraphLaunch(st->graph_prompt, st->stream));
+  for (uint32_t n = 0; n < head_from; ++n)
+    if (int rc = run_step(st, false)) return rc;
   PRG_HIP(hipEventRecord(st->ev0, st->stream));
-  for (uint32_t n = head_from; n < steps; ++n) PRG_HIP(hipGraphLaunch(st->graph_decode, st->stream));
+  for (uint32_t n = head_from; n < steps; ++n)
+    if (int rc = run_step(st, true)) return rc;
   PRG_HIP(hipEventRecord(st->ev1, st->stream));
   PRG_HIP(hipMemcpyAsync(predictions, st->predictions, sizeof(uint32_t) * steps, hipMemcpyDeviceToHost, st->stream));
   PRG_HIP(hipStreamSynchronize(st->stream));

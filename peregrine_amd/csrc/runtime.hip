@@ -25,7 +25,27 @@ int set_error(int code, const char* fmt, ...) {
 
 using prg::set_error;
 
+namespace {
+// Plain streaming copy (16 B per thread per step): the calibration reference
+// for HBM byte counters (FETCH_SIZE / WRITE_SIZE per dispatch).
+__global__ void copy_kernel(const uint4* __restrict__ src, uint4* __restrict__ dst, size_t n16) {
+  for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n16;
+       i += static_cast<size_t>(gridDim.x) * blockDim.x)
+    dst[i] = src[i];
+}
+}  // namespace
+
 extern "C" {
+
+int prg_hip_copy_kernel(void* dst, const void* src, size_t bytes, void* stream) {
+  PRG_CHECK_ARG(dst && src, "prg_hip_copy_kernel: null pointer");
+  PRG_CHECK_ARG(bytes % 16 == 0, "prg_hip_copy_kernel: bytes %zu not a multiple of 16", bytes);
+  const size_t n16 = bytes / 16;
+  hipLaunchKernelGGL(copy_kernel, dim3(2048), dim3(256), 0, prg::as_stream(stream),
+                     static_cast<const uint4*>(src), static_cast<uint4*>(dst), n16);
+  PRG_CHECK_LAUNCH("prg_hip_copy_kernel");
+  return PRG_OK;
+}
 
 const char* prg_last_error(void) { return prg::g_last_error; }
 
