@@ -232,19 +232,38 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnD
 }
 
 // ------------------------------------------------------------------- reduce --
+// One block per q head, one thread per dim. The split statistics (m, denom)
+// are merged in parallel first (weights in LDS), then each thread sums its
+// dim over the splits with independent loads.
+constexpr uint32_t kMaxSplits = 1024;
+
 __global__ __launch_bounds__(kAttnThreads) void attn_reduce_kernel(const AttnDecodeArgs a) {
+  __shared__ float wsh[kMaxSplits];
+  __shared__ float red[kAttnThreads / kWave];
   const uint32_t h = blockIdx.x;  // q head
-  const uint32_t d = threadIdx.x;
+  const uint32_t t = threadIdx.x;
   const float* base = a.partials + static_cast<size_t>(h) * a.nsplit * kAttnPartialStride;
-  float m_all = -INFINITY;
-  for (uint32_t c = 0; c < a.nsplit; ++c) m_all = fmaxf(m_all, base[c * kAttnPartialStride]);
-  float den = 0.0f, acc = 0.0f;
-  for (uint32_t c = 0; c < a.nsplit; ++c) {
-    const float* pc = base + c * kAttnPartialStride;
-    const float wgt = (pc[0] == -INFINITY) ? 0.0f : expf(pc[0] - m_all);
-    den += pc[1] * wgt;
-    acc += pc[2 + d] * wgt;
+  float m_local = -INFINITY;
+  for (uint32_t c = t; c < a.nsplit; c += kAttnThreads) m_local = fmaxf(m_local, base[c * kAttnPartialStride]);
+  m_local = wave_max(m_local);
+  if ((t & 63) == 0) red[t >> 6] = m_local;
+  __syncthreads();
+  float m_all = red[0];
+#pragma unroll
+  for (int i = 1; i < kAttnThreads / kWave; ++i) m_all = fmaxf(m_all, red[i]);
+  __syncthreads();
+  float den_local = 0.0f;
+  for (uint32_t c = t; c < a.nsplit; c += kAttnThreads) {
+    const float mc = base[c * kAttnPartialStride];
+    const float wgt = (mc == -INFINITY) ? 0.0f : expf(mc - m_all);
+    wsh[c] = wgt;
+    den_local += base[c * kAttnPartialStride + 1] * wgt;
   }
+  const float den = block_sum<kAttnThreads>(den_local, red);  // also orders the wsh writes
+  const uint32_t d = t;
+  float acc = 0.0f;
+#pragma unroll 8
+  for (uint32_t c = 0; c < a.nsplit; ++c) acc += base[c * kAttnPartialStride + 2 + d] * wsh[c];
   const size_t i = static_cast<size_t>(h) * kAttnHeadDim + d;
   const float sig = 1.0f / (1.0f + expf(-bf2f(a.gate[i])));
   a.out[i] = f2bf((acc / den) * sig);
@@ -257,7 +276,7 @@ namespace prg {
 uint32_t attn_num_splits(uint32_t capacity) {
   // >= 64 splits per kv head (256 blocks) and <= 1024 tokens per split.
   uint32_t n = 64;
-  while ((capacity + n - 1) / n > 1024) n *= 2;
+  while ((capacity + n - 1) / n > 1024 && n < kMaxSplits) n *= 2;
   return n;
 }
 

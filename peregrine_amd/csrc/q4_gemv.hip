@@ -7,67 +7,37 @@
 //   argmax partial shaders/linear.metal:195-420        (M=1 and M=2)
 //   argmax pairs   shaders/argmax.metal:6-43
 //   dequantize     shaders/linear.metal:422-444
+#include <stdlib.h>
+
 #include <algorithm>
+#include <map>
+#include <mutex>
+#include <utility>
 
 #include "q4_gemv.hpp"
 
 namespace prg {
 
-namespace {
-
-template <int M, int ROWS, int EPI, bool NORM>
-int launch_iters(hipStream_t s, const GemvParams& p, int iters, uint32_t blocks, size_t lds) {
-#define PRG_GEMV_CASE(I)                                                                     \
-  case I:                                                                                    \
-    hipLaunchKernelGGL((q4_gemv_kernel<M, ROWS, I, EPI, NORM>), dim3(blocks), dim3(kGemvThreads), \
-                       lds, s, p);                                                           \
-    return 0;
-  switch (iters) {
-    PRG_GEMV_CASE(1)
-    PRG_GEMV_CASE(2)
-    PRG_GEMV_CASE(3)
-    PRG_GEMV_CASE(4)
-    PRG_GEMV_CASE(6)
-    PRG_GEMV_CASE(8)
-    default:
-      return -1;
-  }
-#undef PRG_GEMV_CASE
-}
-
-template <int M, int EPI, bool NORM>
-int launch_rows(hipStream_t s, const GemvParams& p, int rows, int iters, uint32_t blocks, size_t lds) {
-  if constexpr (EPI == kEpiArgmax) {
-    return launch_iters<M, 8, EPI, NORM>(s, p, iters, blocks, lds);
-  } else {
-    switch (rows) {
-      case 1: return launch_iters<M, 1, EPI, NORM>(s, p, iters, blocks, lds);
-      case 2: return launch_iters<M, 2, EPI, NORM>(s, p, iters, blocks, lds);
-      case 4: return launch_iters<M, 4, EPI, NORM>(s, p, iters, blocks, lds);
-      default: return -1;
-    }
-  }
-}
-
-template <int EPI, bool NORM>
-int launch_m(hipStream_t s, const GemvParams& p, int M, int rows, int iters, uint32_t blocks, size_t lds) {
-  if (M == 1) return launch_rows<1, EPI, NORM>(s, p, rows, iters, blocks, lds);
-  if (M == 2) return launch_rows<2, EPI, NORM>(s, p, rows, iters, blocks, lds);
-  return -1;
-}
-
-}  // namespace
-
 int gemv_rows_per_wave(uint32_t total_rows, uint32_t K, int epi, int M) {
   if (epi == kEpiArgmax) return 8;
   const int nmat = (epi == kEpiSiluGate) ? 2 : 1;
   const int iters = static_cast<int>((K + kGemvKStep - 1) / kGemvKStep);
-  // Keep <= 16 dwordx4 loads in flight per lane and >= ~512 blocks when the
-  // matrix is large enough to fill 256 CUs twice.
-  int rows = 4;
-  while (rows > 1 && rows * nmat * iters > 16) rows >>= 1;
-  while (rows > 1 && total_rows / (kGemvWaves * rows) < 512) rows >>= 1;
+  // One register buffer holds ROWS x NMAT x ITERS dwordx4 loads; keep it at
+  // <= 4 (two buffers in flight) and keep >= 4096 groups so every wave of a
+  // full grid has work.
+  static const int forced = [] {
+    const char* e = getenv("PEREGRINE_GEMV_ROWS");  // tuning override: 1, 2 or 4
+    const int v = e ? atoi(e) : 0;
+    return (v == 1 || v == 2 || v == 4) ? v : 0;
+  }();
+  if (forced) return forced;
+  // Measured on MI355X (2048-wide K steps): one row per wave with a grid of
+  // 3 blocks/CU is fastest for every decode shape; 2 rows only when K is a
+  // single step (more work per wave to amortise the per-group epilogue).
+  int rows = iters == 1 ? 2 : 1;
   (void)M;
+  (void)nmat;
+  (void)total_rows;
   return rows;
 }
 
@@ -84,28 +54,28 @@ int launch_q4_gemv(hipStream_t stream, GemvParams& p, int M, int rows, int epi, 
   p.tail_lanes = rem == 0 ? 64u : rem / 32u;
   if (M < 1 || M > 2) return set_error(PRG_ERR_INVALID_ARG, "%s: M=%d", name, M);
   if (p.nseg < 1 || p.nseg > kGemvMaxSegs) return set_error(PRG_ERR_INVALID_ARG, "%s: nseg", name);
-  const uint32_t rows_per_block = static_cast<uint32_t>(kGemvWaves * rows);
-  uint32_t blocks = 0;
+  uint32_t groups = 0;
   for (uint32_t i = 0; i < p.nseg; ++i) {
     GemvSeg& sg = p.seg[i];
     if (sg.rows == 0 || sg.rows % 8 != 0)
       return set_error(PRG_ERR_INVALID_ARG, "%s: out_dim %u must be a positive multiple of 8", name, sg.rows);
-    sg.block_begin = blocks;
-    blocks += (sg.rows + rows_per_block - 1) / rows_per_block;
+    sg.block_begin = groups;
+    groups += (sg.rows + static_cast<uint32_t>(rows) - 1) / static_cast<uint32_t>(rows);
   }
+  p.total_groups = groups;
   const size_t lds = static_cast<size_t>(M) * p.K * sizeof(uint16_t);
   int rc;
   if (epi == kEpiPlain)
-    rc = norm ? launch_m<kEpiPlain, true>(stream, p, M, rows, iters, blocks, lds)
-              : launch_m<kEpiPlain, false>(stream, p, M, rows, iters, blocks, lds);
+    rc = norm ? launch_m<kEpiPlain, true>(stream, p, M, rows, iters, lds)
+              : launch_m<kEpiPlain, false>(stream, p, M, rows, iters, lds);
   else if (epi == kEpiResidual)
-    rc = norm ? -1 : launch_m<kEpiResidual, false>(stream, p, M, rows, iters, blocks, lds);
+    rc = norm ? -1 : launch_m<kEpiResidual, false>(stream, p, M, rows, iters, lds);
   else if (epi == kEpiSiluGate)
-    rc = norm ? launch_m<kEpiSiluGate, true>(stream, p, M, rows, iters, blocks, lds)
-              : launch_m<kEpiSiluGate, false>(stream, p, M, rows, iters, blocks, lds);
+    rc = norm ? launch_m<kEpiSiluGate, true>(stream, p, M, rows, iters, lds)
+              : launch_m<kEpiSiluGate, false>(stream, p, M, rows, iters, lds);
   else
-    rc = norm ? launch_m<kEpiArgmax, true>(stream, p, M, rows, iters, blocks, lds)
-              : launch_m<kEpiArgmax, false>(stream, p, M, rows, iters, blocks, lds);
+    rc = norm ? launch_m<kEpiArgmax, true>(stream, p, M, rows, iters, lds)
+              : launch_m<kEpiArgmax, false>(stream, p, M, rows, iters, lds);
   if (rc != 0) return set_error(PRG_ERR_INVALID_ARG, "%s: no kernel for M=%d rows=%d iters=%d", name, M, rows, iters);
   PRG_CHECK_LAUNCH(name);
   return PRG_OK;
@@ -174,11 +144,21 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_pairs_kernel(
   __shared__ uint32_t sp[kArgmaxThreads / 64];
   float bv = -INFINITY;
   uint32_t bp = 0xffffffffu;
-  for (uint32_t p = threadIdx.x; p < n; p += kArgmaxThreads) {
-    const float v = values[p];
-    if (argmax_better(v, p, bv, bp)) {
-      bv = v;
-      bp = p;
+  constexpr int kU = 8;  // independent loads in flight per thread
+  for (uint32_t base = threadIdx.x; base < n; base += kArgmaxThreads * kU) {
+    float v[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const uint32_t p = base + u * kArgmaxThreads;
+      v[u] = p < n ? values[p] : -INFINITY;
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const uint32_t p = base + u * kArgmaxThreads;
+      if (argmax_better(v[u], p, bv, bp)) {
+        bv = v[u];
+        bp = p;
+      }
     }
   }
 #pragma unroll

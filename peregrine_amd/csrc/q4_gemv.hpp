@@ -11,12 +11,12 @@
 //   * Lane l reads 16 contiguous bytes (dwordx4 = 32 nibbles) per row per
 //     2048-wide K step, so one wave load covers 1 KiB of a row, fully
 //     coalesced. All ROWS x ITERS weight loads are issued up front.
-//   * Dequant stays in registers: a nibble pair is OR-ed into the mantissa
-//     of two bf16 lanes (0x4300 | q == 128 + q exactly) and multiplied with the
-//     matching activation pair by v_dot2c_f32_bf16 with fp32 accumulation;
-//     the 128*sum(x) offset is removed once per half-group.
-//   * x is staged once per block in LDS, pre-permuted so that the pair
-//     (x[8j+i], x[8j+i+4]) lines up with nibbles i and i+4 of word j.
+//   * Dequant stays in registers: v_perm_b32 places each nibble under the
+//     byte 0x43 (bf16 0x43qq == 128 + q exactly), two per dword, and
+//     v_dot2c_f32_bf16 multiplies them with the matching activation pair in
+//     fp32; the 128*sum(x) offset is removed once per half-group.
+//   * x is staged once per block in LDS, pre-permuted so each activation pair
+//     lines up with the nibble pair the unpack produces.
 //     An optional fused RMSNorm prologue normalises x while staging it.
 //   * Partial sums are reduced across the wave with DPP row ops + readlane.
 //   * Up to 4 independent weight matrices ("segments") that share x run in
@@ -58,7 +58,7 @@ struct GemvSeg {
   const uint16_t* conv_w;     // bf16 [conv_dim, 4]
   uint32_t conv_dim;
   uint32_t rows;              // output rows of this segment
-  uint32_t block_begin;       // first block index of this segment
+  uint32_t block_begin;       // first group index of this segment (set by the launcher)
 };
 
 struct GemvParams {
@@ -69,6 +69,7 @@ struct GemvParams {
   uint32_t K;
   uint32_t nseg;
   uint32_t tail_lanes;        // active lanes in the last K step (64 if full)
+  uint32_t total_groups;      // groups of ROWS rows over all segments (set by the launcher)
 };
 
 // ------------------------------------------------------------ device ---------
@@ -94,156 +95,154 @@ __device__ inline float wave_sum_uniform(float v) {
   return (r0 + r1) + (r2 + r3);
 }
 
-// 8 bf16 (as a uint4 of pairs (x0,x1),(x2,x3),(x4,x5),(x6,x7)) ->
-// dot2 order (x0,x4),(x1,x5),(x2,x6),(x3,x7).
+// 8 bf16 (as a uint4 of pairs (x0,x1),(x2,x3),(x4,x5),(x6,x7)) -> the dot2
+// order of the nibble unpack below: (x0,x2),(x4,x6),(x1,x3),(x5,x7).
 __device__ inline uint4 permute_pairs(uint4 v) {
   uint4 o;
-  o.x = (v.x & 0xffffu) | (v.z << 16);
-  o.y = (v.x >> 16) | (v.z & 0xffff0000u);
-  o.z = (v.y & 0xffffu) | (v.w << 16);
-  o.w = (v.y >> 16) | (v.w & 0xffff0000u);
+  o.x = (v.x & 0xffffu) | (v.y << 16);
+  o.y = (v.z & 0xffffu) | (v.w << 16);
+  o.z = (v.x >> 16) | (v.y & 0xffff0000u);
+  o.w = (v.z >> 16) | (v.w & 0xffff0000u);
   return o;
 }
 
-// Stage the M activation rows into LDS (permuted pairs). With NORM, each row
-// is RMS-normalised first: out = bf16(x * rsqrt(mean(x^2) + eps) * w), the
-// rmsnorm_bf16 formula (reference shaders/rmsnorm.metal:80-116).
-template <int M, bool NORM>
-__device__ inline void gemv_stage_x(const GemvParams& p, uint32_t* xs, float* red) {
-  const uint32_t n8 = p.K / 8;
-#pragma unroll
-  for (int m = 0; m < M; ++m) {
-    const uint4* src = reinterpret_cast<const uint4*>(p.x[m]);
-    uint4* dst = reinterpret_cast<uint4*>(xs + m * (p.K / 2));
-    if constexpr (NORM) {
-      static_assert(kGemvThreads == kNormThreads, "fused norm shares the standalone reduction");
-      const float scale = rms_scale(src, n8, p.K, p.eps, red);
-      const uint4* wsrc = reinterpret_cast<const uint4*>(p.norm_w);
-      for (uint32_t g = threadIdx.x; g < n8; g += kGemvThreads)
-        dst[g] = permute_pairs(rms_apply(src[g], wsrc[g], scale));
-    } else {
-      for (uint32_t g = threadIdx.x; g < n8; g += kGemvThreads) dst[g] = permute_pairs(src[g]);
-    }
-  }
+// Unpack one packed word (nibbles n0..n7, n0 lowest) into four bf16 pairs of
+// the exact values 128 + q: (n0,n2), (n4,n6), (n1,n3), (n5,n7). The low and
+// high nibbles are isolated as bytes, then v_perm_b32 interleaves each nibble
+// byte with the byte 0x43 (bf16 0x43qq == 128 + q, q <= 15).
+__device__ inline void unpack_q4_word(uint32_t word, uint32_t (&t)[4]) {
+  constexpr uint32_t kHigh = 0x43434343u;
+  const uint32_t lo = word & 0x0F0F0F0Fu;         // bytes n0 n2 n4 n6
+  const uint32_t hi = (word >> 4) & 0x0F0F0F0Fu;  // bytes n1 n3 n5 n7
+  // selector byte k: 0..3 = byte of the 2nd operand, 4..7 = byte of kHigh
+  t[0] = __builtin_amdgcn_perm(kHigh, lo, 0x04010400u);
+  t[1] = __builtin_amdgcn_perm(kHigh, lo, 0x04030402u);
+  t[2] = __builtin_amdgcn_perm(kHigh, hi, 0x04010400u);
+  t[3] = __builtin_amdgcn_perm(kHigh, hi, 0x04030402u);
 }
 
-template <int M, int ROWS, int ITERS, int EPI, bool NORM>
-__global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(const GemvParams p) {
-  constexpr int NMAT = (EPI == kEpiSiluGate) ? 2 : 1;
-  extern __shared__ uint32_t xs[];  // [M][K/2] permuted bf16 pairs
-  __shared__ float red[kGemvWaves];
+// Register buffer holding one group's weights for one wave: ROWS rows of each
+// of NMAT matrices, ITERS K-steps, plus the matching scale/bias halves.
+template <int NMAT, int ROWS, int ITERS>
+struct GemvBuf {
+  u32x4 w[NMAT][ROWS][ITERS];
+  uint32_t sb[NMAT][ROWS][ITERS];  // scale bits | bias bits << 16
+};
 
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wid = threadIdx.x / kWave;
+// Where group g of the launch lives: segment index and first row.
+struct GemvLoc {
+  uint32_t seg;
+  uint32_t row0;
+};
 
-  // Segment lookup (uniform).
-  const uint32_t bid = blockIdx.x;
+template <int ROWS>
+__device__ inline GemvLoc gemv_locate(const GemvParams& p, uint32_t g) {
   uint32_t si = 0;
   for (uint32_t i = 1; i < p.nseg; ++i)
-    if (bid >= p.seg[i].block_begin) si = i;
-  const GemvSeg& sg = p.seg[si];
-  const uint32_t row0 = (bid - sg.block_begin) * (kGemvWaves * ROWS) + wid * ROWS;
-  const uint32_t nrows = sg.rows;
-  const uint32_t K = p.K;
-  const uint32_t words_per_row = K / 8;
-  const uint32_t groups = K / 64;
-  const bool tail_active = lane < static_cast<int>(p.tail_lanes);
+    if (g >= p.seg[i].block_begin) si = i;
+  return GemvLoc{si, (g - p.seg[si].block_begin) * ROWS};
+}
 
-  // 1) issue every weight load for this wave's rows.
-  u32x4 wv[NMAT][ROWS][ITERS];
+template <int NMAT, int ROWS, int ITERS, bool TAIL>
+__device__ inline void gemv_load(const GemvParams& p, uint32_t g, int lane, bool tail_active,
+                                 GemvBuf<NMAT, ROWS, ITERS>& b) {
+  const GemvLoc loc = gemv_locate<ROWS>(p, g);
+  const GemvSeg& sg = p.seg[loc.seg];
+  const uint32_t words_per_row = p.K / 8, groups = p.K / 64;
 #pragma unroll
   for (int mat = 0; mat < NMAT; ++mat) {
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) {
-      const uint32_t row = min(row0 + r, nrows - 1);
+      const uint32_t row = min(loc.row0 + r, sg.rows - 1);
       const u32x4* wp = reinterpret_cast<const u32x4*>(sg.w[mat] + static_cast<size_t>(row) * words_per_row) + lane;
+      const size_t meta = static_cast<size_t>(row) * groups + (lane >> 1);
 #pragma unroll
       for (int it = 0; it < ITERS; ++it) {
-        if (it < ITERS - 1 || tail_active)
-          wv[mat][r][it] = __builtin_nontemporal_load(wp + it * (kGemvKStep / 32));
-        else
-          wv[mat][r][it] = u32x4{0u, 0u, 0u, 0u};
+        if (!TAIL || it < ITERS - 1 || tail_active) {
+          b.w[mat][r][it] = __builtin_nontemporal_load(wp + it * (kGemvKStep / 32));
+          const uint32_t sc = sg.s[mat][meta + it * (kGemvKStep / 64)];
+          const uint32_t bi = sg.b[mat][meta + it * (kGemvKStep / 64)];
+          b.sb[mat][r][it] = sc | (bi << 16);
+        } else {
+          b.w[mat][r][it] = u32x4{0u, 0u, 0u, 0u};
+          b.sb[mat][r][it] = 0u;
+        }
       }
     }
   }
+}
 
-  // 2) stage activations (and the fused norm) while the loads are in flight.
-  gemv_stage_x<M, NORM>(p, xs, red);
-  __syncthreads();
+// Activation pairs of one lane for one K-step (16 dwords) + their sum.
+template <int M>
+struct XStep {
+  uint32_t xp[M][16];
+  float xsum[M];
+};
 
-  // 3) dequant + dot.
-  float acc[NMAT][ROWS][M];
+template <int M>
+__device__ inline void gemv_read_x(const uint32_t* xs, uint32_t K, int it, int lane, XStep<M>& x) {
+  constexpr uint32_t kOnes = 0x3F803F80u;  // bf16 pair (1, 1)
 #pragma unroll
-  for (int mat = 0; mat < NMAT; ++mat)
+  for (int m = 0; m < M; ++m) {
+    const uint4* xl = reinterpret_cast<const uint4*>(xs + m * (K / 2) + it * (kGemvKStep / 2) + lane * 16);
 #pragma unroll
-    for (int r = 0; r < ROWS; ++r)
-#pragma unroll
-      for (int m = 0; m < M; ++m) acc[mat][r][m] = 0.0f;
-
-  constexpr uint32_t kMask = 0x000F000Fu;
-  constexpr uint32_t kMagic = 0x43004300u;  // bf16 pair (128, 128)
-  constexpr uint32_t kOnes = 0x3F803F80u;   // bf16 pair (1, 1)
-
-#pragma unroll
-  for (int it = 0; it < ITERS; ++it) {
-    if (it == ITERS - 1 && !tail_active) break;
-    uint32_t xp[M][16];
-    float xsum[M];
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-      const uint4* xl = reinterpret_cast<const uint4*>(xs + m * (K / 2) + it * (kGemvKStep / 2) + lane * 16);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const uint4 v = xl[q];
-        xp[m][4 * q + 0] = v.x;
-        xp[m][4 * q + 1] = v.y;
-        xp[m][4 * q + 2] = v.z;
-        xp[m][4 * q + 3] = v.w;
-      }
-      float s = 0.0f;
-#pragma unroll
-      for (int j = 0; j < 16; ++j) s = dot2_bf16(xp[m][j], kOnes, s);
-      xsum[m] = s;
+    for (int q = 0; q < 4; ++q) {
+      const uint4 v = xl[q];
+      x.xp[m][4 * q + 0] = v.x;
+      x.xp[m][4 * q + 1] = v.y;
+      x.xp[m][4 * q + 2] = v.z;
+      x.xp[m][4 * q + 3] = v.w;
     }
-    const uint32_t group = it * (kGemvKStep / 64) + (lane >> 1);
+    float s = 0.0f;
 #pragma unroll
-    for (int mat = 0; mat < NMAT; ++mat) {
+    for (int j = 0; j < 16; ++j) s = dot2_bf16(x.xp[m][j], kOnes, s);
+    x.xsum[m] = s;
+  }
+}
+
+// acc[mat][r][m] += s*sum(q*x) + b*sum(x) over this lane's 32 values of step it.
+template <int M, int NMAT, int ROWS, int ITERS>
+__device__ inline void gemv_dot_step(const GemvBuf<NMAT, ROWS, ITERS>& b, int it, const XStep<M>& x,
+                                     float (&acc)[NMAT][ROWS][M]) {
 #pragma unroll
-      for (int r = 0; r < ROWS; ++r) {
-        const uint32_t row = min(row0 + r, nrows - 1);
-        const size_t meta = static_cast<size_t>(row) * groups + group;
-        const float sc = bf2f(sg.s[mat][meta]);
-        const float bi = bf2f(sg.b[mat][meta]);
-        const u32x4 w4 = wv[mat][r][it];
-        const uint32_t wd[4] = {w4[0], w4[1], w4[2], w4[3]};
-        float aq[M];
+  for (int mat = 0; mat < NMAT; ++mat) {
 #pragma unroll
-        for (int m = 0; m < M; ++m) aq[m] = 0.0f;
+    for (int r = 0; r < ROWS; ++r) {
+      const u32x4 w4 = b.w[mat][r][it];
+      const uint32_t wd[4] = {w4[0], w4[1], w4[2], w4[3]};
+      // Four independent dot2 chains per activation row: the dependent
+      // v_dot2c latency would otherwise serialise the 16 dot2s of a step.
+      float aq[M][4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint32_t word = wd[j];
-          const uint32_t t0 = (word & kMask) | kMagic;
-          const uint32_t t1 = ((word >> 4) & kMask) | kMagic;
-          const uint32_t t2 = ((word >> 8) & kMask) | kMagic;
-          const uint32_t t3 = ((word >> 12) & kMask) | kMagic;
+      for (int m = 0; m < M; ++m)
 #pragma unroll
-          for (int m = 0; m < M; ++m) {
-            aq[m] = dot2_bf16(t0, xp[m][4 * j + 0], aq[m]);
-            aq[m] = dot2_bf16(t1, xp[m][4 * j + 1], aq[m]);
-            aq[m] = dot2_bf16(t2, xp[m][4 * j + 2], aq[m]);
-            aq[m] = dot2_bf16(t3, xp[m][4 * j + 3], aq[m]);
-          }
-        }
+        for (int c = 0; c < 4; ++c) aq[m][c] = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        uint32_t t[4];
+        unpack_q4_word(wd[j], t);
 #pragma unroll
         for (int m = 0; m < M; ++m) {
-          const float qx = aq[m] - 128.0f * xsum[m];  // sum(q * x)
-          acc[mat][r][m] += sc * qx + bi * xsum[m];
+#pragma unroll
+          for (int c = 0; c < 4; ++c) aq[m][c] = dot2_bf16(t[c], x.xp[m][4 * j + c], aq[m][c]);
         }
+      }
+      const float sc = bf_lo(b.sb[mat][r][it]);
+      const float bi = bf_hi(b.sb[mat][r][it]);
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        const float dq = (aq[m][0] + aq[m][1]) + (aq[m][2] + aq[m][3]);
+        const float qx = dq - 128.0f * x.xsum[m];  // sum(q * x)
+        acc[mat][r][m] += sc * qx + bi * x.xsum[m];
       }
     }
   }
+}
 
-  // 4) reduce across the wave and write.
+// Reduce one group's accumulators across the wave and write its outputs.
+template <int M, int NMAT, int ROWS, int EPI>
+__device__ inline void gemv_epilogue(const GemvParams& p, const GemvLoc& loc, int lane,
+                                     float (&acc)[NMAT][ROWS][M]) {
   float tot[NMAT][ROWS][M];
 #pragma unroll
   for (int mat = 0; mat < NMAT; ++mat)
@@ -251,11 +250,12 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(const GemvParams 
     for (int r = 0; r < ROWS; ++r)
 #pragma unroll
       for (int m = 0; m < M; ++m) tot[mat][r][m] = wave_sum_uniform(acc[mat][r][m]);
-
   if (lane != 0) return;
+  const GemvSeg& sg = p.seg[loc.seg];
+  const uint32_t row0 = loc.row0;
   if constexpr (EPI == kEpiArgmax) {
     static_assert(ROWS == 8, "argmax partials cover 8 rows");
-    if (row0 >= nrows) return;
+    if (row0 >= sg.rows) return;
 #pragma unroll
     for (int m = 0; m < M; ++m) {
       float best = round_bf(tot[0][0][m]);
@@ -275,7 +275,7 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(const GemvParams 
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) {
       const uint32_t row = row0 + r;
-      if (row >= nrows) break;
+      if (row >= sg.rows) break;
 #pragma unroll
       for (int m = 0; m < M; ++m) {
         uint16_t o;
@@ -287,9 +287,9 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(const GemvParams 
         } else if constexpr (EPI == kEpiResidual) {
           o = f2bf(round_bf(tot[0][r][m]) + bf2f(sg.res[m][row]));
         } else {
-          const float g = round_bf(tot[0][r][m]);
-          const float u = round_bf(tot[1][r][m]);
-          o = f2bf(silu(g) * u);
+          const float gt = round_bf(tot[0][r][m]);
+          const float up = round_bf(tot[1][r][m]);
+          o = f2bf(silu(gt) * up);
         }
         sg.out[m][row] = o;
       }
@@ -297,7 +297,124 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(const GemvParams 
   }
 }
 
+// Persistent, software-pipelined GEMV. Work is split into "groups" of ROWS
+// consecutive rows of one segment; wave w of the grid handles groups
+// w, w + W, w + 2W, ... (W = waves in the grid). Each wave keeps two register
+// buffers: while it dequantises and reduces group g the loads of group g + W
+// are in flight, so HBM streaming overlaps the VALU work. The activation rows
+// (and fused-norm weights) are loaded before any weight so they return first;
+// the norm and LDS staging then run while the first group streams in. With XREG the lane's activation pairs for every
+// K-step stay in registers for the whole kernel.
+template <int M, int ROWS, int ITERS, int EPI, bool NORM, bool TAIL>
+__global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(const GemvParams p) {
+  constexpr int NMAT = (EPI == kEpiSiluGate) ? 2 : 1;
+  constexpr bool XREG = ITERS * M <= 4;  // <= 64 VGPRs of activation pairs
+  extern __shared__ uint32_t xs[];  // [M][K/2] permuted bf16 pairs
+  __shared__ float red[kGemvWaves];
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform
+  const uint32_t W = gridDim.x * kGemvWaves;
+  const uint32_t G = p.total_groups;
+  const bool tail_active = !TAIL || lane < static_cast<int>(p.tail_lanes);
+  const uint32_t n8 = p.K / 8;
+
+  // 1) activations (+ norm weights): one uint4 (8 values) per thread per K-step.
+  uint4 xv[M][ITERS];
+  uint4 nw[NORM ? ITERS : 1];
+#pragma unroll
+  for (int it = 0; it < ITERS; ++it) {
+    const uint32_t gi = it * kGemvThreads + threadIdx.x;
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+      xv[m][it] = gi < n8 ? reinterpret_cast<const uint4*>(p.x[m])[gi] : make_uint4(0, 0, 0, 0);
+    if constexpr (NORM) nw[it] = gi < n8 ? reinterpret_cast<const uint4*>(p.norm_w)[gi] : make_uint4(0, 0, 0, 0);
+  }
+
+  // 2) the first group's weights.
+  GemvBuf<NMAT, ROWS, ITERS> b0, b1;
+  uint32_t g = blockIdx.x * kGemvWaves + wid;
+  if (g < G) gemv_load<NMAT, ROWS, ITERS, TAIL>(p, g, lane, tail_active, b0);
+
+  // 3) stage x into LDS (normalised with NORM), then into registers.
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    float scale = 1.0f;
+    if constexpr (NORM) {
+      float ss = 0.0f;
+#pragma unroll
+      for (int it = 0; it < ITERS; ++it) {
+        const uint32_t d[4] = {xv[m][it].x, xv[m][it].y, xv[m][it].z, xv[m][it].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float a = bf_lo(d[i]), b = bf_hi(d[i]);
+          ss += a * a;
+          ss += b * b;
+        }
+      }
+      const float total = block_sum<kGemvThreads>(ss, red);
+      scale = 1.0f / sqrtf(total / static_cast<float>(p.K) + p.eps);
+    }
+    uint4* dst = reinterpret_cast<uint4*>(xs + m * (p.K / 2));
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it) {
+      const uint32_t gi = it * kGemvThreads + threadIdx.x;
+      if (gi < n8) {
+        if constexpr (NORM)
+          dst[gi] = permute_pairs(rms_apply(xv[m][it], nw[it], scale));
+        else
+          dst[gi] = permute_pairs(xv[m][it]);
+      }
+    }
+  }
+  __syncthreads();
+
+  XStep<M> xr[XREG ? ITERS : 1];
+  if constexpr (XREG) {
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it) gemv_read_x<M>(xs, p.K, it, lane, xr[it]);
+  }
+
+  auto process = [&](const GemvBuf<NMAT, ROWS, ITERS>& b, uint32_t grp) {
+    float acc[NMAT][ROWS][M];
+#pragma unroll
+    for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+      for (int r = 0; r < ROWS; ++r)
+#pragma unroll
+        for (int m = 0; m < M; ++m) acc[mat][r][m] = 0.0f;
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it) {
+      if (TAIL && it == ITERS - 1 && !tail_active) break;
+      if constexpr (XREG) {
+        gemv_dot_step<M>(b, it, xr[it], acc);
+      } else {
+        XStep<M> x;
+        gemv_read_x<M>(xs, p.K, it, lane, x);
+        gemv_dot_step<M>(b, it, x, acc);
+      }
+    }
+    gemv_epilogue<M, NMAT, ROWS, EPI>(p, gemv_locate<ROWS>(p, grp), lane, acc);
+  };
+
+  // 4) two buffers: compute g while g+W streams in.
+  while (g < G) {
+    if (g + W < G) gemv_load<NMAT, ROWS, ITERS, TAIL>(p, g + W, lane, tail_active, b1);
+    process(b0, g);
+    g += W;
+    if (g >= G) break;
+    if (g + W < G) gemv_load<NMAT, ROWS, ITERS, TAIL>(p, g + W, lane, tail_active, b0);
+    process(b1, g);
+    g += W;
+  }
+}
+
 // ------------------------------------------------------------- host ----------
+// Instantiated per epilogue in q4_gemv_inst_*.hip. Returns 0, or -1 when no
+// kernel variant exists for (M, rows, iters).
+template <int EPI, bool NORM>
+int launch_m(hipStream_t s, const GemvParams& p, int M, int rows, int iters, size_t lds);
+
 // Launch one GEMV-family kernel. Segment block ranges are filled in here.
 // Returns a PRG_ERR_* code.
 int launch_q4_gemv(hipStream_t stream, GemvParams& p, int M, int rows_per_wave, int epi,

@@ -1,0 +1,6 @@
+// Q4 GEMV kernel variants: epilogue plain.
+#include "q4_gemv_launch.hpp"
+
+namespace prg {
+template int launch_m<kEpiPlain, false>(hipStream_t, const GemvParams&, int, int, int, size_t);
+}  // namespace prg

@@ -1,0 +1,6 @@
+// Q4 GEMV kernel variants: epilogue silu.
+#include "q4_gemv_launch.hpp"
+
+namespace prg {
+template int launch_m<kEpiSiluGate, false>(hipStream_t, const GemvParams&, int, int, int, size_t);
+}  // namespace prg
