@@ -279,6 +279,92 @@ int prg_attn_decode_bf16(void *stream, const uint16_t *q, const uint16_t *key_ca
                          float scale);
 size_t prg_attn_decode_partials_bytes(uint32_t cache_stride_tokens);
 
+/* ======================================================================
+ * Prompt (prefill) path: T tokens at once through MFMA GEMMs.
+ * Row-major [T, dim] activations; the same shape rules as above.
+ * ====================================================================== */
+
+/* out[t, n] = bf16(sum_k x[t, k] * bf16(s*q + b)) on the matrix cores: weights
+ * dequantised in-kernel and rounded to bf16 before the product, f32
+ * accumulation. in_dim % 64 == 0. Replaces
+ * linear_q4_affine_group64_prefill_qmm_m32n64_nt_bf16_tiles_bf16
+ * (shaders/linear.metal:780-964), host Q4Linear.encodePrefillQmmM32N64NtBf16
+ * (src/model/linear_q4.zig:197-214), and the prepared-dense route
+ * (q4_dequantize + MLX NT GEMM, src/model/mlx_nt.zig:139-162). */
+int prg_q4_qmm_bf16(void *stream, const uint16_t *x, const uint32_t *w, const uint16_t *scales,
+                    const uint16_t *biases, uint16_t *out, uint32_t token_count, uint32_t out_dim,
+                    uint32_t in_dim);
+
+/* out = bf16(float(bf16(acc)) + residual). Replaces
+ * ..._prefill_qmm_m32n64_nt_bf16_tiles_residual_add_bf16
+ * (shaders/linear.metal:966-988), host linear_q4.zig:216-233. */
+int prg_q4_qmm_residual_add_bf16(void *stream, const uint16_t *x, const uint32_t *w,
+                                 const uint16_t *scales, const uint16_t *biases,
+                                 const uint16_t *residual, uint16_t *out, uint32_t token_count,
+                                 uint32_t out_dim, uint32_t in_dim);
+
+/* out = bf16(silu(bf16(x.gate)) * bf16(x.up)) in one pass: the gate and up
+ * QMMs plus silu_mul_pair_inplace_bf16 (shaders/elementwise.metal:64-73),
+ * host MlpBlock.encodePrefillGateUpSilu* (src/model/block_mlp.zig:155-214). */
+int prg_q4_qmm_silu_gate_bf16(void *stream, const uint16_t *x, const uint32_t *gate_w,
+                              const uint16_t *gate_scales, const uint16_t *gate_biases,
+                              const uint32_t *up_w, const uint16_t *up_scales,
+                              const uint16_t *up_biases, uint16_t *out, uint32_t token_count,
+                              uint32_t out_dim, uint32_t in_dim);
+
+/* For T tokens: split packed q [T, 16, 512] into q_output/gate_output
+ * [T, 16, 256]; RMSNorm + RoPE (positions start_rope_pos + t) of q and of
+ * k_input [T, 4, 256] (normed value kept in f32 through RoPE); append K/V at
+ * cache slots start_cache_pos + t. Replaces split_qg_many_bf16
+ * (shaders/layout.metal:68-89) + qwen35_qk_norm_rope_append_many_bf16
+ * (shaders/attention.metal:146-220), host block_attn.zig:409-442. */
+int prg_attn_prefill_prepare_bf16(void *stream, const uint16_t *packed_q, const uint16_t *q_weight,
+                                  const uint16_t *k_input, const uint16_t *k_weight,
+                                  const uint16_t *v_input, uint16_t *q_output, uint16_t *gate_output,
+                                  uint16_t *key_cache, uint16_t *value_cache, uint32_t token_count,
+                                  uint32_t start_rope_pos, uint32_t start_cache_pos,
+                                  uint32_t cache_stride_tokens);
+
+/* Causal attention of token_count queries over cache slots
+ * [0, prefix_len + token_count): scores = bf16(q.k), softmax of scale*score
+ * with the mask col <= prefix_len + t, probabilities bf16, then
+ * out = bf16(bf16(P.V) * sigmoid(gate)). q, gate, out [T, 16, 256]. scores: a
+ * device workspace of prg_attn_prefill_scores_bytes(token_count, prefix_len).
+ * Replaces encodeMaterializedPrefillBf16 (src/model/block_attn.zig:500-631:
+ * score GEMM, prefill_softmax_scaled_masked_bf16 attention.metal:1463-1523,
+ * value GEMM) and sigmoid_mul_pair_inplace_bf16 (elementwise.metal:88-99). */
+int prg_attn_prefill_bf16(void *stream, const uint16_t *q, const uint16_t *key_cache,
+                          const uint16_t *value_cache, const uint16_t *gate, uint16_t *out,
+                          uint16_t *scores, uint32_t token_count, uint32_t prefix_len,
+                          uint32_t cache_stride_tokens, float scale);
+size_t prg_attn_prefill_scores_bytes(uint32_t token_count, uint32_t prefix_len);
+
+/* Depthwise causal conv + SiLU over qkv [T, 8192], history from the f32 state
+ * [3, 8192] when has_previous_state (else zeros); the state then holds the
+ * last three inputs. Replaces conv1d_silu_prefill_vec4_bf16 +
+ * conv1d_silu_prefill_state_bf16 (shaders/conv1d.metal:136-198), host
+ * block_linear.zig:363-390. */
+int prg_conv1d_silu_prefill_bf16(void *stream, float *state, const uint16_t *qkv, const uint16_t *weight,
+                                 uint16_t *out, uint32_t token_count, uint32_t conv_dim,
+                                 uint32_t kernel_size, uint32_t has_previous_state);
+
+/* f32 q/k [T, 16, 128] (l2-normed; q also times rsqrt(128)) from conv_out
+ * [T, 8192], and gates g/beta f32 [T, 32] from a, b [T, 32]. Replaces
+ * qk_l2norm_prefill_bf16 + gating_many_bf16 (shaders/gated_norm.metal:191-268),
+ * host block_linear.zig:392-434. */
+int prg_gated_delta_prefill_prepare_bf16(void *stream, const uint16_t *conv_out, const uint16_t *a,
+                                         const uint16_t *b, const float *A_log, const uint16_t *dt_bias,
+                                         float *q_out, float *k_out, float *g_out, float *beta_out,
+                                         uint32_t token_count);
+
+/* Delta-rule recurrence over T tokens with prepared q/k/gates; state f32
+ * [32, 128, 128] in place; y bf16 [T, 4096]. Replaces
+ * gated_delta_prefill_h128_norm_prepared_value_major_r8_bf16
+ * (shaders/gated_delta.metal:35-138), host block_linear.zig:436-469. */
+int prg_gated_delta_prefill_bf16(void *stream, float *state, const float *q, const float *k,
+                                 const uint16_t *conv_out, const float *g, const float *beta, uint16_t *y,
+                                 uint32_t token_count, uint32_t has_previous_state);
+
 #ifdef __cplusplus
 }
 #endif

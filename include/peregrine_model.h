@@ -78,11 +78,14 @@ int prg_model_forward_next_token(PrgModel *model, PrgModelState *state, uint32_t
                                  uint32_t cache_pos, uint32_t rope_pos, uint32_t seq_len,
                                  uint32_t *next_token);
 
-/* Reset the state and ingest prompt[0..prompt_len) at positions 0.. (the lm_head
- * runs only on the last prompt token). *next_token receives the greedy token
- * that follows the prompt; the state is then positioned to decode it.
- * Replaces the prompt half of the serving path (prefill + first token,
- * model.zig:1201-1238) with per-token steps. */
+/* Reset the state and ingest prompt[0..prompt_len) at positions 0.. layer-major
+ * in chunks of up to 2048 tokens (MFMA QMMs, causal prefill attention, GDN
+ * prefill recurrence); the lm_head runs only on the last prompt token.
+ * *next_token receives the greedy token that follows the prompt; the state is
+ * then positioned to decode it (prg_model_decode continues from there).
+ * Replaces DeviceModel's layer-major prefill + argmax tail
+ * (model.zig:940-1060, 1307-1324; DecoderLayer.prefillStepBf16,
+ * decoder_layer.zig:644-760). */
 int prg_model_prefill(PrgModel *model, PrgModelState *state, const uint32_t *prompt,
                       uint32_t prompt_len, uint32_t *next_token);
 

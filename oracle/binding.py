@@ -50,6 +50,20 @@ class Oracle:
         d.orc_attn_decode_prepare_bf16.argtypes = [_u16p, _u16p, _u16p, _u16p, _u16p, _u16p, _u16p, _u16p,
                                                    _u16p, _u32, _u32, _u32, _u32, _u32, _f, _u32, _u32]
         d.orc_attn_decode_bf16.argtypes = [_u16p, _u16p, _u16p, _u16p, _u16p, _u32, _u32, _u32, _u32, _f]
+        _vp = C.c_void_p
+        d.orc_q4_qmm_bf16.argtypes = [_u16p, _u32, _u32p, _u16p, _u16p, _vp, _u16p, _u32, _u32]
+        d.orc_silu_mul_pair_bf16.argtypes = [_u16p, _u16p, C.c_size_t]
+        d.orc_sigmoid_mul_pair_bf16.argtypes = [_u16p, _u16p, C.c_size_t]
+        d.orc_q4_embedding_gather_many_bf16.argtypes = [_u32p, _u16p, _u16p, _u32p, _u32, _u16p, _u32]
+        d.orc_split_qg_many_bf16.argtypes = [_u16p, _u16p, _u16p, _u32, _u32, _u32]
+        d.orc_qk_norm_rope_append_many_bf16.argtypes = [_u16p, _u16p, _u16p, _u16p, _u16p, _u16p, _u16p,
+                                                        _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _f]
+        d.orc_attn_prefill_bf16.argtypes = [_u16p, _u16p, _u16p, _u16p, _u32, _u32, _u32, _u32, _u32, _u32, _f]
+        d.orc_conv1d_silu_prefill_bf16.argtypes = [_f32p, _u16p, _u16p, _u16p, _u32, _u32, _u32, _u32]
+        d.orc_qk_l2norm_prefill_bf16.argtypes = [_u16p, _f32p, _f32p, _u32, _u32, _u32, _u32]
+        d.orc_gating_many_bf16.argtypes = [_f32p, _u16p, _u16p, _u16p, _f32p, _f32p, _u32, _u32]
+        d.orc_gated_delta_prefill_bf16.argtypes = [_f32p, _f32p, _f32p, _u16p, _f32p, _f32p, _u16p,
+                                                   _u32, _u32, _u32, _u32, _u32, _u32, _u32]
 
     # ------------------------------------------------------------------ misc
     def set_threads(self, n: int) -> None:
@@ -182,6 +196,100 @@ class Oracle:
         self.d.orc_attn_decode_bf16(_c(q, np.uint16), _c(key_cache, np.uint16), _c(value_cache, np.uint16),
                                     _c(gate, np.uint16), out, 16, 4, int(stride), int(seq_len), scale)
         return out
+
+
+    # ------------------------------------------------------------ prefill
+    def q4_qmm(self, x, wt, residual=None) -> np.ndarray:
+        """[M, K] x Q4 [N, K]^T -> bf16 [M, N] with bf16-rounded weights."""
+        x = _c(np.atleast_2d(x), np.uint16)
+        N, K = wt.shape
+        M = x.shape[0]
+        out = np.empty((M, N), np.uint16)
+        res = None
+        if residual is not None:
+            res = _c(np.reshape(residual, (M, N)), np.uint16)
+        self.d.orc_q4_qmm_bf16(x, M, _c(wt.w, np.uint32), _c(wt.s, np.uint16), _c(wt.b, np.uint16),
+                               None if res is None else res.ctypes.data, out, N, K)
+        return out
+
+    def silu_mul_pair(self, gate, up) -> np.ndarray:
+        g = np.array(gate, np.uint16, copy=True, order="C")
+        self.d.orc_silu_mul_pair_bf16(g, _c(up, np.uint16), g.size)
+        return g
+
+    def sigmoid_mul_pair(self, x, gate) -> np.ndarray:
+        y = np.array(x, np.uint16, copy=True, order="C")
+        self.d.orc_sigmoid_mul_pair_bf16(y, _c(gate, np.uint16), y.size)
+        return y
+
+    def embedding_many(self, wt, tokens) -> np.ndarray:
+        V, H = wt.shape
+        tok = _c(tokens, np.uint32)
+        out = np.empty((tok.size, H), np.uint16)
+        self.d.orc_q4_embedding_gather_many_bf16(_c(wt.w, np.uint32), _c(wt.s, np.uint16), _c(wt.b, np.uint16),
+                                                 tok, tok.size, out, H)
+        return out
+
+    def split_qg_many(self, qp, heads=16, head_dim=256):
+        qp = _c(qp, np.uint16)
+        T = qp.size // (heads * 2 * head_dim)
+        q = np.empty((T, heads * head_dim), np.uint16)
+        g = np.empty_like(q)
+        self.d.orc_split_qg_many_bf16(qp, q, g, head_dim, heads, T)
+        return q, g
+
+    def qk_norm_rope_append_many(self, q, q_w, k, k_w, v, key_cache, value_cache, start_rope, start_cache,
+                                 stride, theta=1.0e7):
+        """Returns (q', key_cache', value_cache'); inputs are not modified."""
+        qq = np.array(q, np.uint16, copy=True, order="C")
+        kc = np.array(key_cache, np.uint16, copy=True, order="C")
+        vc = np.array(value_cache, np.uint16, copy=True, order="C")
+        T = qq.size // (16 * 256)
+        self.d.orc_qk_norm_rope_append_many_bf16(qq, _c(q_w, np.uint16), _c(k, np.uint16), _c(k_w, np.uint16),
+                                                 _c(v, np.uint16), kc, vc, int(start_rope), T, int(start_cache),
+                                                 int(stride), 16, 4, 256, 64, theta)
+        return qq, kc, vc
+
+    def attn_prefill(self, q, key_cache, value_cache, T, prefix, stride, scale=1.0 / 16.0):
+        out = np.empty((T, 16 * 256), np.uint16)
+        self.d.orc_attn_prefill_bf16(_c(q, np.uint16), _c(key_cache, np.uint16), _c(value_cache, np.uint16), out,
+                                     int(T), int(prefix), int(stride), 16, 4, 256, scale)
+        return out
+
+    def conv1d_prefill(self, state, qkv, w, has_prev=True):
+        """qkv [T, conv_dim] -> (out [T, conv_dim], new_state)."""
+        st = np.array(state, np.float32, copy=True, order="C")
+        qkv = _c(np.atleast_2d(qkv), np.uint16)
+        T, cd = qkv.shape
+        out = np.empty_like(qkv)
+        self.d.orc_conv1d_silu_prefill_bf16(st, qkv, _c(w, np.uint16), out, T, cd, 4, int(bool(has_prev)))
+        return out, st
+
+    def qk_l2norm_prefill(self, conv_out, Hk=16, Dk=128):
+        co = _c(np.atleast_2d(conv_out), np.uint16)
+        T, cd = co.shape
+        qn = np.empty((T, Hk * Dk), np.float32)
+        kn = np.empty_like(qn)
+        self.d.orc_qk_l2norm_prefill_bf16(co, qn, kn, T, Hk, Dk, cd)
+        return qn, kn
+
+    def gating_many(self, A_log, a, dt_bias, b, Hv=32):
+        a = _c(np.atleast_2d(a), np.uint16)
+        T = a.shape[0]
+        g = np.empty((T, Hv), np.float32)
+        beta = np.empty_like(g)
+        self.d.orc_gating_many_bf16(_c(A_log, np.float32), a, _c(dt_bias, np.uint16), _c(b, np.uint16), g, beta,
+                                    Hv, T)
+        return g, beta
+
+    def gated_delta_prefill(self, state, qn, kn, conv_out, g, beta, has_prev=True, Hk=16, Hv=32, Dk=128, Dv=128):
+        st = np.array(state, np.float32, copy=True, order="C")
+        co = _c(np.atleast_2d(conv_out), np.uint16)
+        T, cd = co.shape
+        y = np.empty((T, Hv * Dv), np.uint16)
+        self.d.orc_gated_delta_prefill_bf16(st, _c(qn, np.float32), _c(kn, np.float32), co, _c(g, np.float32),
+                                            _c(beta, np.float32), y, T, Hk, Hv, Dk, Dv, cd, int(bool(has_prev)))
+        return y, st
 
 
 _singleton: Oracle | None = None

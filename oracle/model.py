@@ -1,13 +1,20 @@
-"""TEST INFRASTRUCTURE: CPU restatement of the reference's decode composition.
+"""TEST INFRASTRUCTURE: CPU restatement of the reference's decode and prompt
+(prefill) compositions.
 
 Orchestrates the C oracle primitives exactly as the reference's Zig host code
-dispatches its kernels for one token, without any of the GPU build's fusions:
+dispatches its kernels, without any of the GPU build's fusions. One token:
   DecoderLayer.decodeStepBf16          src/model/decoder_layer.zig:461-566, 756-781
   LinearAttentionBlock.decodeStepBf16  src/model/block_linear.zig:199-263
   FullAttentionBlock.decodeStepBf16    src/model/block_attn.zig:261-359
   MlpBlock.decodeResidualBf16          src/model/block_mlp.zig:260-277
   encodeStackBf16 + argmax tail        src/model/model.zig:686-717, 1346-1388
   decodeFromPrefixCache (no prefix)    src/server/decode_loop.zig:96-160
+A prompt of T tokens at once (layer-major, one chunk):
+  DecoderLayer.prefillStepBf16         src/model/decoder_layer.zig:644-760
+  LinearAttentionBlock prefill         src/model/block_linear.zig:265-469
+  FullAttentionBlock prefill           src/model/block_attn.zig:361-631
+  MlpBlock prefill (gate/up, down)     src/model/block_mlp.zig:155-258
+  encodePrefillArgmaxTailBf16          src/model/model.zig:1307-1324
 Weights are read back from the GPU model (same bits on both sides).
 """
 from __future__ import annotations
@@ -118,6 +125,50 @@ class OracleModel:
         if want_logits:
             logits = bf16_to_f32(o.q4_gemv(normed, self.lm_head)[0])
         return tok, logits
+
+    def _prefill_layer(self, i: int, h: np.ndarray, start: int) -> np.ndarray:
+        o, L, S, eps = self.o, self.layers[i], self.state[i], self.cfg.rms_eps
+        T = h.shape[0]
+        normed = o.rmsnorm(h, L["input_norm"], eps)                # decoder_layer.zig:666
+        if L["linear"]:                                            # block_linear.zig:265-361
+            qkv = o.q4_qmm(normed, L["qkv"])
+            z = o.q4_qmm(normed, L["z"])
+            a = o.q4_qmm(normed, L["a"])
+            b = o.q4_qmm(normed, L["b"])
+            has_prev = start != 0                                  # decoder_layer.zig:635
+            conv_out, S["conv"] = o.conv1d_prefill(S["conv"], qkv, L["conv_w"], has_prev)
+            qn, kn = o.qk_l2norm_prefill(conv_out)
+            g, beta = o.gating_many(L["A_log"], a, L["dt_bias"], b)
+            y, S["recur"] = o.gated_delta_prefill(S["recur"], qn, kn, conv_out, g, beta, has_prev)
+            gated = o.rmsnorm_gated(y, L["norm_w"], z, 128, eps)
+            attn = o.q4_qmm(gated.reshape(T, 4096), L["out"])
+        else:                                                      # block_attn.zig:361-498
+            qp = o.q4_qmm(normed, L["q"])
+            k = o.q4_qmm(normed, L["k"])
+            v = o.q4_qmm(normed, L["v"])
+            q, gate = o.split_qg_many(qp)
+            q, S["k"], S["v"] = o.qk_norm_rope_append_many(q, L["q_norm"], k, L["k_norm"], v, S["k"], S["v"],
+                                                           start, start, self.stride)
+            ctx = o.attn_prefill(q, S["k"], S["v"], T, start, self.stride)
+            ctx = o.sigmoid_mul_pair(ctx, gate)
+            attn = o.q4_qmm(ctx, L["o"])
+        r, normed2 = o.add_rmsnorm(h, attn, L["post_norm"], eps)   # decoder_layer.zig:752
+        inter = o.silu_mul_pair(o.q4_qmm(normed2, L["gate"]), o.q4_qmm(normed2, L["up"]))
+        return o.q4_qmm(inter, L["down"], residual=r)              # block_mlp.zig:216-258
+
+    def prefill(self, tokens, start: int = 0, want_logits: bool = False):
+        """Ingest tokens at positions start.. (state kept from earlier calls);
+        returns (next_token, logits|None) from the last row."""
+        o = self.o
+        tok = np.asarray(tokens, np.uint32)
+        h = o.embedding_many(self.embed, tok)                     # embedding.metal:73-96
+        for i in range(len(self.layers)):
+            h = self._prefill_layer(i, h, start)
+        normed = o.rmsnorm(h[-1], self.final_norm, self.cfg.rms_eps)[0]
+        pv, pi = o.q4_argmax_partial(normed, self.lm_head)
+        nxt = o.argmax_pairs(pv[0], pi[0])
+        logits = bf16_to_f32(o.q4_gemv(normed, self.lm_head)[0]) if want_logits else None
+        return nxt, logits
 
     def teacher_forced(self, tokens, want_logits: bool = False):
         self.reset()

@@ -622,3 +622,367 @@ void orc_attn_decode_bf16(const uint16_t *q, const uint16_t *K, const uint16_t *
     }
   free(partials);
 }
+
+/* =================================================================== */
+/*                         prompt (prefill) path                       */
+/* =================================================================== */
+
+/* ------------------------------------------------------- A22 QMM -------- */
+/* q4_affine_group64_qmm_nt_bf16_tile_impl (shaders/linear.metal:780-941) and
+ * the prepared-dense route it shares semantics with (q4_dequantize_bf16,
+ * linear.metal:422-444, then an MLX bf16 NT GEMM): each weight is rounded to
+ * bf16 as bf16(s*q + b) before the product; products accumulate in f32 (here
+ * in natural k order, the hardware MMA order being unobservable); the output
+ * is bf16(acc), and the residual variant (:932-937) stores
+ * bf16(float(bf16(acc)) + float(res)). */
+typedef struct {
+  const uint16_t *x, *residual;
+  const uint32_t *w;
+  const uint16_t *s, *b;
+  uint16_t *out;
+  uint32_t M, N, K;
+} qmm_ctx;
+
+static void qmm_rows(void *ctx, size_t nb, size_t ne) {
+  const qmm_ctx *c = (const qmm_ctx *)ctx;
+  const uint32_t words = c->K / 8, groups = c->K / 64;
+  float *wrow = (float *)malloc(sizeof(float) * c->K);
+  for (size_t n = nb; n < ne; ++n) {
+    for (uint32_t k = 0; k < c->K; ++k) {
+      const uint32_t q = (c->w[n * words + k / 8] >> ((k & 7u) * 4u)) & 0x0fu;
+      const size_t meta = n * groups + k / 64;
+      wrow[k] = rbf(orc_bf2f(c->s[meta]) * (float)q + orc_bf2f(c->b[meta]));
+    }
+    for (uint32_t m = 0; m < c->M; ++m) {
+      const uint16_t *xr = c->x + (size_t)m * c->K;
+      float acc = 0.0f;
+      for (uint32_t k = 0; k < c->K; ++k) acc += orc_bf2f(xr[k]) * wrow[k];
+      const size_t o = (size_t)m * c->N + n;
+      c->out[o] = c->residual ? orc_f2bf(rbf(acc) + orc_bf2f(c->residual[o])) : orc_f2bf(acc);
+    }
+  }
+  free(wrow);
+}
+
+void orc_q4_qmm_bf16(const uint16_t *x, uint32_t M, const uint32_t *w, const uint16_t *s,
+                     const uint16_t *b, const uint16_t *residual, uint16_t *out, uint32_t N,
+                     uint32_t K) {
+  qmm_ctx c = {x, residual, w, s, b, out, M, N, K};
+  parallel_for(N, qmm_rows, &c);
+}
+
+/* silu_mul_pair_inplace_bf16 (shaders/elementwise.metal:64-73):
+ * gate = bf16(silu(gate) * up), silu(g) = g / (1 + exp(-g)). */
+void orc_silu_mul_pair_bf16(uint16_t *gate, const uint16_t *up, size_t n) {
+  for (size_t i = 0; i < n; ++i) {
+    const float g = orc_bf2f(gate[i]);
+    gate[i] = orc_f2bf((g / (1.0f + expf(-g))) * orc_bf2f(up[i]));
+  }
+}
+
+/* sigmoid_mul_pair_inplace_bf16 (shaders/elementwise.metal:88-99):
+ * x = bf16(x * 1/(1 + exp(-gate))). */
+void orc_sigmoid_mul_pair_bf16(uint16_t *x, const uint16_t *gate, size_t n) {
+  for (size_t i = 0; i < n; ++i) {
+    const float sg = 1.0f / (1.0f + expf(-orc_bf2f(gate[i])));
+    x[i] = orc_f2bf(orc_bf2f(x[i]) * sg);
+  }
+}
+
+/* q4_embedding_gather_many_bf16 (shaders/embedding.metal:73-96). */
+void orc_q4_embedding_gather_many_bf16(const uint32_t *w, const uint16_t *s, const uint16_t *b,
+                                       const uint32_t *tokens, uint32_t T, uint16_t *out,
+                                       uint32_t hidden) {
+  for (uint32_t t = 0; t < T; ++t) orc_q4_embedding_gather_bf16(w, s, b, out + (size_t)t * hidden, tokens[t], hidden);
+}
+
+/* ------------------------------------------- A23 attention prefill ------ */
+/* split_qg_many_bf16 (shaders/layout.metal:68-89): qp [T, H, 2*D] holds
+ * q ‖ gate per head. */
+void orc_split_qg_many_bf16(const uint16_t *qp, uint16_t *q, uint16_t *gate, uint32_t head_dim,
+                            uint32_t heads, uint32_t T) {
+  for (uint32_t t = 0; t < T; ++t)
+    for (uint32_t h = 0; h < heads; ++h)
+      for (uint32_t d = 0; d < head_dim; ++d) {
+        const size_t src = ((size_t)t * heads + h) * 2 * head_dim, dst = ((size_t)t * heads + h) * head_dim + d;
+        q[dst] = qp[src + d];
+        gate[dst] = qp[src + head_dim + d];
+      }
+}
+
+/* qwen35_qk_norm_rope_append_many_bf16 (shaders/attention.metal:146-220).
+ * One 256-thread group per row (q rows then k rows); thread t sums x^2 over
+ * d = t, t+256, ..., then a halving tree. The normed value stays f32 through
+ * RoPE (unlike the decode prepare, which rounds it to bf16 first). q is
+ * rewritten in place; K rows go to cache_k[h, stride, D] at
+ * start_cache + t; V rows to cache_v[h, D, stride]. */
+void orc_qk_norm_rope_append_many_bf16(uint16_t *q, const uint16_t *q_weight, const uint16_t *k,
+                                       const uint16_t *k_weight, const uint16_t *v,
+                                       uint16_t *cache_k, uint16_t *cache_v, uint32_t start_rope,
+                                       uint32_t T, uint32_t start_cache, uint32_t stride,
+                                       uint32_t num_q, uint32_t num_kv, uint32_t head_dim,
+                                       uint32_t rotary_dim, float theta) {
+  float partial[256];
+  const uint32_t q_rows = T * num_q, kv_rows = T * num_kv;
+  for (uint32_t rg = 0; rg < q_rows + kv_rows; ++rg) {
+    const int is_q = rg < q_rows;
+    const uint32_t lr = is_q ? rg : rg - q_rows;
+    const uint32_t heads = is_q ? num_q : num_kv;
+    const uint32_t t = lr / heads, h = lr - t * heads;
+    const uint16_t *src = (is_q ? q : k) + (size_t)lr * head_dim;
+    const uint16_t *wt = is_q ? q_weight : k_weight;
+    for (uint32_t th = 0; th < 256; ++th) {
+      float ss = 0.0f;
+      for (uint32_t d = th; d < head_dim; d += 256) ss += orc_bf2f(src[d]) * orc_bf2f(src[d]);
+      partial[th] = ss;
+    }
+    const float scale = 1.0f / sqrtf(tree_sum(partial, 256) / (float)head_dim + 1.0e-6f);
+    const uint32_t pos = start_rope + t;
+    float x[512];
+    for (uint32_t d = 0; d < head_dim; ++d) x[d] = orc_bf2f(src[d]);
+    uint16_t *dst = is_q ? q + (size_t)lr * head_dim
+                         : cache_k + ((size_t)h * stride + (start_cache + t)) * head_dim;
+    const uint32_t half = rotary_dim / 2;
+    for (uint32_t i = 0; i < half; ++i) {
+      const float a = x[i] * scale * orc_bf2f(wt[i]);
+      const float bb = x[i + half] * scale * orc_bf2f(wt[i + half]);
+      const float inv_freq = powf(theta, -(2.0f * (float)i) / (float)rotary_dim);
+      const float ang = (float)pos * inv_freq;
+      const float cs = cosf(ang), sn = sinf(ang);
+      dst[i] = orc_f2bf(a * cs - bb * sn);
+      dst[i + half] = orc_f2bf(bb * cs + a * sn);
+    }
+    for (uint32_t d = rotary_dim; d < head_dim; ++d) dst[d] = orc_f2bf(x[d] * scale * orc_bf2f(wt[d]));
+    if (!is_q) {
+      const uint16_t *vs = v + (size_t)lr * head_dim;
+      for (uint32_t d = 0; d < head_dim; ++d)
+        cache_v[((size_t)h * head_dim + d) * stride + (start_cache + t)] = vs[d];
+    }
+  }
+}
+
+/* Materialised causal prefill attention (src/model/block_attn.zig:500-631).
+ * Per kv head g, rows r = j*T + t (j = q head within the group):
+ *   score[r][c] = bf16(sum_d q[t, g*G + j, d] * K[g, c, d])   (MLX NT GEMM,
+ *                 f32 accumulation; block_attn.zig:75-109)
+ *   prefill_softmax_scaled_masked_bf16 (shaders/attention.metal:1463-1523):
+ *     visible iff c <= prefix + t; value = float(score) * scale; 256 threads
+ *     stride the row for max and for sum of exp2((v - max) * log2e); each
+ *     reduced by a halving tree; p = bf16(exp2(...) / denom) (0 if masked;
+ *     denom 0 -> 1)
+ *   out[t, g*G + j, d] = bf16(sum_c p[r][c] * V[g, d, c])   (MLX NT GEMM)
+ * The gate sigmoid (orc_sigmoid_mul_pair_bf16) is a separate step, as in the
+ * reference (block_attn.zig:475-490). */
+typedef struct {
+  const uint16_t *q, *K, *V;
+  uint16_t *out;
+  uint32_t T, prefix, stride, num_q, num_kv, D;
+  float scale;
+} attp_ctx;
+
+static void attp_rows(void *ctx, size_t rb, size_t re) {
+  const attp_ctx *c = (const attp_ctx *)ctx;
+  const uint32_t G = c->num_q / c->num_kv, L = c->prefix + c->T;
+  float *s = (float *)malloc(sizeof(float) * L);
+  float *p = (float *)malloc(sizeof(float) * L);
+  float partial[256];
+  const float log2e = 1.4426950408889634f;
+  for (size_t idx = rb; idx < re; ++idx) {
+    const uint32_t g = (uint32_t)(idx / ((size_t)G * c->T));
+    const uint32_t r = (uint32_t)(idx % ((size_t)G * c->T));
+    const uint32_t j = r / c->T, t = r % c->T, hq = g * G + j;
+    const uint16_t *qr = c->q + ((size_t)t * c->num_q + hq) * c->D;
+    for (uint32_t col = 0; col < L; ++col) {
+      const uint16_t *kr = c->K + ((size_t)g * c->stride + col) * c->D;
+      float acc = 0.0f;
+      for (uint32_t d = 0; d < c->D; ++d) acc += orc_bf2f(qr[d]) * orc_bf2f(kr[d]);
+      s[col] = rbf(acc);
+    }
+    const uint32_t vis = c->prefix + t;
+    for (int th = 0; th < 256; ++th) {
+      float m = -INFINITY;
+      for (uint32_t col = (uint32_t)th; col < L; col += 256) {
+        const float v = (col > vis) ? -INFINITY : s[col] * c->scale;
+        m = fmaxf(m, v);
+      }
+      partial[th] = m;
+    }
+    for (int stride = 128; stride > 0; stride >>= 1)
+      for (int th = 0; th < stride; ++th) partial[th] = fmaxf(partial[th], partial[th + stride]);
+    const float row_max = partial[0];
+    for (int th = 0; th < 256; ++th) {
+      float sum = 0.0f;
+      for (uint32_t col = (uint32_t)th; col < L; col += 256)
+        if (col <= vis) sum += exp2f((s[col] * c->scale - row_max) * log2e);
+      partial[th] = sum;
+    }
+    const float total = tree_sum(partial, 256);
+    const float denom = total == 0.0f ? 1.0f : total;
+    for (uint32_t col = 0; col < L; ++col)
+      p[col] = (col > vis) ? 0.0f : rbf(exp2f((s[col] * c->scale - row_max) * log2e) / denom);
+    for (uint32_t d = 0; d < c->D; ++d) {
+      const uint16_t *vr = c->V + ((size_t)g * c->D + d) * c->stride;
+      float acc = 0.0f;
+      for (uint32_t col = 0; col < L; ++col) acc += p[col] * orc_bf2f(vr[col]);
+      c->out[((size_t)t * c->num_q + hq) * c->D + d] = orc_f2bf(acc);
+    }
+  }
+  free(s);
+  free(p);
+}
+
+void orc_attn_prefill_bf16(const uint16_t *q, const uint16_t *cache_k, const uint16_t *cache_v,
+                           uint16_t *out, uint32_t T, uint32_t prefix, uint32_t stride,
+                           uint32_t num_q, uint32_t num_kv, uint32_t head_dim, float scale) {
+  attp_ctx c = {q, cache_k, cache_v, out, T, prefix, stride, num_q, num_kv, head_dim, scale};
+  parallel_for((size_t)num_q * T, attp_rows, &c);
+}
+
+/* ---------------------------------------------- A24 GDN prefill --------- */
+/* conv1d_silu_prefill_vec4_bf16 + conv1d_silu_prefill_state_bf16
+ * (shaders/conv1d.metal:136-198). Source index u = t + j over the virtual
+ * sequence [state rows 0..K-2 ‖ inputs]; state rows count only when
+ * has_previous_state; acc += w[c, j] * x in j order; out = bf16(silu(acc)).
+ * The state is then rewritten with the last K-1 entries of that sequence. */
+void orc_conv1d_silu_prefill_bf16(float *state, const uint16_t *qkv, const uint16_t *w,
+                                  uint16_t *out, uint32_t T, uint32_t conv_dim,
+                                  uint32_t kernel_size, uint32_t has_previous_state) {
+  const uint32_t km1 = kernel_size - 1;
+  for (uint32_t c = 0; c < conv_dim; ++c) {
+    for (uint32_t t = 0; t < T; ++t) {
+      float acc = 0.0f;
+      for (uint32_t j = 0; j < kernel_size; ++j) {
+        const uint32_t u = t + j;
+        float x = 0.0f;
+        if (u < km1) {
+          if (has_previous_state) x = state[(size_t)u * conv_dim + c];
+        } else if (u - km1 < T) {
+          x = orc_bf2f(qkv[(size_t)(u - km1) * conv_dim + c]);
+        }
+        acc += orc_bf2f(w[(size_t)c * kernel_size + j]) * x;
+      }
+      out[(size_t)t * conv_dim + c] = orc_f2bf(acc / (1.0f + expf(-acc)));
+    }
+    float hist[8];
+    for (uint32_t j = 0; j < km1; ++j) {
+      const uint32_t u = T + j;
+      float x = 0.0f;
+      if (u < km1) {
+        if (has_previous_state) x = state[(size_t)u * conv_dim + c];
+      } else if (u - km1 < T) {
+        x = orc_bf2f(qkv[(size_t)(u - km1) * conv_dim + c]);
+      }
+      hist[j] = x;
+    }
+    for (uint32_t j = 0; j < km1; ++j) state[(size_t)j * conv_dim + c] = hist[j];
+  }
+}
+
+/* qk_l2norm_prefill_bf16 (shaders/gated_norm.metal:191-245), 128 threads per
+ * (token, k-head) row; thread t sums dk = t, t+128, ..., halving tree.
+ * q = x * rsqrt(sum q^2 + 1e-6) * rsqrt(Dk); k = x * rsqrt(sum k^2 + 1e-6). */
+void orc_qk_l2norm_prefill_bf16(const uint16_t *conv_out, float *qn, float *kn, uint32_t T,
+                                uint32_t Hk, uint32_t Dk, uint32_t conv_dim) {
+  float qp[128], kp[128];
+  const uint32_t key_dim = Hk * Dk;
+  for (uint32_t row = 0; row < T * Hk; ++row) {
+    const uint32_t t = row / Hk, h = row - t * Hk;
+    const uint16_t *qs = conv_out + (size_t)t * conv_dim + (size_t)h * Dk;
+    const uint16_t *ks = qs + key_dim;
+    for (uint32_t th = 0; th < 128; ++th) {
+      float a = 0.0f, b = 0.0f;
+      for (uint32_t d = th; d < Dk; d += 128) {
+        a += orc_bf2f(qs[d]) * orc_bf2f(qs[d]);
+        b += orc_bf2f(ks[d]) * orc_bf2f(ks[d]);
+      }
+      qp[th] = a;
+      kp[th] = b;
+    }
+    const float qi = 1.0f / sqrtf(tree_sum(qp, 128) + 1.0e-6f);
+    const float ki = 1.0f / sqrtf(tree_sum(kp, 128) + 1.0e-6f);
+    const float qscale = 1.0f / sqrtf((float)Dk);
+    for (uint32_t d = 0; d < Dk; ++d) {
+      qn[(size_t)row * Dk + d] = orc_bf2f(qs[d]) * qi * qscale;
+      kn[(size_t)row * Dk + d] = orc_bf2f(ks[d]) * ki;
+    }
+  }
+}
+
+/* gating_many_bf16 (shaders/gated_norm.metal:247-268). */
+void orc_gating_many_bf16(const float *A_log, const uint16_t *a, const uint16_t *dt_bias,
+                          const uint16_t *b, float *g, float *beta, uint32_t Hv, uint32_t T) {
+  for (uint32_t t = 0; t < T; ++t)
+    for (uint32_t h = 0; h < Hv; ++h) {
+      const size_t o = (size_t)t * Hv + h;
+      const float x = orc_bf2f(a[o]) + orc_bf2f(dt_bias[h]);
+      const float softplus = fmaxf(x, 0.0f) + logf(1.0f + expf(-fabsf(x)));
+      g[o] = expf(-expf(A_log[h]) * softplus);
+      beta[o] = 1.0f / (1.0f + expf(-orc_bf2f(b[o])));
+    }
+}
+
+/* gated_delta_prefill_h128_norm_prepared_value_major_r8_bf16
+ * (shaders/gated_delta.metal:35-138). Per (hv, dv) row over t = 0..T-1 with
+ * prepared f32 q/k [T, Hk, Dk] and gates [T, Hv]; lane L of 32 holds
+ * dk = L + 32*chunk; per-lane chunk sums then simd_sum:
+ *   kq = sum k*q; d = S*decay; kv = sum d*k; ob = sum d*q;
+ *   delta = (v - kv) * beta; S = d + k*delta; y = bf16(ob + delta*kq). */
+typedef struct {
+  float *state;
+  const float *q, *k, *g, *beta;
+  const uint16_t *conv_out;
+  uint16_t *y;
+  uint32_t T, Hk, Hv, Dk, Dv, conv_dim, has_state;
+} gdnp_ctx;
+
+static void gdnp_rows(void *ctx, size_t rb, size_t re) {
+  const gdnp_ctx *c = (const gdnp_ctx *)ctx;
+  const uint32_t key_dim = c->Hk * c->Dk;
+  float lanes[32];
+  for (size_t idx = rb; idx < re; ++idx) {
+    const uint32_t hv = (uint32_t)(idx / c->Dv), dv = (uint32_t)(idx % c->Dv);
+    const uint32_t hk = hv / (c->Hv / c->Hk);
+    float *srow = c->state + ((size_t)hv * c->Dv + dv) * c->Dk;
+    float S[32][4];
+    for (int l = 0; l < 32; ++l)
+      for (int ch = 0; ch < 4; ++ch) S[l][ch] = c->has_state ? srow[l + 32 * ch] : 0.0f;
+    for (uint32_t t = 0; t < c->T; ++t) {
+      const float *qk = c->q + ((size_t)t * c->Hk + hk) * c->Dk;
+      const float *kk = c->k + ((size_t)t * c->Hk + hk) * c->Dk;
+      const float decay = c->g[(size_t)t * c->Hv + hv], beta = c->beta[(size_t)t * c->Hv + hv];
+      for (int l = 0; l < 32; ++l) {
+        float s = 0.0f;
+        for (int ch = 0; ch < 4; ++ch) s += kk[l + 32 * ch] * qk[l + 32 * ch];
+        lanes[l] = s;
+      }
+      const float kq = simd_sum32(lanes);
+      float d[32][4], kvl[32], obl[32];
+      for (int l = 0; l < 32; ++l) {
+        float a = 0.0f, o = 0.0f;
+        for (int ch = 0; ch < 4; ++ch) {
+          d[l][ch] = S[l][ch] * decay;
+          a += d[l][ch] * kk[l + 32 * ch];
+          o += d[l][ch] * qk[l + 32 * ch];
+        }
+        kvl[l] = a;
+        obl[l] = o;
+      }
+      const float kv = simd_sum32(kvl), ob = simd_sum32(obl);
+      const float v = orc_bf2f(c->conv_out[(size_t)t * c->conv_dim + 2 * (size_t)key_dim + (size_t)hv * c->Dv + dv]);
+      const float delta = (v - kv) * beta;
+      for (int l = 0; l < 32; ++l)
+        for (int ch = 0; ch < 4; ++ch) S[l][ch] = d[l][ch] + kk[l + 32 * ch] * delta;
+      c->y[(size_t)t * c->Hv * c->Dv + (size_t)hv * c->Dv + dv] = orc_f2bf(ob + delta * kq);
+    }
+    for (int l = 0; l < 32; ++l)
+      for (int ch = 0; ch < 4; ++ch) srow[l + 32 * ch] = S[l][ch];
+  }
+}
+
+void orc_gated_delta_prefill_bf16(float *state, const float *q, const float *k,
+                                  const uint16_t *conv_out, const float *g, const float *beta,
+                                  uint16_t *y, uint32_t T, uint32_t Hk, uint32_t Hv, uint32_t Dk,
+                                  uint32_t Dv, uint32_t conv_dim, uint32_t has_previous_state) {
+  gdnp_ctx c = {state, q, k, g, beta, conv_out, y, T, Hk, Hv, Dk, Dv, conv_dim, has_previous_state};
+  parallel_for((size_t)Hv * Dv, gdnp_rows, &c);
+}

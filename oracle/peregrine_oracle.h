@@ -109,6 +109,43 @@ void orc_attn_decode_bf16(const uint16_t *q, const uint16_t *K, const uint16_t *
                           const uint16_t *gate, uint16_t *out, uint32_t num_q_heads,
                           uint32_t num_kv_heads, uint32_t stride, uint32_t seq_len, float scale);
 
+/* ---- prompt (prefill) path ---- */
+/* A22: shaders/linear.metal:780-941 (QMM; residual may be NULL) */
+void orc_q4_qmm_bf16(const uint16_t *x, uint32_t M, const uint32_t *w, const uint16_t *s,
+                     const uint16_t *b, const uint16_t *residual, uint16_t *out, uint32_t N,
+                     uint32_t K);
+/* shaders/elementwise.metal:64-73, 88-99 */
+void orc_silu_mul_pair_bf16(uint16_t *gate, const uint16_t *up, size_t n);
+void orc_sigmoid_mul_pair_bf16(uint16_t *x, const uint16_t *gate, size_t n);
+/* A18 many: shaders/embedding.metal:73-96 */
+void orc_q4_embedding_gather_many_bf16(const uint32_t *w, const uint16_t *s, const uint16_t *b,
+                                       const uint32_t *tokens, uint32_t T, uint16_t *out,
+                                       uint32_t hidden);
+/* A23: shaders/layout.metal:68-89; attention.metal:146-220; block_attn.zig:500-631 */
+void orc_split_qg_many_bf16(const uint16_t *qp, uint16_t *q, uint16_t *gate, uint32_t head_dim,
+                            uint32_t heads, uint32_t T);
+void orc_qk_norm_rope_append_many_bf16(uint16_t *q, const uint16_t *q_weight, const uint16_t *k,
+                                       const uint16_t *k_weight, const uint16_t *v,
+                                       uint16_t *cache_k, uint16_t *cache_v, uint32_t start_rope,
+                                       uint32_t T, uint32_t start_cache, uint32_t stride,
+                                       uint32_t num_q, uint32_t num_kv, uint32_t head_dim,
+                                       uint32_t rotary_dim, float theta);
+void orc_attn_prefill_bf16(const uint16_t *q, const uint16_t *cache_k, const uint16_t *cache_v,
+                           uint16_t *out, uint32_t T, uint32_t prefix, uint32_t stride,
+                           uint32_t num_q, uint32_t num_kv, uint32_t head_dim, float scale);
+/* A24: shaders/conv1d.metal:136-198; gated_norm.metal:191-268; gated_delta.metal:35-138 */
+void orc_conv1d_silu_prefill_bf16(float *state, const uint16_t *qkv, const uint16_t *w,
+                                  uint16_t *out, uint32_t T, uint32_t conv_dim,
+                                  uint32_t kernel_size, uint32_t has_previous_state);
+void orc_qk_l2norm_prefill_bf16(const uint16_t *conv_out, float *qn, float *kn, uint32_t T,
+                                uint32_t Hk, uint32_t Dk, uint32_t conv_dim);
+void orc_gating_many_bf16(const float *A_log, const uint16_t *a, const uint16_t *dt_bias,
+                          const uint16_t *b, float *g, float *beta, uint32_t Hv, uint32_t T);
+void orc_gated_delta_prefill_bf16(float *state, const float *q, const float *k,
+                                  const uint16_t *conv_out, const float *g, const float *beta,
+                                  uint16_t *y, uint32_t T, uint32_t Hk, uint32_t Hv, uint32_t Dk,
+                                  uint32_t Dv, uint32_t conv_dim, uint32_t has_previous_state);
+
 #ifdef __cplusplus
 }
 #endif

@@ -106,6 +106,24 @@ __device__ inline float block_sum(float v, float* red) {
   return t;
 }
 
+// v_mov_dpp of an f32 (CTRL a DPP control: 0xB1 / 0x4E quad xor 1 / 2,
+// 0x141 row_half_mirror, 0x140 row_mirror).
+template <int CTRL>
+__device__ inline float dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over each 16-lane DPP row. Every lane of the row receives the same bits:
+// each step adds a lane's value to its partner's in an order both partners
+// share (a + b == b + a), so the rows stay uniform.
+__device__ inline float row16_sum(float v) {
+  v += dpp_f<0xB1>(v);
+  v += dpp_f<0x4E>(v);
+  v += dpp_f<0x141>(v);
+  v += dpp_f<0x140>(v);
+  return v;
+}
+
 __device__ inline float silu(float g) { return g / (1.0f + expf(-g)); }
 __device__ inline float sigmoid(float g) { return 1.0f / (1.0f + expf(-g)); }
 

@@ -1,0 +1,337 @@
+// MFMA GEMM for the prompt path (declarations and tiling notes in gemm.hpp).
+//
+// Reference kernels this replaces:
+//   linear_q4_affine_group64_prefill_qmm_m32n64_nt_bf16_tiles_{,residual_add_}bf16
+//       shaders/linear.metal:780-988 (host Q4Linear.encodePrefillQmm*, linear_q4.zig:197-233)
+//   the prepared-dense route (q4_dequantize_bf16 + MLX bf16 NT GEMM), same numbers
+//       src/model/mlx_nt.zig:139-162
+//   attention score / value GEMMs of the materialised prefill
+//       src/model/block_attn.zig:75-109, 500-631
+//   silu_mul_pair_inplace_bf16 / sigmoid_mul_pair_inplace_bf16 as epilogues
+//       shaders/elementwise.metal:64-99
+#include "gemm.hpp"
+
+namespace {
+
+using namespace prg;
+
+constexpr int kBM = 128, kBN = 128, kBK = 64, kGemmThreads = 256;
+constexpr int kLdsRow = kBK + 8;  // bf16 per LDS row (144 bytes)
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ inline const uint16_t* row_ptr(const uint16_t* base, uint64_t ld, uint64_t ld_hi, uint32_t group,
+                                          uint32_t m) {
+  if (group) return base + static_cast<uint64_t>(m / group) * ld_hi + static_cast<uint64_t>(m % group) * ld;
+  return base + static_cast<uint64_t>(m) * ld;
+}
+
+// Two f32 -> packed bf16 pair, round to nearest even (v_cvt_pk_bf16_f32).
+__device__ inline uint32_t pack_bf16(float lo, float hi) {
+  const bf16x2 v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// One Q4 word (8 nibbles, nibble j = column j) -> 8 bf16(s*q + b) in column
+// order. s*q is exact in f32 (8-bit by 4-bit significands), so the fma rounds
+// once, exactly like the reference's separate multiply and add.
+__device__ inline uint4 dequant_word(uint32_t w, float s, float b) {
+  const uint32_t lo = w & 0x0F0F0F0Fu;         // columns 0, 2, 4, 6 in bytes 0..3
+  const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;  // columns 1, 3, 5, 7
+  uint4 r;
+  r.x = pack_bf16(fmaf(s, static_cast<float>(lo & 0xffu), b), fmaf(s, static_cast<float>(hi & 0xffu), b));
+  r.y = pack_bf16(fmaf(s, static_cast<float>((lo >> 8) & 0xffu), b), fmaf(s, static_cast<float>((hi >> 8) & 0xffu), b));
+  r.z = pack_bf16(fmaf(s, static_cast<float>((lo >> 16) & 0xffu), b), fmaf(s, static_cast<float>((hi >> 16) & 0xffu), b));
+  r.w = pack_bf16(fmaf(s, static_cast<float>(lo >> 24), b), fmaf(s, static_cast<float>(hi >> 24), b));
+  return r;
+}
+
+// 8 bf16 at columns [k, k+8) of a row; columns >= K read as zero.
+__device__ inline uint4 load8(const uint16_t* row, uint32_t k, uint32_t K) {
+  if (!row) return make_uint4(0, 0, 0, 0);
+  if (k + 8 <= K) return *reinterpret_cast<const uint4*>(row + k);
+  uint32_t v[4] = {0, 0, 0, 0};
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    if (k + e < K) v[e >> 1] |= static_cast<uint32_t>(row[k + e]) << (16 * (e & 1));
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
+template <bool Q4, int EPI>
+__global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const GemmArgs g) {
+  __shared__ __attribute__((aligned(16))) uint16_t sA[kBM * kLdsRow];
+  __shared__ __attribute__((aligned(16))) uint16_t sB[kBN * kLdsRow];
+  constexpr bool kPair = (EPI == kGemmSiluPair);
+  constexpr uint32_t kTileN = kPair ? kBN / 2 : kBN;  // output columns per block
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const uint32_t tiles_m = (g.M + kBM - 1) / kBM;
+  const uint32_t m0 = (blockIdx.x % tiles_m) * kBM, n0 = (blockIdx.x / tiles_m) * kTileN;
+  const uint64_t z = blockIdx.z;
+  const uint32_t K = g.K;
+
+  // Global -> register staging. A (and bf16 B): 16-byte chunk i of this
+  // thread is row (tid/8 + 32 i), columns k0 + 8*(tid%8) .. +8.
+  const int ld_row = tid >> 3, ld_c8 = (tid & 7) * 8;
+  const uint16_t* a_row[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t m = m0 + ld_row + 32 * i;
+    a_row[i] = m < g.M ? row_ptr(g.a + z * g.a_z, g.lda, g.lda_hi, g.a_group, m) : nullptr;
+  }
+  uint4 ra[4];
+  // Q4 B: thread owns tile row tid/2 and half tid%2 of each 64-column group.
+  const int q_row = tid >> 1, q_half = tid & 1;
+  const uint32_t* q_w = nullptr;
+  const uint16_t *q_s = nullptr, *q_b = nullptr;
+  const uint16_t* b_row[4];
+  uint4 rb[4];
+  uint4 rw = make_uint4(0, 0, 0, 0);
+  uint16_t rs = 0, rbias = 0;
+  if constexpr (Q4) {
+    const int mat = kPair ? (q_row >> 6) : 0;
+    const uint32_t n = n0 + (kPair ? (q_row & 63) : q_row);
+    if (n < g.N) {
+      q_w = g.qw[mat] + static_cast<uint64_t>(n) * (K / 8) + q_half * 4;
+      q_s = g.qs[mat] + static_cast<uint64_t>(n) * (K / 64);
+      q_b = g.qb[mat] + static_cast<uint64_t>(n) * (K / 64);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t n = n0 + ld_row + 32 * i;
+      b_row[i] = n < g.N ? g.b + z * g.b_z + static_cast<uint64_t>(n) * g.ldb : nullptr;
+    }
+  }
+
+  auto load = [&](uint32_t k0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ra[i] = load8(a_row[i], k0 + ld_c8, K);
+    if constexpr (Q4) {
+      if (q_w) {
+        rw = *reinterpret_cast<const uint4*>(q_w + k0 / 8);
+        rs = q_s[k0 / 64];
+        rbias = q_b[k0 / 64];
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) rb[i] = load8(b_row[i], k0 + ld_c8, K);
+    }
+  };
+
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // Fragment rows: 16x32 A block i of this wave, 16x32 B block j.
+  const int frow = lane & 15, fk = (lane >> 4) * 8;
+  int brow[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) brow[j] = kPair ? ((j < 2) ? wn * 32 + 16 * j : 64 + wn * 32 + 16 * (j - 2)) : wn * 64 + 16 * j;
+
+  load(0);
+  for (uint32_t k0 = 0; k0 < K; k0 += kBK) {
+    __syncthreads();  // the previous step's fragments have been read
+#pragma unroll
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(&sA[(ld_row + 32 * i) * kLdsRow + ld_c8]) = ra[i];
+    if constexpr (Q4) {
+      const float s = bf2f(rs), b = bf2f(rbias);
+      uint4* dst = reinterpret_cast<uint4*>(&sB[q_row * kLdsRow + q_half * 32]);
+      dst[0] = dequant_word(rw.x, s, b);
+      dst[1] = dequant_word(rw.y, s, b);
+      dst[2] = dequant_word(rw.z, s, b);
+      dst[3] = dequant_word(rw.w, s, b);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(&sB[(ld_row + 32 * i) * kLdsRow + ld_c8]) = rb[i];
+    }
+    __syncthreads();
+    if (k0 + kBK < K) load(k0 + kBK);  // in flight while the matrix cores run
+#pragma unroll
+    for (int kk = 0; kk < kBK; kk += 32) {
+      bf16x8 af[4], bfr[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        af[i] = *reinterpret_cast<const bf16x8*>(&sA[(wm * 64 + 16 * i + frow) * kLdsRow + kk + fk]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bfr[j] = *reinterpret_cast<const bf16x8*>(&sB[(brow[j] + frow) * kLdsRow + kk + fk]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+    }
+  }
+
+  // Epilogue: lane holds rows 4*(lane/16) + r, column lane%16 of each block.
+  const int crow = 4 * (lane >> 4), ccol = lane & 15;
+  uint16_t* C = g.c + z * g.c_z;
+  const uint16_t* R = g.res ? g.res + z * g.c_z : nullptr;
+  if constexpr (kPair) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const uint32_t m = m0 + wm * 64 + 16 * i + crow + r;
+        if (m >= g.M) continue;
+        uint16_t* out = const_cast<uint16_t*>(row_ptr(C, g.ldc, g.ldc_hi, g.c_group, m));
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const uint32_t n = n0 + wn * 32 + 16 * j + ccol;
+          if (n >= g.N) continue;
+          const float gate = round_bf(acc[i][j][r]), up = round_bf(acc[i][j + 2][r]);
+          out[n] = f2bf(silu(gate) * up);
+        }
+      }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const uint32_t m = m0 + wm * 64 + 16 * i + crow + r;
+        if (m >= g.M) continue;
+        uint16_t* out = const_cast<uint16_t*>(row_ptr(C, g.ldc, g.ldc_hi, g.c_group, m));
+        const uint16_t* rin = R ? row_ptr(R, g.ldc, g.ldc_hi, g.c_group, m) : nullptr;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t n = n0 + wn * 64 + 16 * j + ccol;
+          if (n >= g.N) continue;
+          const float v = acc[i][j][r];
+          if constexpr (EPI == kGemmStore) {
+            out[n] = f2bf(v);
+          } else if constexpr (EPI == kGemmResidual) {
+            out[n] = f2bf(round_bf(v) + bf2f(rin[n]));
+          } else {
+            out[n] = f2bf(round_bf(v) * sigmoid(bf2f(rin[n])));
+          }
+        }
+      }
+  }
+}
+
+template <bool Q4, int EPI>
+int launch_t(hipStream_t s, const GemmArgs& g, uint32_t batch, const char* name) {
+  constexpr uint32_t kTileN = (EPI == kGemmSiluPair) ? kBN / 2 : kBN;
+  const uint32_t tiles = ((g.M + kBM - 1) / kBM) * ((g.N + kTileN - 1) / kTileN);
+  hipLaunchKernelGGL((gemm_kernel<Q4, EPI>), dim3(tiles, 1, batch), dim3(kGemmThreads), 0, s, g);
+  PRG_CHECK_LAUNCH(name);
+  return PRG_OK;
+}
+
+int check_common(const GemmArgs& g, int epi, const char* name) {
+  PRG_CHECK_ARG(g.a && g.c, "%s: null A or C", name);
+  PRG_CHECK_ARG(g.M > 0 && g.N > 0 && g.K > 0, "%s: empty problem M=%u N=%u K=%u", name, g.M, g.N, g.K);
+  PRG_CHECK_ARG(g.lda % 8 == 0 && g.lda_hi % 8 == 0 && g.a_z % 8 == 0,
+                "%s: A row strides must be multiples of 8 elements", name);
+  PRG_CHECK_ARG(reinterpret_cast<uintptr_t>(g.a) % 16 == 0, "%s: A must be 16-byte aligned", name);
+  PRG_CHECK_ARG(epi >= kGemmStore && epi <= kGemmSigmoidGate, "%s: bad epilogue %d", name, epi);
+  PRG_CHECK_ARG((epi != kGemmResidual && epi != kGemmSigmoidGate) || g.res, "%s: epilogue needs res", name);
+  PRG_CHECK_ARG(static_cast<uint64_t>((g.M + kBM - 1) / kBM) * ((g.N + kBN - 1) / kBN) * 2 < (1ull << 31),
+                "%s: grid too large", name);
+  return PRG_OK;
+}
+
+}  // namespace
+
+namespace prg {
+
+int launch_gemm_q4(hipStream_t s, const GemmArgs& g, int epi, const char* name) {
+  if (int rc = check_common(g, epi, name)) return rc;
+  PRG_CHECK_ARG(g.K % 64 == 0, "%s: in_dim %u must be a multiple of 64", name, g.K);
+  PRG_CHECK_ARG(g.qw[0] && g.qs[0] && g.qb[0], "%s: null Q4 weight", name);
+  PRG_CHECK_ARG(epi != kGemmSiluPair || (g.qw[1] && g.qs[1] && g.qb[1]), "%s: SiLU pair needs two weights", name);
+  PRG_CHECK_ARG(reinterpret_cast<uintptr_t>(g.qw[0]) % 16 == 0 && (epi != kGemmSiluPair ||
+                reinterpret_cast<uintptr_t>(g.qw[1]) % 16 == 0), "%s: Q4 weight must be 16-byte aligned", name);
+  switch (epi) {
+    case kGemmStore: return launch_t<true, kGemmStore>(s, g, 1, name);
+    case kGemmResidual: return launch_t<true, kGemmResidual>(s, g, 1, name);
+    case kGemmSiluPair: return launch_t<true, kGemmSiluPair>(s, g, 1, name);
+    default: return launch_t<true, kGemmSigmoidGate>(s, g, 1, name);
+  }
+}
+
+int launch_gemm_bf16(hipStream_t s, const GemmArgs& g, int epi, uint32_t batch, const char* name) {
+  if (int rc = check_common(g, epi, name)) return rc;
+  PRG_CHECK_ARG(g.b, "%s: null B", name);
+  PRG_CHECK_ARG(epi != kGemmSiluPair, "%s: the SiLU pair epilogue takes Q4 weights", name);
+  PRG_CHECK_ARG(g.ldb % 8 == 0 && g.b_z % 8 == 0 && reinterpret_cast<uintptr_t>(g.b) % 16 == 0,
+                "%s: B rows must be 16-byte aligned", name);
+  PRG_CHECK_ARG(batch >= 1 && batch <= 65535, "%s: batch %u", name, batch);
+  switch (epi) {
+    case kGemmStore: return launch_t<false, kGemmStore>(s, g, batch, name);
+    case kGemmResidual: return launch_t<false, kGemmResidual>(s, g, batch, name);
+    default: return launch_t<false, kGemmSigmoidGate>(s, g, batch, name);
+  }
+}
+
+}  // namespace prg
+
+extern "C" {
+
+int prg_q4_qmm_bf16(void* stream, const uint16_t* x, const uint32_t* w, const uint16_t* scales,
+                    const uint16_t* biases, uint16_t* out, uint32_t token_count, uint32_t out_dim,
+                    uint32_t in_dim) {
+  PRG_CHECK_ARG(x && w && scales && biases && out, "prg_q4_qmm_bf16: null pointer");
+  GemmArgs g;
+  g.a = x;
+  g.lda = in_dim;
+  g.qw[0] = w;
+  g.qs[0] = scales;
+  g.qb[0] = biases;
+  g.c = out;
+  g.ldc = out_dim;
+  g.M = token_count;
+  g.N = out_dim;
+  g.K = in_dim;
+  return launch_gemm_q4(as_stream(stream), g, kGemmStore, "prg_q4_qmm_bf16");
+}
+
+int prg_q4_qmm_residual_add_bf16(void* stream, const uint16_t* x, const uint32_t* w,
+                                 const uint16_t* scales, const uint16_t* biases,
+                                 const uint16_t* residual, uint16_t* out, uint32_t token_count,
+                                 uint32_t out_dim, uint32_t in_dim) {
+  PRG_CHECK_ARG(x && w && scales && biases && residual && out, "prg_q4_qmm_residual_add_bf16: null pointer");
+  GemmArgs g;
+  g.a = x;
+  g.lda = in_dim;
+  g.qw[0] = w;
+  g.qs[0] = scales;
+  g.qb[0] = biases;
+  g.c = out;
+  g.res = residual;
+  g.ldc = out_dim;
+  g.M = token_count;
+  g.N = out_dim;
+  g.K = in_dim;
+  return launch_gemm_q4(as_stream(stream), g, kGemmResidual, "prg_q4_qmm_residual_add_bf16");
+}
+
+int prg_q4_qmm_silu_gate_bf16(void* stream, const uint16_t* x, const uint32_t* gate_w,
+                              const uint16_t* gate_scales, const uint16_t* gate_biases,
+                              const uint32_t* up_w, const uint16_t* up_scales,
+                              const uint16_t* up_biases, uint16_t* out, uint32_t token_count,
+                              uint32_t out_dim, uint32_t in_dim) {
+  PRG_CHECK_ARG(x && gate_w && gate_scales && gate_biases && up_w && up_scales && up_biases && out,
+                "prg_q4_qmm_silu_gate_bf16: null pointer");
+  GemmArgs g;
+  g.a = x;
+  g.lda = in_dim;
+  g.qw[0] = gate_w;
+  g.qs[0] = gate_scales;
+  g.qb[0] = gate_biases;
+  g.qw[1] = up_w;
+  g.qs[1] = up_scales;
+  g.qb[1] = up_biases;
+  g.c = out;
+  g.ldc = out_dim;
+  g.M = token_count;
+  g.N = out_dim;
+  g.K = in_dim;
+  return launch_gemm_q4(as_stream(stream), g, kGemmSiluPair, "prg_q4_qmm_silu_gate_bf16");
+}
+
+}  // extern "C"

@@ -1,0 +1,62 @@
+// MFMA GEMM for the prompt (prefill) path: C = A * B^T with bf16 operands and
+// fp32 accumulation on the gfx950 matrix cores.
+//
+//   A  bf16 [M, K] (activations, attention probabilities, queries)
+//   B  either Q4 weights in the MLX affine group-64 format, dequantised in the
+//      kernel to bf16(s*q + b) exactly as the reference's prefill QMM rounds
+//      them (shaders/linear.metal:862-873), or a bf16 matrix [N, K] (the K
+//      cache for scores, the value-dim-major V cache for P*V)
+//   C  bf16 [M, N]
+//
+// Rows of A and C may be addressed in two levels, row m at
+//   base + (m / group) * ld_hi + (m % group) * ld
+// which lets the attention GEMMs read queries and write contexts in the
+// [token, head, dim] layout directly (rows = head-in-group x token).
+//
+// Tiling: 256 threads (4 wave64s as 2x2) own a 128x128 output tile; each wave a
+// 64x64 sub-tile of 4x4 v_mfma_f32_16x16x32_bf16 blocks. K advances 64 at a
+// time (one Q4 scale group) through LDS with a register prefetch of the next
+// step's global data. LDS rows are padded to 72 bf16 so the 16-byte fragment
+// reads of 16 consecutive rows hit distinct banks.
+#pragma once
+
+#include "common.hpp"
+
+namespace prg {
+
+enum GemmEpi : int {
+  kGemmStore = 0,     // C = bf16(acc)
+  kGemmResidual = 1,  // C = bf16(float(bf16(acc)) + res)          (linear.metal:932-937)
+  kGemmSiluPair = 2,  // C = bf16(silu(bf16(acc_gate)) * bf16(acc_up)), two Q4 matrices
+                      //     (qmm + silu_mul_pair_inplace_bf16, elementwise.metal:64-73)
+  kGemmSigmoidGate = 3,  // C = bf16(float(bf16(acc)) * sigmoid(gate))  (attention context,
+                         //     elementwise.metal:88-99); `res` points at the gate
+};
+
+struct GemmArgs {
+  // A: bf16
+  const uint16_t* a = nullptr;
+  uint64_t lda = 0, lda_hi = 0, a_z = 0;
+  uint32_t a_group = 0;  // 0 = no second level
+  // B, bf16 mode: row n at b + n * ldb; columns k >= K read as zero
+  const uint16_t* b = nullptr;
+  uint64_t ldb = 0, b_z = 0;
+  // B, Q4 mode: weights u32 [N, K/8], scales/biases bf16 [N, K/64]. The SiLU
+  // pair epilogue takes gate in [0] and up in [1].
+  const uint32_t* qw[2] = {nullptr, nullptr};
+  const uint16_t* qs[2] = {nullptr, nullptr};
+  const uint16_t* qb[2] = {nullptr, nullptr};
+  // C (and the residual / gate input, same addressing)
+  uint16_t* c = nullptr;
+  const uint16_t* res = nullptr;
+  uint64_t ldc = 0, ldc_hi = 0, c_z = 0;
+  uint32_t c_group = 0;
+  uint32_t M = 0, N = 0, K = 0;
+};
+
+// Q4 weights. K % 64 == 0; A rows 16-byte aligned (lda % 8 == 0).
+int launch_gemm_q4(hipStream_t s, const GemmArgs& g, int epi, const char* name);
+// bf16 B, `batch` independent problems along grid.z (offsets a_z, b_z, c_z).
+int launch_gemm_bf16(hipStream_t s, const GemmArgs& g, int epi, uint32_t batch, const char* name);
+
+}  // namespace prg

@@ -22,18 +22,27 @@
 // One token's launches are captured once into a HIP graph; the token, positions
 // and sequence length live in device memory (DecodeCtl) and are advanced by the
 // argmax kernel, so replaying the graph runs the greedy loop with no host sync.
+//
+// A prompt is ingested layer-major in chunks of up to kPrefillChunk tokens
+// (DeviceModel.prefillLayerMajor*, model.zig:940-1060; DecoderLayer.prefillStepBf16,
+// decoder_layer.zig:644-760): every projection is an MFMA QMM over the chunk,
+// attention is causal over the cache written so far, and the GDN recurrence
+// runs token-sequentially inside one kernel per layer.
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <map>
 #include <string>
 #include <vector>
 
 #include "attention.hpp"
 #include "gdn.hpp"
+#include "gemm.hpp"
 #include "norm.hpp"
 #include "peregrine_model.h"
+#include "prefill.hpp"
 #include "q4_gemv.hpp"
 
 namespace prg {
@@ -149,6 +158,29 @@ struct LayerState {
 }  // namespace
 }  // namespace prg
 
+namespace prg {
+namespace {
+
+// Prompt-path workspace, allocated on the first prefill ([rows, dim] bf16
+// unless noted).
+struct PrefillWs {
+  uint8_t* arena = nullptr;
+  uint32_t rows = 0;          // tokens per chunk the buffers hold
+  size_t scores_elems = 0;    // bf16 attention score capacity
+  uint16_t *h0 = nullptr, *h1 = nullptr, *normed = nullptr, *attn = nullptr, *resid = nullptr, *inter = nullptr;
+  uint16_t *qkv = nullptr, *conv_out = nullptr, *z = nullptr, *a = nullptr, *b = nullptr, *y = nullptr,
+           *gated = nullptr;
+  float *qn = nullptr, *kn = nullptr, *g = nullptr, *beta = nullptr;  // f32
+  uint16_t *qp = nullptr, *k = nullptr, *v = nullptr, *q = nullptr, *gate = nullptr, *ctx = nullptr,
+           *scores = nullptr;
+};
+
+constexpr uint32_t kPrefillChunk = 2048;
+constexpr size_t kPrefillScoresBytes = size_t(512) << 20;
+
+}  // namespace
+}  // namespace prg
+
 struct PrgModelState {
   PrgModel* model = nullptr;
   uint32_t max_seq = 0, stride = 0;
@@ -177,6 +209,7 @@ struct PrgModelState {
   // replaying the captured graph (same kernels and arguments; for tools such as
   // kernel tracers that do not follow graph launches).
   bool eager = false;
+  prg::PrefillWs pf;
 };
 
 namespace prg {
@@ -462,6 +495,175 @@ uint32_t cache_stride_for(uint32_t max_seq) {  // state.zig:25-32
   return (max_seq + a - 1) / a * a;
 }
 
+// ------------------------------------------------------------ prompt path ---
+int ensure_prefill_ws(PrgModelState* st) {
+  PrefillWs& w = st->pf;
+  if (w.arena) return PRG_OK;
+  const PrgModelConfig& c = st->model->cfg;
+  size_t R = std::min(kPrefillChunk, st->max_seq);
+  // PEREGRINE_PREFILL_CHUNK=n caps the chunk (tests of chunk boundaries).
+  if (const char* e = getenv("PEREGRINE_PREFILL_CHUNK")) {
+    const long v = atol(e);
+    if (v >= 1) R = std::min<size_t>(R, static_cast<size_t>(v));
+  }
+  w.rows = static_cast<uint32_t>(R);
+  w.scores_elems = std::min<size_t>(static_cast<size_t>(kAttnQHeads) * R * align_up(st->max_seq, 64),
+                                    kPrefillScoresBytes / sizeof(uint16_t));
+  const size_t bf = sizeof(uint16_t), f4 = sizeof(float);
+  struct Item {
+    void** slot;
+    size_t bytes;
+  };
+  const Item items[] = {
+      {reinterpret_cast<void**>(&w.h0), bf * R * c.hidden},
+      {reinterpret_cast<void**>(&w.h1), bf * R * c.hidden},
+      {reinterpret_cast<void**>(&w.normed), bf * R * c.hidden},
+      {reinterpret_cast<void**>(&w.attn), bf * R * c.hidden},
+      {reinterpret_cast<void**>(&w.resid), bf * R * c.hidden},
+      {reinterpret_cast<void**>(&w.inter), bf * R * c.intermediate},
+      {reinterpret_cast<void**>(&w.qkv), bf * R * kGdnConvDim},
+      {reinterpret_cast<void**>(&w.conv_out), bf * R * kGdnConvDim},
+      {reinterpret_cast<void**>(&w.z), bf * R * kGdnValDim},
+      {reinterpret_cast<void**>(&w.a), bf * R * kGdnHv},
+      {reinterpret_cast<void**>(&w.b), bf * R * kGdnHv},
+      {reinterpret_cast<void**>(&w.y), bf * R * kGdnValDim},
+      {reinterpret_cast<void**>(&w.gated), bf * R * kGdnValDim},
+      {reinterpret_cast<void**>(&w.qn), f4 * R * kGdnKeyDim},
+      {reinterpret_cast<void**>(&w.kn), f4 * R * kGdnKeyDim},
+      {reinterpret_cast<void**>(&w.g), f4 * R * kGdnHv},
+      {reinterpret_cast<void**>(&w.beta), f4 * R * kGdnHv},
+      {reinterpret_cast<void**>(&w.qp), bf * R * 2 * kAttnQHeads * kAttnHeadDim},
+      {reinterpret_cast<void**>(&w.k), bf * R * kAttnKvHeads * kAttnHeadDim},
+      {reinterpret_cast<void**>(&w.v), bf * R * kAttnKvHeads * kAttnHeadDim},
+      {reinterpret_cast<void**>(&w.q), bf * R * kAttnQHeads * kAttnHeadDim},
+      {reinterpret_cast<void**>(&w.gate), bf * R * kAttnQHeads * kAttnHeadDim},
+      {reinterpret_cast<void**>(&w.ctx), bf * R * kAttnQHeads * kAttnHeadDim},
+      {reinterpret_cast<void**>(&w.scores), bf * w.scores_elems},
+  };
+  size_t total = 0;
+  for (const Item& it : items) total = align_up(total + it.bytes, kAlign);
+  hipError_t e = hipMalloc(reinterpret_cast<void**>(&w.arena), total);
+  if (e != hipSuccess) {
+    w.arena = nullptr;
+    return set_error(PRG_ERR_OOM, "prefill workspace: hipMalloc(%zu): %s", total, hipGetErrorString(e));
+  }
+  size_t off = 0;
+  for (const Item& it : items) {
+    *it.slot = w.arena + off;
+    off = align_up(off + it.bytes, kAlign);
+  }
+  return PRG_OK;
+}
+
+// Largest chunk (<= the workspace rows) whose attention scores fit.
+uint32_t prefill_chunk_tokens(const PrgModelState* st, uint32_t start, uint32_t remaining) {
+  uint32_t T = std::min(remaining, st->pf.rows);
+  while (T > 1 && attn_prefill_scores_elems(T, start) > st->pf.scores_elems) T = (T + 1) / 2;
+  return T;
+}
+
+// x [T, in] -> out [T, out_dim] on the matrix cores (Q4Linear.encodePrefillQmm*,
+// linear_q4.zig:197-233). `up` selects the gate/up SiLU pair.
+int qmm(hipStream_t s, const uint16_t* x, const Q4Linear& l, uint16_t* out, uint32_t T, int epi,
+        const uint16_t* res, const Q4Linear* up, const char* name) {
+  GemmArgs g;
+  g.a = x;
+  g.lda = l.in_dim;
+  g.qw[0] = l.weight;
+  g.qs[0] = l.scales;
+  g.qb[0] = l.biases;
+  if (up) {
+    g.qw[1] = up->weight;
+    g.qs[1] = up->scales;
+    g.qb[1] = up->biases;
+  }
+  g.c = out;
+  g.res = res;
+  g.ldc = l.out_dim;
+  g.M = T;
+  g.N = l.out_dim;
+  g.K = l.in_dim;
+  return launch_gemm_q4(s, g, epi, name);
+}
+
+// DecoderLayer.prefillStepBf16 (decoder_layer.zig:644-760) for T tokens at
+// positions start.. : x -> out.
+int prefill_layer(PrgModel* m, PrgModelState* st, uint32_t li, const uint16_t* x, uint16_t* out, uint32_t T,
+                  uint32_t start) {
+  const DecoderLayer& L = m->layers[li];
+  LayerState& ls = st->layers[li];
+  PrefillWs& w = st->pf;
+  const PrgModelConfig& c = m->cfg;
+  hipStream_t s = st->stream;
+  if (int rc = launch_rmsnorm(s, x, L.input_norm, w.normed, c.hidden, T, c.rms_eps)) return rc;
+  if (L.linear) {  // block_linear.zig:265-361
+    const LinearAttentionBlock& b = L.lin;
+    const uint32_t has_state = start != 0;  // decoder_layer.zig:635
+    if (int rc = qmm(s, w.normed, b.in_qkv, w.qkv, T, kGemmStore, nullptr, nullptr, "prefill.in_proj_qkv")) return rc;
+    if (int rc = qmm(s, w.normed, b.in_z, w.z, T, kGemmStore, nullptr, nullptr, "prefill.in_proj_z")) return rc;
+    if (int rc = qmm(s, w.normed, b.in_a, w.a, T, kGemmStore, nullptr, nullptr, "prefill.in_proj_a")) return rc;
+    if (int rc = qmm(s, w.normed, b.in_b, w.b, T, kGemmStore, nullptr, nullptr, "prefill.in_proj_b")) return rc;
+    if (int rc = launch_conv1d_prefill(s, ls.conv, w.qkv, b.conv_weight, w.conv_out, T, has_state)) return rc;
+    if (int rc = launch_gdn_prefill_prepare(s, w.conv_out, w.a, w.b, b.a_log, b.dt_bias, w.qn, w.kn, w.g, w.beta, T))
+      return rc;
+    if (int rc = launch_gdn_prefill(s, ls.recur, w.qn, w.kn, w.conv_out, w.g, w.beta, w.y, T, has_state)) return rc;
+    if (int rc = prg_rmsnorm_gated_bf16(s, w.y, b.norm_weight, w.z, w.gated, kGdnDv, c.rms_eps, T * kGdnHv))
+      return rc;
+    if (int rc = qmm(s, w.gated, b.out_proj, w.attn, T, kGemmStore, nullptr, nullptr, "prefill.out_proj")) return rc;
+  } else {  // block_attn.zig:361-498
+    const FullAttentionBlock& b = L.full;
+    if (int rc = qmm(s, w.normed, b.q_proj, w.qp, T, kGemmStore, nullptr, nullptr, "prefill.q_proj")) return rc;
+    if (int rc = qmm(s, w.normed, b.k_proj, w.k, T, kGemmStore, nullptr, nullptr, "prefill.k_proj")) return rc;
+    if (int rc = qmm(s, w.normed, b.v_proj, w.v, T, kGemmStore, nullptr, nullptr, "prefill.v_proj")) return rc;
+    if (int rc = launch_attn_prefill_prepare(s, w.qp, b.q_norm, w.k, b.k_norm, w.v, w.q, w.gate, ls.cache_k,
+                                             ls.cache_v, T, start, start, st->stride))
+      return rc;
+    if (int rc = launch_attn_prefill(s, w.q, ls.cache_k, ls.cache_v, w.gate, w.ctx, w.scores, T, start, st->stride,
+                                     kAttnScale))
+      return rc;
+    if (int rc = qmm(s, w.ctx, b.o_proj, w.attn, T, kGemmStore, nullptr, nullptr, "prefill.o_proj")) return rc;
+  }
+  // decoder_layer.zig:717-735: add + post norm, then the MLP (block_mlp.zig:155-258)
+  if (int rc = prg_add_rmsnorm_bf16(s, x, w.attn, L.post_norm, w.resid, w.normed, c.hidden, T, c.rms_eps)) return rc;
+  if (int rc = qmm(s, w.normed, L.mlp.gate_proj, w.inter, T, kGemmSiluPair, nullptr, &L.mlp.up_proj,
+                   "prefill.mlp.gate_up"))
+    return rc;
+  return qmm(s, w.inter, L.mlp.down_proj, out, T, kGemmResidual, w.resid, nullptr, "prefill.mlp.down_proj");
+}
+
+// Ingest st->prompt[0, len) in chunks, then the argmax tail on the last row
+// (encodePrefillArgmaxTailBf16, model.zig:1307-1324). The caller has set ctl
+// to step len-1 of a len-token prompt; the argmax kernel records the
+// prediction and advances ctl to position len.
+int run_prefill(PrgModel* m, PrgModelState* st, uint32_t len) {
+  if (int rc = ensure_prefill_ws(st)) return rc;
+  const PrgModelConfig& c = m->cfg;
+  hipStream_t s = st->stream;
+  PrefillWs& w = st->pf;
+  const uint16_t* last = nullptr;
+  uint32_t T = 0;
+  for (uint32_t start = 0; start < len; start += T) {
+    T = prefill_chunk_tokens(st, start, len - start);
+    if (int rc = launch_embedding(s, m->embed.weight, m->embed.scales, m->embed.biases, w.h0, st->prompt + start, 0,
+                                  T, c.hidden))
+      return rc;
+    uint16_t *x = w.h0, *y = w.h1;
+    for (uint32_t li = 0; li < c.num_layers; ++li) {
+      if (int rc = prefill_layer(m, st, li, x, y, T, start)) return rc;
+      std::swap(x, y);
+    }
+    last = x + static_cast<size_t>(T - 1) * c.hidden;
+  }
+  GemvParams p = gemv_params(last, c.hidden);
+  p.norm_w = m->final_norm;
+  p.eps = c.rms_eps;
+  add_seg(p, m->lm_head, nullptr);
+  p.seg[0].pval[0] = st->pval;
+  p.seg[0].pidx[0] = st->pidx;
+  if (int rc = launch_q4_gemv(s, p, 1, 8, kEpiArgmax, true, "lm_head.argmax")) return rc;
+  return launch_argmax_advance(s, st->pval, st->pidx, c.vocab / 8, st->ctl, st->prompt, st->predictions);
+}
+
 }  // namespace
 }  // namespace prg
 
@@ -618,6 +820,7 @@ void prg_model_state_destroy(PrgModelState* st) {
   if (st->ev1) hipEventDestroy(st->ev1);
   if (st->stream) hipStreamDestroy(st->stream);
   hipFree(st->arena);
+  if (st->pf.arena) hipFree(st->pf.arena);
   delete st;
 }
 
@@ -673,17 +876,17 @@ int prg_model_prefill(PrgModel* model, PrgModelState* st, const uint32_t* prompt
   for (uint32_t i = 0; i < prompt_len; ++i)
     if (prompt[i] >= model->cfg.vocab)
       return set_error(PRG_ERR_INVALID_TOKEN, "prompt[%u] = %u >= vocab %u", i, prompt[i], model->cfg.vocab);
-  if (int rc = ensure_graphs(st)) return rc;
   if (int rc = prg_model_state_reset(st)) return rc;
+  // Control block as if step prompt_len-1 were running: the argmax tail
+  // records predictions[prompt_len-1] and moves the decode loop to prompt_len.
   DecodeCtl ctl{};
-  ctl.s = StepScalars{prompt[0], 0, 0, 1};
+  ctl.s = StepScalars{prompt[prompt_len - 1], prompt_len - 1, prompt_len - 1, prompt_len};
+  ctl.n = prompt_len - 1;
   ctl.prompt_len = prompt_len;
   ctl.capacity = st->max_seq;
   PRG_HIP(hipMemcpyAsync(st->prompt, prompt, sizeof(uint32_t) * prompt_len, hipMemcpyHostToDevice, st->stream));
   PRG_HIP(hipMemcpyAsync(st->ctl, &ctl, sizeof(ctl), hipMemcpyHostToDevice, st->stream));
-  for (uint32_t n = 0; n + 1 < prompt_len; ++n)
-    if (int rc = run_step(st, false)) return rc;
-  if (int rc = run_step(st, true)) return rc;
+  if (int rc = run_prefill(model, st, prompt_len)) return rc;
   PRG_HIP(hipMemcpyAsync(next_token, st->predictions + (prompt_len - 1), sizeof(uint32_t), hipMemcpyDeviceToHost,
                          st->stream));
   PRG_HIP(hipStreamSynchronize(st->stream));

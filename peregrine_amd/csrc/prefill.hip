@@ -1,0 +1,454 @@
+// Prompt-path (prefill) kernels other than the GEMMs: attention prepare and
+// softmax, the materialised causal attention driver, conv1d prefill with its
+// state publish, and the Gated DeltaNet prefill (q/k norms + gates, then the
+// token-sequential recurrence).
+//
+// Reference semantics (file:line in the reference tree):
+//   split_qg_many_bf16                       shaders/layout.metal:68-89
+//   qwen35_qk_norm_rope_append_many_bf16     shaders/attention.metal:146-220
+//   encodeMaterializedPrefillBf16            src/model/block_attn.zig:500-631
+//   prefill_softmax_scaled_masked_bf16       shaders/attention.metal:1463-1523
+//   sigmoid_mul_pair_inplace_bf16            shaders/elementwise.metal:88-99
+//   conv1d_silu_prefill_vec4_bf16 / _state   shaders/conv1d.metal:136-198
+//   qk_l2norm_prefill_bf16, gating_many_bf16 shaders/gated_norm.metal:191-268
+//   gated_delta_prefill_h128_norm_prepared_value_major_r8_bf16
+//                                            shaders/gated_delta.metal:35-138
+//   composition                              src/model/block_linear.zig:265-469,
+//                                            src/model/block_attn.zig:361-500
+#include "attention.hpp"
+#include "gdn.hpp"
+#include "gemm.hpp"
+#include "prefill.hpp"
+
+namespace {
+
+using namespace prg;
+
+constexpr int kPrepThreads = 256;     // QWEN35_QK_PREPARE_THREADS (attention.metal:9)
+constexpr int kSoftmaxThreads = 256;  // PREFILL_SOFTMAX_THREADS (attention.metal:42)
+constexpr int kQkNormThreads = 128;   // QK_NORM_PREFILL_THREADS_PER_THREADGROUP (gated_norm.metal:55)
+constexpr float kLog2e = 1.4426950408889634f;
+
+// Halving tree over blockDim.x == N threads in the reference's order
+// (partial[t] += partial[t + stride], stride N/2 .. 1). Every thread gets the
+// root. `sh` holds N floats.
+template <int N>
+__device__ inline float tree_sum(float v, float* sh) {
+  sh[threadIdx.x] = v;
+  __syncthreads();
+#pragma unroll
+  for (int stride = N / 2; stride > 0; stride >>= 1) {
+    if (static_cast<int>(threadIdx.x) < stride) sh[threadIdx.x] += sh[threadIdx.x + stride];
+    __syncthreads();
+  }
+  const float r = sh[0];
+  __syncthreads();
+  return r;
+}
+
+template <int N>
+__device__ inline float tree_max(float v, float* sh) {
+  sh[threadIdx.x] = v;
+  __syncthreads();
+#pragma unroll
+  for (int stride = N / 2; stride > 0; stride >>= 1) {
+    if (static_cast<int>(threadIdx.x) < stride) sh[threadIdx.x] = fmaxf(sh[threadIdx.x], sh[threadIdx.x + stride]);
+    __syncthreads();
+  }
+  const float r = sh[0];
+  __syncthreads();
+  return r;
+}
+
+// ------------------------------------------------------- attention ----------
+// One block per row: rows [0, 16T) are query heads (t = row/16, h = row%16),
+// rows [16T, 20T) key heads (t = r/4, h = r%4). Thread d owns dimension d.
+// Queries: split from the packed q ‖ gate projection, RMS-normed, partial
+// NeoX RoPE on dims [0, 64), written to q_out; gate copied to gate_out. Keys:
+// same norm/RoPE into cache_k[h, stride, 256] at start_cache + t; values copied
+// to cache_v[h, 256, stride]. The normed value stays f32 through RoPE.
+__global__ __launch_bounds__(kPrepThreads) void attn_prefill_prepare_kernel(
+    const uint16_t* __restrict__ qp, const uint16_t* __restrict__ q_w, const uint16_t* __restrict__ k_in,
+    const uint16_t* __restrict__ k_w, const uint16_t* __restrict__ v_in, uint16_t* __restrict__ q_out,
+    uint16_t* __restrict__ gate_out, uint16_t* __restrict__ cache_k, uint16_t* __restrict__ cache_v, uint32_t T,
+    uint32_t start_rope, uint32_t start_cache, uint32_t stride) {
+  __shared__ float sh[kPrepThreads];
+  const uint32_t rg = blockIdx.x, d = threadIdx.x;
+  const uint32_t q_rows = T * kAttnQHeads;
+  const bool is_q = rg < q_rows;
+  const uint32_t lr = is_q ? rg : rg - q_rows;
+  const uint32_t heads = is_q ? kAttnQHeads : kAttnKvHeads;
+  const uint32_t t = lr / heads, h = lr - t * heads;
+  const uint16_t* src = is_q ? qp + static_cast<size_t>(lr) * 2 * kAttnHeadDim : k_in + static_cast<size_t>(lr) * kAttnHeadDim;
+  const uint16_t* w = is_q ? q_w : k_w;
+  const float x = bf2f(src[d]);
+  if (is_q) gate_out[static_cast<size_t>(lr) * kAttnHeadDim + d] = src[kAttnHeadDim + d];
+  else cache_v[(static_cast<size_t>(h) * kAttnHeadDim + d) * stride + start_cache + t] = v_in[static_cast<size_t>(lr) * kAttnHeadDim + d];
+  const float ss = tree_sum<kPrepThreads>(__fmul_rn(x, x), sh);
+  const float scale = 1.0f / sqrtf(ss / static_cast<float>(kAttnHeadDim) + kAttnEps);
+  uint16_t* dst = is_q ? q_out + static_cast<size_t>(lr) * kAttnHeadDim
+                       : cache_k + (static_cast<size_t>(h) * stride + start_cache + t) * kAttnHeadDim;
+  constexpr uint32_t half = kAttnRotary / 2;
+  if (d < half) {
+    const float a = __fmul_rn(__fmul_rn(x, scale), bf2f(w[d]));
+    const float b = __fmul_rn(__fmul_rn(bf2f(src[d + half]), scale), bf2f(w[d + half]));
+    const float inv_freq = powf(kAttnTheta, -(2.0f * static_cast<float>(d)) / static_cast<float>(kAttnRotary));
+    const float th = static_cast<float>(start_rope + t) * inv_freq;
+    const float c = cosf(th), s = sinf(th);
+    dst[d] = f2bf(__fsub_rn(__fmul_rn(a, c), __fmul_rn(b, s)));
+    dst[d + half] = f2bf(__fadd_rn(__fmul_rn(b, c), __fmul_rn(a, s)));
+  } else if (d >= kAttnRotary) {
+    dst[d] = f2bf(__fmul_rn(__fmul_rn(x, scale), bf2f(w[d])));
+  }
+}
+
+// Causal softmax over one row of bf16 scores, in place (reference order: row
+// max of float(s)*scale over visible columns, then the sum of
+// exp2((v - max) * log2e), each thread striding the row, each reduced by a
+// halving tree). Row r of kv head z (rows z*4T .. ) is token r % T; column c is
+// visible iff c <= prefix + t. Columns [L, ld) are zeroed for the P*V GEMM.
+__global__ __launch_bounds__(kSoftmaxThreads) void attn_prefill_softmax_kernel(uint16_t* __restrict__ scores,
+                                                                               uint32_t ld, uint32_t L, uint32_t T,
+                                                                               uint32_t prefix, float scale) {
+  __shared__ float sh[kSoftmaxThreads];
+  uint16_t* row = scores + static_cast<size_t>(blockIdx.x) * ld;
+  const uint32_t t = (blockIdx.x % (kAttnGroup * T)) % T;
+  const uint32_t vis = prefix + t;
+  float m = -INFINITY;
+  for (uint32_t c = threadIdx.x; c < L; c += kSoftmaxThreads)
+    m = fmaxf(m, c > vis ? -INFINITY : __fmul_rn(bf2f(row[c]), scale));
+  const float row_max = tree_max<kSoftmaxThreads>(m, sh);
+  float sum = 0.0f;
+  for (uint32_t c = threadIdx.x; c < L; c += kSoftmaxThreads)
+    if (c <= vis) sum += exp2f(__fmul_rn(__fsub_rn(__fmul_rn(bf2f(row[c]), scale), row_max), kLog2e));
+  const float total = tree_sum<kSoftmaxThreads>(sum, sh);
+  const float denom = total == 0.0f ? 1.0f : total;
+  for (uint32_t c = threadIdx.x; c < ld; c += kSoftmaxThreads) {
+    uint16_t p = 0;
+    if (c < L && c <= vis) p = f2bf(exp2f(__fmul_rn(__fsub_rn(__fmul_rn(bf2f(row[c]), scale), row_max), kLog2e)) / denom);
+    row[c] = p;
+  }
+}
+
+// ------------------------------------------------------------- GDN ----------
+constexpr uint32_t kConvChunk = 16;  // tokens per thread
+
+// x(u) over the virtual sequence [state rows 0..2 ‖ inputs] for channels c, c+1.
+__device__ inline float2 conv_src(const float* state, const uint16_t* qkv, uint32_t u, uint32_t c, bool has_state) {
+  if (u < kGdnConvK - 1) {
+    if (!has_state) return make_float2(0.0f, 0.0f);
+    return make_float2(state[u * kGdnConvDim + c], state[u * kGdnConvDim + c + 1]);
+  }
+  const uint32_t p = *reinterpret_cast<const uint32_t*>(qkv + static_cast<size_t>(u - (kGdnConvK - 1)) * kGdnConvDim + c);
+  return make_float2(bf_lo(p), bf_hi(p));
+}
+
+__device__ inline float conv_tap(float acc, float w, float x) { return __fadd_rn(acc, __fmul_rn(w, x)); }
+
+// Thread = (channel pair, 16-token chunk): out[t, c] = bf16(silu(sum_j w[c, j] * x(t + j))).
+__global__ __launch_bounds__(256) void conv1d_prefill_kernel(const float* __restrict__ state,
+                                                             const uint16_t* __restrict__ qkv,
+                                                             const uint16_t* __restrict__ w,
+                                                             uint16_t* __restrict__ out, uint32_t T,
+                                                             uint32_t has_state) {
+  constexpr uint32_t pairs = kGdnConvDim / 2;
+  const uint32_t idx = blockIdx.x * blockDim.x + threadIdx.x;
+  const uint32_t c = 2 * (idx % pairs), t0 = (idx / pairs) * kConvChunk;
+  if (t0 >= T) return;
+  const uint4 wv = *reinterpret_cast<const uint4*>(w + static_cast<size_t>(c) * kGdnConvK);
+  const float w0[4] = {bf_lo(wv.x), bf_hi(wv.x), bf_lo(wv.y), bf_hi(wv.y)};
+  const float w1[4] = {bf_lo(wv.z), bf_hi(wv.z), bf_lo(wv.w), bf_hi(wv.w)};
+  const bool hs = has_state != 0;
+  float2 h0 = conv_src(state, qkv, t0, c, hs), h1 = conv_src(state, qkv, t0 + 1, c, hs),
+         h2 = conv_src(state, qkv, t0 + 2, c, hs);
+  const uint32_t t1 = min(t0 + kConvChunk, T);
+  for (uint32_t t = t0; t < t1; ++t) {
+    const float2 h3 = conv_src(state, qkv, t + 3, c, hs);
+    float a0 = 0.0f, a1 = 0.0f;
+    a0 = conv_tap(a0, w0[0], h0.x); a0 = conv_tap(a0, w0[1], h1.x); a0 = conv_tap(a0, w0[2], h2.x); a0 = conv_tap(a0, w0[3], h3.x);
+    a1 = conv_tap(a1, w1[0], h0.y); a1 = conv_tap(a1, w1[1], h1.y); a1 = conv_tap(a1, w1[2], h2.y); a1 = conv_tap(a1, w1[3], h3.y);
+    const uint32_t o = static_cast<uint32_t>(f2bf(a0 / (1.0f + expf(-a0)))) |
+                       (static_cast<uint32_t>(f2bf(a1 / (1.0f + expf(-a1)))) << 16);
+    *reinterpret_cast<uint32_t*>(out + static_cast<size_t>(t) * kGdnConvDim + c) = o;
+    h0 = h1;
+    h1 = h2;
+    h2 = h3;
+  }
+}
+
+// state[j, c] = x(T + j): the last three entries of the virtual sequence.
+// Runs after conv1d_prefill_kernel (which reads the old state).
+__global__ void conv1d_prefill_state_kernel(float* __restrict__ state, const uint16_t* __restrict__ qkv, uint32_t T,
+                                            uint32_t has_state) {
+  const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= kGdnConvDim) return;
+  for (uint32_t j = 0; j < kGdnConvK - 1; ++j) {
+    const uint32_t u = T + j;  // u > j: state[u] is read before it is rewritten
+    float x = 0.0f;
+    if (u < kGdnConvK - 1) x = has_state ? state[u * kGdnConvDim + c] : 0.0f;
+    else x = bf2f(qkv[static_cast<size_t>(u - (kGdnConvK - 1)) * kGdnConvDim + c]);
+    state[j * kGdnConvDim + c] = x;
+  }
+}
+
+// Block (t, hk), 128 threads: f32 l2-normed q (x rsqrt(Dk)) and k of k-head hk;
+// threads 0, 1 also produce the gates of v-heads 2hk, 2hk+1.
+__global__ __launch_bounds__(kQkNormThreads) void gdn_prefill_prepare_kernel(
+    const uint16_t* __restrict__ conv_out, const uint16_t* __restrict__ a, const uint16_t* __restrict__ b,
+    const float* __restrict__ A_log, const uint16_t* __restrict__ dt_bias, float* __restrict__ qn,
+    float* __restrict__ kn, float* __restrict__ g, float* __restrict__ beta) {
+  __shared__ float sh[kQkNormThreads];
+  const uint32_t t = blockIdx.x / kGdnHk, hk = blockIdx.x % kGdnHk, d = threadIdx.x;
+  const uint16_t* row = conv_out + static_cast<size_t>(t) * kGdnConvDim;
+  const float qv = bf2f(row[hk * kGdnDk + d]), kv = bf2f(row[kGdnKeyDim + hk * kGdnDk + d]);
+  const float qs = tree_sum<kQkNormThreads>(__fmul_rn(qv, qv), sh);
+  const float ks = tree_sum<kQkNormThreads>(__fmul_rn(kv, kv), sh);
+  const float q_inv = 1.0f / sqrtf(qs + 1.0e-6f), k_inv = 1.0f / sqrtf(ks + 1.0e-6f);
+  const float q_scale = 1.0f / sqrtf(static_cast<float>(kGdnDk));
+  const size_t o = (static_cast<size_t>(t) * kGdnHk + hk) * kGdnDk + d;
+  qn[o] = __fmul_rn(__fmul_rn(qv, q_inv), q_scale);
+  kn[o] = __fmul_rn(kv, k_inv);
+  if (d < kGdnHv / kGdnHk) {
+    const uint32_t hv = hk * (kGdnHv / kGdnHk) + d;
+    const size_t go = static_cast<size_t>(t) * kGdnHv + hv;
+    const float x = __fadd_rn(bf2f(a[go]), bf2f(dt_bias[hv]));
+    const float softplus = __fadd_rn(fmaxf(x, 0.0f), logf(1.0f + expf(-fabsf(x))));
+    g[go] = expf(__fmul_rn(-expf(A_log[hv]), softplus));
+    beta[go] = 1.0f / (1.0f + expf(-bf2f(b[go])));
+  }
+}
+
+// Token-sequential delta rule. Block = 16 state rows of one v-head (4 wave64s,
+// each 16-lane DPP row owns one state row; lane j holds dk = 8j..8j+7 in
+// registers for the whole prompt). Per token:
+//   kq = k.q; d = S*decay; kv = d.k; ob = d.q; delta = (v - kv)*beta;
+//   S = d + k*delta; y = bf16(ob + delta*kq)
+// The next token's q, k, gates and v are loaded while the current one runs.
+constexpr int kGdnPRowsPerBlock = 16;
+
+__global__ __launch_bounds__(256) void gdn_prefill_kernel(float* __restrict__ state, const float* __restrict__ qn,
+                                                          const float* __restrict__ kn,
+                                                          const uint16_t* __restrict__ conv_out,
+                                                          const float* __restrict__ g,
+                                                          const float* __restrict__ beta,
+                                                          uint16_t* __restrict__ y, uint32_t T,
+                                                          uint32_t has_state) {
+  constexpr uint32_t blocks_per_head = kGdnDv / kGdnPRowsPerBlock;
+  const uint32_t hv = blockIdx.x / blocks_per_head;
+  const uint32_t row = (blockIdx.x % blocks_per_head) * kGdnPRowsPerBlock + (threadIdx.x >> 4);
+  const uint32_t j = threadIdx.x & 15;
+  const uint32_t hk = hv / (kGdnHv / kGdnHk);
+  float4* srow = reinterpret_cast<float4*>(state + (static_cast<size_t>(hv) * kGdnDv + row) * kGdnDk + 8 * j);
+  float S[8];
+  {
+    const float4 s0 = has_state ? srow[0] : make_float4(0.f, 0.f, 0.f, 0.f);
+    const float4 s1 = has_state ? srow[1] : make_float4(0.f, 0.f, 0.f, 0.f);
+    S[0] = s0.x; S[1] = s0.y; S[2] = s0.z; S[3] = s0.w;
+    S[4] = s1.x; S[5] = s1.y; S[6] = s1.z; S[7] = s1.w;
+  }
+  const float4* qb = reinterpret_cast<const float4*>(qn + hk * kGdnDk + 8 * j);
+  const float4* kb = reinterpret_cast<const float4*>(kn + hk * kGdnDk + 8 * j);
+  constexpr size_t qk_step = kGdnKeyDim / 4;  // float4 per token
+  const uint16_t* vb = conv_out + 2 * kGdnKeyDim + hv * kGdnDv + row;
+  uint16_t* yb = y + hv * kGdnDv + row;
+
+  float4 q0 = qb[0], q1 = qb[1], k0 = kb[0], k1 = kb[1];
+  float gd = g[hv], bt = beta[hv];
+  uint16_t vv = vb[0];
+  for (uint32_t t = 0; t < T; ++t) {
+    const float q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+    const float k[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+    const float decay = gd, bet = bt, v = bf2f(vv);
+    if (t + 1 < T) {
+      const size_t n = static_cast<size_t>(t + 1);
+      q0 = qb[n * qk_step]; q1 = qb[n * qk_step + 1];
+      k0 = kb[n * qk_step]; k1 = kb[n * qk_step + 1];
+      gd = g[n * kGdnHv + hv];
+      bt = beta[n * kGdnHv + hv];
+      vv = vb[n * kGdnConvDim];
+    }
+    float kq = 0.f, kvp = 0.f, obp = 0.f, d[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      kq += k[i] * q[i];
+      d[i] = S[i] * decay;
+      kvp += d[i] * k[i];
+      obp += d[i] * q[i];
+    }
+    kq = row16_sum(kq);
+    const float kv = row16_sum(kvp), ob = row16_sum(obp);
+    const float delta = (v - kv) * bet;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) S[i] = d[i] + k[i] * delta;
+    if (j == 0) yb[static_cast<size_t>(t) * kGdnValDim] = f2bf(ob + delta * kq);
+  }
+  srow[0] = make_float4(S[0], S[1], S[2], S[3]);
+  srow[1] = make_float4(S[4], S[5], S[6], S[7]);
+}
+
+}  // namespace
+
+namespace prg {
+
+size_t attn_prefill_scores_elems(uint32_t T, uint32_t prefix) {
+  const size_t L = static_cast<size_t>(prefix) + T, ld = (L + 63) / 64 * 64;
+  return static_cast<size_t>(kAttnQHeads) * T * ld;
+}
+
+int launch_attn_prefill_prepare(hipStream_t s, const uint16_t* qp, const uint16_t* q_w, const uint16_t* k_in,
+                                const uint16_t* k_w, const uint16_t* v_in, uint16_t* q_out, uint16_t* gate_out,
+                                uint16_t* cache_k, uint16_t* cache_v, uint32_t T, uint32_t start_rope,
+                                uint32_t start_cache, uint32_t stride) {
+  hipLaunchKernelGGL(attn_prefill_prepare_kernel, dim3(T * (kAttnQHeads + kAttnKvHeads)), dim3(kPrepThreads), 0, s,
+                     qp, q_w, k_in, k_w, v_in, q_out, gate_out, cache_k, cache_v, T, start_rope, start_cache, stride);
+  PRG_CHECK_LAUNCH("attn_prefill_prepare");
+  return PRG_OK;
+}
+
+int launch_attn_prefill(hipStream_t s, const uint16_t* q, const uint16_t* cache_k, const uint16_t* cache_v,
+                        const uint16_t* gate, uint16_t* out, uint16_t* scores, uint32_t T, uint32_t prefix,
+                        uint32_t stride, float scale) {
+  const uint32_t L = prefix + T, ld = (L + 63) / 64 * 64;
+  const uint32_t rows = kAttnGroup * T;  // per kv head: q head in group x token
+  GemmArgs sc;
+  sc.a = q;
+  sc.lda = static_cast<uint64_t>(kAttnQHeads) * kAttnHeadDim;  // next token
+  sc.lda_hi = kAttnHeadDim;                                    // next q head of the group
+  sc.a_group = T;
+  sc.a_z = static_cast<uint64_t>(kAttnGroup) * kAttnHeadDim;
+  sc.b = cache_k;
+  sc.ldb = kAttnHeadDim;
+  sc.b_z = static_cast<uint64_t>(stride) * kAttnHeadDim;
+  sc.c = scores;
+  sc.ldc = ld;
+  sc.c_z = static_cast<uint64_t>(rows) * ld;
+  sc.M = rows;
+  sc.N = L;
+  sc.K = kAttnHeadDim;
+  if (int rc = launch_gemm_bf16(s, sc, kGemmStore, kAttnKvHeads, "attn_prefill.scores")) return rc;
+  hipLaunchKernelGGL(attn_prefill_softmax_kernel, dim3(kAttnKvHeads * rows), dim3(kSoftmaxThreads), 0, s, scores, ld,
+                     L, T, prefix, scale);
+  PRG_CHECK_LAUNCH("attn_prefill.softmax");
+  GemmArgs pv;
+  pv.a = scores;
+  pv.lda = ld;
+  pv.a_z = static_cast<uint64_t>(rows) * ld;
+  pv.b = cache_v;
+  pv.ldb = stride;
+  pv.b_z = static_cast<uint64_t>(kAttnHeadDim) * stride;
+  pv.c = out;
+  pv.res = gate;
+  pv.ldc = static_cast<uint64_t>(kAttnQHeads) * kAttnHeadDim;
+  pv.ldc_hi = kAttnHeadDim;
+  pv.c_group = T;
+  pv.c_z = static_cast<uint64_t>(kAttnGroup) * kAttnHeadDim;
+  pv.M = rows;
+  pv.N = kAttnHeadDim;
+  pv.K = L;
+  return launch_gemm_bf16(s, pv, kGemmSigmoidGate, kAttnKvHeads, "attn_prefill.values");
+}
+
+int launch_conv1d_prefill(hipStream_t s, float* state, const uint16_t* qkv, const uint16_t* w, uint16_t* out,
+                          uint32_t T, uint32_t has_state) {
+  const size_t threads = static_cast<size_t>(kGdnConvDim / 2) * ((T + kConvChunk - 1) / kConvChunk);
+  hipLaunchKernelGGL(conv1d_prefill_kernel, dim3(static_cast<uint32_t>((threads + 255) / 256)), dim3(256), 0, s, state,
+                     qkv, w, out, T, has_state);
+  PRG_CHECK_LAUNCH("conv1d_prefill");
+  hipLaunchKernelGGL(conv1d_prefill_state_kernel, dim3(kGdnConvDim / 256), dim3(256), 0, s, state, qkv, T, has_state);
+  PRG_CHECK_LAUNCH("conv1d_prefill_state");
+  return PRG_OK;
+}
+
+int launch_gdn_prefill_prepare(hipStream_t s, const uint16_t* conv_out, const uint16_t* a, const uint16_t* b,
+                               const float* A_log, const uint16_t* dt_bias, float* qn, float* kn, float* g,
+                               float* beta, uint32_t T) {
+  hipLaunchKernelGGL(gdn_prefill_prepare_kernel, dim3(T * kGdnHk), dim3(kQkNormThreads), 0, s, conv_out, a, b, A_log,
+                     dt_bias, qn, kn, g, beta);
+  PRG_CHECK_LAUNCH("gdn_prefill_prepare");
+  return PRG_OK;
+}
+
+int launch_gdn_prefill(hipStream_t s, float* state, const float* qn, const float* kn, const uint16_t* conv_out,
+                       const float* g, const float* beta, uint16_t* y, uint32_t T, uint32_t has_state) {
+  hipLaunchKernelGGL(gdn_prefill_kernel, dim3(kGdnHv * (kGdnDv / kGdnPRowsPerBlock)), dim3(256), 0, s, state, qn, kn,
+                     conv_out, g, beta, y, T, has_state);
+  PRG_CHECK_LAUNCH("gdn_prefill");
+  return PRG_OK;
+}
+
+}  // namespace prg
+
+extern "C" {
+
+size_t prg_attn_prefill_scores_bytes(uint32_t token_count, uint32_t prefix_len) {
+  return sizeof(uint16_t) * prg::attn_prefill_scores_elems(token_count, prefix_len);
+}
+
+int prg_attn_prefill_prepare_bf16(void* stream, const uint16_t* packed_q, const uint16_t* q_weight,
+                                  const uint16_t* k_input, const uint16_t* k_weight,
+                                  const uint16_t* v_input, uint16_t* q_output, uint16_t* gate_output,
+                                  uint16_t* key_cache, uint16_t* value_cache, uint32_t token_count,
+                                  uint32_t start_rope_pos, uint32_t start_cache_pos,
+                                  uint32_t cache_stride_tokens) {
+  PRG_CHECK_ARG(packed_q && q_weight && k_input && k_weight && v_input && q_output && gate_output && key_cache &&
+                    value_cache,
+                "prg_attn_prefill_prepare_bf16: null pointer");
+  PRG_CHECK_ARG(token_count > 0, "prg_attn_prefill_prepare_bf16: token_count == 0");
+  PRG_CHECK_ARG(static_cast<uint64_t>(start_cache_pos) + token_count <= cache_stride_tokens,
+                "prg_attn_prefill_prepare_bf16: cache slots [%u, %u) exceed the stride %u", start_cache_pos,
+                start_cache_pos + token_count, cache_stride_tokens);
+  PRG_CHECK_ARG(static_cast<uint64_t>(token_count) * (kAttnQHeads + kAttnKvHeads) < (1ull << 31),
+                "prg_attn_prefill_prepare_bf16: token_count %u too large", token_count);
+  return prg::launch_attn_prefill_prepare(as_stream(stream), packed_q, q_weight, k_input, k_weight, v_input, q_output,
+                                          gate_output, key_cache, value_cache, token_count, start_rope_pos,
+                                          start_cache_pos, cache_stride_tokens);
+}
+
+int prg_attn_prefill_bf16(void* stream, const uint16_t* q, const uint16_t* key_cache,
+                          const uint16_t* value_cache, const uint16_t* gate, uint16_t* out,
+                          uint16_t* scores, uint32_t token_count, uint32_t prefix_len,
+                          uint32_t cache_stride_tokens, float scale) {
+  PRG_CHECK_ARG(q && key_cache && value_cache && gate && out && scores, "prg_attn_prefill_bf16: null pointer");
+  PRG_CHECK_ARG(token_count > 0, "prg_attn_prefill_bf16: token_count == 0");
+  PRG_CHECK_ARG(cache_stride_tokens % 8 == 0, "prg_attn_prefill_bf16: stride %u must be a multiple of 8",
+                cache_stride_tokens);
+  PRG_CHECK_ARG(static_cast<uint64_t>(prefix_len) + token_count <= cache_stride_tokens,
+                "prg_attn_prefill_bf16: %u + %u tokens exceed the stride %u", prefix_len, token_count,
+                cache_stride_tokens);
+  PRG_CHECK_ARG(static_cast<uint64_t>(kAttnQHeads) * token_count < (1ull << 31),
+                "prg_attn_prefill_bf16: token_count %u too large", token_count);
+  return prg::launch_attn_prefill(as_stream(stream), q, key_cache, value_cache, gate, out, scores, token_count,
+                                  prefix_len, cache_stride_tokens, scale);
+}
+
+int prg_conv1d_silu_prefill_bf16(void* stream, float* state, const uint16_t* qkv, const uint16_t* weight,
+                                 uint16_t* out, uint32_t token_count, uint32_t conv_dim,
+                                 uint32_t kernel_size, uint32_t has_previous_state) {
+  PRG_CHECK_ARG(state && qkv && weight && out, "prg_conv1d_silu_prefill_bf16: null pointer");
+  PRG_CHECK_ARG(conv_dim == prg::kGdnConvDim && kernel_size == prg::kGdnConvK,
+                "prg_conv1d_silu_prefill_bf16: only conv_dim 8192, kernel 4 is built");
+  PRG_CHECK_ARG(token_count > 0, "prg_conv1d_silu_prefill_bf16: token_count == 0");
+  return prg::launch_conv1d_prefill(as_stream(stream), state, qkv, weight, out, token_count, has_previous_state);
+}
+
+int prg_gated_delta_prefill_prepare_bf16(void* stream, const uint16_t* conv_out, const uint16_t* a,
+                                         const uint16_t* b, const float* A_log, const uint16_t* dt_bias,
+                                         float* q_out, float* k_out, float* g_out, float* beta_out,
+                                         uint32_t token_count) {
+  PRG_CHECK_ARG(conv_out && a && b && A_log && dt_bias && q_out && k_out && g_out && beta_out,
+                "prg_gated_delta_prefill_prepare_bf16: null pointer");
+  PRG_CHECK_ARG(token_count > 0, "prg_gated_delta_prefill_prepare_bf16: token_count == 0");
+  return prg::launch_gdn_prefill_prepare(as_stream(stream), conv_out, a, b, A_log, dt_bias, q_out, k_out, g_out,
+                                         beta_out, token_count);
+}
+
+int prg_gated_delta_prefill_bf16(void* stream, float* state, const float* q, const float* k,
+                                 const uint16_t* conv_out, const float* g, const float* beta, uint16_t* y,
+                                 uint32_t token_count, uint32_t has_previous_state) {
+  PRG_CHECK_ARG(state && q && k && conv_out && g && beta && y, "prg_gated_delta_prefill_bf16: null pointer");
+  PRG_CHECK_ARG(token_count > 0, "prg_gated_delta_prefill_bf16: token_count == 0");
+  return prg::launch_gdn_prefill(as_stream(stream), state, q, k, conv_out, g, beta, y, token_count,
+                                 has_previous_state);
+}
+
+}  // extern "C"

@@ -68,6 +68,16 @@ class Q4Linear:
     def dequantize(self, out, stream=None) -> None:
         call("prg_q4_dequantize_bf16", _s(stream), *self._wsb(), ptr(out), self.out_dim, self.in_dim)
 
+    # linear_q4.zig:197-214 (prompt path, MFMA QMM)
+    def encode_prefill_qmm(self, x, out, token_count: int, stream=None) -> None:
+        call("prg_q4_qmm_bf16", _s(stream), ptr(x), *self._wsb(), ptr(out), token_count, self.out_dim,
+             self.in_dim)
+
+    # linear_q4.zig:216-233
+    def encode_prefill_qmm_residual_add(self, x, residual, out, token_count: int, stream=None) -> None:
+        call("prg_q4_qmm_residual_add_bf16", _s(stream), ptr(x), *self._wsb(), ptr(residual), ptr(out),
+             token_count, self.out_dim, self.in_dim)
+
 
 # block_mlp.zig:313-345 / :347-383
 def gate_up_silu(gate: Q4Linear, up: Q4Linear, x, out, stream=None) -> None:
@@ -78,6 +88,12 @@ def gate_up_silu(gate: Q4Linear, up: Q4Linear, x, out, stream=None) -> None:
 def gate_up_silu2(gate: Q4Linear, up: Q4Linear, x0, x1, o0, o1, stream=None) -> None:
     call("prg_q4_gemv_silu_gate2_bf16", _s(stream), ptr(x0), ptr(x1), *gate._wsb(), *up._wsb(), ptr(o0),
          ptr(o1), gate.out_dim, gate.in_dim)
+
+
+# block_mlp.zig:155-214 (prompt path): gate/up QMMs + silu_mul_pair in one pass
+def prefill_gate_up_silu(gate: Q4Linear, up: Q4Linear, x, out, token_count: int, stream=None) -> None:
+    call("prg_q4_qmm_silu_gate_bf16", _s(stream), ptr(x), *gate._wsb(), *up._wsb(), ptr(out), token_count,
+         gate.out_dim, gate.in_dim)
 
 
 # argmax.zig:14-35
@@ -139,3 +155,40 @@ def attn_decode(q, key_cache, value_cache, gate, out, partials, stride: int, seq
                 scale: float = 1.0 / 16.0, stream=None) -> None:
     call("prg_attn_decode_bf16", _s(stream), ptr(q), ptr(key_cache), ptr(value_cache), ptr(gate), ptr(out),
          ptr(partials), stride, seq_len, scale)
+
+
+# ------------------------------------------------------------- prefill ops
+def attn_prefill_prepare(packed_q, q_w, k_in, k_w, v_in, q_out, gate_out, key_cache, value_cache,
+                         token_count: int, start_rope: int, start_cache: int, stride: int, stream=None) -> None:
+    call("prg_attn_prefill_prepare_bf16", _s(stream), ptr(packed_q), ptr(q_w), ptr(k_in), ptr(k_w), ptr(v_in),
+         ptr(q_out), ptr(gate_out), ptr(key_cache), ptr(value_cache), token_count, start_rope, start_cache, stride)
+
+
+def attn_prefill_scores_bytes(token_count: int, prefix: int) -> int:
+    from ._lib import lib
+
+    return int(lib.prg_attn_prefill_scores_bytes(token_count, prefix))
+
+
+def attn_prefill(q, key_cache, value_cache, gate, out, scores, token_count: int, prefix: int, stride: int,
+                 scale: float = 1.0 / 16.0, stream=None) -> None:
+    call("prg_attn_prefill_bf16", _s(stream), ptr(q), ptr(key_cache), ptr(value_cache), ptr(gate), ptr(out),
+         ptr(scores), token_count, prefix, stride, scale)
+
+
+def conv1d_silu_prefill(state, qkv, w, out, token_count: int, has_previous_state: bool = True,
+                        stream=None) -> None:
+    call("prg_conv1d_silu_prefill_bf16", _s(stream), ptr(state), ptr(qkv), ptr(w), ptr(out), token_count, 8192,
+         4, int(bool(has_previous_state)))
+
+
+def gated_delta_prefill_prepare(conv_out, a, b, A_log, dt_bias, q_out, k_out, g_out, beta_out,
+                                token_count: int, stream=None) -> None:
+    call("prg_gated_delta_prefill_prepare_bf16", _s(stream), ptr(conv_out), ptr(a), ptr(b), ptr(A_log),
+         ptr(dt_bias), ptr(q_out), ptr(k_out), ptr(g_out), ptr(beta_out), token_count)
+
+
+def gated_delta_prefill(state, q, k, conv_out, g, beta, y, token_count: int, has_previous_state: bool = True,
+                        stream=None) -> None:
+    call("prg_gated_delta_prefill_bf16", _s(stream), ptr(state), ptr(q), ptr(k), ptr(conv_out), ptr(g),
+         ptr(beta), ptr(y), token_count, int(bool(has_previous_state)))

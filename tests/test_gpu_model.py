@@ -115,6 +115,83 @@ def test_step_api_errors(small):
     assert e.value.code == 5
 
 
+def _state_close(st, om, upto, what):
+    for i, L in enumerate(om.layers):
+        if L["linear"]:
+            g = st.read(f"layers.{i}.recur", np.float32).reshape(32, 128, 128).astype(np.float64)
+            r = om.state[i]["recur"].astype(np.float64)
+            rel = np.linalg.norm(g - r) / np.linalg.norm(r)
+            print(f"{what}: layer {i} recur rel-frobenius {rel:.2e}")
+            assert rel <= 3e-2, f"{what}: layer {i} recur rel {rel}"
+            gc = st.read(f"layers.{i}.conv", np.float32).reshape(3, 8192).astype(np.float64)
+            rc = om.state[i]["conv"].astype(np.float64)
+            assert np.linalg.norm(gc - rc) <= 3e-2 * np.linalg.norm(rc)
+        else:
+            gk = st.read(f"layers.{i}.cache_k", np.uint16).reshape(4, st.stride, 256)[:, :upto]
+            assert_bf16_close(gk, om.state[i]["k"][:, :upto], rtol=5e-2, atol_frac=5e-2, what=f"{what} layer {i} K")
+
+
+def test_prefill_matches_oracle_prefill(small):
+    """Layer-major prompt ingestion (MFMA QMMs, prefill attention, GDN prefill)
+    vs the oracle's prefill composition (decoder_layer.zig:644-760): the
+    first generated token, then 8 decode steps continuing from the prefilled
+    state, each against the oracle teacher-forced on the GPU's tokens."""
+    m, st, om = small
+    rng = np.random.default_rng(3)
+    prompt = rng.integers(0, SMALL["vocab"], size=40).astype(np.uint32)
+    first = st.prefill(prompt)
+    om.reset()
+    ref_first, lg = om.prefill(prompt, want_logits=True)
+    _compare([first], [ref_first], [lg], min_checked=0.0, what="prefill first token")
+    _state_close(st, om, 40, "after prefill")
+    toks, _ = st.decode(8)
+    seq = np.concatenate([[first], toks[:-1]])
+    preds, logits = [], []
+    for j, t in enumerate(seq):
+        tok, lgj = om.step(int(t), 40 + j, want_logits=True)
+        preds.append(tok)
+        logits.append(lgj)
+    _compare(toks, np.array(preds, np.uint32), logits, what="decode after prefill")
+
+
+def test_chunked_prefill_is_bitwise_identical(gpu, monkeypatch):
+    """Chunks of 16 tokens (second and later chunks attend to the cached
+    prefix and continue the GDN/conv states) give the same token and the same
+    states, bit for bit, as one 40-token chunk."""
+    from peregrine_amd.model import DeviceModel, ModelConfig, ModelState
+
+    m = DeviceModel(ModelConfig(**SMALL), seed=5)
+    rng = np.random.default_rng(4)
+    prompt = rng.integers(0, SMALL["vocab"], size=40).astype(np.uint32)
+    whole = ModelState(m, max_seq=96)
+    t_whole = whole.prefill(prompt)
+    monkeypatch.setenv("PEREGRINE_PREFILL_CHUNK", "16")
+    chunked = ModelState(m, max_seq=96)
+    t_chunked = chunked.prefill(prompt)
+    assert t_whole == t_chunked
+    for i in range(SMALL["num_layers"]):
+        names = ["recur", "conv"] if ModelConfig(**SMALL).is_linear(i) else ["cache_k", "cache_v"]
+        for n in names:
+            np.testing.assert_array_equal(whole.read(f"layers.{i}.{n}", np.uint16),
+                                          chunked.read(f"layers.{i}.{n}", np.uint16), err_msg=f"layer {i} {n}")
+    np.testing.assert_array_equal(whole.decode(6)[0], chunked.decode(6)[0])
+    whole.close()
+    chunked.close()
+    m.close()
+
+
+def test_prefill_errors(small):
+    from peregrine_amd._lib import PrgError
+
+    m, st, om = small
+    with pytest.raises(PrgError) as e:
+        st.prefill(np.array([1, SMALL["vocab"]], np.uint32))
+    assert e.value.code == 6
+    with pytest.raises(PrgError) as e:
+        st.prefill(np.zeros(97, np.uint32))
+    assert e.value.code == 5
+
+
 def test_qwen35_9b_shape_first_steps(gpu):
     """The full 9B shape (32 layers, hidden 4096, FFN 12288, vocab 248320):
     4 teacher-forced steps against the oracle."""
@@ -130,5 +207,10 @@ def test_qwen35_9b_shape_first_steps(gpu):
     om = OracleModel(m, 64)
     ref, logits = om.teacher_forced(prompt, want_logits=True)
     _compare(preds, ref, logits, min_checked=0.5, what="9B shape")
+    # The same 4 tokens through the prompt path vs the oracle's prefill.
+    first = st.prefill(prompt)
+    om.reset()
+    ref_first, lg = om.prefill(prompt, want_logits=True)
+    _compare([first], [ref_first], [lg], min_checked=0.0, what="9B shape prefill")
     st.close()
     m.close()
