@@ -81,6 +81,22 @@ def dominant_kernel_roofline(iters: int = 100) -> dict:
             "algo_bytes_per_launch": int(algo), "launches": iters, "ring_copies": copies}
 
 
+def prefill_flops(cfg, T: int) -> float:
+    """Matmul FLOPs of one T-token prompt from an empty cache: 2 per weight per
+    token over every Q4 projection (embedding gather and lm_head excluded; the
+    lm_head runs on the last token only), plus causal attention (QK^T and PV,
+    2 * 2 * T*(T+1)/2 * 256 per q head)."""
+    h, f = cfg.hidden, cfg.intermediate
+    gdn = (8192 + 4096 + 32 + 32) * h + h * 4096
+    att = (8192 + 1024 + 1024) * h + h * 4096
+    mlp = 3 * f * h
+    n_att = sum(1 for i in range(cfg.num_layers) if not cfg.is_linear(i))
+    n_gdn = cfg.num_layers - n_att
+    weights = n_gdn * gdn + n_att * att + cfg.num_layers * mlp
+    attn = n_att * 16 * 2 * 2 * (T * (T + 1) / 2) * 256
+    return 2.0 * weights * T + attn + 2.0 * cfg.vocab * h
+
+
 def gemv_sweep() -> list[dict]:
     from peregrine_amd.gemv_bench import sweep
 
@@ -160,8 +176,17 @@ def main() -> int:
     rng = np.random.default_rng(0)
     prompt = rng.integers(0, QWEN35_9B.vocab, size=PROMPT_TOKENS).astype(np.uint32)
     t0 = time.time()
+    st.prefill(prompt)  # first call also allocates the prompt-path workspace
+    cold_s = time.time() - t0
+    t0 = time.time()
     first = st.prefill(prompt)
-    log(f"[bench] prompt ingest {PROMPT_TOKENS} tokens {time.time() - t0:.2f}s, first token {first}")
+    prefill_s = time.time() - t0
+    prefill = {"tokens": PROMPT_TOKENS, "ms": round(prefill_s * 1e3, 2),
+               "tok_s": round(PROMPT_TOKENS / prefill_s, 1),
+               "tflops": round(prefill_flops(QWEN35_9B, PROMPT_TOKENS) / prefill_s / 1e12, 2),
+               "first_call_ms": round(cold_s * 1e3, 2)}
+    log(f"[bench] prompt ingest {PROMPT_TOKENS} tokens {prefill_s * 1e3:.1f} ms "
+        f"({prefill['tok_s']} tok/s, {prefill['tflops']} TFLOP/s), first token {first}")
     if a.warmup:
         st.decode(a.warmup)
     device.synchronize()
@@ -194,6 +219,7 @@ def main() -> int:
                    "execution": "eager launches" if a.eager else "one HIP graph replay per token"},
         "roofline": roof,
         "cpu_baseline": cpu,
+        "prefill": prefill,
         **extra,
     }
     model.close()

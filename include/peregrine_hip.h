@@ -349,13 +349,14 @@ int prg_conv1d_silu_prefill_bf16(void *stream, float *state, const uint16_t *qkv
                                  uint32_t kernel_size, uint32_t has_previous_state);
 
 /* f32 q/k [T, 16, 128] (l2-normed; q also times rsqrt(128)) from conv_out
- * [T, 8192], and gates g/beta f32 [T, 32] from a, b [T, 32]. Replaces
+ * [T, 8192], and gates g/beta f32 [T, 32] from a, b [T, 32]. kq_out (may be
+ * NULL) receives k.q per (token, k-head), f32 [T, 16]. Replaces
  * qk_l2norm_prefill_bf16 + gating_many_bf16 (shaders/gated_norm.metal:191-268),
  * host block_linear.zig:392-434. */
 int prg_gated_delta_prefill_prepare_bf16(void *stream, const uint16_t *conv_out, const uint16_t *a,
                                          const uint16_t *b, const float *A_log, const uint16_t *dt_bias,
                                          float *q_out, float *k_out, float *g_out, float *beta_out,
-                                         uint32_t token_count);
+                                         float *kq_out, uint32_t token_count);
 
 /* Delta-rule recurrence over T tokens with prepared q/k/gates; state f32
  * [32, 128, 128] in place; y bf16 [T, 4096]. Replaces

@@ -69,7 +69,16 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const GemmArgs g) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const uint32_t tiles_m = (g.M + kBM - 1) / kBM;
-  const uint32_t m0 = (blockIdx.x % tiles_m) * kBM, n0 = (blockIdx.x / tiles_m) * kTileN;
+  const uint32_t tn = blockIdx.x / tiles_m;
+  uint32_t seg = 0;  // Q4 weight segment of this output tile
+  if constexpr (Q4 && !kPair) {
+#pragma unroll
+    for (int i = 1; i < kGemmMaxSegs; ++i)
+      if (i < static_cast<int>(g.nq) && tn >= g.q[i].tile0) seg = i;
+  }
+  const uint32_t m0 = (blockIdx.x % tiles_m) * kBM;
+  const uint32_t n0 = (tn - (Q4 ? g.q[seg].tile0 : 0)) * kTileN;
+  const uint32_t N = Q4 ? g.q[seg].n : g.N;
   const uint64_t z = blockIdx.z;
   const uint32_t K = g.K;
 
@@ -92,18 +101,18 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const GemmArgs g) {
   uint4 rw = make_uint4(0, 0, 0, 0);
   uint16_t rs = 0, rbias = 0;
   if constexpr (Q4) {
-    const int mat = kPair ? (q_row >> 6) : 0;
+    const GemmQ4& Q = g.q[kPair ? (q_row >> 6) : seg];
     const uint32_t n = n0 + (kPair ? (q_row & 63) : q_row);
-    if (n < g.N) {
-      q_w = g.qw[mat] + static_cast<uint64_t>(n) * (K / 8) + q_half * 4;
-      q_s = g.qs[mat] + static_cast<uint64_t>(n) * (K / 64);
-      q_b = g.qb[mat] + static_cast<uint64_t>(n) * (K / 64);
+    if (n < N) {
+      q_w = Q.w + static_cast<uint64_t>(n) * (K / 8) + q_half * 4;
+      q_s = Q.s + static_cast<uint64_t>(n) * (K / 64);
+      q_b = Q.b + static_cast<uint64_t>(n) * (K / 64);
     }
   } else {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint32_t n = n0 + ld_row + 32 * i;
-      b_row[i] = n < g.N ? g.b + z * g.b_z + static_cast<uint64_t>(n) * g.ldb : nullptr;
+      b_row[i] = n < N ? g.b + z * g.b_z + static_cast<uint64_t>(n) * g.ldb : nullptr;
     }
   }
 
@@ -169,8 +178,11 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const GemmArgs g) {
 
   // Epilogue: lane holds rows 4*(lane/16) + r, column lane%16 of each block.
   const int crow = 4 * (lane >> 4), ccol = lane & 15;
-  uint16_t* C = g.c + z * g.c_z;
-  const uint16_t* R = g.res ? g.res + z * g.c_z : nullptr;
+  // Q4: segment output [M, n] row-major; bf16: two-level rows, z offset.
+  uint16_t* C = Q4 ? g.q[seg].c : g.c + z * g.c_z;
+  const uint16_t* R = g.res ? (Q4 ? g.res : g.res + z * g.c_z) : nullptr;
+  const uint64_t ldc = Q4 ? N : g.ldc, ldc_hi = Q4 ? 0 : g.ldc_hi;
+  const uint32_t c_group = Q4 ? 0 : g.c_group;
   if constexpr (kPair) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -178,11 +190,11 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const GemmArgs g) {
       for (int r = 0; r < 4; ++r) {
         const uint32_t m = m0 + wm * 64 + 16 * i + crow + r;
         if (m >= g.M) continue;
-        uint16_t* out = const_cast<uint16_t*>(row_ptr(C, g.ldc, g.ldc_hi, g.c_group, m));
+        uint16_t* out = const_cast<uint16_t*>(row_ptr(C, ldc, ldc_hi, c_group, m));
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
           const uint32_t n = n0 + wn * 32 + 16 * j + ccol;
-          if (n >= g.N) continue;
+          if (n >= N) continue;
           const float gate = round_bf(acc[i][j][r]), up = round_bf(acc[i][j + 2][r]);
           out[n] = f2bf(silu(gate) * up);
         }
@@ -194,12 +206,12 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const GemmArgs g) {
       for (int r = 0; r < 4; ++r) {
         const uint32_t m = m0 + wm * 64 + 16 * i + crow + r;
         if (m >= g.M) continue;
-        uint16_t* out = const_cast<uint16_t*>(row_ptr(C, g.ldc, g.ldc_hi, g.c_group, m));
-        const uint16_t* rin = R ? row_ptr(R, g.ldc, g.ldc_hi, g.c_group, m) : nullptr;
+        uint16_t* out = const_cast<uint16_t*>(row_ptr(C, ldc, ldc_hi, c_group, m));
+        const uint16_t* rin = R ? row_ptr(R, ldc, ldc_hi, c_group, m) : nullptr;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const uint32_t n = n0 + wn * 64 + 16 * j + ccol;
-          if (n >= g.N) continue;
+          if (n >= N) continue;
           const float v = acc[i][j][r];
           if constexpr (EPI == kGemmStore) {
             out[n] = f2bf(v);
@@ -216,14 +228,17 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const GemmArgs g) {
 template <bool Q4, int EPI>
 int launch_t(hipStream_t s, const GemmArgs& g, uint32_t batch, const char* name) {
   constexpr uint32_t kTileN = (EPI == kGemmSiluPair) ? kBN / 2 : kBN;
-  const uint32_t tiles = ((g.M + kBM - 1) / kBM) * ((g.N + kTileN - 1) / kTileN);
+  uint32_t tiles_n = (g.N + kTileN - 1) / kTileN;
+  if (Q4) tiles_n = (EPI == kGemmSiluPair) ? (g.q[0].n + kTileN - 1) / kTileN : g.q[g.nq - 1].tile0 +
+                    (g.q[g.nq - 1].n + kTileN - 1) / kTileN;
+  const uint32_t tiles = ((g.M + kBM - 1) / kBM) * tiles_n;
   hipLaunchKernelGGL((gemm_kernel<Q4, EPI>), dim3(tiles, 1, batch), dim3(kGemmThreads), 0, s, g);
   PRG_CHECK_LAUNCH(name);
   return PRG_OK;
 }
 
 int check_common(const GemmArgs& g, int epi, const char* name) {
-  PRG_CHECK_ARG(g.a && g.c, "%s: null A or C", name);
+  PRG_CHECK_ARG(g.a, "%s: null A", name);
   PRG_CHECK_ARG(g.M > 0 && g.N > 0 && g.K > 0, "%s: empty problem M=%u N=%u K=%u", name, g.M, g.N, g.K);
   PRG_CHECK_ARG(g.lda % 8 == 0 && g.lda_hi % 8 == 0 && g.a_z % 8 == 0,
                 "%s: A row strides must be multiples of 8 elements", name);
@@ -239,13 +254,25 @@ int check_common(const GemmArgs& g, int epi, const char* name) {
 
 namespace prg {
 
-int launch_gemm_q4(hipStream_t s, const GemmArgs& g, int epi, const char* name) {
+int launch_gemm_q4(hipStream_t s, GemmArgs g, int epi, const char* name) {
+  PRG_CHECK_ARG(g.nq >= 1 && g.nq <= kGemmMaxSegs, "%s: %u weight segments", name, g.nq);
+  PRG_CHECK_ARG(epi != kGemmSiluPair || g.nq == 2, "%s: the SiLU pair takes exactly two weights", name);
+  PRG_CHECK_ARG(epi != kGemmResidual || g.nq == 1, "%s: the residual epilogue takes one weight", name);
+  PRG_CHECK_ARG(epi != kGemmSigmoidGate, "%s: the sigmoid gate epilogue takes bf16 B", name);
+  uint32_t tile = 0;
+  g.N = 0;
+  for (uint32_t i = 0; i < g.nq; ++i) {
+    GemmQ4& q = g.q[i];
+    PRG_CHECK_ARG(q.w && q.s && q.b && q.n > 0, "%s: Q4 segment %u incomplete", name, i);
+    PRG_CHECK_ARG(reinterpret_cast<uintptr_t>(q.w) % 16 == 0, "%s: Q4 weight must be 16-byte aligned", name);
+    PRG_CHECK_ARG(epi == kGemmSiluPair ? (i == 1 || q.c) : q.c != nullptr, "%s: null output", name);
+    PRG_CHECK_ARG(epi != kGemmSiluPair || q.n == g.q[0].n, "%s: gate and up differ in size", name);
+    q.tile0 = tile;
+    tile += (q.n + kBN - 1) / kBN;
+    g.N += q.n;
+  }
   if (int rc = check_common(g, epi, name)) return rc;
   PRG_CHECK_ARG(g.K % 64 == 0, "%s: in_dim %u must be a multiple of 64", name, g.K);
-  PRG_CHECK_ARG(g.qw[0] && g.qs[0] && g.qb[0], "%s: null Q4 weight", name);
-  PRG_CHECK_ARG(epi != kGemmSiluPair || (g.qw[1] && g.qs[1] && g.qb[1]), "%s: SiLU pair needs two weights", name);
-  PRG_CHECK_ARG(reinterpret_cast<uintptr_t>(g.qw[0]) % 16 == 0 && (epi != kGemmSiluPair ||
-                reinterpret_cast<uintptr_t>(g.qw[1]) % 16 == 0), "%s: Q4 weight must be 16-byte aligned", name);
   switch (epi) {
     case kGemmStore: return launch_t<true, kGemmStore>(s, g, 1, name);
     case kGemmResidual: return launch_t<true, kGemmResidual>(s, g, 1, name);
@@ -256,6 +283,7 @@ int launch_gemm_q4(hipStream_t s, const GemmArgs& g, int epi, const char* name) 
 
 int launch_gemm_bf16(hipStream_t s, const GemmArgs& g, int epi, uint32_t batch, const char* name) {
   if (int rc = check_common(g, epi, name)) return rc;
+  PRG_CHECK_ARG(g.c, "%s: null C", name);
   PRG_CHECK_ARG(g.b, "%s: null B", name);
   PRG_CHECK_ARG(epi != kGemmSiluPair, "%s: the SiLU pair epilogue takes Q4 weights", name);
   PRG_CHECK_ARG(g.ldb % 8 == 0 && g.b_z % 8 == 0 && reinterpret_cast<uintptr_t>(g.b) % 16 == 0,
@@ -279,13 +307,9 @@ int prg_q4_qmm_bf16(void* stream, const uint16_t* x, const uint32_t* w, const ui
   GemmArgs g;
   g.a = x;
   g.lda = in_dim;
-  g.qw[0] = w;
-  g.qs[0] = scales;
-  g.qb[0] = biases;
-  g.c = out;
-  g.ldc = out_dim;
+  g.q[0] = GemmQ4{w, scales, biases, out, out_dim, 0};
+  g.nq = 1;
   g.M = token_count;
-  g.N = out_dim;
   g.K = in_dim;
   return launch_gemm_q4(as_stream(stream), g, kGemmStore, "prg_q4_qmm_bf16");
 }
@@ -298,14 +322,10 @@ int prg_q4_qmm_residual_add_bf16(void* stream, const uint16_t* x, const uint32_t
   GemmArgs g;
   g.a = x;
   g.lda = in_dim;
-  g.qw[0] = w;
-  g.qs[0] = scales;
-  g.qb[0] = biases;
-  g.c = out;
+  g.q[0] = GemmQ4{w, scales, biases, out, out_dim, 0};
+  g.nq = 1;
   g.res = residual;
-  g.ldc = out_dim;
   g.M = token_count;
-  g.N = out_dim;
   g.K = in_dim;
   return launch_gemm_q4(as_stream(stream), g, kGemmResidual, "prg_q4_qmm_residual_add_bf16");
 }
@@ -320,16 +340,10 @@ int prg_q4_qmm_silu_gate_bf16(void* stream, const uint16_t* x, const uint32_t* g
   GemmArgs g;
   g.a = x;
   g.lda = in_dim;
-  g.qw[0] = gate_w;
-  g.qs[0] = gate_scales;
-  g.qb[0] = gate_biases;
-  g.qw[1] = up_w;
-  g.qs[1] = up_scales;
-  g.qb[1] = up_biases;
-  g.c = out;
-  g.ldc = out_dim;
+  g.q[0] = GemmQ4{gate_w, gate_scales, gate_biases, out, out_dim, 0};
+  g.q[1] = GemmQ4{up_w, up_scales, up_biases, nullptr, out_dim, 0};
+  g.nq = 2;
   g.M = token_count;
-  g.N = out_dim;
   g.K = in_dim;
   return launch_gemm_q4(as_stream(stream), g, kGemmSiluPair, "prg_q4_qmm_silu_gate_bf16");
 }

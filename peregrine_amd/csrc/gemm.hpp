@@ -33,6 +33,17 @@ enum GemmEpi : int {
                          //     elementwise.metal:88-99); `res` points at the gate
 };
 
+constexpr int kGemmMaxSegs = 4;
+
+struct GemmQ4 {
+  const uint32_t* w = nullptr;  // u32 [n, K/8]
+  const uint16_t* s = nullptr;  // bf16 [n, K/64]
+  const uint16_t* b = nullptr;
+  uint16_t* c = nullptr;        // bf16 [M, n]
+  uint32_t n = 0;
+  uint32_t tile0 = 0;           // first output tile of the segment (set by the launcher)
+};
+
 struct GemmArgs {
   // A: bf16
   const uint16_t* a = nullptr;
@@ -41,12 +52,13 @@ struct GemmArgs {
   // B, bf16 mode: row n at b + n * ldb; columns k >= K read as zero
   const uint16_t* b = nullptr;
   uint64_t ldb = 0, b_z = 0;
-  // B, Q4 mode: weights u32 [N, K/8], scales/biases bf16 [N, K/64]. The SiLU
-  // pair epilogue takes gate in [0] and up in [1].
-  const uint32_t* qw[2] = {nullptr, nullptr};
-  const uint16_t* qs[2] = {nullptr, nullptr};
-  const uint16_t* qb[2] = {nullptr, nullptr};
-  // C (and the residual / gate input, same addressing)
+  // B, Q4 mode: up to 4 weight segments sharing A, each with its own output
+  // [M, n] (one launch for projections that read the same activations). The
+  // SiLU pair epilogue takes gate in q[0] and up in q[1] (same n, output
+  // q[0].c).
+  GemmQ4 q[kGemmMaxSegs];
+  uint32_t nq = 0;
+  // C (bf16 mode; and the residual / gate input, same addressing)
   uint16_t* c = nullptr;
   const uint16_t* res = nullptr;
   uint64_t ldc = 0, ldc_hi = 0, c_z = 0;
@@ -54,8 +66,9 @@ struct GemmArgs {
   uint32_t M = 0, N = 0, K = 0;
 };
 
-// Q4 weights. K % 64 == 0; A rows 16-byte aligned (lda % 8 == 0).
-int launch_gemm_q4(hipStream_t s, const GemmArgs& g, int epi, const char* name);
+// Q4 weights in g.q[0..nq). K % 64 == 0; A rows 16-byte aligned (lda % 8 == 0).
+// The residual epilogue reads g.res [M, q[0].n].
+int launch_gemm_q4(hipStream_t s, GemmArgs g, int epi, const char* name);
 // bf16 B, `batch` independent problems along grid.z (offsets a_z, b_z, c_z).
 int launch_gemm_bf16(hipStream_t s, const GemmArgs& g, int epi, uint32_t batch, const char* name);
 

@@ -33,6 +33,8 @@
 #include <string.h>
 
 #include <algorithm>
+#include <initializer_list>
+#include <utility>
 #include <map>
 #include <string>
 #include <vector>
@@ -170,7 +172,7 @@ struct PrefillWs {
   uint16_t *h0 = nullptr, *h1 = nullptr, *normed = nullptr, *attn = nullptr, *resid = nullptr, *inter = nullptr;
   uint16_t *qkv = nullptr, *conv_out = nullptr, *z = nullptr, *a = nullptr, *b = nullptr, *y = nullptr,
            *gated = nullptr;
-  float *qn = nullptr, *kn = nullptr, *g = nullptr, *beta = nullptr;  // f32
+  float *qn = nullptr, *kn = nullptr, *g = nullptr, *beta = nullptr, *kq = nullptr;  // f32
   uint16_t *qp = nullptr, *k = nullptr, *v = nullptr, *q = nullptr, *gate = nullptr, *ctx = nullptr,
            *scores = nullptr;
 };
@@ -532,6 +534,7 @@ int ensure_prefill_ws(PrgModelState* st) {
       {reinterpret_cast<void**>(&w.kn), f4 * R * kGdnKeyDim},
       {reinterpret_cast<void**>(&w.g), f4 * R * kGdnHv},
       {reinterpret_cast<void**>(&w.beta), f4 * R * kGdnHv},
+      {reinterpret_cast<void**>(&w.kq), f4 * R * kGdnHk},
       {reinterpret_cast<void**>(&w.qp), bf * R * 2 * kAttnQHeads * kAttnHeadDim},
       {reinterpret_cast<void**>(&w.k), bf * R * kAttnKvHeads * kAttnHeadDim},
       {reinterpret_cast<void**>(&w.v), bf * R * kAttnKvHeads * kAttnHeadDim},
@@ -569,21 +572,32 @@ int qmm(hipStream_t s, const uint16_t* x, const Q4Linear& l, uint16_t* out, uint
   GemmArgs g;
   g.a = x;
   g.lda = l.in_dim;
-  g.qw[0] = l.weight;
-  g.qs[0] = l.scales;
-  g.qb[0] = l.biases;
+  g.q[0] = GemmQ4{l.weight, l.scales, l.biases, out, l.out_dim, 0};
+  g.nq = 1;
   if (up) {
-    g.qw[1] = up->weight;
-    g.qs[1] = up->scales;
-    g.qb[1] = up->biases;
+    g.q[1] = GemmQ4{up->weight, up->scales, up->biases, nullptr, up->out_dim, 0};
+    g.nq = 2;
   }
-  g.c = out;
   g.res = res;
-  g.ldc = l.out_dim;
   g.M = T;
-  g.N = l.out_dim;
   g.K = l.in_dim;
   return launch_gemm_q4(s, g, epi, name);
+}
+
+// Several projections of the same activations in one launch (each keeps its
+// own output buffer); the reference encodes them one after another.
+int qmm_multi(hipStream_t s, const uint16_t* x, uint32_t K, uint32_t T, std::initializer_list<std::pair<const Q4Linear*, uint16_t*>> segs,
+              const char* name) {
+  GemmArgs g;
+  g.a = x;
+  g.lda = K;
+  for (const auto& sg : segs) {
+    const Q4Linear& l = *sg.first;
+    g.q[g.nq++] = GemmQ4{l.weight, l.scales, l.biases, sg.second, l.out_dim, 0};
+  }
+  g.M = T;
+  g.K = K;
+  return launch_gemm_q4(s, g, kGemmStore, name);
 }
 
 // DecoderLayer.prefillStepBf16 (decoder_layer.zig:644-760) for T tokens at
@@ -599,22 +613,24 @@ int prefill_layer(PrgModel* m, PrgModelState* st, uint32_t li, const uint16_t* x
   if (L.linear) {  // block_linear.zig:265-361
     const LinearAttentionBlock& b = L.lin;
     const uint32_t has_state = start != 0;  // decoder_layer.zig:635
-    if (int rc = qmm(s, w.normed, b.in_qkv, w.qkv, T, kGemmStore, nullptr, nullptr, "prefill.in_proj_qkv")) return rc;
-    if (int rc = qmm(s, w.normed, b.in_z, w.z, T, kGemmStore, nullptr, nullptr, "prefill.in_proj_z")) return rc;
-    if (int rc = qmm(s, w.normed, b.in_a, w.a, T, kGemmStore, nullptr, nullptr, "prefill.in_proj_a")) return rc;
-    if (int rc = qmm(s, w.normed, b.in_b, w.b, T, kGemmStore, nullptr, nullptr, "prefill.in_proj_b")) return rc;
-    if (int rc = launch_conv1d_prefill(s, ls.conv, w.qkv, b.conv_weight, w.conv_out, T, has_state)) return rc;
-    if (int rc = launch_gdn_prefill_prepare(s, w.conv_out, w.a, w.b, b.a_log, b.dt_bias, w.qn, w.kn, w.g, w.beta, T))
+    if (int rc = qmm_multi(s, w.normed, c.hidden, T,
+                           {{&b.in_qkv, w.qkv}, {&b.in_z, w.z}, {&b.in_a, w.a}, {&b.in_b, w.b}},
+                           "prefill.in_proj"))
       return rc;
-    if (int rc = launch_gdn_prefill(s, ls.recur, w.qn, w.kn, w.conv_out, w.g, w.beta, w.y, T, has_state)) return rc;
+    if (int rc = launch_conv1d_prefill(s, ls.conv, w.qkv, b.conv_weight, w.conv_out, T, has_state)) return rc;
+    if (int rc = launch_gdn_prefill_prepare(s, w.conv_out, w.a, w.b, b.a_log, b.dt_bias, w.qn, w.kn, w.g, w.beta,
+                                            w.kq, T))
+      return rc;
+    if (int rc = launch_gdn_prefill(s, ls.recur, w.qn, w.kn, w.conv_out, w.g, w.beta, w.kq, w.y, T, has_state))
+      return rc;
     if (int rc = prg_rmsnorm_gated_bf16(s, w.y, b.norm_weight, w.z, w.gated, kGdnDv, c.rms_eps, T * kGdnHv))
       return rc;
     if (int rc = qmm(s, w.gated, b.out_proj, w.attn, T, kGemmStore, nullptr, nullptr, "prefill.out_proj")) return rc;
   } else {  // block_attn.zig:361-498
     const FullAttentionBlock& b = L.full;
-    if (int rc = qmm(s, w.normed, b.q_proj, w.qp, T, kGemmStore, nullptr, nullptr, "prefill.q_proj")) return rc;
-    if (int rc = qmm(s, w.normed, b.k_proj, w.k, T, kGemmStore, nullptr, nullptr, "prefill.k_proj")) return rc;
-    if (int rc = qmm(s, w.normed, b.v_proj, w.v, T, kGemmStore, nullptr, nullptr, "prefill.v_proj")) return rc;
+    if (int rc = qmm_multi(s, w.normed, c.hidden, T, {{&b.q_proj, w.qp}, {&b.k_proj, w.k}, {&b.v_proj, w.v}},
+                           "prefill.qkv_proj"))
+      return rc;
     if (int rc = launch_attn_prefill_prepare(s, w.qp, b.q_norm, w.k, b.k_norm, w.v, w.q, w.gate, ls.cache_k,
                                              ls.cache_v, T, start, start, st->stride))
       return rc;

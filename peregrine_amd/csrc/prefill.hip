@@ -191,12 +191,13 @@ __global__ void conv1d_prefill_state_kernel(float* __restrict__ state, const uin
   }
 }
 
-// Block (t, hk), 128 threads: f32 l2-normed q (x rsqrt(Dk)) and k of k-head hk;
-// threads 0, 1 also produce the gates of v-heads 2hk, 2hk+1.
+// Block (t, hk), 128 threads: f32 l2-normed q (x rsqrt(Dk)) and k of k-head hk
+// and their dot product kq; threads 0, 1 also produce the gates of v-heads
+// 2hk, 2hk+1.
 __global__ __launch_bounds__(kQkNormThreads) void gdn_prefill_prepare_kernel(
     const uint16_t* __restrict__ conv_out, const uint16_t* __restrict__ a, const uint16_t* __restrict__ b,
     const float* __restrict__ A_log, const uint16_t* __restrict__ dt_bias, float* __restrict__ qn,
-    float* __restrict__ kn, float* __restrict__ g, float* __restrict__ beta) {
+    float* __restrict__ kn, float* __restrict__ g, float* __restrict__ beta, float* __restrict__ kq) {
   __shared__ float sh[kQkNormThreads];
   const uint32_t t = blockIdx.x / kGdnHk, hk = blockIdx.x % kGdnHk, d = threadIdx.x;
   const uint16_t* row = conv_out + static_cast<size_t>(t) * kGdnConvDim;
@@ -206,8 +207,12 @@ __global__ __launch_bounds__(kQkNormThreads) void gdn_prefill_prepare_kernel(
   const float q_inv = 1.0f / sqrtf(qs + 1.0e-6f), k_inv = 1.0f / sqrtf(ks + 1.0e-6f);
   const float q_scale = 1.0f / sqrtf(static_cast<float>(kGdnDk));
   const size_t o = (static_cast<size_t>(t) * kGdnHk + hk) * kGdnDk + d;
-  qn[o] = __fmul_rn(__fmul_rn(qv, q_inv), q_scale);
-  kn[o] = __fmul_rn(kv, k_inv);
+  const float qo = __fmul_rn(__fmul_rn(qv, q_inv), q_scale), ko = __fmul_rn(kv, k_inv);
+  qn[o] = qo;
+  kn[o] = ko;
+  // k.q of the normalised pair: shared by every state row of the two v-heads.
+  const float kqs = tree_sum<kQkNormThreads>(__fmul_rn(ko, qo), sh);
+  if (kq && d == 0) kq[static_cast<size_t>(t) * kGdnHk + hk] = kqs;
   if (d < kGdnHv / kGdnHk) {
     const uint32_t hv = hk * (kGdnHv / kGdnHk) + d;
     const size_t go = static_cast<size_t>(t) * kGdnHv + hv;
@@ -223,22 +228,33 @@ __global__ __launch_bounds__(kQkNormThreads) void gdn_prefill_prepare_kernel(
 // registers for the whole prompt). Per token:
 //   kq = k.q; d = S*decay; kv = d.k; ob = d.q; delta = (v - kv)*beta;
 //   S = d + k*delta; y = bf16(ob + delta*kq)
-// The next token's q, k, gates and v are loaded while the current one runs.
+// The per-token inputs (q, k of the k-head, gates, v of the block's rows) are
+// staged through LDS in chunks of kGdnChunk tokens, double-buffered: the
+// next chunk's global loads are in flight while the current chunk runs, so the
+// sequential loop only waits on LDS.
 constexpr int kGdnPRowsPerBlock = 16;
+constexpr int kGdnChunk = 32;
 
+template <bool PRE_KQ>
 __global__ __launch_bounds__(256) void gdn_prefill_kernel(float* __restrict__ state, const float* __restrict__ qn,
                                                           const float* __restrict__ kn,
                                                           const uint16_t* __restrict__ conv_out,
                                                           const float* __restrict__ g,
                                                           const float* __restrict__ beta,
+                                                          const float* __restrict__ kqv,
                                                           uint16_t* __restrict__ y, uint32_t T,
                                                           uint32_t has_state) {
+  __shared__ float4 sq[2][kGdnChunk][kGdnDk / 4];
+  __shared__ float4 sk[2][kGdnChunk][kGdnDk / 4];
+  __shared__ float sg[2][kGdnChunk], sb[2][kGdnChunk], skq[2][kGdnChunk];
+  __shared__ float sv[2][kGdnChunk][kGdnPRowsPerBlock];
   constexpr uint32_t blocks_per_head = kGdnDv / kGdnPRowsPerBlock;
+  const uint32_t tid = threadIdx.x;
   const uint32_t hv = blockIdx.x / blocks_per_head;
-  const uint32_t row = (blockIdx.x % blocks_per_head) * kGdnPRowsPerBlock + (threadIdx.x >> 4);
-  const uint32_t j = threadIdx.x & 15;
+  const uint32_t row0 = (blockIdx.x % blocks_per_head) * kGdnPRowsPerBlock;
+  const uint32_t rb = tid >> 4, j = tid & 15;  // row in block, lane in DPP row
   const uint32_t hk = hv / (kGdnHv / kGdnHk);
-  float4* srow = reinterpret_cast<float4*>(state + (static_cast<size_t>(hv) * kGdnDv + row) * kGdnDk + 8 * j);
+  float4* srow = reinterpret_cast<float4*>(state + (static_cast<size_t>(hv) * kGdnDv + row0 + rb) * kGdnDk + 8 * j);
   float S[8];
   {
     const float4 s0 = has_state ? srow[0] : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -246,41 +262,91 @@ __global__ __launch_bounds__(256) void gdn_prefill_kernel(float* __restrict__ st
     S[0] = s0.x; S[1] = s0.y; S[2] = s0.z; S[3] = s0.w;
     S[4] = s1.x; S[5] = s1.y; S[6] = s1.z; S[7] = s1.w;
   }
-  const float4* qb = reinterpret_cast<const float4*>(qn + hk * kGdnDk + 8 * j);
-  const float4* kb = reinterpret_cast<const float4*>(kn + hk * kGdnDk + 8 * j);
-  constexpr size_t qk_step = kGdnKeyDim / 4;  // float4 per token
-  const uint16_t* vb = conv_out + 2 * kGdnKeyDim + hv * kGdnDv + row;
-  uint16_t* yb = y + hv * kGdnDv + row;
+  // Chunk loader: q/k 32 tokens x 32 float4 = 4 float4 per thread each;
+  // v 32 tokens x 16 rows = 2 per thread; gates by threads 0..31.
+  const float4* q4 = reinterpret_cast<const float4*>(qn) + hk * (kGdnDk / 4);
+  const float4* k4 = reinterpret_cast<const float4*>(kn) + hk * (kGdnDk / 4);
+  constexpr uint32_t qk_step = kGdnKeyDim / 4;  // float4 per token
+  float4 rq[4], rk[4];
+  float rv[2], rg = 0.f, rbt = 0.f, rkq = 0.f;
+  auto load = [&](uint32_t c0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t idx = tid + 256 * i, t = c0 + idx / 32, f = idx % 32;
+      rq[i] = t < T ? q4[static_cast<size_t>(t) * qk_step + f] : make_float4(0.f, 0.f, 0.f, 0.f);
+      rk[i] = t < T ? k4[static_cast<size_t>(t) * qk_step + f] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint32_t idx = tid + 256 * i, t = c0 + idx / 16, r = idx % 16;
+      rv[i] = t < T ? bf2f(conv_out[static_cast<size_t>(t) * kGdnConvDim + 2 * kGdnKeyDim + hv * kGdnDv + row0 + r])
+                    : 0.f;
+    }
+    if (tid < kGdnChunk && c0 + tid < T) {
+      rg = g[static_cast<size_t>(c0 + tid) * kGdnHv + hv];
+      rbt = beta[static_cast<size_t>(c0 + tid) * kGdnHv + hv];
+      if constexpr (PRE_KQ) rkq = kqv[static_cast<size_t>(c0 + tid) * kGdnHk + hk];
+    }
+  };
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t idx = tid + 256 * i;
+      sq[buf][idx / 32][idx % 32] = rq[i];
+      sk[buf][idx / 32][idx % 32] = rk[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint32_t idx = tid + 256 * i;
+      sv[buf][idx / 16][idx % 16] = rv[i];
+    }
+    if (tid < kGdnChunk) {
+      sg[buf][tid] = rg;
+      sb[buf][tid] = rbt;
+      skq[buf][tid] = rkq;
+    }
+  };
 
-  float4 q0 = qb[0], q1 = qb[1], k0 = kb[0], k1 = kb[1];
-  float gd = g[hv], bt = beta[hv];
-  uint16_t vv = vb[0];
-  for (uint32_t t = 0; t < T; ++t) {
-    const float q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-    const float k[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
-    const float decay = gd, bet = bt, v = bf2f(vv);
-    if (t + 1 < T) {
-      const size_t n = static_cast<size_t>(t + 1);
-      q0 = qb[n * qk_step]; q1 = qb[n * qk_step + 1];
-      k0 = kb[n * qk_step]; k1 = kb[n * qk_step + 1];
-      gd = g[n * kGdnHv + hv];
-      bt = beta[n * kGdnHv + hv];
-      vv = vb[n * kGdnConvDim];
-    }
-    float kq = 0.f, kvp = 0.f, obp = 0.f, d[8];
+  uint16_t* yb = y + hv * kGdnDv + row0 + rb;
+  load(0);
+  store(0);
+  __syncthreads();
+  int buf = 0;
+  for (uint32_t c0 = 0; c0 < T; c0 += kGdnChunk, buf ^= 1) {
+    const bool more = c0 + kGdnChunk < T;
+    if (more) load(c0 + kGdnChunk);
+    const uint32_t n = min(static_cast<uint32_t>(kGdnChunk), T - c0);
+    // Operands of token tt are read from LDS one step ahead.
+    float4 qa = sq[buf][0][2 * j], qc = sq[buf][0][2 * j + 1];
+    float4 ka = sk[buf][0][2 * j], kc = sk[buf][0][2 * j + 1];
+    float decay = sg[buf][0], bet = sb[buf][0], kq = skq[buf][0], v = sv[buf][0][rb];
+    for (uint32_t tt = 0; tt < n; ++tt) {
+      const float q[8] = {qa.x, qa.y, qa.z, qa.w, qc.x, qc.y, qc.z, qc.w};
+      const float k[8] = {ka.x, ka.y, ka.z, ka.w, kc.x, kc.y, kc.z, kc.w};
+      const float dec = decay, bt = bet, kqt = kq, vt = v;
+      const uint32_t nx = tt + 1 < n ? tt + 1 : tt;
+      qa = sq[buf][nx][2 * j]; qc = sq[buf][nx][2 * j + 1];
+      ka = sk[buf][nx][2 * j]; kc = sk[buf][nx][2 * j + 1];
+      decay = sg[buf][nx]; bet = sb[buf][nx]; kq = skq[buf][nx]; v = sv[buf][nx][rb];
+      float d[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      kq += k[i] * q[i];
-      d[i] = S[i] * decay;
-      kvp += d[i] * k[i];
-      obp += d[i] * q[i];
-    }
-    kq = row16_sum(kq);
-    const float kv = row16_sum(kvp), ob = row16_sum(obp);
-    const float delta = (v - kv) * bet;
+      for (int i = 0; i < 8; ++i) d[i] = S[i] * dec;
+      // two independent partial sums per dot product shorten the chain
+      const float kv = row16_sum((d[0] * k[0] + d[1] * k[1] + d[2] * k[2] + d[3] * k[3]) +
+                                 (d[4] * k[4] + d[5] * k[5] + d[6] * k[6] + d[7] * k[7]));
+      const float ob = row16_sum((d[0] * q[0] + d[1] * q[1] + d[2] * q[2] + d[3] * q[3]) +
+                                 (d[4] * q[4] + d[5] * q[5] + d[6] * q[6] + d[7] * q[7]));
+      const float delta = (vt - kv) * bt;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) S[i] = d[i] + k[i] * delta;
-    if (j == 0) yb[static_cast<size_t>(t) * kGdnValDim] = f2bf(ob + delta * kq);
+      for (int i = 0; i < 8; ++i) S[i] = d[i] + k[i] * delta;
+      float kqd = kqt;
+      if constexpr (!PRE_KQ)
+        kqd = row16_sum((k[0] * q[0] + k[1] * q[1] + k[2] * q[2] + k[3] * q[3]) +
+                        (k[4] * q[4] + k[5] * q[5] + k[6] * q[6] + k[7] * q[7]));
+      if (j == 0) yb[static_cast<size_t>(c0 + tt) * kGdnValDim] = f2bf(ob + delta * kqd);
+    }
+    if (more) store(buf ^ 1);
+    __syncthreads();
   }
   srow[0] = make_float4(S[0], S[1], S[2], S[3]);
   srow[1] = make_float4(S[4], S[5], S[6], S[7]);
@@ -361,17 +427,23 @@ int launch_conv1d_prefill(hipStream_t s, float* state, const uint16_t* qkv, cons
 
 int launch_gdn_prefill_prepare(hipStream_t s, const uint16_t* conv_out, const uint16_t* a, const uint16_t* b,
                                const float* A_log, const uint16_t* dt_bias, float* qn, float* kn, float* g,
-                               float* beta, uint32_t T) {
+                               float* beta, float* kq, uint32_t T) {
   hipLaunchKernelGGL(gdn_prefill_prepare_kernel, dim3(T * kGdnHk), dim3(kQkNormThreads), 0, s, conv_out, a, b, A_log,
-                     dt_bias, qn, kn, g, beta);
+                     dt_bias, qn, kn, g, beta, kq);
   PRG_CHECK_LAUNCH("gdn_prefill_prepare");
   return PRG_OK;
 }
 
 int launch_gdn_prefill(hipStream_t s, float* state, const float* qn, const float* kn, const uint16_t* conv_out,
-                       const float* g, const float* beta, uint16_t* y, uint32_t T, uint32_t has_state) {
-  hipLaunchKernelGGL(gdn_prefill_kernel, dim3(kGdnHv * (kGdnDv / kGdnPRowsPerBlock)), dim3(256), 0, s, state, qn, kn,
-                     conv_out, g, beta, y, T, has_state);
+                       const float* g, const float* beta, const float* kq, uint16_t* y, uint32_t T,
+                       uint32_t has_state) {
+  // kq == nullptr: the recurrence forms k.q itself
+  if (kq)
+    hipLaunchKernelGGL(gdn_prefill_kernel<true>, dim3(kGdnHv * (kGdnDv / kGdnPRowsPerBlock)), dim3(256), 0, s, state,
+                       qn, kn, conv_out, g, beta, kq, y, T, has_state);
+  else
+    hipLaunchKernelGGL(gdn_prefill_kernel<false>, dim3(kGdnHv * (kGdnDv / kGdnPRowsPerBlock)), dim3(256), 0, s, state,
+                       qn, kn, conv_out, g, beta, kq, y, T, has_state);
   PRG_CHECK_LAUNCH("gdn_prefill");
   return PRG_OK;
 }
@@ -434,12 +506,12 @@ int prg_conv1d_silu_prefill_bf16(void* stream, float* state, const uint16_t* qkv
 int prg_gated_delta_prefill_prepare_bf16(void* stream, const uint16_t* conv_out, const uint16_t* a,
                                          const uint16_t* b, const float* A_log, const uint16_t* dt_bias,
                                          float* q_out, float* k_out, float* g_out, float* beta_out,
-                                         uint32_t token_count) {
+                                         float* kq_out, uint32_t token_count) {
   PRG_CHECK_ARG(conv_out && a && b && A_log && dt_bias && q_out && k_out && g_out && beta_out,
                 "prg_gated_delta_prefill_prepare_bf16: null pointer");
   PRG_CHECK_ARG(token_count > 0, "prg_gated_delta_prefill_prepare_bf16: token_count == 0");
   return prg::launch_gdn_prefill_prepare(as_stream(stream), conv_out, a, b, A_log, dt_bias, q_out, k_out, g_out,
-                                         beta_out, token_count);
+                                         beta_out, kq_out, token_count);
 }
 
 int prg_gated_delta_prefill_bf16(void* stream, float* state, const float* q, const float* k,
@@ -447,7 +519,7 @@ int prg_gated_delta_prefill_bf16(void* stream, float* state, const float* q, con
                                  uint32_t token_count, uint32_t has_previous_state) {
   PRG_CHECK_ARG(state && q && k && conv_out && g && beta && y, "prg_gated_delta_prefill_bf16: null pointer");
   PRG_CHECK_ARG(token_count > 0, "prg_gated_delta_prefill_bf16: token_count == 0");
-  return prg::launch_gdn_prefill(as_stream(stream), state, q, k, conv_out, g, beta, y, token_count,
+  return prg::launch_gdn_prefill(as_stream(stream), state, q, k, conv_out, g, beta, nullptr, y, token_count,
                                  has_previous_state);
 }
 

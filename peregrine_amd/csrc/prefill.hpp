@@ -27,13 +27,16 @@ int launch_attn_prefill(hipStream_t s, const uint16_t* q, const uint16_t* cache_
 int launch_conv1d_prefill(hipStream_t s, float* state, const uint16_t* qkv, const uint16_t* w, uint16_t* out,
                           uint32_t T, uint32_t has_state);
 
-// f32 q/k [T, 16, 128] (l2-normed, q also x rsqrt(128)) and gates g/beta [T, 32].
+// f32 q/k [T, 16, 128] (l2-normed, q also x rsqrt(128)), gates g/beta [T, 32]
+// and, when kq != nullptr, k.q per (token, k-head) [T, 16].
 int launch_gdn_prefill_prepare(hipStream_t s, const uint16_t* conv_out, const uint16_t* a, const uint16_t* b,
                                const float* A_log, const uint16_t* dt_bias, float* qn, float* kn, float* g,
-                               float* beta, uint32_t T);
+                               float* beta, float* kq, uint32_t T);
 
-// The delta-rule recurrence over T tokens; y [T, 32 * 128] bf16.
+// The delta-rule recurrence over T tokens; y [T, 32 * 128] bf16. kq from the
+// prepare step, or nullptr to form it in the recurrence.
 int launch_gdn_prefill(hipStream_t s, float* state, const float* qn, const float* kn, const uint16_t* conv_out,
-                       const float* g, const float* beta, uint16_t* y, uint32_t T, uint32_t has_state);
+                       const float* g, const float* beta, const float* kq, uint16_t* y, uint32_t T,
+                       uint32_t has_state);
 
 }  // namespace prg

@@ -183,9 +183,10 @@ def conv1d_silu_prefill(state, qkv, w, out, token_count: int, has_previous_state
 
 
 def gated_delta_prefill_prepare(conv_out, a, b, A_log, dt_bias, q_out, k_out, g_out, beta_out,
-                                token_count: int, stream=None) -> None:
+                                token_count: int, kq_out=None, stream=None) -> None:
     call("prg_gated_delta_prefill_prepare_bf16", _s(stream), ptr(conv_out), ptr(a), ptr(b), ptr(A_log),
-         ptr(dt_bias), ptr(q_out), ptr(k_out), ptr(g_out), ptr(beta_out), token_count)
+         ptr(dt_bias), ptr(q_out), ptr(k_out), ptr(g_out), ptr(beta_out),
+         None if kq_out is None else ptr(kq_out), token_count)
 
 
 def gated_delta_prefill(state, q, k, conv_out, g, beta, y, token_count: int, has_previous_state: bool = True,

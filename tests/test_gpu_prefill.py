@@ -230,9 +230,14 @@ def test_gdn_prefill_prepare_vs_oracle(gpu, orc):
     co, a, b, A_log, dtb, _ = _gdn_inputs(rng, T)
     qn, kn = _e((T, 2048), np.float32), _e((T, 2048), np.float32)
     g, beta = _e((T, 32), np.float32), _e((T, 32), np.float32)
-    ops.gated_delta_prefill_prepare(_d(co), _d(a), _d(b), _d(A_log), _d(dtb), qn, kn, g, beta, T)
+    kq = _e((T, 16), np.float32)
+    ops.gated_delta_prefill_prepare(_d(co), _d(a), _d(b), _d(A_log), _d(dtb), qn, kn, g, beta, T, kq_out=kq)
     gpu.synchronize()
     rq, rk = orc.qk_l2norm_prefill(co)
+    # k.q of the normalised pair, per (token, k-head): the float64 dot of the
+    # oracle's vectors (|kq| <= 1/sqrt(128) since both are unit-norm up to it).
+    ref_kq = np.einsum("thd,thd->th", rq.reshape(T, 16, 128).astype(np.float64), rk.reshape(T, 16, 128))
+    np.testing.assert_allclose(kq.numpy(), ref_kq, rtol=1e-4, atol=1e-6)
     rg, rb = orc.gating_many(A_log, a, dtb, b)
     np.testing.assert_allclose(qn.numpy(), rq, rtol=1e-5, atol=1e-8)
     np.testing.assert_allclose(kn.numpy(), rk, rtol=1e-5, atol=1e-8)
