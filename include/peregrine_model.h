@@ -36,6 +36,7 @@ typedef struct PrgModelConfig {
   uint32_t vocab;                   /* 248320, multiple of 8 */
   uint32_t full_attention_interval; /* 4: layer i is full attention iff (i+1) % 4 == 0 */
   float rms_eps;                    /* 1e-6 */
+  uint32_t mtp_layers;              /* 0, or 1: the MTP drafter (src/model/mtp.zig) */
 } PrgModelConfig;
 
 /* Qwen3.5-9B shape (src/model/config.zig:58-72, dims.zig:3-7). */
@@ -115,6 +116,50 @@ int prg_model_decode(PrgModel *model, PrgModelState *state, uint32_t n_steps, ui
 int prg_model_generate(PrgModel *model, PrgModelState *state, const uint32_t *prompt,
                        uint32_t prompt_len, uint32_t n_new, int teacher_force,
                        uint32_t *predictions, float *decode_ms);
+
+/* ======================================================================
+ * Multi-token prediction (needs cfg.mtp_layers == 1).
+ * ====================================================================== */
+
+/* Two tokens through the target at cache slots cache_pos, cache_pos + 1
+ * (rope_pos, rope_pos + 1; seq_len must be cache_pos + 1): the state advances
+ * by both. verify_token = argmax after token0, bonus_token = argmax after
+ * token1; hidden_out (device bf16 [2, hidden], may be NULL) receives the two
+ * final-normed hidden rows. Errors: SEQUENCE_TOO_LONG, INVALID_TOKEN.
+ * Replaces DeviceModel.forwardTwoTokenDecodeVerifierBf16WithPrefixProfiled
+ * (model.zig:1627-1659; encodeStack2Bf16 :719-760, decodeStep2Bf16
+ * decoder_layer.zig:485-516). */
+int prg_model_forward_two_tokens(PrgModel *model, PrgModelState *state, uint32_t token0, uint32_t token1,
+                                 uint32_t cache_pos, uint32_t rope_pos, uint32_t seq_len,
+                                 uint32_t *verify_token, uint32_t *bonus_token, uint16_t *hidden_out);
+
+/* One drafter step: norm(embed(token)) ‖ norm(hidden) -> fc -> the drafter's
+ * decoder layer at its own cache slot cache_pos -> norm -> lm_head argmax.
+ * hidden: device bf16 [hidden], the target's final-normed hidden of the
+ * previous position. Replaces Drafter.forwardDraftTokenProfiled
+ * (src/model/mtp.zig:187-242). */
+int prg_model_mtp_draft(PrgModel *model, PrgModelState *state, uint32_t token, const uint16_t *hidden,
+                        uint32_t cache_pos, uint32_t rope_pos, uint32_t seq_len, uint32_t *draft_token);
+
+/* Drafter prefill of token_count rows (tokens: host u32; hidden_rows: device
+ * bf16 [token_count, hidden]) at drafter slots start_pos.. . Replaces
+ * Drafter.forwardPrefill (src/model/mtp.zig:137-185). */
+int prg_model_mtp_prefill(PrgModel *model, PrgModelState *state, const uint32_t *tokens, uint32_t token_count,
+                          const uint16_t *hidden_rows, uint32_t start_pos);
+
+/* Greedy generation with MTP speculation: reset, prefill the prompt (seeding
+ * the drafter), then draft / verify / accept-or-reject until n_new tokens are
+ * emitted into tokens_out (the first is the token after the prompt). The
+ * tokens equal prg_model_prefill + prg_model_decode's greedy tokens.
+ * accepted / attempted: drafts accepted / verified (may be NULL). decode_ms:
+ * GPU time of the loop (may be NULL). The whole step runs as one replayed HIP
+ * graph with positions in device memory. Requires prompt_len + n_new + 2 <=
+ * max_seq. Replaces decodeSpeculativeFromPrefixCache
+ * (src/server/decode_loop.zig:163-293) without its per-token host sync and
+ * without the reject-path recompute. */
+int prg_model_generate_speculative(PrgModel *model, PrgModelState *state, const uint32_t *prompt,
+                                   uint32_t prompt_len, uint32_t n_new, uint32_t *tokens_out,
+                                   uint32_t *accepted, uint32_t *attempted, float *decode_ms);
 
 #ifdef __cplusplus
 }

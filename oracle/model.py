@@ -73,6 +73,26 @@ class OracleModel:
             self.layers.append(L)
         self.final_norm = model.read(ROOT + ".norm.weight", np.uint16)
         self.lm_head = _q4(model, "language_model.lm_head", c.vocab, c.hidden)
+        self.mtp = None
+        if getattr(c, "mtp_layers", 0):                              # mtp.zig:86-116
+            p = "mtp.layers.0"
+            a = p + ".self_attn"
+            self.mtp = {"linear": False,
+                        "pre_e": model.read("mtp.pre_fc_norm_embedding.weight", np.uint16),
+                        "pre_h": model.read("mtp.pre_fc_norm_hidden.weight", np.uint16),
+                        "fc": _q4(model, "mtp.fc", c.hidden, 2 * c.hidden),
+                        "norm": model.read("mtp.norm.weight", np.uint16),
+                        "input_norm": model.read(p + ".input_layernorm.weight", np.uint16),
+                        "post_norm": model.read(p + ".post_attention_layernorm.weight", np.uint16),
+                        "gate": _q4(model, p + ".mlp.gate_proj", c.intermediate, c.hidden),
+                        "up": _q4(model, p + ".mlp.up_proj", c.intermediate, c.hidden),
+                        "down": _q4(model, p + ".mlp.down_proj", c.hidden, c.intermediate),
+                        "q": _q4(model, a + ".q_proj", 8192, c.hidden),
+                        "k": _q4(model, a + ".k_proj", 1024, c.hidden),
+                        "v": _q4(model, a + ".v_proj", 1024, c.hidden),
+                        "o": _q4(model, a + ".o_proj", c.hidden, 4096),
+                        "q_norm": model.read(a + ".q_norm.weight", np.uint16),
+                        "k_norm": model.read(a + ".k_norm.weight", np.uint16)}
         a = 64 if max_seq >= 16000 else 256
         self.stride = (max_seq + a - 1) // a * a  # state.zig:25-32
         self.reset()
@@ -86,9 +106,14 @@ class OracleModel:
             else:
                 self.state.append({"k": np.zeros((4, self.stride, 256), np.uint16),
                                    "v": np.zeros((4, 256, self.stride), np.uint16)})
+        self.mtp_state = {"k": np.zeros((4, self.stride, 256), np.uint16),
+                          "v": np.zeros((4, 256, self.stride), np.uint16)}
 
     def _layer(self, i: int, h: np.ndarray, pos: int) -> np.ndarray:
-        o, L, S, eps = self.o, self.layers[i], self.state[i], self.cfg.rms_eps
+        return self._decode_layer(self.layers[i], self.state[i], h, pos)
+
+    def _decode_layer(self, L, S, h: np.ndarray, pos: int) -> np.ndarray:
+        o, eps = self.o, self.cfg.rms_eps
         normed = o.rmsnorm(h, L["input_norm"], eps)[0]            # decoder_layer.zig:531
         if L["linear"]:                                            # block_linear.zig:222-262
             qkv = o.q4_gemv(normed, L["qkv"])[0]
@@ -112,22 +137,50 @@ class OracleModel:
         inter = o.q4_gemv_silu_gate(normed2, L["gate"], L["up"])   # block_mlp.zig:272
         return o.q4_gemv_residual_add(inter, L["down"], r)[0]      # block_mlp.zig:276
 
-    def step(self, token: int, pos: int, want_logits: bool = False):
-        """One decode step at position pos; returns (next_token, logits|None)."""
+    def step(self, token: int, pos: int, want_logits: bool = False, want_hidden: bool = False):
+        """One decode step at position pos; returns (next_token, logits|None)
+        (and the final-normed hidden when want_hidden)."""
         o = self.o
         h = o.embedding(self.embed, token)                          # model.zig:700
         for i in range(len(self.layers)):
             h = self._layer(i, h, pos)
         normed = o.rmsnorm(h, self.final_norm, self.cfg.rms_eps)[0]  # model.zig:1355
+        tok, logits = self._head(normed, want_logits)
+        return (tok, logits, normed) if want_hidden else (tok, logits)
+
+    def _head(self, normed, want_logits: bool):
+        o = self.o
         pv, pi = o.q4_argmax_partial(normed, self.lm_head)          # model.zig:1386
         tok = o.argmax_pairs(pv[0], pi[0])                          # model.zig:1387
-        logits = None
-        if want_logits:
-            logits = bf16_to_f32(o.q4_gemv(normed, self.lm_head)[0])
+        logits = bf16_to_f32(o.q4_gemv(normed, self.lm_head)[0]) if want_logits else None
         return tok, logits
 
+    # ------------------------------------------------------- MTP drafter ---
+    def _pre_fc(self, tokens, hidden_rows):                       # mtp.zig:244-280
+        o, t, eps = self.o, self.mtp, self.cfg.rms_eps
+        e = o.embedding_many(self.embed, np.atleast_1d(np.asarray(tokens, np.uint32)))
+        ne = o.rmsnorm(e, t["pre_e"], eps)
+        nh = o.rmsnorm(np.atleast_2d(hidden_rows), t["pre_h"], eps)
+        return np.ascontiguousarray(np.concatenate([ne, nh], axis=1))
+
+    def mtp_step(self, token: int, hidden, pos: int, want_logits: bool = False):
+        """Drafter.forwardDraftTokenProfiled (mtp.zig:187-242) at drafter slot pos."""
+        o, t = self.o, self.mtp
+        fused = o.q4_gemv(self._pre_fc([token], hidden)[0], t["fc"])[0]
+        out = self._decode_layer(t, self.mtp_state, fused, pos)
+        normed = o.rmsnorm(out, t["norm"], self.cfg.rms_eps)[0]
+        return self._head(normed, want_logits)
+
+    def mtp_prefill(self, tokens, hidden_rows, start: int) -> None:
+        """Drafter.forwardPrefill (mtp.zig:137-185)."""
+        fused = self.o.q4_qmm(self._pre_fc(tokens, hidden_rows), self.mtp["fc"])
+        self._prefill_layer_impl(self.mtp, self.mtp_state, fused, start)
+
     def _prefill_layer(self, i: int, h: np.ndarray, start: int) -> np.ndarray:
-        o, L, S, eps = self.o, self.layers[i], self.state[i], self.cfg.rms_eps
+        return self._prefill_layer_impl(self.layers[i], self.state[i], h, start)
+
+    def _prefill_layer_impl(self, L, S, h: np.ndarray, start: int) -> np.ndarray:
+        o, eps = self.o, self.cfg.rms_eps
         T = h.shape[0]
         normed = o.rmsnorm(h, L["input_norm"], eps)                # decoder_layer.zig:666
         if L["linear"]:                                            # block_linear.zig:265-361
@@ -156,19 +209,18 @@ class OracleModel:
         inter = o.silu_mul_pair(o.q4_qmm(normed2, L["gate"]), o.q4_qmm(normed2, L["up"]))
         return o.q4_qmm(inter, L["down"], residual=r)              # block_mlp.zig:216-258
 
-    def prefill(self, tokens, start: int = 0, want_logits: bool = False):
+    def prefill(self, tokens, start: int = 0, want_logits: bool = False, want_hidden: bool = False):
         """Ingest tokens at positions start.. (state kept from earlier calls);
-        returns (next_token, logits|None) from the last row."""
+        returns (next_token, logits|None) from the last row (and all rows'
+        final-normed hiddens when want_hidden)."""
         o = self.o
         tok = np.asarray(tokens, np.uint32)
         h = o.embedding_many(self.embed, tok)                     # embedding.metal:73-96
         for i in range(len(self.layers)):
             h = self._prefill_layer(i, h, start)
-        normed = o.rmsnorm(h[-1], self.final_norm, self.cfg.rms_eps)[0]
-        pv, pi = o.q4_argmax_partial(normed, self.lm_head)
-        nxt = o.argmax_pairs(pv[0], pi[0])
-        logits = bf16_to_f32(o.q4_gemv(normed, self.lm_head)[0]) if want_logits else None
-        return nxt, logits
+        normed = o.rmsnorm(h, self.final_norm, self.cfg.rms_eps)
+        nxt, logits = self._head(normed[-1], want_logits)
+        return (nxt, logits, normed) if want_hidden else (nxt, logits)
 
     def teacher_forced(self, tokens, want_logits: bool = False):
         self.reset()

@@ -31,11 +31,11 @@ constexpr int kRowsPerHalfWave = 8;
 __device__ inline float hsum32(float v) { return group_sum<32>(v); }
 
 __global__ __launch_bounds__(kGdnThreads) void gdn_decode_kernel(
-    float* __restrict__ state, const uint16_t* __restrict__ conv_out, const uint16_t* __restrict__ a,
+    const float* state, const uint16_t* __restrict__ conv_out, const uint16_t* __restrict__ a,
     const uint16_t* __restrict__ bgate, const float* __restrict__ A_log,
     const uint16_t* __restrict__ dt_bias, uint16_t* __restrict__ y_out,
     const StepScalars* __restrict__ step, uint32_t has_state_host,
-    const uint16_t* __restrict__ norm_w, const uint16_t* __restrict__ z, float eps) {
+    const uint16_t* __restrict__ norm_w, const uint16_t* __restrict__ z, float eps, float* state_out) {
   __shared__ float ysh[kGdnDv];
   __shared__ float red[kGdnThreads / kWave];
 
@@ -48,7 +48,9 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_decode_kernel(
 
   // State rows for this half-wave, issued first.
   float4 S[kRowsPerHalfWave];
-  float4* srow = reinterpret_cast<float4*>(state + (static_cast<size_t>(hv) * kGdnDv + hw * kRowsPerHalfWave) * kGdnDk) + j;
+  const size_t row_off = (static_cast<size_t>(hv) * kGdnDv + hw * kRowsPerHalfWave) * kGdnDk;
+  const float4* srow = reinterpret_cast<const float4*>(state + row_off) + j;
+  float4* sout = reinterpret_cast<float4*>(state_out + row_off) + j;
 #pragma unroll
   for (int r = 0; r < kRowsPerHalfWave; ++r)
     S[r] = has_state ? srow[r * (kGdnDk / 4)] : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -94,7 +96,7 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_decode_kernel(
     kvm = hsum32(kvm);
     ob = hsum32(ob);
     const float delta = (bf2f(vsrc[r]) - kvm) * beta;
-    srow[r * (kGdnDk / 4)] = make_float4(d[0] + kn[0] * delta, d[1] + kn[1] * delta,
+    sout[r * (kGdnDk / 4)] = make_float4(d[0] + kn[0] * delta, d[1] + kn[1] * delta,
                                          d[2] + kn[2] * delta, d[3] + kn[3] * delta);
     const uint16_t yb = f2bf(ob + delta * kq);
     if (j == 0) {
@@ -124,7 +126,7 @@ __global__ void conv1d_decode_kernel(float* __restrict__ state, const uint16_t* 
                                      uint32_t conv_dim) {
   const uint32_t c = blockIdx.x * blockDim.x + threadIdx.x;
   if (c >= conv_dim) return;
-  out[c] = conv1d_silu_step(state, w, conv_dim, c, bf2f(qkv[c]));
+  out[c] = conv1d_silu_step(state, state, w, conv_dim, c, bf2f(qkv[c]));
 }
 
 __global__ void rmsnorm_gated_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
@@ -150,9 +152,10 @@ namespace prg {
 int launch_gdn_decode(hipStream_t s, float* state, const uint16_t* conv_out, const uint16_t* a,
                       const uint16_t* b, const float* A_log, const uint16_t* dt_bias,
                       uint16_t* y_out, const StepScalars* step_dev, uint32_t has_state_host,
-                      const uint16_t* norm_w, const uint16_t* z, float eps) {
+                      const uint16_t* norm_w, const uint16_t* z, float eps, float* state_out) {
   hipLaunchKernelGGL(gdn_decode_kernel, dim3(kGdnHv), dim3(kGdnThreads), 0, s, state, conv_out, a, b,
-                     A_log, dt_bias, y_out, step_dev, has_state_host, norm_w, z, eps);
+                     A_log, dt_bias, y_out, step_dev, has_state_host, norm_w, z, eps,
+                     state_out ? state_out : state);
   PRG_CHECK_LAUNCH("gated_delta_decode");
   return PRG_OK;
 }

@@ -17,9 +17,10 @@ constexpr uint32_t kGdnConvK = 4;
 
 // conv1d + SiLU decode for one channel, rolling the f32 state
 // (reference shaders/conv1d.metal:40-62). Unfused multiply/add in the
-// reference's order. Returns the bf16 output.
-__device__ inline uint16_t conv1d_silu_step(float* state, const uint16_t* w, uint32_t conv_dim,
-                                            uint32_t c, float xnew) {
+// reference's order. The rolled state goes to state_out (== state for the
+// in-place update). Returns the bf16 output.
+__device__ inline uint16_t conv1d_silu_step(const float* state, float* state_out, const uint16_t* w,
+                                            uint32_t conv_dim, uint32_t c, float xnew) {
   const float s0 = state[c], s1 = state[conv_dim + c], s2 = state[2 * conv_dim + c];
   const uint2 wv = *reinterpret_cast<const uint2*>(w + static_cast<size_t>(c) * kGdnConvK);
   float acc = 0.0f;
@@ -27,19 +28,20 @@ __device__ inline uint16_t conv1d_silu_step(float* state, const uint16_t* w, uin
   acc = __fadd_rn(acc, __fmul_rn(bf_hi(wv.x), s1));
   acc = __fadd_rn(acc, __fmul_rn(bf_lo(wv.y), s2));
   acc = __fadd_rn(acc, __fmul_rn(bf_hi(wv.y), xnew));
-  state[c] = s1;
-  state[conv_dim + c] = s2;
-  state[2 * conv_dim + c] = xnew;
+  state_out[c] = s1;
+  state_out[conv_dim + c] = s2;
+  state_out[2 * conv_dim + c] = xnew;
   return f2bf(acc / (1.0f + expf(-acc)));
 }
 
 // One block per v-head. With norm_w != nullptr the gated RMSNorm is fused and
 // y_out receives the normalised output. The state counts as present when
 // step_dev->rope_pos != 0 (decoder_layer.zig:564), or per has_state_host when
-// step_dev is null.
+// step_dev is null. The updated state is written to state_out (nullptr: in
+// place).
 int launch_gdn_decode(hipStream_t s, float* state, const uint16_t* conv_out, const uint16_t* a,
                       const uint16_t* b, const float* A_log, const uint16_t* dt_bias,
                       uint16_t* y_out, const StepScalars* step_dev, uint32_t has_state_host,
-                      const uint16_t* norm_w, const uint16_t* z, float eps);
+                      const uint16_t* norm_w, const uint16_t* z, float eps, float* state_out = nullptr);
 
 }  // namespace prg

@@ -6,7 +6,7 @@
 //   DecoderLayer.decodeStepBf16                           src/model/decoder_layer.zig:461-566, 756-781
 //   LinearAttentionBlock.decodeStepBf16                   src/model/block_linear.zig:199-263
 //   FullAttentionBlock.decodeStepBf16                     src/model/block_attn.zig:261-359
-//   MlpBlock.decodeResidualBf16                           src/model/block_mlp.zig:260-277
+//   MlpBlock.decodeResidualBf16 / decodeResidual2Bf16     src/model/block_mlp.zig:260-311
 //   encodeArgmaxFromHiddenBf16 (final norm, lm_head, argmax) src/model/model.zig:1346-1388
 //   ModelState (GDN conv/recurrent state, bf16 KV caches)  src/model/state.zig:11-118
 //   decodeFromPrefixCache                                 src/server/decode_loop.zig:96-160
@@ -22,30 +22,13 @@
 // One token's launches are captured once into a HIP graph; the token, positions
 // and sequence length live in device memory (DecodeCtl) and are advanced by the
 // argmax kernel, so replaying the graph runs the greedy loop with no host sync.
-//
-// A prompt is ingested layer-major in chunks of up to kPrefillChunk tokens
-// (DeviceModel.prefillLayerMajor*, model.zig:940-1060; DecoderLayer.prefillStepBf16,
-// decoder_layer.zig:644-760): every projection is an MFMA QMM over the chunk,
-// attention is causal over the cache written so far, and the GDN recurrence
-// runs token-sequentially inside one kernel per layer.
+// The prompt path lives in model_prefill.hip, the MTP drafter and speculative
+// loop in model_spec.hip.
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 
-#include <algorithm>
-#include <initializer_list>
-#include <utility>
-#include <map>
-#include <string>
-#include <vector>
-
-#include "attention.hpp"
-#include "gdn.hpp"
-#include "gemm.hpp"
-#include "norm.hpp"
-#include "peregrine_model.h"
-#include "prefill.hpp"
-#include "q4_gemv.hpp"
+#include "model.hpp"
 
 namespace prg {
 namespace {
@@ -88,134 +71,6 @@ __global__ void fill_kernel(void* dst, size_t n, uint64_t key, int kind, float a
   else
     static_cast<uint16_t*>(dst)[i] = f2bf(v);
 }
-
-constexpr size_t kAlign = 256;
-inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
-
-}  // namespace
-
-// ------------------------------------------------------------ structures ---
-struct Q4Linear {  // linear_q4.zig:17-25
-  uint32_t* weight = nullptr;
-  uint16_t* scales = nullptr;
-  uint16_t* biases = nullptr;
-  uint32_t out_dim = 0, in_dim = 0;
-};
-
-struct LinearAttentionBlock {  // block_linear.zig:143-184
-  Q4Linear in_qkv, in_z, in_a, in_b, out_proj;
-  uint16_t* conv_weight = nullptr;  // bf16 [8192, 4]
-  float* a_log = nullptr;           // f32 [32]
-  uint16_t* dt_bias = nullptr;      // bf16 [32]
-  uint16_t* norm_weight = nullptr;  // bf16 [128]
-};
-
-struct FullAttentionBlock {  // block_attn.zig:227-255
-  Q4Linear q_proj, k_proj, v_proj, o_proj;
-  uint16_t* q_norm = nullptr;  // bf16 [256]
-  uint16_t* k_norm = nullptr;
-};
-
-struct MlpBlock {  // block_mlp.zig:110-130
-  Q4Linear gate_proj, up_proj, down_proj;
-};
-
-struct DecoderLayer {  // decoder_layer.zig:360-412
-  bool linear = true;
-  uint16_t* input_norm = nullptr;
-  uint16_t* post_norm = nullptr;
-  LinearAttentionBlock lin;
-  FullAttentionBlock full;
-  MlpBlock mlp;
-};
-
-struct TensorRef {
-  void* ptr;
-  size_t bytes;
-};
-
-}  // namespace prg
-
-struct PrgModel {
-  PrgModelConfig cfg{};
-  uint8_t* arena = nullptr;
-  size_t arena_bytes = 0;
-  std::map<std::string, prg::TensorRef> tensors;
-  prg::Q4Linear embed;
-  std::vector<prg::DecoderLayer> layers;
-  uint16_t* final_norm = nullptr;
-  prg::Q4Linear lm_head;
-};
-
-namespace prg {
-namespace {
-
-struct LayerState {
-  float* conv = nullptr;       // f32 [3, 8192]
-  float* recur = nullptr;      // f32 [32, 128, 128]
-  uint16_t* cache_k = nullptr; // bf16 [4, stride, 256]
-  uint16_t* cache_v = nullptr; // bf16 [4, 256, stride]
-};
-
-}  // namespace
-}  // namespace prg
-
-namespace prg {
-namespace {
-
-// Prompt-path workspace, allocated on the first prefill ([rows, dim] bf16
-// unless noted).
-struct PrefillWs {
-  uint8_t* arena = nullptr;
-  uint32_t rows = 0;          // tokens per chunk the buffers hold
-  size_t scores_elems = 0;    // bf16 attention score capacity
-  uint16_t *h0 = nullptr, *h1 = nullptr, *normed = nullptr, *attn = nullptr, *resid = nullptr, *inter = nullptr;
-  uint16_t *qkv = nullptr, *conv_out = nullptr, *z = nullptr, *a = nullptr, *b = nullptr, *y = nullptr,
-           *gated = nullptr;
-  float *qn = nullptr, *kn = nullptr, *g = nullptr, *beta = nullptr, *kq = nullptr;  // f32
-  uint16_t *qp = nullptr, *k = nullptr, *v = nullptr, *q = nullptr, *gate = nullptr, *ctx = nullptr,
-           *scores = nullptr;
-};
-
-constexpr uint32_t kPrefillChunk = 2048;
-constexpr size_t kPrefillScoresBytes = size_t(512) << 20;
-
-}  // namespace
-}  // namespace prg
-
-struct PrgModelState {
-  PrgModel* model = nullptr;
-  uint32_t max_seq = 0, stride = 0;
-  uint8_t* arena = nullptr;
-  size_t arena_bytes = 0;
-  std::map<std::string, prg::TensorRef> tensors;
-  std::vector<prg::LayerState> layers;
-  // workspace
-  uint16_t *hA = nullptr, *hB = nullptr;
-  uint16_t *conv_out = nullptr, *zbuf = nullptr, *abuf = nullptr, *bbuf = nullptr, *gated = nullptr;
-  uint16_t *qp = nullptr, *kbuf = nullptr, *vbuf = nullptr, *qbuf = nullptr, *gatebuf = nullptr, *ctx = nullptr;
-  float* partials = nullptr;
-  uint16_t* inter = nullptr;
-  float* pval = nullptr;
-  uint32_t* pidx = nullptr;
-  prg::DecodeCtl* ctl = nullptr;
-  uint32_t* prompt = nullptr;
-  uint32_t* predictions = nullptr;
-  uint32_t nsplit = 0, split_tokens = 0;
-  // execution
-  hipStream_t stream = nullptr;
-  hipGraphExec_t graph_decode = nullptr;  // layers + lm_head argmax + advance
-  hipGraphExec_t graph_prompt = nullptr;  // layers + forced advance
-  hipEvent_t ev0 = nullptr, ev1 = nullptr;
-  // PEREGRINE_EAGER=1: launch each token's kernels directly instead of
-  // replaying the captured graph (same kernels and arguments; for tools such as
-  // kernel tracers that do not follow graph launches).
-  bool eager = false;
-  prg::PrefillWs pf;
-};
-
-namespace prg {
-namespace {
 
 // ------------------------------------------------------------ builders -----
 struct Builder {
@@ -275,8 +130,38 @@ struct Builder {
   }
 };
 
+}  // namespace
+
 bool is_linear_layer(const PrgModelConfig& c, uint32_t i) {  // decoder_layer.zig:29-31
   return (i + 1) % c.full_attention_interval != 0;
+}
+
+uint32_t cache_stride_for(uint32_t max_seq) {  // state.zig:25-32
+  const uint32_t a = max_seq >= 16000 ? 64u : 256u;
+  return (max_seq + a - 1) / a * a;
+}
+
+namespace {
+
+// Full-attention decoder layer weights under `p` (decoder_layer.zig:376-412).
+void build_full_attention_layer(Builder& b, DecoderLayer& L, const std::string& p, const PrgModelConfig& c) {
+  L.linear = false;
+  L.input_norm = b.bf16(p + ".input_layernorm.weight", c.hidden, 1.0f, 0.1f);
+  L.post_norm = b.bf16(p + ".post_attention_layernorm.weight", c.hidden, 1.0f, 0.1f);
+  const std::string a = p + ".self_attn";
+  L.full.q_proj = b.q4(a + ".q_proj", 2 * kAttnQHeads * kAttnHeadDim, c.hidden);
+  L.full.k_proj = b.q4(a + ".k_proj", kAttnKvHeads * kAttnHeadDim, c.hidden);
+  L.full.v_proj = b.q4(a + ".v_proj", kAttnKvHeads * kAttnHeadDim, c.hidden);
+  L.full.o_proj = b.q4(a + ".o_proj", c.hidden, kAttnQHeads * kAttnHeadDim);
+  L.full.q_norm = b.bf16(a + ".q_norm.weight", kAttnHeadDim, 1.0f, 0.1f);
+  L.full.k_norm = b.bf16(a + ".k_norm.weight", kAttnHeadDim, 1.0f, 0.1f);
+}
+
+void build_mlp(Builder& b, DecoderLayer& L, const std::string& p, const PrgModelConfig& c) {
+  const std::string mp = p + ".mlp";
+  L.mlp.gate_proj = b.q4(mp + ".gate_proj", c.intermediate, c.hidden);
+  L.mlp.up_proj = b.q4(mp + ".up_proj", c.intermediate, c.hidden);
+  L.mlp.down_proj = b.q4(mp + ".down_proj", c.hidden, c.intermediate);
 }
 
 void build_model(Builder& b) {
@@ -288,10 +173,10 @@ void build_model(Builder& b) {
   for (uint32_t i = 0; i < c.num_layers; ++i) {
     DecoderLayer& L = m->layers[i];
     const std::string p = root + ".layers." + std::to_string(i);
-    L.linear = is_linear_layer(c, i);
-    L.input_norm = b.bf16(p + ".input_layernorm.weight", c.hidden, 1.0f, 0.1f);
-    L.post_norm = b.bf16(p + ".post_attention_layernorm.weight", c.hidden, 1.0f, 0.1f);
-    if (L.linear) {
+    if (is_linear_layer(c, i)) {
+      L.linear = true;
+      L.input_norm = b.bf16(p + ".input_layernorm.weight", c.hidden, 1.0f, 0.1f);
+      L.post_norm = b.bf16(p + ".post_attention_layernorm.weight", c.hidden, 1.0f, 0.1f);
       const std::string a = p + ".linear_attn";
       L.lin.in_qkv = b.q4(a + ".in_proj_qkv", kGdnConvDim, c.hidden);
       L.lin.in_z = b.q4(a + ".in_proj_z", kGdnValDim, c.hidden);
@@ -303,24 +188,26 @@ void build_model(Builder& b) {
       L.lin.dt_bias = b.bf16(a + ".dt_bias", kGdnHv, 0.0f, 0.5f);
       L.lin.norm_weight = b.bf16(a + ".norm.weight", kGdnDv, 1.0f, 0.1f);
     } else {
-      const std::string a = p + ".self_attn";
-      L.full.q_proj = b.q4(a + ".q_proj", 2 * kAttnQHeads * kAttnHeadDim, c.hidden);
-      L.full.k_proj = b.q4(a + ".k_proj", kAttnKvHeads * kAttnHeadDim, c.hidden);
-      L.full.v_proj = b.q4(a + ".v_proj", kAttnKvHeads * kAttnHeadDim, c.hidden);
-      L.full.o_proj = b.q4(a + ".o_proj", c.hidden, kAttnQHeads * kAttnHeadDim);
-      L.full.q_norm = b.bf16(a + ".q_norm.weight", kAttnHeadDim, 1.0f, 0.1f);
-      L.full.k_norm = b.bf16(a + ".k_norm.weight", kAttnHeadDim, 1.0f, 0.1f);
+      build_full_attention_layer(b, L, p, c);
     }
-    const std::string mp = p + ".mlp";
-    L.mlp.gate_proj = b.q4(mp + ".gate_proj", c.intermediate, c.hidden);
-    L.mlp.up_proj = b.q4(mp + ".up_proj", c.intermediate, c.hidden);
-    L.mlp.down_proj = b.q4(mp + ".down_proj", c.hidden, c.intermediate);
+    build_mlp(b, L, p, c);
   }
   m->final_norm = b.bf16(root + ".norm.weight", c.hidden, 1.0f, 0.1f);
   m->lm_head = b.q4("language_model.lm_head", c.vocab, c.hidden);
+  if (c.mtp_layers) {  // mtp.zig:72-116 (tensor names under the "mtp." root)
+    MtpWeights& t = m->mtp;
+    t.present = true;
+    t.pre_fc_norm_embedding = b.bf16("mtp.pre_fc_norm_embedding.weight", c.hidden, 1.0f, 0.1f);
+    t.pre_fc_norm_hidden = b.bf16("mtp.pre_fc_norm_hidden.weight", c.hidden, 1.0f, 0.1f);
+    t.fc = b.q4("mtp.fc", c.hidden, 2 * c.hidden);
+    build_full_attention_layer(b, t.layer, "mtp.layers.0", c);
+    build_mlp(b, t.layer, "mtp.layers.0", c);
+    t.norm = b.bf16("mtp.norm.weight", c.hidden, 1.0f, 0.1f);
+  }
 }
 
 int validate_config(const PrgModelConfig& c) {
+  PRG_CHECK_ARG(c.mtp_layers <= 1, "config: mtp_layers %u (0 or 1)", c.mtp_layers);
   PRG_CHECK_ARG(c.num_layers >= 1 && c.num_layers <= 256, "config: num_layers %u", c.num_layers);
   PRG_CHECK_ARG(c.hidden >= 512 && c.hidden % 512 == 0 && c.hidden <= 16384, "config: hidden %u", c.hidden);
   PRG_CHECK_ARG(c.intermediate >= 512 && c.intermediate % 512 == 0 && c.intermediate <= 16384,
@@ -330,6 +217,8 @@ int validate_config(const PrgModelConfig& c) {
   PRG_CHECK_ARG(c.rms_eps > 0.0f, "config: rms_eps");
   return PRG_OK;
 }
+
+}  // namespace
 
 // ------------------------------------------------------- per-token chain ---
 GemvParams gemv_params(const uint16_t* x, uint32_t K) {
@@ -348,48 +237,54 @@ void add_seg(GemvParams& p, const Q4Linear& l, uint16_t* out) {
   s.rows = l.out_dim;
 }
 
+namespace {
 uint32_t total_rows(const GemvParams& p) {
   uint32_t r = 0;
   for (uint32_t i = 0; i < p.nseg; ++i) r += p.seg[i].rows;
   return r;
 }
+}  // namespace
 
 int run_gemv(hipStream_t s, GemvParams& p, int epi, bool norm, const char* name) {
-  const int rows = gemv_rows_per_wave(total_rows(p), p.K, epi, 1);
-  return launch_q4_gemv(s, p, 1, rows, epi, norm, name);
+  int M = p.x[1] ? 2 : 1;
+  const int rows = gemv_rows_per_wave(total_rows(p), p.K, epi, M);
+  return launch_q4_gemv(s, p, M, rows, epi, norm, name);
 }
 
 // GDN layer: norm+in_proj(+conv) -> recurrence+gated norm -> out_proj + residual.
-int encode_linear_attention(PrgModel* m, PrgModelState* st, const DecoderLayer& L, LayerState& ls) {
+int encode_linear_attention(PrgModel* m, PrgModelState* st, const DecoderLayer& L, const GdnIO& io,
+                            const uint16_t* x, uint16_t* h, const StepScalars* step) {
   const LinearAttentionBlock& b = L.lin;
   const PrgModelConfig& c = m->cfg;
   hipStream_t s = st->stream;
-  GemvParams p = gemv_params(st->hA, c.hidden);
+  GemvParams p = gemv_params(x, c.hidden);
   p.norm_w = L.input_norm;
   p.eps = c.rms_eps;
   add_seg(p, b.in_qkv, st->conv_out);
-  p.seg[0].conv_state = ls.conv;
+  p.seg[0].conv_state = io.conv_in;
+  p.seg[0].conv_state_out = io.conv_out;
   p.seg[0].conv_w = b.conv_weight;
   p.seg[0].conv_dim = kGdnConvDim;
   add_seg(p, b.in_z, st->zbuf);
   add_seg(p, b.in_a, st->abuf);
   add_seg(p, b.in_b, st->bbuf);
   if (int rc = run_gemv(s, p, kEpiPlain, true, "linear_attn.in_proj")) return rc;
-  if (int rc = launch_gdn_decode(s, ls.recur, st->conv_out, st->abuf, st->bbuf, b.a_log, b.dt_bias, st->gated,
-                                 &st->ctl->s, 0, b.norm_weight, st->zbuf, c.rms_eps))
+  if (int rc = launch_gdn_decode(s, io.recur_in, st->conv_out, st->abuf, st->bbuf, b.a_log, b.dt_bias, st->gated,
+                                 step, 0, b.norm_weight, st->zbuf, c.rms_eps, io.recur_out))
     return rc;
   GemvParams o = gemv_params(st->gated, kGdnValDim);
-  add_seg(o, b.out_proj, st->hB);
-  o.seg[0].res[0] = st->hA;
+  add_seg(o, b.out_proj, h);
+  o.seg[0].res[0] = x;
   return run_gemv(s, o, kEpiResidual, false, "linear_attn.out_proj");
 }
 
 // Attention layer: norm+q/k/v -> prepare/append -> flash decode -> o_proj + residual.
-int encode_full_attention(PrgModel* m, PrgModelState* st, const DecoderLayer& L, LayerState& ls) {
+int encode_full_attention(PrgModel* m, PrgModelState* st, const DecoderLayer& L, LayerState& ls, const uint16_t* x,
+                          uint16_t* h, const StepScalars* step) {
   const FullAttentionBlock& b = L.full;
   const PrgModelConfig& c = m->cfg;
   hipStream_t s = st->stream;
-  GemvParams p = gemv_params(st->hA, c.hidden);
+  GemvParams p = gemv_params(x, c.hidden);
   p.norm_w = L.input_norm;
   p.eps = c.rms_eps;
   add_seg(p, b.q_proj, st->qp);
@@ -397,7 +292,7 @@ int encode_full_attention(PrgModel* m, PrgModelState* st, const DecoderLayer& L,
   add_seg(p, b.v_proj, st->vbuf);
   if (int rc = run_gemv(s, p, kEpiPlain, true, "self_attn.qkv_proj")) return rc;
   AttnPrepareArgs pa{st->qp, b.q_norm, st->kbuf, st->vbuf, b.k_norm, st->qbuf, st->gatebuf, ls.cache_k, ls.cache_v,
-                     st->stride, 0, 0, &st->ctl->s};
+                     st->stride, 0, 0, step};
   if (int rc = launch_attn_prepare(s, pa)) return rc;
   AttnDecodeArgs da{};
   da.q = st->qbuf;
@@ -409,45 +304,63 @@ int encode_full_attention(PrgModel* m, PrgModelState* st, const DecoderLayer& L,
   da.stride = st->stride;
   da.nsplit = st->nsplit;
   da.split_tokens = st->split_tokens;
-  da.step = &st->ctl->s;
+  da.step = step;
   da.scale = kAttnScale;
   if (int rc = launch_attn_decode(s, da)) return rc;
   GemvParams o = gemv_params(st->ctx, kAttnQHeads * kAttnHeadDim);
-  add_seg(o, b.o_proj, st->hB);
-  o.seg[0].res[0] = st->hA;
+  add_seg(o, b.o_proj, h);
+  o.seg[0].res[0] = x;
   return run_gemv(s, o, kEpiResidual, false, "self_attn.o_proj");
 }
 
-// MLP: post_attention_layernorm + gate/up SiLU -> down + residual (into hA).
-int encode_mlp(PrgModel* m, PrgModelState* st, const DecoderLayer& L) {
+// MLP for M rows: post_attention_layernorm + gate/up SiLU -> down + residual.
+int encode_mlp(PrgModel* m, PrgModelState* st, const DecoderLayer& L, int M, const uint16_t* const* h,
+               uint16_t* const* inter, uint16_t* const* out) {
   const PrgModelConfig& c = m->cfg;
   hipStream_t s = st->stream;
-  GemvParams p = gemv_params(st->hB, c.hidden);
+  GemvParams p = gemv_params(h[0], c.hidden);
   p.norm_w = L.post_norm;
   p.eps = c.rms_eps;
-  add_seg(p, L.mlp.gate_proj, st->inter);
+  add_seg(p, L.mlp.gate_proj, inter[0]);
   p.seg[0].w[1] = L.mlp.up_proj.weight;
   p.seg[0].s[1] = L.mlp.up_proj.scales;
   p.seg[0].b[1] = L.mlp.up_proj.biases;
+  if (M == 2) {
+    p.x[1] = h[1];
+    p.seg[0].out[1] = inter[1];
+  }
   if (int rc = run_gemv(s, p, kEpiSiluGate, true, "mlp.gate_up")) return rc;
-  GemvParams d = gemv_params(st->inter, c.intermediate);
-  add_seg(d, L.mlp.down_proj, st->hA);
-  d.seg[0].res[0] = st->hB;
+  GemvParams d = gemv_params(inter[0], c.intermediate);
+  add_seg(d, L.mlp.down_proj, out[0]);
+  d.seg[0].res[0] = h[0];
+  if (M == 2) {
+    d.x[1] = inter[1];
+    d.seg[0].out[1] = out[1];
+    d.seg[0].res[1] = h[1];
+  }
   return run_gemv(s, d, kEpiResidual, false, "mlp.down_proj");
 }
+
+namespace {
 
 // One token: embed(ctl.token) -> layers -> (lm_head argmax | forced) + advance.
 int encode_token(PrgModel* m, PrgModelState* st, bool with_head) {
   hipStream_t s = st->stream;
+  const StepScalars* step = &st->ctl->s;
   if (int rc = launch_embedding(s, m->embed.weight, m->embed.scales, m->embed.biases, st->hA, &st->ctl->s.token, 0,
                                 1, m->cfg.hidden))
     return rc;
   for (size_t i = 0; i < m->layers.size(); ++i) {
     const DecoderLayer& L = m->layers[i];
-    int rc = L.linear ? encode_linear_attention(m, st, L, st->layers[i])
-                      : encode_full_attention(m, st, L, st->layers[i]);
+    LayerState& ls = st->layers[i];
+    int rc = L.linear ? encode_linear_attention(m, st, L, GdnIO{ls.conv, nullptr, ls.recur, nullptr}, st->hA, st->hB,
+                                                step)
+                      : encode_full_attention(m, st, L, ls, st->hA, st->hB, step);
     if (rc) return rc;
-    if ((rc = encode_mlp(m, st, L))) return rc;
+    const uint16_t* h[1] = {st->hB};
+    uint16_t* inter[1] = {st->inter};
+    uint16_t* out[1] = {st->hA};
+    if ((rc = encode_mlp(m, st, L, 1, h, inter, out))) return rc;
   }
   if (!with_head) return launch_advance_forced(s, st->ctl, st->prompt);
   GemvParams p = gemv_params(st->hA, m->cfg.hidden);
@@ -492,194 +405,6 @@ int run_step(PrgModelState* st, bool with_head) {
   return PRG_OK;
 }
 
-uint32_t cache_stride_for(uint32_t max_seq) {  // state.zig:25-32
-  const uint32_t a = max_seq >= 16000 ? 64u : 256u;
-  return (max_seq + a - 1) / a * a;
-}
-
-// ------------------------------------------------------------ prompt path ---
-int ensure_prefill_ws(PrgModelState* st) {
-  PrefillWs& w = st->pf;
-  if (w.arena) return PRG_OK;
-  const PrgModelConfig& c = st->model->cfg;
-  size_t R = std::min(kPrefillChunk, st->max_seq);
-  // PEREGRINE_PREFILL_CHUNK=n caps the chunk (tests of chunk boundaries).
-  if (const char* e = getenv("PEREGRINE_PREFILL_CHUNK")) {
-    const long v = atol(e);
-    if (v >= 1) R = std::min<size_t>(R, static_cast<size_t>(v));
-  }
-  w.rows = static_cast<uint32_t>(R);
-  w.scores_elems = std::min<size_t>(static_cast<size_t>(kAttnQHeads) * R * align_up(st->max_seq, 64),
-                                    kPrefillScoresBytes / sizeof(uint16_t));
-  const size_t bf = sizeof(uint16_t), f4 = sizeof(float);
-  struct Item {
-    void** slot;
-    size_t bytes;
-  };
-  const Item items[] = {
-      {reinterpret_cast<void**>(&w.h0), bf * R * c.hidden},
-      {reinterpret_cast<void**>(&w.h1), bf * R * c.hidden},
-      {reinterpret_cast<void**>(&w.normed), bf * R * c.hidden},
-      {reinterpret_cast<void**>(&w.attn), bf * R * c.hidden},
-      {reinterpret_cast<void**>(&w.resid), bf * R * c.hidden},
-      {reinterpret_cast<void**>(&w.inter), bf * R * c.intermediate},
-      {reinterpret_cast<void**>(&w.qkv), bf * R * kGdnConvDim},
-      {reinterpret_cast<void**>(&w.conv_out), bf * R * kGdnConvDim},
-      {reinterpret_cast<void**>(&w.z), bf * R * kGdnValDim},
-      {reinterpret_cast<void**>(&w.a), bf * R * kGdnHv},
-      {reinterpret_cast<void**>(&w.b), bf * R * kGdnHv},
-      {reinterpret_cast<void**>(&w.y), bf * R * kGdnValDim},
-      {reinterpret_cast<void**>(&w.gated), bf * R * kGdnValDim},
-      {reinterpret_cast<void**>(&w.qn), f4 * R * kGdnKeyDim},
-      {reinterpret_cast<void**>(&w.kn), f4 * R * kGdnKeyDim},
-      {reinterpret_cast<void**>(&w.g), f4 * R * kGdnHv},
-      {reinterpret_cast<void**>(&w.beta), f4 * R * kGdnHv},
-      {reinterpret_cast<void**>(&w.kq), f4 * R * kGdnHk},
-      {reinterpret_cast<void**>(&w.qp), bf * R * 2 * kAttnQHeads * kAttnHeadDim},
-      {reinterpret_cast<void**>(&w.k), bf * R * kAttnKvHeads * kAttnHeadDim},
-      {reinterpret_cast<void**>(&w.v), bf * R * kAttnKvHeads * kAttnHeadDim},
-      {reinterpret_cast<void**>(&w.q), bf * R * kAttnQHeads * kAttnHeadDim},
-      {reinterpret_cast<void**>(&w.gate), bf * R * kAttnQHeads * kAttnHeadDim},
-      {reinterpret_cast<void**>(&w.ctx), bf * R * kAttnQHeads * kAttnHeadDim},
-      {reinterpret_cast<void**>(&w.scores), bf * w.scores_elems},
-  };
-  size_t total = 0;
-  for (const Item& it : items) total = align_up(total + it.bytes, kAlign);
-  hipError_t e = hipMalloc(reinterpret_cast<void**>(&w.arena), total);
-  if (e != hipSuccess) {
-    w.arena = nullptr;
-    return set_error(PRG_ERR_OOM, "prefill workspace: hipMalloc(%zu): %s", total, hipGetErrorString(e));
-  }
-  size_t off = 0;
-  for (const Item& it : items) {
-    *it.slot = w.arena + off;
-    off = align_up(off + it.bytes, kAlign);
-  }
-  return PRG_OK;
-}
-
-// Largest chunk (<= the workspace rows) whose attention scores fit.
-uint32_t prefill_chunk_tokens(const PrgModelState* st, uint32_t start, uint32_t remaining) {
-  uint32_t T = std::min(remaining, st->pf.rows);
-  while (T > 1 && attn_prefill_scores_elems(T, start) > st->pf.scores_elems) T = (T + 1) / 2;
-  return T;
-}
-
-// x [T, in] -> out [T, out_dim] on the matrix cores (Q4Linear.encodePrefillQmm*,
-// linear_q4.zig:197-233). `up` selects the gate/up SiLU pair.
-int qmm(hipStream_t s, const uint16_t* x, const Q4Linear& l, uint16_t* out, uint32_t T, int epi,
-        const uint16_t* res, const Q4Linear* up, const char* name) {
-  GemmArgs g;
-  g.a = x;
-  g.lda = l.in_dim;
-  g.q[0] = GemmQ4{l.weight, l.scales, l.biases, out, l.out_dim, 0};
-  g.nq = 1;
-  if (up) {
-    g.q[1] = GemmQ4{up->weight, up->scales, up->biases, nullptr, up->out_dim, 0};
-    g.nq = 2;
-  }
-  g.res = res;
-  g.M = T;
-  g.K = l.in_dim;
-  return launch_gemm_q4(s, g, epi, name);
-}
-
-// Several projections of the same activations in one launch (each keeps its
-// own output buffer); the reference encodes them one after another.
-int qmm_multi(hipStream_t s, const uint16_t* x, uint32_t K, uint32_t T, std::initializer_list<std::pair<const Q4Linear*, uint16_t*>> segs,
-              const char* name) {
-  GemmArgs g;
-  g.a = x;
-  g.lda = K;
-  for (const auto& sg : segs) {
-    const Q4Linear& l = *sg.first;
-    g.q[g.nq++] = GemmQ4{l.weight, l.scales, l.biases, sg.second, l.out_dim, 0};
-  }
-  g.M = T;
-  g.K = K;
-  return launch_gemm_q4(s, g, kGemmStore, name);
-}
-
-// DecoderLayer.prefillStepBf16 (decoder_layer.zig:644-760) for T tokens at
-// positions start.. : x -> out.
-int prefill_layer(PrgModel* m, PrgModelState* st, uint32_t li, const uint16_t* x, uint16_t* out, uint32_t T,
-                  uint32_t start) {
-  const DecoderLayer& L = m->layers[li];
-  LayerState& ls = st->layers[li];
-  PrefillWs& w = st->pf;
-  const PrgModelConfig& c = m->cfg;
-  hipStream_t s = st->stream;
-  if (int rc = launch_rmsnorm(s, x, L.input_norm, w.normed, c.hidden, T, c.rms_eps)) return rc;
-  if (L.linear) {  // block_linear.zig:265-361
-    const LinearAttentionBlock& b = L.lin;
-    const uint32_t has_state = start != 0;  // decoder_layer.zig:635
-    if (int rc = qmm_multi(s, w.normed, c.hidden, T,
-                           {{&b.in_qkv, w.qkv}, {&b.in_z, w.z}, {&b.in_a, w.a}, {&b.in_b, w.b}},
-                           "prefill.in_proj"))
-      return rc;
-    if (int rc = launch_conv1d_prefill(s, ls.conv, w.qkv, b.conv_weight, w.conv_out, T, has_state)) return rc;
-    if (int rc = launch_gdn_prefill_prepare(s, w.conv_out, w.a, w.b, b.a_log, b.dt_bias, w.qn, w.kn, w.g, w.beta,
-                                            w.kq, T))
-      return rc;
-    if (int rc = launch_gdn_prefill(s, ls.recur, w.qn, w.kn, w.conv_out, w.g, w.beta, w.kq, w.y, T, has_state))
-      return rc;
-    if (int rc = prg_rmsnorm_gated_bf16(s, w.y, b.norm_weight, w.z, w.gated, kGdnDv, c.rms_eps, T * kGdnHv))
-      return rc;
-    if (int rc = qmm(s, w.gated, b.out_proj, w.attn, T, kGemmStore, nullptr, nullptr, "prefill.out_proj")) return rc;
-  } else {  // block_attn.zig:361-498
-    const FullAttentionBlock& b = L.full;
-    if (int rc = qmm_multi(s, w.normed, c.hidden, T, {{&b.q_proj, w.qp}, {&b.k_proj, w.k}, {&b.v_proj, w.v}},
-                           "prefill.qkv_proj"))
-      return rc;
-    if (int rc = launch_attn_prefill_prepare(s, w.qp, b.q_norm, w.k, b.k_norm, w.v, w.q, w.gate, ls.cache_k,
-                                             ls.cache_v, T, start, start, st->stride))
-      return rc;
-    if (int rc = launch_attn_prefill(s, w.q, ls.cache_k, ls.cache_v, w.gate, w.ctx, w.scores, T, start, st->stride,
-                                     kAttnScale))
-      return rc;
-    if (int rc = qmm(s, w.ctx, b.o_proj, w.attn, T, kGemmStore, nullptr, nullptr, "prefill.o_proj")) return rc;
-  }
-  // decoder_layer.zig:717-735: add + post norm, then the MLP (block_mlp.zig:155-258)
-  if (int rc = prg_add_rmsnorm_bf16(s, x, w.attn, L.post_norm, w.resid, w.normed, c.hidden, T, c.rms_eps)) return rc;
-  if (int rc = qmm(s, w.normed, L.mlp.gate_proj, w.inter, T, kGemmSiluPair, nullptr, &L.mlp.up_proj,
-                   "prefill.mlp.gate_up"))
-    return rc;
-  return qmm(s, w.inter, L.mlp.down_proj, out, T, kGemmResidual, w.resid, nullptr, "prefill.mlp.down_proj");
-}
-
-// Ingest st->prompt[0, len) in chunks, then the argmax tail on the last row
-// (encodePrefillArgmaxTailBf16, model.zig:1307-1324). The caller has set ctl
-// to step len-1 of a len-token prompt; the argmax kernel records the
-// prediction and advances ctl to position len.
-int run_prefill(PrgModel* m, PrgModelState* st, uint32_t len) {
-  if (int rc = ensure_prefill_ws(st)) return rc;
-  const PrgModelConfig& c = m->cfg;
-  hipStream_t s = st->stream;
-  PrefillWs& w = st->pf;
-  const uint16_t* last = nullptr;
-  uint32_t T = 0;
-  for (uint32_t start = 0; start < len; start += T) {
-    T = prefill_chunk_tokens(st, start, len - start);
-    if (int rc = launch_embedding(s, m->embed.weight, m->embed.scales, m->embed.biases, w.h0, st->prompt + start, 0,
-                                  T, c.hidden))
-      return rc;
-    uint16_t *x = w.h0, *y = w.h1;
-    for (uint32_t li = 0; li < c.num_layers; ++li) {
-      if (int rc = prefill_layer(m, st, li, x, y, T, start)) return rc;
-      std::swap(x, y);
-    }
-    last = x + static_cast<size_t>(T - 1) * c.hidden;
-  }
-  GemvParams p = gemv_params(last, c.hidden);
-  p.norm_w = m->final_norm;
-  p.eps = c.rms_eps;
-  add_seg(p, m->lm_head, nullptr);
-  p.seg[0].pval[0] = st->pval;
-  p.seg[0].pidx[0] = st->pidx;
-  if (int rc = launch_q4_gemv(s, p, 1, 8, kEpiArgmax, true, "lm_head.argmax")) return rc;
-  return launch_argmax_advance(s, st->pval, st->pidx, c.vocab / 8, st->ctl, st->prompt, st->predictions);
-}
-
 }  // namespace
 }  // namespace prg
 
@@ -695,6 +420,7 @@ void prg_model_default_config(PrgModelConfig* cfg) {
   cfg->vocab = 248320;
   cfg->full_attention_interval = 4;
   cfg->rms_eps = 1e-6f;
+  cfg->mtp_layers = 0;
 }
 
 int prg_model_create_random(const PrgModelConfig* cfg, uint64_t seed, PrgModel** out) {
@@ -767,12 +493,18 @@ int prg_model_state_create(PrgModel* model, uint32_t max_seq, PrgModelState** ou
   };
   std::vector<Item> items;
   st->layers.assign(c.num_layers, LayerState{});
+  // GDN states first, as one contiguous block.
   for (uint32_t i = 0; i < c.num_layers; ++i) {
     const std::string p = "layers." + std::to_string(i);
     if (model->layers[i].linear) {
       items.push_back({p + ".conv", sizeof(float) * (kGdnConvK - 1) * kGdnConvDim, reinterpret_cast<void**>(&st->layers[i].conv)});
       items.push_back({p + ".recur", sizeof(float) * kGdnHv * kGdnDv * kGdnDk, reinterpret_cast<void**>(&st->layers[i].recur)});
-    } else {
+    }
+  }
+  const size_t gdn_items = items.size();
+  for (uint32_t i = 0; i < c.num_layers; ++i) {
+    const std::string p = "layers." + std::to_string(i);
+    if (!model->layers[i].linear) {
       const size_t kv = sizeof(uint16_t) * kAttnKvHeads * static_cast<size_t>(st->stride) * kAttnHeadDim;
       items.push_back({p + ".cache_k", kv, reinterpret_cast<void**>(&st->layers[i].cache_k)});
       items.push_back({p + ".cache_v", kv, reinterpret_cast<void**>(&st->layers[i].cache_v)});
@@ -810,11 +542,14 @@ int prg_model_state_create(PrgModel* model, uint32_t max_seq, PrgModelState** ou
   }
   st->arena_bytes = total;
   size_t off = 0;
-  for (auto& it : items) {
+  for (size_t i = 0; i < items.size(); ++i) {
+    const Item& it = items[i];
     *it.slot = st->arena + off;
     st->tensors[it.name] = TensorRef{st->arena + off, it.bytes};
     off = align_up(off + it.bytes, kAlign);
+    if (i + 1 == gdn_items) st->gdn_bytes = off;
   }
+  st->gdn_base = st->arena;
   (void)state_items;
   // Everything starts at zero (GDN states, caches, workspace).
   if ((e = hipMemset(st->arena, 0, total)) != hipSuccess ||
@@ -834,9 +569,11 @@ void prg_model_state_destroy(PrgModelState* st) {
   if (st->graph_prompt) hipGraphExecDestroy(st->graph_prompt);
   if (st->ev0) hipEventDestroy(st->ev0);
   if (st->ev1) hipEventDestroy(st->ev1);
+  if (st->graph_spec) hipGraphExecDestroy(st->graph_spec);
   if (st->stream) hipStreamDestroy(st->stream);
   hipFree(st->arena);
   if (st->pf.arena) hipFree(st->pf.arena);
+  if (st->spec_arena) hipFree(st->spec_arena);
   delete st;
 }
 
@@ -879,32 +616,6 @@ int prg_model_forward_next_token(PrgModel* model, PrgModelState* st, uint32_t to
   PRG_HIP(hipMemcpyAsync(st->ctl, &ctl, sizeof(ctl), hipMemcpyHostToDevice, st->stream));
   if (int rc = run_step(st, true)) return rc;
   PRG_HIP(hipMemcpyAsync(next_token, st->predictions, sizeof(uint32_t), hipMemcpyDeviceToHost, st->stream));
-  PRG_HIP(hipStreamSynchronize(st->stream));
-  return PRG_OK;
-}
-
-int prg_model_prefill(PrgModel* model, PrgModelState* st, const uint32_t* prompt, uint32_t prompt_len,
-                      uint32_t* next_token) {
-  PRG_CHECK_ARG(model && st && prompt && next_token && st->model == model, "prg_model_prefill: bad argument");
-  PRG_CHECK_ARG(prompt_len >= 1, "prg_model_prefill: empty prompt");
-  if (prompt_len > st->max_seq)
-    return set_error(PRG_ERR_SEQUENCE_TOO_LONG, "prompt of %u tokens exceeds max_seq %u", prompt_len, st->max_seq);
-  for (uint32_t i = 0; i < prompt_len; ++i)
-    if (prompt[i] >= model->cfg.vocab)
-      return set_error(PRG_ERR_INVALID_TOKEN, "prompt[%u] = %u >= vocab %u", i, prompt[i], model->cfg.vocab);
-  if (int rc = prg_model_state_reset(st)) return rc;
-  // Control block as if step prompt_len-1 were running: the argmax tail
-  // records predictions[prompt_len-1] and moves the decode loop to prompt_len.
-  DecodeCtl ctl{};
-  ctl.s = StepScalars{prompt[prompt_len - 1], prompt_len - 1, prompt_len - 1, prompt_len};
-  ctl.n = prompt_len - 1;
-  ctl.prompt_len = prompt_len;
-  ctl.capacity = st->max_seq;
-  PRG_HIP(hipMemcpyAsync(st->prompt, prompt, sizeof(uint32_t) * prompt_len, hipMemcpyHostToDevice, st->stream));
-  PRG_HIP(hipMemcpyAsync(st->ctl, &ctl, sizeof(ctl), hipMemcpyHostToDevice, st->stream));
-  if (int rc = run_prefill(model, st, prompt_len)) return rc;
-  PRG_HIP(hipMemcpyAsync(next_token, st->predictions + (prompt_len - 1), sizeof(uint32_t), hipMemcpyDeviceToHost,
-                         st->stream));
   PRG_HIP(hipStreamSynchronize(st->stream));
   return PRG_OK;
 }

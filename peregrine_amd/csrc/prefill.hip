@@ -352,9 +352,30 @@ __global__ __launch_bounds__(256) void gdn_prefill_kernel(float* __restrict__ st
   srow[1] = make_float4(S[4], S[5], S[6], S[7]);
 }
 
+// out[r] = a[r] ‖ b[r] for rows of `width` bf16 (concat_two_rows_bf16, the
+// drafter's fc input, src/model/mtp.zig:262-270). One uint4 per thread.
+__global__ void concat_rows_kernel(const uint4* __restrict__ a, const uint4* __restrict__ b, uint4* __restrict__ out,
+                                   uint32_t rows, uint32_t w8) {
+  const size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= static_cast<size_t>(rows) * 2 * w8) return;
+  const size_t r = i / (2 * w8), c = i % (2 * w8);
+  out[i] = c < w8 ? a[r * w8 + c] : b[r * w8 + c - w8];
+}
+
 }  // namespace
 
 namespace prg {
+
+int launch_concat_rows(hipStream_t s, const uint16_t* a, const uint16_t* b, uint16_t* out, uint32_t rows,
+                       uint32_t width) {
+  const uint32_t w8 = width / 8;
+  const size_t n = static_cast<size_t>(rows) * 2 * w8;
+  hipLaunchKernelGGL(concat_rows_kernel, dim3(static_cast<uint32_t>((n + 255) / 256)), dim3(256), 0, s,
+                     reinterpret_cast<const uint4*>(a), reinterpret_cast<const uint4*>(b), reinterpret_cast<uint4*>(out),
+                     rows, w8);
+  PRG_CHECK_LAUNCH("concat_rows");
+  return PRG_OK;
+}
 
 size_t attn_prefill_scores_elems(uint32_t T, uint32_t prefix) {
   const size_t L = static_cast<size_t>(prefix) + T, ld = (L + 63) / 64 * 64;

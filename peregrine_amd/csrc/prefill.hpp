@@ -39,4 +39,8 @@ int launch_gdn_prefill(hipStream_t s, float* state, const float* qn, const float
                        const float* g, const float* beta, const float* kq, uint16_t* y, uint32_t T,
                        uint32_t has_state);
 
+// out[r] = a[r] ‖ b[r], rows of `width` bf16 (width % 8 == 0).
+int launch_concat_rows(hipStream_t s, const uint16_t* a, const uint16_t* b, uint16_t* out, uint32_t rows,
+                       uint32_t width);
+
 }  // namespace prg

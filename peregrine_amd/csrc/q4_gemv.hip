@@ -248,6 +248,12 @@ int launch_argmax_advance(hipStream_t s, const float* values, const uint32_t* in
   PRG_CHECK_LAUNCH("argmax_advance");
   return PRG_OK;
 }
+int launch_argmax_pairs(hipStream_t s, const float* values, const uint32_t* indices, uint32_t n, uint32_t* out) {
+  hipLaunchKernelGGL(argmax_pairs_kernel<false>, dim3(1), dim3(kArgmaxThreads), 0, s, values, indices, out, n,
+                     nullptr, nullptr, nullptr);
+  PRG_CHECK_LAUNCH("argmax_pairs");
+  return PRG_OK;
+}
 int launch_advance_forced(hipStream_t s, DecodeCtl* ctl, const uint32_t* prompt) {
   hipLaunchKernelGGL(advance_forced_kernel, dim3(1), dim3(64), 0, s, ctl, prompt);
   PRG_CHECK_LAUNCH("advance_forced");

@@ -55,6 +55,7 @@ struct GemvSeg {
   // state [3, conv_dim] is rolled in place; out receives the conv output.
   // This fuses in_proj_qkv with conv1d_silu_decode_bf16 (block_linear.zig:230-240).
   float* conv_state;
+  float* conv_state_out;      // rolled state destination (nullptr: in place)
   const uint16_t* conv_w;     // bf16 [conv_dim, 4]
   uint32_t conv_dim;
   uint32_t rows;              // output rows of this segment
@@ -281,7 +282,8 @@ __device__ inline void gemv_epilogue(const GemvParams& p, const GemvLoc& loc, in
         uint16_t o;
         if constexpr (EPI == kEpiPlain) {
           if (M == 1 && sg.conv_state != nullptr)
-            o = conv1d_silu_step(sg.conv_state, sg.conv_w, sg.conv_dim, row, round_bf(tot[0][r][m]));
+            o = conv1d_silu_step(sg.conv_state, sg.conv_state_out ? sg.conv_state_out : sg.conv_state, sg.conv_w,
+                                 sg.conv_dim, row, round_bf(tot[0][r][m]));
           else
             o = f2bf(tot[0][r][m]);
         } else if constexpr (EPI == kEpiResidual) {
@@ -426,6 +428,8 @@ int gemv_rows_per_wave(uint32_t total_rows, uint32_t K, int epi, int M);
 // Final argmax over partials + advance of the device token loop.
 int launch_argmax_advance(hipStream_t s, const float* values, const uint32_t* indices, uint32_t n,
                           DecodeCtl* ctl, const uint32_t* prompt, uint32_t* predictions);
+// Final argmax over partials into out[0] (no control-block update).
+int launch_argmax_pairs(hipStream_t s, const float* values, const uint32_t* indices, uint32_t n, uint32_t* out);
 // Advance with the next token forced from prompt (no lm_head this step).
 int launch_advance_forced(hipStream_t s, DecodeCtl* ctl, const uint32_t* prompt);
 

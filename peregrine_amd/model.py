@@ -17,7 +17,8 @@ from .device import init
 
 class PrgModelConfig(C.Structure):
     _fields_ = [("num_layers", C.c_uint32), ("hidden", C.c_uint32), ("intermediate", C.c_uint32),
-                ("vocab", C.c_uint32), ("full_attention_interval", C.c_uint32), ("rms_eps", C.c_float)]
+                ("vocab", C.c_uint32), ("full_attention_interval", C.c_uint32), ("rms_eps", C.c_float),
+                ("mtp_layers", C.c_uint32)]
 
 
 @dataclass
@@ -28,10 +29,11 @@ class ModelConfig:
     vocab: int = 248320
     full_attention_interval: int = 4
     rms_eps: float = 1e-6
+    mtp_layers: int = 0  # 1: with the MTP drafter (src/model/mtp.zig)
 
     def c(self) -> PrgModelConfig:
         return PrgModelConfig(self.num_layers, self.hidden, self.intermediate, self.vocab,
-                              self.full_attention_interval, self.rms_eps)
+                              self.full_attention_interval, self.rms_eps, self.mtp_layers)
 
     def is_linear(self, i: int) -> bool:  # decoder_layer.zig:29-31
         return (i + 1) % self.full_attention_interval != 0
@@ -138,6 +140,41 @@ class ModelState:
              0 if teacher_force else n_new, 1 if teacher_force else 0, preds.ctypes.data_as(C.c_void_p),
              C.byref(ms))
         return preds, float(ms.value)
+
+    # decode_loop.zig:163-293 (device-resident; returns tokens, accepted, attempted, ms)
+    def generate_speculative(self, prompt, n_new: int) -> tuple[np.ndarray, int, int, float]:
+        prompt = np.ascontiguousarray(prompt, np.uint32)
+        out = np.empty(n_new, np.uint32)
+        acc, att, ms = C.c_uint32(0), C.c_uint32(0), C.c_float(0.0)
+        call("prg_model_generate_speculative", self.model.handle, self.handle, prompt.ctypes.data_as(C.c_void_p),
+             len(prompt), n_new, out.ctypes.data_as(C.c_void_p), C.byref(acc), C.byref(att), C.byref(ms))
+        return out, int(acc.value), int(att.value), float(ms.value)
+
+    # model.zig:1627-1659
+    def forward_two_tokens(self, t0: int, t1: int, cache_pos: int, hidden_out=None) -> tuple[int, int]:
+        v, b = C.c_uint32(0), C.c_uint32(0)
+        from .device import ptr
+
+        call("prg_model_forward_two_tokens", self.model.handle, self.handle, t0, t1, cache_pos, cache_pos,
+             cache_pos + 1, C.byref(v), C.byref(b), ptr(hidden_out))
+        return int(v.value), int(b.value)
+
+    # mtp.zig:187-242
+    def mtp_draft(self, token: int, hidden, cache_pos: int) -> int:
+        from .device import ptr
+
+        d = C.c_uint32(0)
+        call("prg_model_mtp_draft", self.model.handle, self.handle, token, ptr(hidden), cache_pos, cache_pos,
+             cache_pos + 1, C.byref(d))
+        return int(d.value)
+
+    # mtp.zig:137-185
+    def mtp_prefill(self, tokens, hidden_rows, start: int) -> None:
+        from .device import ptr
+
+        tokens = np.ascontiguousarray(tokens, np.uint32)
+        call("prg_model_mtp_prefill", self.model.handle, self.handle, tokens.ctypes.data_as(C.c_void_p), len(tokens),
+             ptr(hidden_rows), start)
 
     def close(self) -> None:
         if self.handle:
