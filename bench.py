@@ -28,6 +28,10 @@ sys.path.insert(0, str(ROOT))
 METRIC = "decode tok/s @batch1 (9B-shaped Q4) + Q4 GEMV achieved HBM GB/s vs peak"
 HBM_PEAK_GBS = 8000.0
 PROMPT_TOKENS = 1600
+# HBM bytes per launch of the dominant kernel, from two rocprofv3 --pmc passes
+# (FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000, the factors a plain 256 MiB copy
+# kernel reads on the same counters); profiles/gemv_silu_gate_hbm_traffic.md.
+DOMINANT_TRAFFIC_BYTES = 56_990_000
 
 
 def log(*a) -> None:
@@ -76,7 +80,8 @@ def dominant_kernel_roofline(iters: int = 100) -> dict:
     gbs = algo / (avg_us * 1e-6) / 1e9
     return {"kernel": "q4_gemv_kernel<M=1,EPI=silu_gate,NORM> (mlp.gate_up, 2x12288x4096 Q4)",
             "bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": DOMINANT_TRAFFIC_BYTES,
+            "traffic_unit": "bytes/launch (PMC, calibrated)",
             "avg_us": round(avg_us, 3), "median_us": round(float(np.median(ms) * 1e3), 3),
             "algo_bytes_per_launch": int(algo), "launches": iters, "ring_copies": copies}
 

@@ -30,12 +30,15 @@ constexpr int kRowsPerHalfWave = 8;
 
 __device__ inline float hsum32(float v) { return group_sum<32>(v); }
 
+// IN_PLACE: state_out is state (each thread reads its rows before writing
+// them); otherwise the two buffers are distinct.
+template <bool IN_PLACE>
 __global__ __launch_bounds__(kGdnThreads) void gdn_decode_kernel(
-    const float* state, const uint16_t* __restrict__ conv_out, const uint16_t* __restrict__ a,
+    float* __restrict__ state, const uint16_t* __restrict__ conv_out, const uint16_t* __restrict__ a,
     const uint16_t* __restrict__ bgate, const float* __restrict__ A_log,
     const uint16_t* __restrict__ dt_bias, uint16_t* __restrict__ y_out,
     const StepScalars* __restrict__ step, uint32_t has_state_host,
-    const uint16_t* __restrict__ norm_w, const uint16_t* __restrict__ z, float eps, float* state_out) {
+    const uint16_t* __restrict__ norm_w, const uint16_t* __restrict__ z, float eps, float* __restrict__ state_out) {
   __shared__ float ysh[kGdnDv];
   __shared__ float red[kGdnThreads / kWave];
 
@@ -50,7 +53,7 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_decode_kernel(
   float4 S[kRowsPerHalfWave];
   const size_t row_off = (static_cast<size_t>(hv) * kGdnDv + hw * kRowsPerHalfWave) * kGdnDk;
   const float4* srow = reinterpret_cast<const float4*>(state + row_off) + j;
-  float4* sout = reinterpret_cast<float4*>(state_out + row_off) + j;
+  float4* sout = reinterpret_cast<float4*>((IN_PLACE ? state : state_out) + row_off) + j;
 #pragma unroll
   for (int r = 0; r < kRowsPerHalfWave; ++r)
     S[r] = has_state ? srow[r * (kGdnDk / 4)] : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -153,9 +156,12 @@ int launch_gdn_decode(hipStream_t s, float* state, const uint16_t* conv_out, con
                       const uint16_t* b, const float* A_log, const uint16_t* dt_bias,
                       uint16_t* y_out, const StepScalars* step_dev, uint32_t has_state_host,
                       const uint16_t* norm_w, const uint16_t* z, float eps, float* state_out) {
-  hipLaunchKernelGGL(gdn_decode_kernel, dim3(kGdnHv), dim3(kGdnThreads), 0, s, state, conv_out, a, b,
-                     A_log, dt_bias, y_out, step_dev, has_state_host, norm_w, z, eps,
-                     state_out ? state_out : state);
+  if (state_out && state_out != state)
+    hipLaunchKernelGGL(gdn_decode_kernel<false>, dim3(kGdnHv), dim3(kGdnThreads), 0, s, state, conv_out, a, b,
+                       A_log, dt_bias, y_out, step_dev, has_state_host, norm_w, z, eps, state_out);
+  else
+    hipLaunchKernelGGL(gdn_decode_kernel<true>, dim3(kGdnHv), dim3(kGdnThreads), 0, s, state, conv_out, a, b,
+                       A_log, dt_bias, y_out, step_dev, has_state_host, norm_w, z, eps, nullptr);
   PRG_CHECK_LAUNCH("gated_delta_decode");
   return PRG_OK;
 }

@@ -13,12 +13,13 @@ import numpy as np
 
 def f32_to_bf16(a) -> np.ndarray:
     """Round-to-nearest-even f32 -> bf16 bits (NaN stays NaN)."""
+    shape = np.shape(a)
     u = np.ascontiguousarray(np.asarray(a, dtype=np.float32)).view(np.uint32).astype(np.uint64)
     nan = (u & 0x7FFFFFFF) > 0x7F800000
     r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
     if nan.any():
         r[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint16)
-    return r
+    return r.reshape(shape)
 
 
 def bf16_to_f32(b) -> np.ndarray:
