@@ -18,7 +18,10 @@
 //   * x is staged once per block in LDS, pre-permuted so each activation pair
 //     lines up with the nibble pair the unpack produces.
 //     An optional fused RMSNorm prologue normalises x while staging it.
-//   * Partial sums are reduced across the wave with DPP row ops + readlane.
+//   * One-row-per-wave launches work in rounds of four groups: the four rows'
+//     lane partials are reduced together (v_permlane32/16_swap halve the
+//     lanes while trading rows, then a DPP row sum), and one lane per row runs
+//     the epilogue. Multi-row launches reduce per row with DPP + readlane.
 //   * Up to 4 independent weight matrices ("segments") that share x run in
 //     one launch (e.g. in_proj qkv | z | a | b), cutting launches per layer.
 #pragma once
@@ -240,6 +243,91 @@ __device__ inline void gemv_dot_step(const GemvBuf<NMAT, ROWS, ITERS>& b, int it
   }
 }
 
+// Where one finished row goes (all epilogues but argmax), selected per lane.
+struct GemvRowDst {
+  uint16_t* out[2];
+  const uint16_t* res[2];
+  float* conv_state;
+  float* conv_state_out;
+  const uint16_t* conv_w;
+  uint32_t conv_dim;
+  uint32_t row;
+};
+
+__device__ inline GemvRowDst gemv_row_dst(const GemvSeg& sg, uint32_t row) {
+  GemvRowDst d;
+  d.out[0] = sg.out[0];
+  d.out[1] = sg.out[1];
+  d.res[0] = sg.res[0];
+  d.res[1] = sg.res[1];
+  d.conv_state = sg.conv_state;
+  d.conv_state_out = sg.conv_state_out ? sg.conv_state_out : sg.conv_state;
+  d.conv_w = sg.conv_w;
+  d.conv_dim = sg.conv_dim;
+  d.row = row;
+  return d;
+}
+
+// Epilogue of one row: tot[mat][m] are its finished dot products.
+template <int M, int NMAT, int EPI>
+__device__ inline void gemv_store_row(const GemvRowDst& d, const float (&tot)[NMAT][M]) {
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+    uint16_t o;
+    if constexpr (EPI == kEpiPlain) {
+      if (M == 1 && d.conv_state != nullptr)
+        o = conv1d_silu_step(d.conv_state, d.conv_state_out, d.conv_w, d.conv_dim, d.row, round_bf(tot[0][m]));
+      else
+        o = f2bf(tot[0][m]);
+    } else if constexpr (EPI == kEpiResidual) {
+      o = f2bf(round_bf(tot[0][m]) + bf2f(d.res[m][d.row]));
+    } else {
+      o = f2bf(silu(round_bf(tot[0][m])) * round_bf(tot[NMAT - 1][m]));
+    }
+    d.out[m][d.row] = o;
+  }
+}
+
+// Transposed reduction of four groups' accumulators (one row each) across
+// the wave: v[q][e] is lane-partial e of group q. Lanes l and l^32 are merged
+// with v_permlane32_swap (groups q and q+2 trade halves), then l and l^16 with
+// v_permlane16_swap (q and q+1), so 16-lane row r ends up holding group r,
+// which a DPP row sum finishes. 10 ops per value instead of a full 64-lane
+// reduction per group; the combination order of every value is the same for
+// any E, so M = 1 and M = 2 launches give identical bits per row.
+// v_permlane32_swap / v_permlane16_swap of two floats: returns {new a, new b}.
+// Both results are copied out of the builtin's pair into scalars before use.
+__device__ inline void swap32(float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b),
+                                                  false, false);
+  const uint32_t x = r[0], y = r[1];
+  a = __builtin_bit_cast(float, x);
+  b = __builtin_bit_cast(float, y);
+}
+__device__ inline void swap16(float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b),
+                                                  false, false);
+  const uint32_t x = r[0], y = r[1];
+  a = __builtin_bit_cast(float, x);
+  b = __builtin_bit_cast(float, y);
+}
+
+template <int E>
+__device__ inline void reduce4_rows(float (&v)[4][E]) {
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      float a = v[q][e], b = v[q + 2][e];
+      swap32(a, b);
+      v[q][e] = a + b;
+    }
+    float a = v[0][e], b = v[1][e];
+    swap16(a, b);
+    v[0][e] = row16_sum(a + b);
+  }
+}
+
 // Reduce one group's accumulators across the wave and write its outputs.
 template <int M, int NMAT, int ROWS, int EPI>
 __device__ inline void gemv_epilogue(const GemvParams& p, const GemvLoc& loc, int lane,
@@ -334,6 +422,7 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(const GemvParams 
   }
 
   // 2) the first group's weights.
+  constexpr bool kRounds = (ROWS == 1 && EPI != kEpiArgmax);
   GemvBuf<NMAT, ROWS, ITERS> b0, b1;
   uint32_t g = blockIdx.x * kGemvWaves + wid;
   if (g < G) gemv_load<NMAT, ROWS, ITERS, TAIL>(p, g, lane, tail_active, b0);
@@ -377,8 +466,7 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(const GemvParams 
     for (int it = 0; it < ITERS; ++it) gemv_read_x<M>(xs, p.K, it, lane, xr[it]);
   }
 
-  auto process = [&](const GemvBuf<NMAT, ROWS, ITERS>& b, uint32_t grp) {
-    float acc[NMAT][ROWS][M];
+  auto accumulate = [&](const GemvBuf<NMAT, ROWS, ITERS>& b, float (&acc)[NMAT][ROWS][M]) {
 #pragma unroll
     for (int mat = 0; mat < NMAT; ++mat)
 #pragma unroll
@@ -396,18 +484,78 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(const GemvParams 
         gemv_dot_step<M>(b, it, x, acc);
       }
     }
-    gemv_epilogue<M, NMAT, ROWS, EPI>(p, gemv_locate<ROWS>(p, grp), lane, acc);
   };
 
-  // 4) two buffers: compute g while g+W streams in.
-  while (g < G) {
-    if (g + W < G) gemv_load<NMAT, ROWS, ITERS, TAIL>(p, g + W, lane, tail_active, b1);
-    process(b0, g);
-    g += W;
-    if (g >= G) break;
-    if (g + W < G) gemv_load<NMAT, ROWS, ITERS, TAIL>(p, g + W, lane, tail_active, b0);
-    process(b1, g);
-    g += W;
+  if constexpr (kRounds) {
+    // 4) rounds of four groups g, g+W, g+2W, g+3W: two register buffers (the
+    // next group streams in while the current one is dequantised), then one
+    // transposed reduction for the round and a one-lane-per-group epilogue.
+    constexpr int E = NMAT * M;
+    auto step = [&](const GemvBuf<NMAT, 1, ITERS>& cur, GemvBuf<NMAT, 1, ITERS>& nxt, uint32_t gq,
+                    float (&vq)[E]) {
+      float acc[NMAT][1][M];
+      if (gq < G) {
+        if (gq + W < G) gemv_load<NMAT, 1, ITERS, TAIL>(p, gq + W, lane, tail_active, nxt);
+        accumulate(cur, acc);
+      } else {
+#pragma unroll
+        for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+          for (int m = 0; m < M; ++m) acc[mat][0][m] = 0.0f;
+      }
+#pragma unroll
+      for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+        for (int m = 0; m < M; ++m) vq[mat * M + m] = acc[mat][0][m];
+    };
+    while (g < G) {
+      float v[4][E];
+      step(b0, b1, g, v[0]);
+      step(b1, b0, g + W, v[1]);
+      step(b0, b1, g + 2 * W, v[2]);
+      step(b1, b0, g + 3 * W, v[3]);
+      reduce4_rows<E>(v);
+      // 16-lane row q now holds group g + qW; its first lane writes the row.
+      GemvRowDst dst{};
+      bool valid = false;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t gq = g + q * W;
+        if (gq < G) {
+          const GemvLoc loc = gemv_locate<1>(p, gq);
+          const GemvRowDst dq = gemv_row_dst(p.seg[loc.seg], loc.row0);
+          if ((lane >> 4) == q) {
+            dst = dq;
+            valid = true;
+          }
+        }
+      }
+      if (valid && (lane & 15) == 0) {
+        float tot[NMAT][M];
+#pragma unroll
+        for (int mat = 0; mat < NMAT; ++mat)
+#pragma unroll
+          for (int m = 0; m < M; ++m) tot[mat][m] = v[0][mat * M + m];
+        gemv_store_row<M, NMAT, EPI>(dst, tot);
+      }
+      g += 4 * W;
+    }
+  } else {
+    auto process = [&](const GemvBuf<NMAT, ROWS, ITERS>& b, uint32_t grp) {
+      float acc[NMAT][ROWS][M];
+      accumulate(b, acc);
+      gemv_epilogue<M, NMAT, ROWS, EPI>(p, gemv_locate<ROWS>(p, grp), lane, acc);
+    };
+    // 4) two buffers: compute g while g+W streams in.
+    while (g < G) {
+      if (g + W < G) gemv_load<NMAT, ROWS, ITERS, TAIL>(p, g + W, lane, tail_active, b1);
+      process(b0, g);
+      g += W;
+      if (g >= G) break;
+      if (g + W < G) gemv_load<NMAT, ROWS, ITERS, TAIL>(p, g + W, lane, tail_active, b0);
+      process(b1, g);
+      g += W;
+    }
   }
 }
 
