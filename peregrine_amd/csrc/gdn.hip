@@ -13,49 +13,57 @@
 //   per row: d = S*decay; kv = d.k; ob = d.q; delta = (v - kv)*beta;
 //            S = d + k*delta; y = bf16(ob + delta*(k.q))
 //
-// gfx950 layout: one 512-thread block per v-head (8 wave64s = 16 half-waves);
-// half-wave h owns rows 8h..8h+7; lane j of a half-wave holds dk = 4j..4j+3 of
-// each row as a float4, so one wave load moves two 512-byte state rows. Dot
-// products reduce over the 32 lanes of a half-wave. With the fused gated norm
-// the block then holds all 128 outputs of its head and normalises them in place
-// (no second dispatch, no cross-block traffic).
+// gfx950 layout: lane j of a half-wave (32 lanes) holds dk = 4j..4j+3 of a
+// state row as a float4, so one wave load moves two 512-byte state rows; dot
+// products reduce over the 32 lanes of a half-wave. Each block recomputes the
+// head's gates and q/k norms (256 values) and updates RPH rows per half-wave.
+//   * Unfused (the decode model): 256-thread blocks of 16 rows, 8 blocks per
+//     head, 256 blocks in all, so the 4 MiB state stream is spread over the
+//     whole chip. The gated RMSNorm then runs in the out_proj GEMV prologue.
+//   * Fused gated norm: one 512-thread block per head (16 half-waves x 8 rows)
+//     holds all 128 outputs of its head and normalises them in place.
 #include "gdn.hpp"
 
 namespace {
 
 using namespace prg;
 
-constexpr int kGdnThreads = 512;
-constexpr int kRowsPerHalfWave = 8;
+constexpr int kGdnFusedThreads = 512;  // fused gated norm: 16 half-waves x 8 rows = one head
+constexpr int kGdnSplitThreads = 256;  // unfused: 8 half-waves x 2 rows = 16 rows per block
 
 __device__ inline float hsum32(float v) { return group_sum<32>(v); }
 
 // IN_PLACE: state_out is state (each thread reads its rows before writing
-// them); otherwise the two buffers are distinct.
-template <bool IN_PLACE>
-__global__ __launch_bounds__(kGdnThreads) void gdn_decode_kernel(
+// them); otherwise the two buffers are distinct. NT threads, RPH rows per
+// half-wave; FUSE_NORM needs the whole head in one block.
+template <bool IN_PLACE, int NT, int RPH, bool FUSE_NORM>
+__global__ __launch_bounds__(NT) void gdn_decode_kernel(
     float* __restrict__ state, const uint16_t* __restrict__ conv_out, const uint16_t* __restrict__ a,
     const uint16_t* __restrict__ bgate, const float* __restrict__ A_log,
     const uint16_t* __restrict__ dt_bias, uint16_t* __restrict__ y_out,
     const StepScalars* __restrict__ step, uint32_t has_state_host,
     const uint16_t* __restrict__ norm_w, const uint16_t* __restrict__ z, float eps, float* __restrict__ state_out) {
+  constexpr int kRowsPerBlock = (NT / 32) * RPH;
+  constexpr int kBlocksPerHead = kGdnDv / kRowsPerBlock;
+  static_assert(!FUSE_NORM || kBlocksPerHead == 1, "the fused norm needs a whole head per block");
   __shared__ float ysh[kGdnDv];
-  __shared__ float red[kGdnThreads / kWave];
+  __shared__ float red[NT / kWave];
 
-  const uint32_t hv = blockIdx.x;
+  const uint32_t hv = blockIdx.x / kBlocksPerHead;
   const uint32_t hk = hv / (kGdnHv / kGdnHk);
   const int tid = threadIdx.x;
-  const int hw = tid >> 5;   // half-wave 0..15
+  const int hw = tid >> 5;   // half-wave
   const int j = tid & 31;    // lane in half-wave
+  const uint32_t row0 = (blockIdx.x % kBlocksPerHead) * kRowsPerBlock + hw * RPH;  // first dv row
   const bool has_state = step ? (step->rope_pos != 0) : (has_state_host != 0);
 
   // State rows for this half-wave, issued first.
-  float4 S[kRowsPerHalfWave];
-  const size_t row_off = (static_cast<size_t>(hv) * kGdnDv + hw * kRowsPerHalfWave) * kGdnDk;
+  float4 S[RPH];
+  const size_t row_off = (static_cast<size_t>(hv) * kGdnDv + row0) * kGdnDk;
   const float4* srow = reinterpret_cast<const float4*>(state + row_off) + j;
   float4* sout = reinterpret_cast<float4*>((IN_PLACE ? state : state_out) + row_off) + j;
 #pragma unroll
-  for (int r = 0; r < kRowsPerHalfWave; ++r)
+  for (int r = 0; r < RPH; ++r)
     S[r] = has_state ? srow[r * (kGdnDk / 4)] : make_float4(0.f, 0.f, 0.f, 0.f);
 
   // Gates (gating_many_bf16 math, shaders/gated_norm.metal:247-268).
@@ -86,9 +94,9 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_decode_kernel(
   }
   kq = hsum32(kq);
 
-  const uint16_t* vsrc = conv_out + 2 * kGdnKeyDim + hv * kGdnDv + hw * kRowsPerHalfWave;
+  const uint16_t* vsrc = conv_out + 2 * kGdnKeyDim + hv * kGdnDv + row0;
 #pragma unroll
-  for (int r = 0; r < kRowsPerHalfWave; ++r) {
+  for (int r = 0; r < RPH; ++r) {
     const float d[4] = {S[r].x * decay, S[r].y * decay, S[r].z * decay, S[r].w * decay};
     float kvm = 0.f, ob = 0.f;
 #pragma unroll
@@ -103,19 +111,19 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_decode_kernel(
                                          d[2] + kn[2] * delta, d[3] + kn[3] * delta);
     const uint16_t yb = f2bf(ob + delta * kq);
     if (j == 0) {
-      if (norm_w)
-        ysh[hw * kRowsPerHalfWave + r] = bf2f(yb);
+      if constexpr (FUSE_NORM)
+        ysh[row0 + r] = bf2f(yb);
       else
-        y_out[hv * kGdnDv + hw * kRowsPerHalfWave + r] = yb;
+        y_out[hv * kGdnDv + row0 + r] = yb;
     }
   }
-  if (!norm_w) return;
+  if constexpr (!FUSE_NORM) return;
 
   // Gated RMSNorm over the head's 128 outputs (shaders/gated_norm.metal:163-189):
   // out = bf16(y * rsqrt(mean(y^2) + eps) * w * silu(z)).
   __syncthreads();
   const float yv = tid < static_cast<int>(kGdnDv) ? ysh[tid] : 0.0f;
-  const float ss = block_sum<kGdnThreads>(yv * yv, red);
+  const float ss = block_sum<NT>(yv * yv, red);
   const float scale = rsqrtf(ss / static_cast<float>(kGdnDv) + eps);
   if (tid < static_cast<int>(kGdnDv)) {
     const float n = yv * scale * bf2f(norm_w[tid]);
@@ -156,12 +164,30 @@ int launch_gdn_decode(hipStream_t s, float* state, const uint16_t* conv_out, con
                       const uint16_t* b, const float* A_log, const uint16_t* dt_bias,
                       uint16_t* y_out, const StepScalars* step_dev, uint32_t has_state_host,
                       const uint16_t* norm_w, const uint16_t* z, float eps, float* state_out) {
-  if (state_out && state_out != state)
-    hipLaunchKernelGGL(gdn_decode_kernel<false>, dim3(kGdnHv), dim3(kGdnThreads), 0, s, state, conv_out, a, b,
-                       A_log, dt_bias, y_out, step_dev, has_state_host, norm_w, z, eps, state_out);
-  else
-    hipLaunchKernelGGL(gdn_decode_kernel<true>, dim3(kGdnHv), dim3(kGdnThreads), 0, s, state, conv_out, a, b,
-                       A_log, dt_bias, y_out, step_dev, has_state_host, norm_w, z, eps, nullptr);
+  const bool in_place = !(state_out && state_out != state);
+  if (norm_w) {
+    constexpr int kRph = 8;
+    const dim3 grid(kGdnHv);
+    if (in_place)
+      hipLaunchKernelGGL((gdn_decode_kernel<true, kGdnFusedThreads, kRph, true>), grid, dim3(kGdnFusedThreads), 0, s,
+                         state, conv_out, a, b, A_log, dt_bias, y_out, step_dev, has_state_host, norm_w, z, eps,
+                         nullptr);
+    else
+      hipLaunchKernelGGL((gdn_decode_kernel<false, kGdnFusedThreads, kRph, true>), grid, dim3(kGdnFusedThreads), 0,
+                         s, state, conv_out, a, b, A_log, dt_bias, y_out, step_dev, has_state_host, norm_w, z, eps,
+                         state_out);
+  } else {
+    constexpr int kRph = 2;
+    const dim3 grid(kGdnHv * (kGdnDv / ((kGdnSplitThreads / 32) * kRph)));
+    if (in_place)
+      hipLaunchKernelGGL((gdn_decode_kernel<true, kGdnSplitThreads, kRph, false>), grid, dim3(kGdnSplitThreads), 0,
+                         s, state, conv_out, a, b, A_log, dt_bias, y_out, step_dev, has_state_host, nullptr, nullptr,
+                         0.0f, nullptr);
+    else
+      hipLaunchKernelGGL((gdn_decode_kernel<false, kGdnSplitThreads, kRph, false>), grid, dim3(kGdnSplitThreads), 0,
+                         s, state, conv_out, a, b, A_log, dt_bias, y_out, step_dev, has_state_host, nullptr, nullptr,
+                         0.0f, state_out);
+  }
   PRG_CHECK_LAUNCH("gated_delta_decode");
   return PRG_OK;
 }

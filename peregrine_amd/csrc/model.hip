@@ -17,7 +17,7 @@
 //   input_layernorm / post_attention_layernorm / final norm -> GEMV prologue
 //   conv1d_silu_decode -> in_proj_qkv GEMV epilogue
 //   add_rmsnorm's add (bf16(x + bf16(attn))) -> out_proj / o_proj residual epilogue
-//   rmsnorm_gated -> gated-delta kernel
+//   rmsnorm_gated -> out_proj GEMV prologue (per-head norm x silu(z))
 // giving 5 launches per GDN layer, 7 per attention layer and 3 for embed + tail.
 // One token's launches are captured once into a HIP graph; the token, positions
 // and sequence length live in device memory (DecodeCtl) and are advanced by the
@@ -245,13 +245,13 @@ uint32_t total_rows(const GemvParams& p) {
 }
 }  // namespace
 
-int run_gemv(hipStream_t s, GemvParams& p, int epi, bool norm, const char* name) {
+int run_gemv(hipStream_t s, GemvParams& p, int epi, int norm, const char* name) {
   int M = p.x[1] ? 2 : 1;
   const int rows = gemv_rows_per_wave(total_rows(p), p.K, epi, M);
   return launch_q4_gemv(s, p, M, rows, epi, norm, name);
 }
 
-// GDN layer: norm+in_proj(+conv) -> recurrence+gated norm -> out_proj + residual.
+// GDN layer: norm+in_proj(+conv) -> recurrence -> gated norm+out_proj + residual.
 int encode_linear_attention(PrgModel* m, PrgModelState* st, const DecoderLayer& L, const GdnIO& io,
                             const uint16_t* x, uint16_t* h, const StepScalars* step) {
   const LinearAttentionBlock& b = L.lin;
@@ -265,17 +265,23 @@ int encode_linear_attention(PrgModel* m, PrgModelState* st, const DecoderLayer& 
   p.seg[0].conv_state_out = io.conv_out;
   p.seg[0].conv_w = b.conv_weight;
   p.seg[0].conv_dim = kGdnConvDim;
-  add_seg(p, b.in_z, st->zbuf);
+  add_seg(p, b.in_z, nullptr);
+  p.seg[1].silu_out = st->zsilu;
   add_seg(p, b.in_a, st->abuf);
   add_seg(p, b.in_b, st->bbuf);
-  if (int rc = run_gemv(s, p, kEpiPlain, true, "linear_attn.in_proj")) return rc;
+  if (int rc = run_gemv(s, p, kEpiPlain, kNormRms, "linear_attn.in_proj")) return rc;
+  // Recurrence -> raw y (bf16); the gated RMSNorm runs in the out_proj
+  // GEMV's prologue (per 128-wide head, gate z from in_proj).
   if (int rc = launch_gdn_decode(s, io.recur_in, st->conv_out, st->abuf, st->bbuf, b.a_log, b.dt_bias, st->gated,
-                                 step, 0, b.norm_weight, st->zbuf, c.rms_eps, io.recur_out))
+                                 step, 0, nullptr, nullptr, 0.0f, io.recur_out))
     return rc;
   GemvParams o = gemv_params(st->gated, kGdnValDim);
+  o.norm_w = b.norm_weight;
+  o.eps = c.rms_eps;
+  o.gz[0] = st->zsilu;
   add_seg(o, b.out_proj, h);
   o.seg[0].res[0] = x;
-  return run_gemv(s, o, kEpiResidual, false, "linear_attn.out_proj");
+  return run_gemv(s, o, kEpiResidual, kNormGated, "linear_attn.out_proj");
 }
 
 // Attention layer: norm+q/k/v -> prepare/append -> flash decode -> o_proj + residual.
@@ -290,7 +296,7 @@ int encode_full_attention(PrgModel* m, PrgModelState* st, const DecoderLayer& L,
   add_seg(p, b.q_proj, st->qp);
   add_seg(p, b.k_proj, st->kbuf);
   add_seg(p, b.v_proj, st->vbuf);
-  if (int rc = run_gemv(s, p, kEpiPlain, true, "self_attn.qkv_proj")) return rc;
+  if (int rc = run_gemv(s, p, kEpiPlain, kNormRms, "self_attn.qkv_proj")) return rc;
   AttnPrepareArgs pa{st->qp, b.q_norm, st->kbuf, st->vbuf, b.k_norm, st->qbuf, st->gatebuf, ls.cache_k, ls.cache_v,
                      st->stride, 0, 0, step};
   if (int rc = launch_attn_prepare(s, pa)) return rc;
@@ -310,7 +316,7 @@ int encode_full_attention(PrgModel* m, PrgModelState* st, const DecoderLayer& L,
   GemvParams o = gemv_params(st->ctx, kAttnQHeads * kAttnHeadDim);
   add_seg(o, b.o_proj, h);
   o.seg[0].res[0] = x;
-  return run_gemv(s, o, kEpiResidual, false, "self_attn.o_proj");
+  return run_gemv(s, o, kEpiResidual, kNormNone, "self_attn.o_proj");
 }
 
 // MLP for M rows: post_attention_layernorm + gate/up SiLU -> down + residual.
@@ -329,7 +335,7 @@ int encode_mlp(PrgModel* m, PrgModelState* st, const DecoderLayer& L, int M, con
     p.x[1] = h[1];
     p.seg[0].out[1] = inter[1];
   }
-  if (int rc = run_gemv(s, p, kEpiSiluGate, true, "mlp.gate_up")) return rc;
+  if (int rc = run_gemv(s, p, kEpiSiluGate, kNormRms, "mlp.gate_up")) return rc;
   GemvParams d = gemv_params(inter[0], c.intermediate);
   add_seg(d, L.mlp.down_proj, out[0]);
   d.seg[0].res[0] = h[0];
@@ -338,7 +344,7 @@ int encode_mlp(PrgModel* m, PrgModelState* st, const DecoderLayer& L, int M, con
     d.seg[0].out[1] = out[1];
     d.seg[0].res[1] = h[1];
   }
-  return run_gemv(s, d, kEpiResidual, false, "mlp.down_proj");
+  return run_gemv(s, d, kEpiResidual, kNormNone, "mlp.down_proj");
 }
 
 namespace {
@@ -369,7 +375,7 @@ int encode_token(PrgModel* m, PrgModelState* st, bool with_head) {
   add_seg(p, m->lm_head, nullptr);
   p.seg[0].pval[0] = st->pval;
   p.seg[0].pidx[0] = st->pidx;
-  if (int rc = launch_q4_gemv(s, p, 1, 8, kEpiArgmax, true, "lm_head.argmax")) return rc;
+  if (int rc = launch_q4_gemv(s, p, 1, 8, kEpiArgmax, kNormRms, "lm_head.argmax")) return rc;
   return launch_argmax_advance(s, st->pval, st->pidx, m->cfg.vocab / 8, st->ctl, st->prompt, st->predictions);
 }
 
@@ -515,7 +521,7 @@ int prg_model_state_create(PrgModel* model, uint32_t max_seq, PrgModelState** ou
   items.push_back({"ws.hA", bf * c.hidden, reinterpret_cast<void**>(&st->hA)});
   items.push_back({"ws.hB", bf * c.hidden, reinterpret_cast<void**>(&st->hB)});
   items.push_back({"ws.conv_out", bf * kGdnConvDim, reinterpret_cast<void**>(&st->conv_out)});
-  items.push_back({"ws.z", bf * kGdnValDim, reinterpret_cast<void**>(&st->zbuf)});
+  items.push_back({"ws.z_silu", sizeof(float) * kGdnValDim, reinterpret_cast<void**>(&st->zsilu)});
   items.push_back({"ws.a", bf * kGdnHv, reinterpret_cast<void**>(&st->abuf)});
   items.push_back({"ws.b", bf * kGdnHv, reinterpret_cast<void**>(&st->bbuf)});
   items.push_back({"ws.gated", bf * kGdnValDim, reinterpret_cast<void**>(&st->gated)});

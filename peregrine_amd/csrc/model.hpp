@@ -154,7 +154,8 @@ struct PrgModelState {
   size_t gdn_bytes = 0;
   // decode workspace
   uint16_t *hA = nullptr, *hB = nullptr;
-  uint16_t *conv_out = nullptr, *zbuf = nullptr, *abuf = nullptr, *bbuf = nullptr, *gated = nullptr;
+  uint16_t *conv_out = nullptr, *abuf = nullptr, *bbuf = nullptr, *gated = nullptr;
+  float* zsilu = nullptr;  // silu(z) of the GDN gate, f32 (feeds the gated norm)
   uint16_t *qp = nullptr, *kbuf = nullptr, *vbuf = nullptr, *qbuf = nullptr, *gatebuf = nullptr, *ctx = nullptr;
   float* partials = nullptr;
   uint16_t* inter = nullptr;
@@ -194,7 +195,7 @@ namespace prg {
 // ------------------------------------------------- single-token encoders ---
 GemvParams gemv_params(const uint16_t* x, uint32_t K);
 void add_seg(GemvParams& p, const Q4Linear& l, uint16_t* out);
-int run_gemv(hipStream_t s, GemvParams& p, int epi, bool norm, const char* name);
+int run_gemv(hipStream_t s, GemvParams& p, int epi, int norm, const char* name);
 
 // Where a layer's GDN state is read and written for one token (in == out for
 // the ordinary in-place update).

@@ -105,7 +105,7 @@ int encode_mtp_step(PrgModel* m, PrgModelState* st, const uint32_t* token_dev, c
   if (int rc = launch_rmsnorm(s, hidden, t.pre_fc_norm_hidden, st->fc_in + H, H, 1, c.rms_eps)) return rc;
   GemvParams f = gemv_params(st->fc_in, 2 * H);
   add_seg(f, t.fc, st->mtp_h);
-  if (int rc = run_gemv(s, f, kEpiPlain, false, "mtp.fc")) return rc;
+  if (int rc = run_gemv(s, f, kEpiPlain, kNormNone, "mtp.fc")) return rc;
   // the drafter's decoder layer on its own KV cache
   if (int rc = encode_full_attention(m, st, t.layer, st->mtp, st->mtp_h, st->mtp_x, step)) return rc;
   const uint16_t* h[1] = {st->mtp_x};
@@ -119,7 +119,7 @@ int encode_mtp_step(PrgModel* m, PrgModelState* st, const uint32_t* token_dev, c
   add_seg(p, m->lm_head, nullptr);
   p.seg[0].pval[0] = st->pval;
   p.seg[0].pidx[0] = st->pidx;
-  if (int rc = launch_q4_gemv(s, p, 1, 8, kEpiArgmax, true, "mtp.lm_head.argmax")) return rc;
+  if (int rc = launch_q4_gemv(s, p, 1, 8, kEpiArgmax, kNormRms, "mtp.lm_head.argmax")) return rc;
   return launch_argmax_pairs(s, st->pval, st->pidx, c.vocab / 8, out_token);
 }
 
@@ -167,7 +167,7 @@ int encode_verify(PrgModel* m, PrgModelState* st) {
   p.seg[0].pidx[0] = st->pidx;
   p.seg[0].pval[1] = st->pval2;
   p.seg[0].pidx[1] = st->pidx2;
-  if (int rc = launch_q4_gemv(s, p, 2, 8, kEpiArgmax, false, "lm_head.argmax2")) return rc;
+  if (int rc = launch_q4_gemv(s, p, 2, 8, kEpiArgmax, kNormNone, "lm_head.argmax2")) return rc;
   if (int rc = launch_argmax_pairs(s, st->pval, st->pidx, c.vocab / 8, &sc->verify)) return rc;
   return launch_argmax_pairs(s, st->pval2, st->pidx2, c.vocab / 8, &sc->bonus);
 }

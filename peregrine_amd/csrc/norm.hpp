@@ -42,6 +42,22 @@ __device__ inline uint4 rms_apply(uint4 v, uint4 w, float scale) {
   return make_uint4(o[0], o[1], o[2], o[3]);
 }
 
+// bf16(((y * scale) * w) * sz) for 8 values, sz = silu(z) in f32: the gated
+// RMSNorm of one GDN head row (reference shaders/gated_norm.metal:163-189).
+__device__ inline uint4 gated_rms_apply(uint4 v, uint4 w, float4 z0, float4 z1, float scale) {
+  const uint32_t d[4] = {v.x, v.y, v.z, v.w};
+  const uint32_t e[4] = {w.x, w.y, w.z, w.w};
+  const float g[8] = {z0.x, z0.y, z0.z, z0.w, z1.x, z1.y, z1.z, z1.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t lo = f2bf(bf_lo(d[i]) * scale * bf_lo(e[i]) * g[2 * i]);
+    const uint32_t hi = f2bf(bf_hi(d[i]) * scale * bf_hi(e[i]) * g[2 * i + 1]);
+    o[i] = lo | (hi << 16);
+  }
+  return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
 int launch_rmsnorm(hipStream_t s, const uint16_t* x, const uint16_t* w, uint16_t* out,
                    uint32_t hidden, uint32_t rows, float eps);
 int launch_embedding(hipStream_t s, const uint32_t* w, const uint16_t* sc, const uint16_t* bi,

@@ -41,7 +41,7 @@ int gemv_rows_per_wave(uint32_t total_rows, uint32_t K, int epi, int M) {
   return rows;
 }
 
-int launch_q4_gemv(hipStream_t stream, GemvParams& p, int M, int rows, int epi, bool norm,
+int launch_q4_gemv(hipStream_t stream, GemvParams& p, int M, int rows, int epi, int norm,
                    const char* name) {
   if (p.K == 0 || p.K % 512 != 0)
     return set_error(PRG_ERR_INVALID_ARG, "%s: in_dim %u must be a positive multiple of 512", name, p.K);
@@ -65,17 +65,25 @@ int launch_q4_gemv(hipStream_t stream, GemvParams& p, int M, int rows, int epi, 
   p.total_groups = groups;
   const size_t lds = static_cast<size_t>(M) * p.K * sizeof(uint16_t);
   int rc;
+  if (norm == kNormGated && (p.K % kGdnDv != 0 || p.norm_w == nullptr || p.gz[0] == nullptr ||
+                             (M == 2 && p.gz[1] == nullptr)))
+    return set_error(PRG_ERR_INVALID_ARG, "%s: gated norm needs K %% 128 == 0, norm_w and gz", name);
   if (epi == kEpiPlain)
-    rc = norm ? launch_m<kEpiPlain, true>(stream, p, M, rows, iters, lds)
-              : launch_m<kEpiPlain, false>(stream, p, M, rows, iters, lds);
+    rc = norm == kNormRms    ? launch_m<kEpiPlain, kNormRms>(stream, p, M, rows, iters, lds)
+         : norm == kNormNone ? launch_m<kEpiPlain, kNormNone>(stream, p, M, rows, iters, lds)
+                             : -1;
   else if (epi == kEpiResidual)
-    rc = norm ? -1 : launch_m<kEpiResidual, false>(stream, p, M, rows, iters, lds);
+    rc = norm == kNormGated  ? launch_m<kEpiResidual, kNormGated>(stream, p, M, rows, iters, lds)
+         : norm == kNormNone ? launch_m<kEpiResidual, kNormNone>(stream, p, M, rows, iters, lds)
+                             : -1;
   else if (epi == kEpiSiluGate)
-    rc = norm ? launch_m<kEpiSiluGate, true>(stream, p, M, rows, iters, lds)
-              : launch_m<kEpiSiluGate, false>(stream, p, M, rows, iters, lds);
+    rc = norm == kNormRms    ? launch_m<kEpiSiluGate, kNormRms>(stream, p, M, rows, iters, lds)
+         : norm == kNormNone ? launch_m<kEpiSiluGate, kNormNone>(stream, p, M, rows, iters, lds)
+                             : -1;
   else
-    rc = norm ? launch_m<kEpiArgmax, true>(stream, p, M, rows, iters, lds)
-              : launch_m<kEpiArgmax, false>(stream, p, M, rows, iters, lds);
+    rc = norm == kNormRms    ? launch_m<kEpiArgmax, kNormRms>(stream, p, M, rows, iters, lds)
+         : norm == kNormNone ? launch_m<kEpiArgmax, kNormNone>(stream, p, M, rows, iters, lds)
+                             : -1;
   if (rc != 0) return set_error(PRG_ERR_INVALID_ARG, "%s: no kernel for M=%d rows=%d iters=%d", name, M, rows, iters);
   PRG_CHECK_LAUNCH(name);
   return PRG_OK;
@@ -280,7 +288,7 @@ int prg_q4_gemv_bf16(void* stream, const uint16_t* x, const uint32_t* w, const u
       p.seg[0].out[m] = y + static_cast<size_t>(t + m) * out_dim;
     }
     const int rows = prg::gemv_rows_per_wave(out_dim, in_dim, prg::kEpiPlain, M);
-    if (int rc = launch_q4_gemv(s, p, M, rows, prg::kEpiPlain, false, name)) return rc;
+    if (int rc = launch_q4_gemv(s, p, M, rows, prg::kEpiPlain, prg::kNormNone, name)) return rc;
   }
   return PRG_OK;
 }
@@ -303,7 +311,7 @@ int prg_q4_gemv_residual_add_bf16(void* stream, const uint16_t* x, const uint32_
       p.seg[0].res[m] = residual + static_cast<size_t>(t + m) * out_dim;
     }
     const int rows = prg::gemv_rows_per_wave(out_dim, in_dim, prg::kEpiResidual, M);
-    if (int rc = launch_q4_gemv(s, p, M, rows, prg::kEpiResidual, false, name)) return rc;
+    if (int rc = launch_q4_gemv(s, p, M, rows, prg::kEpiResidual, prg::kNormNone, name)) return rc;
   }
   return PRG_OK;
 }
@@ -324,7 +332,7 @@ int prg_q4_gemv2_residual_add_bf16(void* stream, const uint16_t* x0, const uint1
   p.seg[0].res[0] = residual0;
   p.seg[0].res[1] = residual1;
   const int rows = prg::gemv_rows_per_wave(out_dim, in_dim, prg::kEpiResidual, 2);
-  return launch_q4_gemv(prg::as_stream(stream), p, 2, rows, prg::kEpiResidual, false, name);
+  return launch_q4_gemv(prg::as_stream(stream), p, 2, rows, prg::kEpiResidual, prg::kNormNone, name);
 }
 
 int prg_q4_gemv_silu_gate_bf16(void* stream, const uint16_t* x, const uint32_t* gate_w,
@@ -341,7 +349,7 @@ int prg_q4_gemv_silu_gate_bf16(void* stream, const uint16_t* x, const uint32_t* 
   p.x[0] = x;
   p.seg[0].out[0] = out;
   const int rows = prg::gemv_rows_per_wave(out_dim, in_dim, prg::kEpiSiluGate, 1);
-  return launch_q4_gemv(prg::as_stream(stream), p, 1, rows, prg::kEpiSiluGate, false, name);
+  return launch_q4_gemv(prg::as_stream(stream), p, 1, rows, prg::kEpiSiluGate, prg::kNormNone, name);
 }
 
 int prg_q4_gemv_silu_gate2_bf16(void* stream, const uint16_t* x0, const uint16_t* x1,
@@ -361,7 +369,7 @@ int prg_q4_gemv_silu_gate2_bf16(void* stream, const uint16_t* x0, const uint16_t
   p.seg[0].out[0] = out0;
   p.seg[0].out[1] = out1;
   const int rows = prg::gemv_rows_per_wave(out_dim, in_dim, prg::kEpiSiluGate, 2);
-  return launch_q4_gemv(prg::as_stream(stream), p, 2, rows, prg::kEpiSiluGate, false, name);
+  return launch_q4_gemv(prg::as_stream(stream), p, 2, rows, prg::kEpiSiluGate, prg::kNormNone, name);
 }
 
 int prg_q4_gemv_norm_bf16(void* stream, const uint16_t* x, const uint16_t* norm_weight, float eps,
@@ -376,7 +384,7 @@ int prg_q4_gemv_norm_bf16(void* stream, const uint16_t* x, const uint16_t* norm_
   p.eps = eps;
   p.seg[0].out[0] = y;
   const int rows = prg::gemv_rows_per_wave(out_dim, in_dim, prg::kEpiPlain, 1);
-  return launch_q4_gemv(prg::as_stream(stream), p, 1, rows, prg::kEpiPlain, true, name);
+  return launch_q4_gemv(prg::as_stream(stream), p, 1, rows, prg::kEpiPlain, prg::kNormRms, name);
 }
 
 int prg_q4_gemv_silu_gate_norm_bf16(void* stream, const uint16_t* x, const uint16_t* norm_weight, float eps,
@@ -395,7 +403,7 @@ int prg_q4_gemv_silu_gate_norm_bf16(void* stream, const uint16_t* x, const uint1
   p.eps = eps;
   p.seg[0].out[0] = out;
   const int rows = prg::gemv_rows_per_wave(out_dim, in_dim, prg::kEpiSiluGate, 1);
-  return launch_q4_gemv(prg::as_stream(stream), p, 1, rows, prg::kEpiSiluGate, true, name);
+  return launch_q4_gemv(prg::as_stream(stream), p, 1, rows, prg::kEpiSiluGate, prg::kNormRms, name);
 }
 
 int prg_q4_gemv_argmax_partial_bf16(void* stream, const uint16_t* x, const uint32_t* w,
@@ -409,7 +417,7 @@ int prg_q4_gemv_argmax_partial_bf16(void* stream, const uint16_t* x, const uint3
   p.x[0] = x;
   p.seg[0].pval[0] = partial_values;
   p.seg[0].pidx[0] = partial_indices;
-  return launch_q4_gemv(prg::as_stream(stream), p, 1, 8, prg::kEpiArgmax, false, name);
+  return launch_q4_gemv(prg::as_stream(stream), p, 1, 8, prg::kEpiArgmax, prg::kNormNone, name);
 }
 
 int prg_q4_gemv_argmax2_partial_bf16(void* stream, const uint16_t* x0, const uint16_t* x1,
@@ -429,7 +437,7 @@ int prg_q4_gemv_argmax2_partial_bf16(void* stream, const uint16_t* x0, const uin
   p.seg[0].pidx[0] = partial_indices0;
   p.seg[0].pval[1] = partial_values1;
   p.seg[0].pidx[1] = partial_indices1;
-  return launch_q4_gemv(prg::as_stream(stream), p, 2, 8, prg::kEpiArgmax, false, name);
+  return launch_q4_gemv(prg::as_stream(stream), p, 2, 8, prg::kEpiArgmax, prg::kNormNone, name);
 }
 
 int prg_argmax_pairs_f32_u32(void* stream, const float* values, const uint32_t* indices,

@@ -38,6 +38,13 @@ constexpr int kGemvKStep = 2048;  // K values one wave consumes per step
 constexpr int kGemvMaxIters = 8;  // in_dim <= 16384
 constexpr int kGemvMaxSegs = 4;
 
+// Prologue applied to x while it is staged.
+enum GemvNorm : int {
+  kNormNone = 0,
+  kNormRms = 1,    // RMSNorm over the whole row with norm_w [K] (rmsnorm.metal:80-116)
+  kNormGated = 2,  // per 128-wide head: RMSNorm with norm_w [128], times gz = silu(z) (gated_norm.metal:163-189)
+};
+
 enum GemvEpi : int {
   kEpiPlain = 0,     // out = bf16(dot)
   kEpiResidual = 1,  // out = bf16(float(bf16(dot)) + float(res))
@@ -61,6 +68,9 @@ struct GemvSeg {
   float* conv_state_out;      // rolled state destination (nullptr: in place)
   const uint16_t* conv_w;     // bf16 [conv_dim, 4]
   uint32_t conv_dim;
+  // Optional SiLU epilogue (plain epilogue, M == 1): row c writes
+  // silu(bf16(dot)) in f32 here instead of bf16 to out (the GDN z gate).
+  float* silu_out;
   uint32_t rows;              // output rows of this segment
   uint32_t block_begin;       // first group index of this segment (set by the launcher)
 };
@@ -69,6 +79,7 @@ struct GemvParams {
   GemvSeg seg[kGemvMaxSegs];
   const uint16_t* x[2];       // activation rows (M of them)
   const uint16_t* norm_w;     // fused RMSNorm weight (NORM variants)
+  const float* gz[2];         // per activation row: silu(z) in f32 for kNormGated
   float eps;
   uint32_t K;
   uint32_t nseg;
@@ -246,6 +257,7 @@ __device__ inline void gemv_dot_step(const GemvBuf<NMAT, ROWS, ITERS>& b, int it
 // Where one finished row goes (all epilogues but argmax), selected per lane.
 struct GemvRowDst {
   uint16_t* out[2];
+  float* silu_out;
   const uint16_t* res[2];
   float* conv_state;
   float* conv_state_out;
@@ -258,6 +270,7 @@ __device__ inline GemvRowDst gemv_row_dst(const GemvSeg& sg, uint32_t row) {
   GemvRowDst d;
   d.out[0] = sg.out[0];
   d.out[1] = sg.out[1];
+  d.silu_out = sg.silu_out;
   d.res[0] = sg.res[0];
   d.res[1] = sg.res[1];
   d.conv_state = sg.conv_state;
@@ -271,6 +284,11 @@ __device__ inline GemvRowDst gemv_row_dst(const GemvSeg& sg, uint32_t row) {
 // Epilogue of one row: tot[mat][m] are its finished dot products.
 template <int M, int NMAT, int EPI>
 __device__ inline void gemv_store_row(const GemvRowDst& d, const float (&tot)[NMAT][M]) {
+  if (EPI == kEpiPlain && M == 1 && d.silu_out != nullptr) {
+    const float zb = round_bf(tot[0][0]);
+    d.silu_out[d.row] = zb / (1.0f + expf(-zb));
+    return;
+  }
 #pragma unroll
   for (int m = 0; m < M; ++m) {
     uint16_t o;
@@ -369,6 +387,11 @@ __device__ inline void gemv_epilogue(const GemvParams& p, const GemvLoc& loc, in
       for (int m = 0; m < M; ++m) {
         uint16_t o;
         if constexpr (EPI == kEpiPlain) {
+          if (M == 1 && sg.silu_out != nullptr) {
+            const float zb = round_bf(tot[0][r][m]);
+            sg.silu_out[row] = zb / (1.0f + expf(-zb));
+            continue;
+          }
           if (M == 1 && sg.conv_state != nullptr)
             o = conv1d_silu_step(sg.conv_state, sg.conv_state_out ? sg.conv_state_out : sg.conv_state, sg.conv_w,
                                  sg.conv_dim, row, round_bf(tot[0][r][m]));
@@ -395,7 +418,7 @@ __device__ inline void gemv_epilogue(const GemvParams& p, const GemvLoc& loc, in
 // (and fused-norm weights) are loaded before any weight so they return first;
 // the norm and LDS staging then run while the first group streams in. With XREG the lane's activation pairs for every
 // K-step stay in registers for the whole kernel.
-template <int M, int ROWS, int ITERS, int EPI, bool NORM, bool TAIL>
+template <int M, int ROWS, int ITERS, int EPI, int NORM, bool TAIL>
 __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(const GemvParams p) {
   constexpr int NMAT = (EPI == kEpiSiluGate) ? 2 : 1;
   constexpr bool XREG = ITERS * M <= 4;  // <= 64 VGPRs of activation pairs
@@ -409,16 +432,33 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(const GemvParams 
   const bool tail_active = !TAIL || lane < static_cast<int>(p.tail_lanes);
   const uint32_t n8 = p.K / 8;
 
-  // 1) activations (+ norm weights): one uint4 (8 values) per thread per K-step.
-  uint4 xv[M][ITERS];
-  uint4 nw[NORM ? ITERS : 1];
+  // 1) activations (+ norm weights, + gates): one uint4 (8 values) per thread
+  // per K-step.
+  constexpr int XU = (ITERS * (kGemvKStep / 8) + kGemvThreads - 1) / kGemvThreads;  // uint4 units per thread
+  uint4 xv[M][XU];
+  uint4 nw[NORM != kNormNone ? XU : 1];
+  float4 zv[NORM == kNormGated ? M : 1][NORM == kNormGated ? XU : 1][2];
 #pragma unroll
-  for (int it = 0; it < ITERS; ++it) {
+  for (int it = 0; it < XU; ++it) {
     const uint32_t gi = it * kGemvThreads + threadIdx.x;
 #pragma unroll
     for (int m = 0; m < M; ++m)
       xv[m][it] = gi < n8 ? reinterpret_cast<const uint4*>(p.x[m])[gi] : make_uint4(0, 0, 0, 0);
-    if constexpr (NORM) nw[it] = gi < n8 ? reinterpret_cast<const uint4*>(p.norm_w)[gi] : make_uint4(0, 0, 0, 0);
+    if constexpr (NORM == kNormRms)
+      nw[it] = gi < n8 ? reinterpret_cast<const uint4*>(p.norm_w)[gi] : make_uint4(0, 0, 0, 0);
+    if constexpr (NORM == kNormGated) {
+      // 8 values of head gi / 16: weight entries 8 (gi % 16) .. +8 of the [128] vector.
+      nw[it] = reinterpret_cast<const uint4*>(p.norm_w)[gi % (kGdnDv / 8)];
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        zv[m][it][0] = zv[m][it][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (gi < n8) {
+          const float4* zp = reinterpret_cast<const float4*>(p.gz[m]) + 2 * gi;
+          zv[m][it][0] = zp[0];
+          zv[m][it][1] = zp[1];
+        }
+      }
+    }
   }
 
   // 2) the first group's weights.
@@ -431,10 +471,10 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(const GemvParams 
 #pragma unroll
   for (int m = 0; m < M; ++m) {
     float scale = 1.0f;
-    if constexpr (NORM) {
+    if constexpr (NORM == kNormRms) {
       float ss = 0.0f;
 #pragma unroll
-      for (int it = 0; it < ITERS; ++it) {
+      for (int it = 0; it < XU; ++it) {
         const uint32_t d[4] = {xv[m][it].x, xv[m][it].y, xv[m][it].z, xv[m][it].w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -448,10 +488,22 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(const GemvParams 
     }
     uint4* dst = reinterpret_cast<uint4*>(xs + m * (p.K / 2));
 #pragma unroll
-    for (int it = 0; it < ITERS; ++it) {
+    for (int it = 0; it < XU; ++it) {
       const uint32_t gi = it * kGemvThreads + threadIdx.x;
-      if (gi < n8) {
-        if constexpr (NORM)
+      if constexpr (NORM == kNormGated) {
+        // The 16 lanes of a DPP row hold the 128 values of one head.
+        float ss = 0.0f;
+        const uint32_t d[4] = {xv[m][it].x, xv[m][it].y, xv[m][it].z, xv[m][it].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float a = bf_lo(d[i]), b = bf_hi(d[i]);
+          ss += a * a;
+          ss += b * b;
+        }
+        const float hscale = rsqrtf(row16_sum(ss) / static_cast<float>(kGdnDv) + p.eps);
+        if (gi < n8) dst[gi] = permute_pairs(gated_rms_apply(xv[m][it], nw[it], zv[m][it][0], zv[m][it][1], hscale));
+      } else if (gi < n8) {
+        if constexpr (NORM == kNormRms)
           dst[gi] = permute_pairs(rms_apply(xv[m][it], nw[it], scale));
         else
           dst[gi] = permute_pairs(xv[m][it]);
@@ -562,13 +614,13 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(const GemvParams 
 // ------------------------------------------------------------- host ----------
 // Instantiated per epilogue in q4_gemv_inst_*.hip. Returns 0, or -1 when no
 // kernel variant exists for (M, rows, iters).
-template <int EPI, bool NORM>
+template <int EPI, int NORM>
 int launch_m(hipStream_t s, const GemvParams& p, int M, int rows, int iters, size_t lds);
 
 // Launch one GEMV-family kernel. Segment block ranges are filled in here.
 // Returns a PRG_ERR_* code.
 int launch_q4_gemv(hipStream_t stream, GemvParams& p, int M, int rows_per_wave, int epi,
-                   bool norm, const char* name);
+                   int norm, const char* name);
 
 // Rows per wave picked for a launch of `total_rows` rows at in_dim K.
 int gemv_rows_per_wave(uint32_t total_rows, uint32_t K, int epi, int M);

@@ -2,5 +2,5 @@
 #include "q4_gemv_launch.hpp"
 
 namespace prg {
-template int launch_m<kEpiResidual, false>(hipStream_t, const GemvParams&, int, int, int, size_t);
+template int launch_m<kEpiResidual, kNormNone>(hipStream_t, const GemvParams&, int, int, int, size_t);
 }  // namespace prg

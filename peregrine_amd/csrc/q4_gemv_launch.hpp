@@ -59,14 +59,15 @@ inline int max_resident_blocks(const void* fn, size_t lds) {
   return total;
 }
 
-template <int M, int ROWS, int ITERS, int EPI, bool NORM, bool TAIL>
+template <int M, int ROWS, int ITERS, int EPI, int NORM, bool TAIL>
 int launch_one_t(hipStream_t s, const GemvParams& p, size_t lds) {
   const void* fn = reinterpret_cast<const void*>(&q4_gemv_kernel<M, ROWS, ITERS, EPI, NORM, TAIL>);
   const uint32_t resident = static_cast<uint32_t>(max_resident_blocks(fn, lds));
   // A grid of a few blocks per CU (not the occupancy maximum) gives every
   // wave several groups, so its next group's loads overlap the dequant. For
   // small matrices more waves with partly empty rounds beat fewer full ones
-  // (measured: 4096 x 4096 takes 5.5 us at 3 blocks/CU, 6.4 us at 1).
+  // (measured: 4096 x 4096 takes 5.5 us at 3 blocks/CU, 6.4 us at 1). One
+  // 768-thread block per CU (x staged once per CU) spills at K = 12288.
   const uint32_t want = (p.total_groups + kGemvWaves - 1) / kGemvWaves;
   const uint32_t cap = std::min<uint32_t>(resident, static_cast<uint32_t>(device_cus() * gemv_blocks_per_cu()));
   const uint32_t blocks = std::max<uint32_t>(1, std::min<uint32_t>(want, cap));
@@ -75,13 +76,13 @@ int launch_one_t(hipStream_t s, const GemvParams& p, size_t lds) {
 }
 
 // K a multiple of 2048 (every model shape) takes the branch-free variant.
-template <int M, int ROWS, int ITERS, int EPI, bool NORM>
+template <int M, int ROWS, int ITERS, int EPI, int NORM>
 int launch_one(hipStream_t s, const GemvParams& p, size_t lds) {
   if (p.tail_lanes == 64) return launch_one_t<M, ROWS, ITERS, EPI, NORM, false>(s, p, lds);
   return launch_one_t<M, ROWS, ITERS, EPI, NORM, true>(s, p, lds);
 }
 
-template <int M, int ROWS, int EPI, bool NORM>
+template <int M, int ROWS, int EPI, int NORM>
 int launch_iters(hipStream_t s, const GemvParams& p, int iters, size_t lds) {
   switch (iters) {
     case 1: return launch_one<M, ROWS, 1, EPI, NORM>(s, p, lds);
@@ -94,7 +95,7 @@ int launch_iters(hipStream_t s, const GemvParams& p, int iters, size_t lds) {
   }
 }
 
-template <int M, int EPI, bool NORM>
+template <int M, int EPI, int NORM>
 int launch_rows(hipStream_t s, const GemvParams& p, int rows, int iters, size_t lds) {
   if constexpr (EPI == kEpiArgmax) {
     return launch_iters<M, 8, EPI, NORM>(s, p, iters, lds);
@@ -108,7 +109,7 @@ int launch_rows(hipStream_t s, const GemvParams& p, int rows, int iters, size_t 
   }
 }
 
-template <int EPI, bool NORM>
+template <int EPI, int NORM>
 int launch_m_impl(hipStream_t s, const GemvParams& p, int M, int rows, int iters, size_t lds) {
   if (M == 1) return launch_rows<1, EPI, NORM>(s, p, rows, iters, lds);
   if (M == 2) return launch_rows<2, EPI, NORM>(s, p, rows, iters, lds);
@@ -118,7 +119,7 @@ int launch_m_impl(hipStream_t s, const GemvParams& p, int M, int rows, int iters
 
 }  // namespace gemv_detail
 
-template <int EPI, bool NORM>
+template <int EPI, int NORM>
 int launch_m(hipStream_t s, const GemvParams& p, int M, int rows, int iters, size_t lds) {
   return gemv_detail::launch_m_impl<EPI, NORM>(s, p, M, rows, iters, lds);
 }
