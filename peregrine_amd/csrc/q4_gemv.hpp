@@ -461,11 +461,18 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(const GemvParams 
     }
   }
 
-  // 2) the first group's weights.
+  // 2) the first group's weights (the first three with kDeep).
   constexpr bool kRounds = (ROWS == 1 && EPI != kEpiArgmax);
-  GemvBuf<NMAT, ROWS, ITERS> b0, b1;
+  // Measured on MI355X: three groups in flight per wave (four buffers) is
+  // slower than one (gate/up 17.9 vs 15.7 us), so the deep variant is off.
+  constexpr bool kDeep = false;
+  GemvBuf<NMAT, ROWS, ITERS> b0, b1, b2, b3;
   uint32_t g = blockIdx.x * kGemvWaves + wid;
   if (g < G) gemv_load<NMAT, ROWS, ITERS, TAIL>(p, g, lane, tail_active, b0);
+  if constexpr (kDeep) {
+    if (g + W < G) gemv_load<NMAT, ROWS, ITERS, TAIL>(p, g + W, lane, tail_active, b1);
+    if (g + 2 * W < G) gemv_load<NMAT, ROWS, ITERS, TAIL>(p, g + 2 * W, lane, tail_active, b2);
+  }
 
   // 3) stage x into LDS (normalised with NORM), then into registers.
 #pragma unroll
@@ -539,15 +546,17 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(const GemvParams 
   };
 
   if constexpr (kRounds) {
-    // 4) rounds of four groups g, g+W, g+2W, g+3W: two register buffers (the
-    // next group streams in while the current one is dequantised), then one
+    // 4) rounds of four groups g, g+W, g+2W, g+3W: the group `ahead` steps
+    // later streams into a free register buffer while the current one is
+    // dequantised (ahead = 3 with four buffers, else 1 with two); then one
     // transposed reduction for the round and a one-lane-per-group epilogue.
     constexpr int E = NMAT * M;
+    constexpr uint32_t ahead = kDeep ? 3 : 1;
     auto step = [&](const GemvBuf<NMAT, 1, ITERS>& cur, GemvBuf<NMAT, 1, ITERS>& nxt, uint32_t gq,
                     float (&vq)[E]) {
       float acc[NMAT][1][M];
       if (gq < G) {
-        if (gq + W < G) gemv_load<NMAT, 1, ITERS, TAIL>(p, gq + W, lane, tail_active, nxt);
+        if (gq + ahead * W < G) gemv_load<NMAT, 1, ITERS, TAIL>(p, gq + ahead * W, lane, tail_active, nxt);
         accumulate(cur, acc);
       } else {
 #pragma unroll
@@ -562,10 +571,17 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(const GemvParams 
     };
     while (g < G) {
       float v[4][E];
-      step(b0, b1, g, v[0]);
-      step(b1, b0, g + W, v[1]);
-      step(b0, b1, g + 2 * W, v[2]);
-      step(b1, b0, g + 3 * W, v[3]);
+      if constexpr (kDeep) {
+        step(b0, b3, g, v[0]);
+        step(b1, b0, g + W, v[1]);
+        step(b2, b1, g + 2 * W, v[2]);
+        step(b3, b2, g + 3 * W, v[3]);
+      } else {
+        step(b0, b1, g, v[0]);
+        step(b1, b0, g + W, v[1]);
+        step(b0, b1, g + 2 * W, v[2]);
+        step(b1, b0, g + 3 * W, v[3]);
+      }
       reduce4_rows<E>(v);
       // 16-lane row q now holds group g + qW; its first lane writes the row.
       GemvRowDst dst{};
