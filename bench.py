@@ -31,7 +31,7 @@ PROMPT_TOKENS = 1600
 # HBM bytes per launch of the dominant kernel, from two rocprofv3 --pmc passes
 # (FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000, the factors a plain 256 MiB copy
 # kernel reads on the same counters); profiles/gemv_silu_gate_hbm_traffic.md.
-DOMINANT_TRAFFIC_BYTES = 56_990_000
+DOMINANT_TRAFFIC_BYTES = 57_050_112
 
 
 def log(*a) -> None:
@@ -40,13 +40,16 @@ def log(*a) -> None:
 
 def dominant_kernel_roofline(iters: int = 100) -> dict:
     """Fused post_attention_layernorm + gate/up SiLU GEMV at the MLP shape
-    (2 x 12288x4096 Q4): ~40% of the bytes a decode step streams. Timed with HIP
-    events around each launch over a ring of >= 512 MiB of distinct weights so
-    that every launch reads HBM, not the 256 MiB Infinity Cache."""
+    (2 x 12288x4096 Q4): ~40% of the bytes a decode step streams. One launch per
+    ring copy (>= 512 MiB of distinct weights, so every launch reads HBM, not
+    the 256 MiB Infinity Cache) is captured into a HIP graph on its own stream;
+    the graph is replayed `iters / copies` times between two HIP events on that
+    stream, as the decode loop replays its graph, so the average launch
+    duration carries no host launch overhead."""
     import ctypes as C
 
     from peregrine_amd._lib import call
-    from peregrine_amd.device import DeviceArray, Event, synchronize
+    from peregrine_amd.device import DeviceArray, Event, Graph, Stream, synchronize
     from peregrine_amd.gemv_bench import ROTATE_BYTES, q4_bytes
     from peregrine_amd.ops import Q4Linear
     from peregrine_amd.synth import random_bf16, random_q4
@@ -59,31 +62,41 @@ def dominant_kernel_roofline(iters: int = 100) -> dict:
     x = DeviceArray.from_numpy(random_bf16(rng, (K,), std=3.0))
     nw = DeviceArray.from_numpy(random_bf16(rng, (K,), std=0.1, mean=1.0))
     out = DeviceArray((N,), np.uint16)
+    stream = Stream()
 
     def launch(i: int) -> None:
         gl, ul = ring[i % len(ring)]
-        call("prg_q4_gemv_silu_gate_norm_bf16", None, C.c_void_p(x.ptr), C.c_void_p(nw.ptr), C.c_float(1e-6),
-             *gl._wsb(), *ul._wsb(), C.c_void_p(out.ptr), N, K)
+        call("prg_q4_gemv_silu_gate_norm_bf16", C.c_void_p(stream.handle), C.c_void_p(x.ptr), C.c_void_p(nw.ptr),
+             C.c_float(1e-6), *gl._wsb(), *ul._wsb(), C.c_void_p(out.ptr), N, K)
 
-    for i in range(10):
-        launch(i)
+    launch(0)  # eager first launch: kernel selection and occupancy queries happen outside the capture
+    stream.synchronize()
+    with Graph.capture(stream) as graph:
+        for i in range(copies):
+            launch(i)
+    reps = max(1, iters // copies)
+    for _ in range(2):
+        graph.launch()
+    stream.synchronize()
+    a, b = Event(), Event()
+    a.record(C.c_void_p(stream.handle))
+    for _ in range(reps):
+        graph.launch()
+    b.record(C.c_void_p(stream.handle))
+    stream.synchronize()
+    launches = reps * copies
+    avg_us = a.elapsed_ms(b) * 1e3 / launches
+    graph.close()
+    stream.close()
     synchronize()
-    evs = [(Event(), Event()) for _ in range(iters)]
-    for i, (a, b) in enumerate(evs):
-        a.record()
-        launch(i)
-        b.record()
-    synchronize()
-    ms = np.array([a.elapsed_ms(b) for a, b in evs])
     algo = 2 * q4_bytes(N, K) + 2 * K * 2 + N * 2  # gate+up weights, x + norm weight, out
-    avg_us = float(ms.mean() * 1e3)
     gbs = algo / (avg_us * 1e-6) / 1e9
-    return {"kernel": "q4_gemv_kernel<M=1,EPI=silu_gate,NORM> (mlp.gate_up, 2x12288x4096 Q4)",
+    return {"kernel": "q4_gemv_kernel<M=1,ROWS=1,ITERS=2,EPI=silu_gate,NORM=rms> (mlp.gate_up, 2x12288x4096 Q4)",
             "bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": DOMINANT_TRAFFIC_BYTES,
             "traffic_unit": "bytes/launch (PMC, calibrated)",
-            "avg_us": round(avg_us, 3), "median_us": round(float(np.median(ms) * 1e3), 3),
-            "algo_bytes_per_launch": int(algo), "launches": iters, "ring_copies": copies}
+            "avg_us": round(avg_us, 3), "timing": "HIP events around graph replays (no host launch overhead)",
+            "algo_bytes_per_launch": int(algo), "launches": launches, "ring_copies": copies}
 
 
 def prefill_flops(cfg, T: int) -> float:

@@ -74,6 +74,19 @@ int prg_hip_event_create(void **event);
 int prg_hip_event_destroy(void *event);
 int prg_hip_event_record(void *event, void *stream);
 int prg_hip_event_elapsed_ms(void *start, void *stop, float *ms);
+/* Recorded command sequences. The reference encodes kernels into a command
+ * buffer and commits it once (prg_cmdbuf_create / _encode / _commit /
+ * _commit_wait / _destroy, bridge.h:60-97); here the ops issued on `stream`
+ * between begin and end are captured into a HIP graph that can be replayed
+ * any number of times with one launch each.
+ *   prg_hip_graph_begin   : start capturing `stream` (not the NULL stream)
+ *   prg_hip_graph_end     : stop capturing; *graph receives an executable graph
+ *   prg_hip_graph_launch  : replay it on `stream` (asynchronous)
+ *   prg_hip_graph_destroy : free it */
+int prg_hip_graph_begin(void *stream);
+int prg_hip_graph_end(void *stream, void **graph);
+int prg_hip_graph_launch(void *graph, void *stream);
+int prg_hip_graph_destroy(void *graph);
 /* Plain device-to-device copy kernel (bytes % 16 == 0); the reference dispatch
  * for calibrating HBM byte counters. */
 int prg_hip_copy_kernel(void *dst, const void *src, size_t bytes, void *stream);

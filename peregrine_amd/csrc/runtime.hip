@@ -189,4 +189,34 @@ int prg_hip_event_elapsed_ms(void* start, void* stop, float* ms) {
   return PRG_OK;
 }
 
+// Command-sequence capture (bridge.h:60-97 command buffers -> HIP graphs).
+int prg_hip_graph_begin(void* stream) {
+  PRG_CHECK_ARG(stream, "prg_hip_graph_begin: capture needs a created stream, not the NULL stream");
+  PRG_HIP(hipStreamBeginCapture(prg::as_stream(stream), hipStreamCaptureModeRelaxed));
+  return PRG_OK;
+}
+
+int prg_hip_graph_end(void* stream, void** graph) {
+  PRG_CHECK_ARG(stream && graph, "prg_hip_graph_end: null argument");
+  hipGraph_t g = nullptr;
+  PRG_HIP(hipStreamEndCapture(prg::as_stream(stream), &g));
+  hipGraphExec_t exec = nullptr;
+  const hipError_t e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+  hipGraphDestroy(g);
+  if (e != hipSuccess) return prg::set_error(PRG_ERR_HIP, "prg_hip_graph_end: instantiate: %s", hipGetErrorString(e));
+  *graph = exec;
+  return PRG_OK;
+}
+
+int prg_hip_graph_launch(void* graph, void* stream) {
+  PRG_CHECK_ARG(graph, "prg_hip_graph_launch: null graph");
+  PRG_HIP(hipGraphLaunch(reinterpret_cast<hipGraphExec_t>(graph), prg::as_stream(stream)));
+  return PRG_OK;
+}
+
+int prg_hip_graph_destroy(void* graph) {
+  if (graph) PRG_HIP(hipGraphExecDestroy(reinterpret_cast<hipGraphExec_t>(graph)));
+  return PRG_OK;
+}
+
 }  // extern "C"

@@ -134,6 +134,39 @@ class Event:
             self.handle = None
 
 
+class Graph:
+    """Ops issued on `stream` inside `with Graph.capture(stream) as g:` are
+    recorded once and replayed by g.launch() (prg_hip_graph_*)."""
+
+    def __init__(self, stream: Stream) -> None:
+        self.stream = stream
+        self.handle = None
+
+    @classmethod
+    def capture(cls, stream: Stream) -> "Graph":
+        return cls(stream)
+
+    def __enter__(self) -> "Graph":
+        call("prg_hip_graph_begin", C.c_void_p(self.stream.handle))
+        return self
+
+    def __exit__(self, exc_type, exc, tb) -> None:
+        h = C.c_void_p(0)
+        rc = lib.prg_hip_graph_end(C.c_void_p(self.stream.handle), C.byref(h))
+        if exc_type is None:
+            if rc != 0:
+                raise RuntimeError(f"prg_hip_graph_end failed ({rc}): {lib.prg_last_error().decode()}")
+            self.handle = h.value
+
+    def launch(self) -> None:
+        call("prg_hip_graph_launch", C.c_void_p(self.handle), C.c_void_p(self.stream.handle))
+
+    def close(self) -> None:
+        if self.handle:
+            lib.prg_hip_graph_destroy(C.c_void_p(self.handle))
+            self.handle = None
+
+
 def ptr(x) -> C.c_void_p:
     """Device pointer argument for a DeviceArray, int or None."""
     if x is None:
