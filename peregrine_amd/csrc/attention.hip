@@ -120,9 +120,33 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnD
   }
   const uint32_t T = t1 - t0;
   const uint32_t ld = a.split_tokens;
+  // A range of <= 64 tokens (every split of a cache up to 4096 tokens) issues
+  // all of its q, K and V loads before any arithmetic: one memory round trip.
+  const bool one_tile = T <= 64;
+  const int jd = lane & 15, r = lane >> 4;
+  const int rr = lane >> 3, ts = lane & 7;
+  const uint16_t* kbase = a.key_cache + static_cast<size_t>(kvh) * a.stride * kAttnHeadDim + 16 * jd;
+  const uint16_t* vbase = a.value_cache + (static_cast<size_t>(kvh) * kAttnHeadDim + 64 * w + rr) * a.stride;
+  uint4 kt[4][2], vt[8];
+  if (one_tile) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t tt = 4 * w + r + 16 * i;
+      kt[i][0] = kt[i][1] = make_uint4(0, 0, 0, 0);
+      if (tt < T) {
+        const uint4* kp = reinterpret_cast<const uint4*>(kbase + static_cast<size_t>(t0 + tt) * kAttnHeadDim);
+        kt[i][0] = kp[0];
+        kt[i][1] = kp[1];
+      }
+    }
+    if (static_cast<uint32_t>(8 * ts) < T) {
+#pragma unroll
+      for (int p = 0; p < 8; ++p)
+        vt[p] = *reinterpret_cast<const uint4*>(vbase + static_cast<size_t>(8 * p) * a.stride + t0 + 8 * ts);
+    }
+  }
 
   // ---- phase 1: scores. lane -> (token row r = lane/16, dims 16*jd .. +16)
-  const int jd = lane & 15, r = lane >> 4;
   uint32_t qd[kAttnGroup][8];
 #pragma unroll
   for (int g = 0; g < static_cast<int>(kAttnGroup); ++g) {
@@ -131,10 +155,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnD
     qd[g][0] = q0.x; qd[g][1] = q0.y; qd[g][2] = q0.z; qd[g][3] = q0.w;
     qd[g][4] = q1.x; qd[g][5] = q1.y; qd[g][6] = q1.z; qd[g][7] = q1.w;
   }
-  const uint16_t* kbase = a.key_cache + static_cast<size_t>(kvh) * a.stride * kAttnHeadDim + 16 * jd;
-  for (uint32_t tt = 4 * w + r; tt < T; tt += 16) {
-    const uint4* kp = reinterpret_cast<const uint4*>(kbase + static_cast<size_t>(t0 + tt) * kAttnHeadDim);
-    const uint4 k0 = kp[0], k1 = kp[1];
+  auto score = [&](uint32_t tt, uint4 k0, uint4 k1, bool valid) {
     const uint32_t kd[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
     float s[kAttnGroup];
 #pragma unroll
@@ -144,9 +165,22 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnD
       for (int i = 0; i < 8; ++i) acc = dot2(qd[g][i], kd[i], acc);
       s[g] = row16_sum(acc);
     }
-    if (jd == 0) {
+    if (valid && jd == 0) {
 #pragma unroll
       for (int g = 0; g < static_cast<int>(kAttnGroup); ++g) sc[g * ld + tt] = s[g] * a.scale;
+    }
+  };
+  if (one_tile) {
+    // rows past T compute on zeros and store nothing (row16_sum stays row-local)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t tt = 4 * w + r + 16 * i;
+      if (4 * w + 16 * i < T) score(tt, kt[i][0], kt[i][1], tt < T);
+    }
+  } else {
+    for (uint32_t tt = 4 * w + r; tt < T; tt += 16) {
+      const uint4* kp = reinterpret_cast<const uint4*>(kbase + static_cast<size_t>(t0 + tt) * kAttnHeadDim);
+      score(tt, kp[0], kp[1], true);
     }
   }
   __syncthreads();
@@ -175,13 +209,11 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnD
   __syncthreads();
 
   // ---- phase 3: P.V. wave w owns dims [64w, 64w+64): 8 passes x 8 rows.
-  const int rr = lane >> 3, ts = lane & 7;
   float acc[8][kAttnGroup];
 #pragma unroll
   for (int p = 0; p < 8; ++p)
 #pragma unroll
     for (int g = 0; g < static_cast<int>(kAttnGroup); ++g) acc[p][g] = 0.0f;
-  const uint16_t* vbase = a.value_cache + (static_cast<size_t>(kvh) * kAttnHeadDim + 64 * w + rr) * a.stride;
   for (uint32_t tb = 0; tb < T; tb += 64) {
     const uint32_t tl = tb + 8 * ts;  // first of this lane's 8 tokens (block-local)
     if (tl >= T) continue;
@@ -192,9 +224,14 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnD
 #pragma unroll
       for (int i = 0; i < 8; ++i) pv[g][i] = (static_cast<uint32_t>(i) < nvalid) ? sc[g * ld + tl + i] : 0.0f;
     uint4 vv[8];
+    if (one_tile) {
 #pragma unroll
-    for (int p = 0; p < 8; ++p)
-      vv[p] = *reinterpret_cast<const uint4*>(vbase + static_cast<size_t>(8 * p) * a.stride + t0 + tl);
+      for (int p = 0; p < 8; ++p) vv[p] = vt[p];
+    } else {
+#pragma unroll
+      for (int p = 0; p < 8; ++p)
+        vv[p] = *reinterpret_cast<const uint4*>(vbase + static_cast<size_t>(8 * p) * a.stride + t0 + tl);
+    }
 #pragma unroll
     for (int p = 0; p < 8; ++p) {
       const uint32_t vd[4] = {vv[p].x, vv[p].y, vv[p].z, vv[p].w};
@@ -243,8 +280,20 @@ __global__ __launch_bounds__(kAttnThreads) void attn_reduce_kernel(const AttnDec
   const uint32_t h = blockIdx.x;  // q head
   const uint32_t t = threadIdx.x;
   const float* base = a.partials + static_cast<size_t>(h) * a.nsplit * kAttnPartialStride;
+  // Only splits that hold tokens carry weight (the others are neutral), and
+  // for a short cache their accumulators are loaded up front, together with
+  // the statistics: one memory round trip.
+  const uint32_t L = min(a.step ? a.step->seq_len : a.seq_len_host, a.stride);
+  uint32_t chunk = (L + a.nsplit - 1) / a.nsplit;
+  chunk = (chunk + 63u) & ~63u;
+  const uint32_t nact = min(a.nsplit, (L + chunk - 1) / chunk);
+  const uint32_t d = t;
+  constexpr uint32_t kPre = 64;
+  float pre[kPre];
+#pragma unroll
+  for (uint32_t c = 0; c < kPre; ++c) pre[c] = c < nact ? base[c * kAttnPartialStride + 2 + d] : 0.0f;
   float m_local = -INFINITY;
-  for (uint32_t c = t; c < a.nsplit; c += kAttnThreads) m_local = fmaxf(m_local, base[c * kAttnPartialStride]);
+  for (uint32_t c = t; c < nact; c += kAttnThreads) m_local = fmaxf(m_local, base[c * kAttnPartialStride]);
   m_local = wave_max(m_local);
   if ((t & 63) == 0) red[t >> 6] = m_local;
   __syncthreads();
@@ -253,17 +302,19 @@ __global__ __launch_bounds__(kAttnThreads) void attn_reduce_kernel(const AttnDec
   for (int i = 1; i < kAttnThreads / kWave; ++i) m_all = fmaxf(m_all, red[i]);
   __syncthreads();
   float den_local = 0.0f;
-  for (uint32_t c = t; c < a.nsplit; c += kAttnThreads) {
+  for (uint32_t c = t; c < nact; c += kAttnThreads) {
     const float mc = base[c * kAttnPartialStride];
     const float wgt = (mc == -INFINITY) ? 0.0f : expf(mc - m_all);
     wsh[c] = wgt;
     den_local += base[c * kAttnPartialStride + 1] * wgt;
   }
   const float den = block_sum<kAttnThreads>(den_local, red);  // also orders the wsh writes
-  const uint32_t d = t;
   float acc = 0.0f;
+#pragma unroll
+  for (uint32_t c = 0; c < kPre; ++c)
+    if (c < nact) acc += pre[c] * wsh[c];
 #pragma unroll 8
-  for (uint32_t c = 0; c < a.nsplit; ++c) acc += base[c * kAttnPartialStride + 2 + d] * wsh[c];
+  for (uint32_t c = kPre; c < nact; ++c) acc += base[c * kAttnPartialStride + 2 + d] * wsh[c];
   const size_t i = static_cast<size_t>(h) * kAttnHeadDim + d;
   const float sig = 1.0f / (1.0f + expf(-bf2f(a.gate[i])));
   a.out[i] = f2bf((acc / den) * sig);
