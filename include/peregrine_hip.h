@@ -37,7 +37,14 @@ enum {
   PRG_ERR_OOM = 4,           /* allocation failed                          */
   PRG_ERR_SEQUENCE_TOO_LONG = 5, /* cache_pos >= cache capacity (model.zig:805) */
   PRG_ERR_INVALID_TOKEN = 6, /* token id >= vocab (model.zig:806)           */
-  PRG_ERR_EMPTY_INPUT = 7    /* zero token_count (linear_q4.zig:85)         */
+  PRG_ERR_EMPTY_INPUT = 7,   /* zero token_count (linear_q4.zig:85)         */
+  PRG_ERR_NOT_FOUND = 8,     /* FileNotFound / TensorNotFound               */
+  PRG_ERR_MALFORMED = 9,     /* TruncatedHeader / MalformedHeader / MalformedIndex /
+                                NoShardsFound / MissingField / InvalidTensorShape
+                                (safetensors.zig, std.json)                  */
+  PRG_ERR_UNSUPPORTED = 10,  /* UnsupportedArchitecture / UnsupportedQuantization /
+                                InvalidConfig / NotQwen35_9B (config.zig:44-72) */
+  PRG_ERR_IO = 11            /* read / write failure                         */
 };
 
 /* Last error message of the calling thread ("" if none). */

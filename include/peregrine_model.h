@@ -10,8 +10,11 @@
  *   FullAttentionBlock     src/model/block_attn.zig:261-359
  *   MlpBlock               src/model/block_mlp.zig:260-311
  *   decodeFromPrefixCache  src/server/decode_loop.zig:96-160 (no prefix)
- * The checkpoint loader is out of scope: models are random-initialised on the
- * GPU from a seed, in the reference's tensor layout and names.
+ *   Repository (safetensors) src/model/safetensors.zig:17-220
+ *   verifyFingerprint      src/model/config.zig:34-73, src/model/mtp.zig:318-345
+ * Models are either loaded from an MLX safetensors checkpoint
+ * (prg_model_load) or random-initialised on the GPU from a seed; both use the
+ * reference's tensor layout and names.
  * All functions return 0 or a PRG_ERR_* code (see peregrine_hip.h).
  */
 #ifndef PEREGRINE_MODEL_H
@@ -55,6 +58,63 @@ size_t prg_model_weight_bytes(const PrgModel *model);
  * "language_model.model.layers.3.self_attn.q_proj.weight" (names as the
  * reference's checkpoint, decoder_layer.zig:376-412). */
 int prg_model_tensor(const PrgModel *model, const char *name, void **ptr, size_t *bytes);
+/* The model's tensors in name order: count, name of entry `index`, and the
+ * checkpoint dtype ("U32", "BF16", "F32") and shape each is stored with (Q4
+ * weight [out, in/8] u32, scales / biases [out, in/64] bf16;
+ * linear_q4.zig:261-268). */
+uint32_t prg_model_tensor_count(const PrgModel *model);
+int prg_model_tensor_name(const PrgModel *model, uint32_t index, char *buf, size_t len);
+int prg_model_tensor_info(const PrgModel *model, const char *name, char *dtype, size_t dtype_len,
+                          uint64_t *shape, uint32_t max_dims, uint32_t *ndim);
+
+/* ======================================================================
+ * Checkpoints (host code; no GPU needed except for prg_model_load).
+ * ====================================================================== */
+
+/* A directory of safetensors shards named by model.safetensors.index.json.
+ * Replaces safetensors.Repository.open / deinit (safetensors.zig:25-87):
+ * shards are the index's unique weight_map values, sorted; each header is
+ * parsed into the tensor table. Errors: NOT_FOUND (no index or shard),
+ * MALFORMED (TruncatedHeader, MalformedHeader, MalformedIndex, NoShardsFound). */
+typedef struct PrgSafetensors PrgSafetensors;
+int prg_safetensors_open(const char *dir, PrgSafetensors **out);
+void prg_safetensors_close(PrgSafetensors *st);
+uint32_t prg_safetensors_shard_count(const PrgSafetensors *st);
+int prg_safetensors_shard_name(const PrgSafetensors *st, uint32_t index, char *buf, size_t len);
+/* Tensors in name order. */
+uint32_t prg_safetensors_tensor_count(const PrgSafetensors *st);
+int prg_safetensors_tensor_name(const PrgSafetensors *st, uint32_t index, char *buf, size_t len);
+/* Repository.get + tensorByteLen (safetensors.zig:98-104, 123-141): dtype
+ * string, shape (up to max_dims), byte length and shard index (each output
+ * may be NULL except ndim and bytes). NOT_FOUND for an unknown name. */
+int prg_safetensors_tensor_info(const PrgSafetensors *st, const char *name, char *dtype, size_t dtype_len,
+                                uint64_t *shape, uint32_t max_dims, uint32_t *ndim, uint64_t *bytes,
+                                uint32_t *shard);
+/* Repository.readInto (safetensors.zig:89-100): the tensor's bytes into host
+ * memory `dst` of exactly `bytes` (InvalidTensorBuffer otherwise). */
+int prg_safetensors_read(const PrgSafetensors *st, const char *name, void *dst, uint64_t bytes);
+
+/* config.verifyFingerprint (config.zig:34-73): the exact Qwen3.5-9B MLX
+ * affine 4-bit group-64 checkpoint, else UNSUPPORTED with the reference's
+ * error name in prg_last_error(). */
+int prg_checkpoint_verify_config(const char *dir);
+/* mtp.verifyFingerprint (mtp.zig:318-345) for the MTP sidecar directory. */
+int prg_checkpoint_verify_mtp_config(const char *dir);
+/* config.json -> PrgModelConfig (layers, widths, vocab, attention interval,
+ * rms_norm_eps). Applies verifyFingerprint's generic checks, then requires
+ * the head geometry the kernels implement; depth and widths are free. */
+int prg_checkpoint_read_config(const char *dir, PrgModelConfig *cfg);
+
+/* Allocate a model of shape *cfg and fill every tensor from the checkpoint
+ * in target_dir (and, with cfg->mtp_layers == 1, the drafter from mtp_dir,
+ * whose tensor root is detected as in mtp.zig:347-355). Each tensor must be
+ * present with the dtype and shape prg_model_tensor_info reports (A_log may
+ * also be stored as bf16; it is widened to f32). Bytes go file -> pinned
+ * staging -> device, double-buffered. Replaces DeviceModel.upload
+ * (model.zig:580-658), DecoderLayer.upload (decoder_layer.zig:376-412),
+ * Q4Linear.upload (linear_q4.zig:28-63), Drafter.upload (mtp.zig:86-116) and
+ * upload.tensorPrivate (upload.zig:6-21). */
+int prg_model_load(const PrgModelConfig *cfg, const char *target_dir, const char *mtp_dir, PrgModel **out);
 
 /* Per-sequence state for up to max_seq tokens: GDN conv f32 [3, 8192] and
  * recurrent f32 [32, 128, 128] per linear layer, bf16 K [4, stride, 256] and

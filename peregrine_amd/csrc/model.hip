@@ -90,12 +90,13 @@ struct Builder {
   };
   std::vector<Fill> fills;
 
-  void* take(const std::string& name, size_t bytes) {
+  void* take(const std::string& name, size_t bytes, const char* dtype, std::vector<uint64_t> shape) {
     const size_t off = offset;
     offset = align_up(offset + bytes, kAlign);
     if (sizing) return nullptr;
     void* p = m->arena + off;
     m->tensors[name] = TensorRef{p, bytes};
+    m->specs[name] = TensorSpec{dtype, std::move(shape)};
     return p;
   }
   uint64_t next_key() { return mix64(seed ^ mix64(++tensor_id * 0x632be59bd9b4e019ull)); }
@@ -105,9 +106,10 @@ struct Builder {
     l.out_dim = out_dim;
     l.in_dim = in_dim;
     const size_t nw = static_cast<size_t>(out_dim) * in_dim / 8, ng = static_cast<size_t>(out_dim) * in_dim / 64;
-    l.weight = static_cast<uint32_t*>(take(base + ".weight", nw * 4));
-    l.scales = static_cast<uint16_t*>(take(base + ".scales", ng * 2));
-    l.biases = static_cast<uint16_t*>(take(base + ".biases", ng * 2));
+    // checkpoint shapes: weight u32 [out, in/8], scales / biases bf16 [out, in/64]
+    l.weight = static_cast<uint32_t*>(take(base + ".weight", nw * 4, "U32", {out_dim, in_dim / 8u}));
+    l.scales = static_cast<uint16_t*>(take(base + ".scales", ng * 2, "BF16", {out_dim, in_dim / 64u}));
+    l.biases = static_cast<uint16_t*>(take(base + ".biases", ng * 2, "BF16", {out_dim, in_dim / 64u}));
     const uint64_t k0 = next_key(), k1 = next_key(), k2 = next_key();
     if (!sizing) {
       fills.push_back({l.weight, nw, kFillBits, 0, 0, 0, nullptr, k0});
@@ -116,14 +118,15 @@ struct Builder {
     }
     return l;
   }
-  uint16_t* bf16(const std::string& name, size_t n, float mean, float stddev) {
-    auto* p = static_cast<uint16_t*>(take(name, n * 2));
+  uint16_t* bf16(const std::string& name, size_t n, float mean, float stddev, std::vector<uint64_t> shape = {}) {
+    if (shape.empty()) shape = {n};
+    auto* p = static_cast<uint16_t*>(take(name, n * 2, "BF16", std::move(shape)));
     const uint64_t k = next_key();
     if (!sizing) fills.push_back({p, n, kFillNormal, mean, stddev, 0, nullptr, k});
     return p;
   }
   float* f32(const std::string& name, size_t n, float mean, float stddev) {
-    auto* p = static_cast<float*>(take(name, n * 4));
+    auto* p = static_cast<float*>(take(name, n * 4, "F32", {n}));
     const uint64_t k = next_key();
     if (!sizing) fills.push_back({p, n, kFillNormal, mean, stddev, 1, nullptr, k});
     return p;
@@ -183,7 +186,9 @@ void build_model(Builder& b) {
       L.lin.in_a = b.q4(a + ".in_proj_a", kGdnHv, c.hidden);
       L.lin.in_b = b.q4(a + ".in_proj_b", kGdnHv, c.hidden);
       L.lin.out_proj = b.q4(a + ".out_proj", c.hidden, kGdnValDim);
-      L.lin.conv_weight = b.bf16(a + ".conv1d.weight", static_cast<size_t>(kGdnConvDim) * kGdnConvK, 0.0f, 0.5f);
+      // MLX Conv1d layout [channels, kernel, in_channels / groups]
+      L.lin.conv_weight = b.bf16(a + ".conv1d.weight", static_cast<size_t>(kGdnConvDim) * kGdnConvK, 0.0f, 0.5f,
+                                 {kGdnConvDim, kGdnConvK, 1});
       L.lin.a_log = b.f32(a + ".A_log", kGdnHv, 0.0f, 0.5f);
       L.lin.dt_bias = b.bf16(a + ".dt_bias", kGdnHv, 0.0f, 0.5f);
       L.lin.norm_weight = b.bf16(a + ".norm.weight", kGdnDv, 1.0f, 0.1f);
@@ -206,6 +211,25 @@ void build_model(Builder& b) {
   }
 }
 
+}  // namespace
+
+int layout_model(PrgModel* m) {
+  Builder sizing{m, 0};
+  build_model(sizing);
+  m->arena_bytes = sizing.offset;
+  const hipError_t e = hipMalloc(reinterpret_cast<void**>(&m->arena), m->arena_bytes);
+  if (e != hipSuccess) {
+    m->arena = nullptr;
+    return set_error(PRG_ERR_OOM, "model weights: hipMalloc(%zu): %s", sizing.offset, hipGetErrorString(e));
+  }
+  Builder b{m, 0};
+  b.sizing = false;
+  build_model(b);
+  return PRG_OK;
+}
+
+namespace {
+
 int validate_config(const PrgModelConfig& c) {
   PRG_CHECK_ARG(c.mtp_layers <= 1, "config: mtp_layers %u (0 or 1)", c.mtp_layers);
   PRG_CHECK_ARG(c.num_layers >= 1 && c.num_layers <= 256, "config: num_layers %u", c.num_layers);
@@ -219,6 +243,8 @@ int validate_config(const PrgModelConfig& c) {
 }
 
 }  // namespace
+
+int validate_model_config(const PrgModelConfig& c) { return validate_config(c); }
 
 // ------------------------------------------------------- per-token chain ---
 GemvParams gemv_params(const uint16_t* x, uint32_t K) {
@@ -468,6 +494,38 @@ void prg_model_destroy(PrgModel* model) {
 }
 
 size_t prg_model_weight_bytes(const PrgModel* model) { return model ? model->arena_bytes : 0; }
+
+uint32_t prg_model_tensor_count(const PrgModel* model) {
+  return model ? static_cast<uint32_t>(model->tensors.size()) : 0u;
+}
+
+int prg_model_tensor_name(const PrgModel* model, uint32_t index, char* buf, size_t len) {
+  PRG_CHECK_ARG(model && buf && len, "prg_model_tensor_name: null argument");
+  PRG_CHECK_ARG(index < model->tensors.size(), "prg_model_tensor_name: index %u of %zu", index,
+                model->tensors.size());
+  const std::string& n = std::next(model->tensors.begin(), index)->first;
+  PRG_CHECK_ARG(n.size() < len, "prg_model_tensor_name: buffer of %zu bytes too small", len);
+  memcpy(buf, n.c_str(), n.size() + 1);
+  return PRG_OK;
+}
+
+int prg_model_tensor_info(const PrgModel* model, const char* name, char* dtype, size_t dtype_len, uint64_t* shape,
+                          uint32_t max_dims, uint32_t* ndim) {
+  PRG_CHECK_ARG(model && name && ndim, "prg_model_tensor_info: null argument");
+  auto it = model->specs.find(name);
+  if (it == model->specs.end()) return set_error(PRG_ERR_INVALID_ARG, "prg_model_tensor_info: no tensor '%s'", name);
+  const TensorSpec& sp = it->second;
+  *ndim = static_cast<uint32_t>(sp.shape.size());
+  if (shape) {
+    PRG_CHECK_ARG(sp.shape.size() <= max_dims, "prg_model_tensor_info: %zu dims > %u", sp.shape.size(), max_dims);
+    for (size_t k = 0; k < sp.shape.size(); ++k) shape[k] = sp.shape[k];
+  }
+  if (dtype) {
+    PRG_CHECK_ARG(sp.dtype.size() < dtype_len, "prg_model_tensor_info: dtype buffer too small");
+    memcpy(dtype, sp.dtype.c_str(), sp.dtype.size() + 1);
+  }
+  return PRG_OK;
+}
 
 int prg_model_tensor(const PrgModel* model, const char* name, void** ptr, size_t* bytes) {
   PRG_CHECK_ARG(model && name && ptr && bytes, "prg_model_tensor: null argument");

@@ -80,6 +80,12 @@ struct TensorRef {
   size_t bytes;
 };
 
+// How a tensor is stored in a checkpoint: safetensors dtype and shape.
+struct TensorSpec {
+  std::string dtype;
+  std::vector<uint64_t> shape;
+};
+
 struct LayerState {
   float* conv = nullptr;        // f32 [3, 8192]
   float* recur = nullptr;       // f32 [32, 128, 128]
@@ -125,6 +131,10 @@ struct SpecCtl {
 };
 
 bool is_linear_layer(const PrgModelConfig& c, uint32_t i);
+int validate_model_config(const PrgModelConfig& c);
+// Lay out every tensor of m->cfg in one device arena: m->tensors and m->specs
+// filled, contents undefined. Returns a PRG_ERR_* code.
+int layout_model(PrgModel* m);
 uint32_t cache_stride_for(uint32_t max_seq);
 
 }  // namespace prg
@@ -134,6 +144,7 @@ struct PrgModel {
   uint8_t* arena = nullptr;
   size_t arena_bytes = 0;
   std::map<std::string, prg::TensorRef> tensors;
+  std::map<std::string, prg::TensorSpec> specs;
   prg::Q4Linear embed;
   std::vector<prg::DecoderLayer> layers;
   uint16_t* final_norm = nullptr;

@@ -65,6 +65,36 @@ class DeviceModel:
         call("prg_model_create_random", C.byref(cfg.c()), C.c_uint64(seed), C.byref(h))
         self.handle = h
 
+    @classmethod
+    def load(cls, cfg: ModelConfig, target_dir: str, mtp_dir: str | None = None) -> "DeviceModel":
+        """Upload a model of shape cfg from an MLX safetensors checkpoint
+        (DeviceModel.upload, model.zig:580-658)."""
+        init()
+        self = cls.__new__(cls)
+        self.cfg = cfg
+        h = C.c_void_p(0)
+        self.handle = None
+        call("prg_model_load", C.byref(cfg.c()), str(target_dir).encode(),
+             str(mtp_dir).encode() if mtp_dir is not None else None, C.byref(h))
+        self.handle = h
+        return self
+
+    def tensor_names(self) -> list[str]:
+        buf = C.create_string_buffer(512)
+        out = []
+        for i in range(int(lib.prg_model_tensor_count(self.handle))):
+            call("prg_model_tensor_name", self.handle, i, buf, len(buf))
+            out.append(buf.value.decode())
+        return out
+
+    def tensor_info(self, name: str) -> tuple[str, tuple[int, ...]]:
+        """Checkpoint dtype string and shape of a tensor."""
+        dt = C.create_string_buffer(16)
+        shape = (C.c_uint64 * 8)()
+        nd = C.c_uint32(0)
+        call("prg_model_tensor_info", self.handle, name.encode(), dt, len(dt), shape, 8, C.byref(nd))
+        return dt.value.decode(), tuple(int(shape[k]) for k in range(nd.value))
+
     @property
     def weight_bytes(self) -> int:
         return int(lib.prg_model_weight_bytes(self.handle))
