@@ -68,6 +68,135 @@ int prg_model_tensor_info(const PrgModel *model, const char *name, char *dtype, 
                           uint64_t *shape, uint32_t max_dims, uint32_t *ndim);
 
 /* ======================================================================
+ * Prefix reuse: state copies and prefill on top of a restored prefix.
+ * ====================================================================== */
+
+/* ModelState.copyPrefixFrom (state.zig:124-128): K/V of positions
+ * [0, token_count) of every attention layer and all GDN conv / recurrent
+ * states, from src to dst (same model; strides may differ). Ordered after
+ * src's pending work; complete on return. */
+int prg_model_state_copy_prefix(PrgModelState *dst, const PrgModelState *src, uint32_t token_count);
+/* copyFullAttentionRangeFrom (state.zig:144-180): K/V positions
+ * [src_start, +token_count) of src to [dst_start, ...) of dst. */
+int prg_model_state_copy_range(PrgModelState *dst, uint32_t dst_start, const PrgModelState *src,
+                               uint32_t src_start, uint32_t token_count);
+/* copyLinearStateFrom (state.zig:130-142): the GDN conv / recurrent states. */
+int prg_model_state_copy_linear(PrgModelState *dst, const PrgModelState *src);
+
+/* Prefill prompt[prefix_len, prompt_len) on top of a state that already holds
+ * prompt[0, prefix_len) (restored from a prefix cache entry, or left by an
+ * earlier prefill), then the greedy argmax tail; the state is positioned to
+ * decode from prompt_len as after prg_model_prefill. 1 <= prefix_len <
+ * prompt_len. Replaces the prefix-hit prefill (model.zig:940-1060 with a
+ * PrefixState). The prefix is copied into the working state instead of being
+ * bound as a second KV source, so positions are absolute. */
+int prg_model_prefill_from(PrgModel *model, PrgModelState *state, const uint32_t *prompt, uint32_t prompt_len,
+                           uint32_t prefix_len, uint32_t *next_token);
+
+/* ======================================================================
+ * Prompt-prefix cache (src/server/prefix_state_cache.zig:21-795) and its
+ * PRGPFXS1 v3 file (src/server/prefix_persist.zig:31-412).
+ * ====================================================================== */
+
+typedef struct PrgPrefixCache PrgPrefixCache;
+/* Cache.Match: entry index and matched length (len 0 = no match). Indexes
+ * shift when entries are removed; use the match a mutator returns. */
+typedef struct PrgPrefixMatch {
+  uint32_t index;
+  uint32_t len;
+} PrgPrefixMatch;
+/* Cache.Stats (prefix_state_cache.zig:343-366) plus resident_tokens. */
+typedef struct PrgPrefixCacheStats {
+  uint64_t hits, misses, hit_tokens, computed_tokens;
+  uint64_t reserved_tokens, resident_tokens, max_tokens, entry_count, evictions;
+} PrgPrefixCacheStats;
+
+/* Cache.init(max_cache_tokens, prefill_chunk_tokens). Entries own a state of
+ * max(tokens, min(max_cache_tokens, prefill_chunk_tokens)) positions; the sum
+ * of those capacities stays within max_cache_tokens by evicting the least
+ * recently used unpinned entry. model may be NULL: the cache then keeps tokens
+ * and accounting only (store takes a NULL work state; restore, save and load
+ * need a model). */
+int prg_prefix_cache_create(PrgModel *model, uint32_t max_cache_tokens, uint32_t prefill_chunk_tokens,
+                            PrgPrefixCache **out);
+void prg_prefix_cache_destroy(PrgPrefixCache *cache);
+int prg_prefix_cache_clear(PrgPrefixCache *cache);                 /* clearAll */
+uint32_t prg_prefix_cache_entry_count(const PrgPrefixCache *cache);
+uint32_t prg_prefix_cache_pinned_count(const PrgPrefixCache *cache);
+uint32_t prg_prefix_cache_active_tokens(const PrgPrefixCache *cache);
+int prg_prefix_cache_stats(const PrgPrefixCache *cache, PrgPrefixCacheStats *stats);
+void prg_prefix_cache_record_hit(PrgPrefixCache *cache, uint32_t reused_tokens);
+void prg_prefix_cache_record_miss(PrgPrefixCache *cache);
+void prg_prefix_cache_record_computed(PrgPrefixCache *cache, uint32_t token_count);
+/* findPrefix: the longest cached entry that is a prefix of prompt. */
+int prg_prefix_cache_find(const PrgPrefixCache *cache, const uint32_t *prompt, uint32_t prompt_len,
+                          PrgPrefixMatch *match);
+/* containsPromptPrefix: 1 when prompt[0, prefix_len) is an entry, else 0. */
+int prg_prefix_cache_contains(const PrgPrefixCache *cache, const uint32_t *prompt, uint32_t prompt_len,
+                              uint32_t prefix_len);
+int prg_prefix_cache_touch(PrgPrefixCache *cache, PrgPrefixMatch match);
+int prg_prefix_cache_remove(PrgPrefixCache *cache, uint32_t index);  /* removeEntry */
+int prg_prefix_cache_entry_info(const PrgPrefixCache *cache, uint32_t index, uint32_t *token_count,
+                                uint32_t *capacity, int *pinned, uint64_t *hits);
+int prg_prefix_cache_entry_tokens(const PrgPrefixCache *cache, uint32_t index, uint32_t *tokens, uint32_t capacity);
+/* entryStateMut: the entry's state (prefill into it after start_direct). */
+int prg_prefix_cache_entry_state(PrgPrefixCache *cache, uint32_t index, PrgModelState **state);
+int prg_prefix_cache_cached_next_token(const PrgPrefixCache *cache, PrgPrefixMatch match, uint32_t *token,
+                                       int *valid);
+/* startDirectEntry / finishDirectEntry: reserve (or reuse) the entry for ids,
+ * reset its state for a direct prefill, then record its next token. */
+int prg_prefix_cache_start_direct(PrgPrefixCache *cache, const uint32_t *ids, uint32_t n, int pinned,
+                                  PrgPrefixMatch *out);
+int prg_prefix_cache_finish_direct(PrgPrefixCache *cache, PrgPrefixMatch match, uint32_t next_token);
+/* storePrefixFromWork: cache ids[0, n) from a working state that holds those
+ * positions. With `reuse` (a match the work state was restored from) that
+ * entry is re-keyed to the longer prefix and takes positions [reuse->len, n)
+ * plus the GDN state; otherwise positions [0, n) are copied. work_hidden
+ * (device bf16 rows, may be NULL) feeds the hidden rows when tracking is on;
+ * next_token (host, may be NULL) is the cached greedy successor. */
+int prg_prefix_cache_store(PrgPrefixCache *cache, const uint32_t *ids, uint32_t n, const PrgPrefixMatch *reuse,
+                           const PrgModelState *work, const uint16_t *work_hidden, uint32_t work_hidden_base_rows,
+                           const uint32_t *next_token, int pinned, PrgPrefixMatch *out);
+/* Copy a full-entry match into a working state (positions [0, match.len) and
+ * the GDN states); continue with prg_model_prefill_from. */
+int prg_prefix_cache_restore(const PrgPrefixCache *cache, PrgPrefixMatch match, PrgModelState *work);
+/* Normalised hidden rows per entry (MTP drafter seeding):
+ * enableHiddenTracking, entryHidden / entryHiddenValid, setEntryHidden. */
+int prg_prefix_cache_enable_hidden(PrgPrefixCache *cache);
+int prg_prefix_cache_entry_hidden(const PrgPrefixCache *cache, PrgPrefixMatch match, uint16_t **rows, int *valid);
+int prg_prefix_cache_set_entry_hidden(PrgPrefixCache *cache, PrgPrefixMatch match, const uint16_t *rows);
+
+/* PRGPFXS1 v3: 48-byte header {magic u64, version u32 = 3, dtype u32 = 0
+ * (bf16), model_fingerprint u64, token_count u64, next_token u32,
+ * next_token_valid u32, hidden_valid u32, pad}, the token ids u32, then per
+ * layer in order the GDN conv f32 [3, 8192] and recurrent f32 [32, 128, 128],
+ * or K [4][T][256] and V [4][256][T] bf16 compacted to the T cached tokens,
+ * then the hidden rows bf16 [T, hidden] (zeros unless hidden_valid). Little
+ * endian (prefix_persist.zig:36-80, 253-328). */
+/* save: atomically (temp file + rename) write the active entry, else the most
+ * recently used one. EMPTY_INPUT when nothing is cached. */
+int prg_prefix_cache_save(const PrgPrefixCache *cache, const char *path, uint64_t model_fingerprint);
+/* load: validate magic, version, dtype, fingerprint, next token < vocab,
+ * flags, token count within the budget and the exact file length; a missing
+ * or invalid file leaves the cache unchanged and sets *loaded_tokens = 0
+ * (prg_last_error() says why). A valid file replaces the cache's contents with
+ * one pinned, active entry. Errors only for failures while reading, after
+ * which the cache is empty. */
+int prg_prefix_cache_load(PrgPrefixCache *cache, const char *path, uint64_t model_fingerprint,
+                          uint32_t *loaded_tokens);
+/* Byte length of a PRGPFXS1 file of token_count tokens for this topology
+ * (expectedFileBytes, prefix_persist.zig:71-80). */
+int prg_prefix_state_file_bytes(const PrgModelConfig *cfg, uint64_t token_count, uint64_t *bytes);
+/* $HOME/.cache/peregrine/qwen35-9b-q4-prefix-state.bin (resolveDefaultPath). */
+int prg_prefix_state_default_path(char *buf, size_t len);
+/* modelFingerprint (prefix_persist.zig:149-190): Wyhash seeded with
+ * MAGIC ^ VERSION over config.json, then each *.safetensors file in bytewise
+ * name order (name, then content). */
+int prg_model_fingerprint(const char *model_dir, uint64_t *out);
+/* The Wyhash used above (std.hash.Wyhash: final-v4 rounds, original secret). */
+int prg_wyhash(const void *data, size_t len, uint64_t seed, uint64_t *out);
+
+/* ======================================================================
  * Checkpoints (host code; no GPU needed except for prg_model_load).
  * ====================================================================== */
 

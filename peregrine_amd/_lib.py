@@ -30,6 +30,14 @@ _SCALARS = {
     "void": None,
 }
 
+class PrgPrefixMatch(C.Structure):
+    """struct PrgPrefixMatch (passed by value)."""
+    _fields_ = [("index", C.c_uint32), ("len", C.c_uint32)]
+
+
+# Structs passed by value in the C ABI.
+_STRUCTS = {"PrgPrefixMatch": PrgPrefixMatch}
+
 _PROTO = re.compile(r"^\s*([A-Za-z_][\w\s\*]*?)\s*\b(prg_\w+)\s*\(([^;]*?)\)\s*;", re.M | re.S)
 
 
@@ -43,6 +51,8 @@ def _ctype(decl: str):
     toks = decl.split()
     if not toks:
         return None
+    if toks[0] in _STRUCTS:
+        return _STRUCTS[toks[0]]
     return _SCALARS[toks[-1] if toks[-1] in _SCALARS else toks[0]]
 
 

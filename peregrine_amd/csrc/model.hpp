@@ -230,9 +230,18 @@ int encode_mlp(PrgModel* m, PrgModelState* st, const DecoderLayer& L, int M, con
 int ensure_prefill_ws(PrgModelState* st);
 int prefill_layer(PrgModel* m, PrgModelState* st, const DecoderLayer& L, LayerState& ls, const uint16_t* x,
                   uint16_t* out, uint32_t T, uint32_t start);
-// Ingest st->prompt[0, len); with_mtp also seeds the drafter's KV cache and
-// leaves the last prompt row's normalised hidden in st->cur_hidden.
-int run_prefill(PrgModel* m, PrgModelState* st, uint32_t len, bool with_mtp);
+// Ingest st->prompt[from, len) on top of positions [0, from); with_mtp also
+// seeds the drafter's KV cache and leaves the last prompt row's normalised
+// hidden in st->cur_hidden.
+int run_prefill(PrgModel* m, PrgModelState* st, uint32_t from, uint32_t len, bool with_mtp);
+
+// ------------------------------------------------------ state transfers ---
+// ModelState.copyFullAttentionRangeFrom / copyLinearStateFrom
+// (state.zig:124-180) between two states of one model, ordered after the
+// source's pending work and complete on return.
+int copy_attention_range(PrgModelState* dst, uint32_t dst_start, const PrgModelState* src, uint32_t src_start,
+                         uint32_t count);
+int copy_linear_state(PrgModelState* dst, const PrgModelState* src);
 
 // ------------------------------------------------------ speculative path ---
 int ensure_spec_ws(PrgModelState* st);

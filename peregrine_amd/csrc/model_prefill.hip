@@ -166,21 +166,22 @@ int prefill_layer(PrgModel* m, PrgModelState* st, const DecoderLayer& L, LayerSt
   return qmm(s, w.inter, L.mlp.down_proj, out, T, kGemmResidual, w.resid, nullptr, "prefill.mlp.down_proj");
 }
 
-// Ingest st->prompt[0, len) in chunks, then the argmax tail on the last row
+// Ingest st->prompt[from, len) in chunks on top of a state that holds
+// positions [0, from), then the argmax tail on the last row
 // (encodePrefillArgmaxTailBf16, model.zig:1307-1324). The caller has set ctl
 // to step len-1 of a len-token prompt; the argmax kernel records the
 // prediction and advances ctl to position len. With the drafter, each chunk's
 // final-normed hidden rows also seed its KV cache (server.zig:1286-1325: the
 // drafter consumes hidden[t] with token[t+1]) and the last row is kept in
 // st->cur_hidden for the speculative loop.
-int run_prefill(PrgModel* m, PrgModelState* st, uint32_t len, bool with_mtp) {
+int run_prefill(PrgModel* m, PrgModelState* st, uint32_t from, uint32_t len, bool with_mtp) {
   if (int rc = ensure_prefill_ws(st)) return rc;
   const PrgModelConfig& c = m->cfg;
   hipStream_t s = st->stream;
   PrefillWs& w = st->pf;
   const uint16_t* last = nullptr;
   uint32_t T = 0, tail_rows = 0, tail_start = 0;
-  for (uint32_t start = 0; start < len; start += T) {
+  for (uint32_t start = from; start < len; start += T) {
     T = prefill_chunk_tokens(st, start, len - start);
     if (int rc = launch_embedding(s, m->embed.weight, m->embed.scales, m->embed.biases, w.h0, st->prompt + start, 0,
                                   T, c.hidden))
@@ -263,7 +264,7 @@ int prg_model_prefill(PrgModel* model, PrgModelState* st, const uint32_t* prompt
   ctl.capacity = st->max_seq;
   PRG_HIP(hipMemcpyAsync(st->prompt, prompt, sizeof(uint32_t) * prompt_len, hipMemcpyHostToDevice, st->stream));
   PRG_HIP(hipMemcpyAsync(st->ctl, &ctl, sizeof(ctl), hipMemcpyHostToDevice, st->stream));
-  if (int rc = run_prefill(model, st, prompt_len, false)) return rc;
+  if (int rc = run_prefill(model, st, 0, prompt_len, false)) return rc;
   PRG_HIP(hipMemcpyAsync(next_token, st->predictions + (prompt_len - 1), sizeof(uint32_t), hipMemcpyDeviceToHost,
                          st->stream));
   PRG_HIP(hipStreamSynchronize(st->stream));

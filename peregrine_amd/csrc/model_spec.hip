@@ -368,7 +368,7 @@ int prg_model_generate_speculative(PrgModel* model, PrgModelState* st, const uin
   ctl.capacity = st->max_seq;
   PRG_HIP(hipMemcpyAsync(st->prompt, prompt, sizeof(uint32_t) * prompt_len, hipMemcpyHostToDevice, st->stream));
   PRG_HIP(hipMemcpyAsync(st->ctl, &ctl, sizeof(ctl), hipMemcpyHostToDevice, st->stream));
-  if (int rc = run_prefill(model, st, prompt_len, true)) return rc;
+  if (int rc = run_prefill(model, st, 0, prompt_len, true)) return rc;
   uint32_t first = 0;
   PRG_HIP(hipMemcpyAsync(&first, st->predictions + (prompt_len - 1), sizeof(uint32_t), hipMemcpyDeviceToHost,
                          st->stream));

@@ -153,6 +153,17 @@ class ModelState:
              C.byref(out))
         return int(out.value)
 
+    def prefill_from(self, prompt, prefix_len: int) -> int:
+        """Prefill prompt[prefix_len:] on top of a state holding prompt[:prefix_len]."""
+        prompt = np.ascontiguousarray(prompt, np.uint32)
+        out = C.c_uint32(0)
+        call("prg_model_prefill_from", self.model.handle, self.handle, prompt.ctypes.data_as(C.c_void_p),
+             len(prompt), prefix_len, C.byref(out))
+        return int(out.value)
+
+    def copy_prefix_from(self, src: "ModelState", token_count: int) -> None:  # state.zig:124-128
+        call("prg_model_state_copy_prefix", self.handle, src.handle, token_count)
+
     def decode(self, n_steps: int) -> tuple[np.ndarray, float]:
         toks = np.empty(n_steps, np.uint32)
         ms = C.c_float(0.0)
