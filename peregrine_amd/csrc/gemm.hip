@@ -61,8 +61,10 @@ __device__ inline uint4 load8(const uint16_t* row, uint32_t k, uint32_t K) {
 
 template <bool Q4, int EPI>
 __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const GemmArgs g) {
-  __shared__ __attribute__((aligned(16))) uint16_t sA[kBM * kLdsRow];
-  __shared__ __attribute__((aligned(16))) uint16_t sB[kBN * kLdsRow];
+  // two LDS stages: step k's tiles are read by the matrix cores while step
+  // k+1's are written
+  __shared__ __attribute__((aligned(16))) uint16_t sA[2][kBM * kLdsRow];
+  __shared__ __attribute__((aligned(16))) uint16_t sB[2][kBN * kLdsRow];
   constexpr bool kPair = (EPI == kGemmSiluPair);
   constexpr uint32_t kTileN = kPair ? kBN / 2 : kBN;  // output columns per block
 
@@ -143,37 +145,52 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const GemmArgs g) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) brow[j] = kPair ? ((j < 2) ? wn * 32 + 16 * j : 64 + wn * 32 + 16 * (j - 2)) : wn * 64 + 16 * j;
 
-  load(0);
-  for (uint32_t k0 = 0; k0 < K; k0 += kBK) {
-    __syncthreads();  // the previous step's fragments have been read
+  // Registers -> LDS stage st (A as loaded, Q4 B dequantised once here).
+  auto store_stage = [&](int st) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(&sA[(ld_row + 32 * i) * kLdsRow + ld_c8]) = ra[i];
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(&sA[st][(ld_row + 32 * i) * kLdsRow + ld_c8]) = ra[i];
     if constexpr (Q4) {
       const float s = bf2f(rs), b = bf2f(rbias);
-      uint4* dst = reinterpret_cast<uint4*>(&sB[q_row * kLdsRow + q_half * 32]);
+      uint4* dst = reinterpret_cast<uint4*>(&sB[st][q_row * kLdsRow + q_half * 32]);
       dst[0] = dequant_word(rw.x, s, b);
       dst[1] = dequant_word(rw.y, s, b);
       dst[2] = dequant_word(rw.z, s, b);
       dst[3] = dequant_word(rw.w, s, b);
     } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(&sB[(ld_row + 32 * i) * kLdsRow + ld_c8]) = rb[i];
+      for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(&sB[st][(ld_row + 32 * i) * kLdsRow + ld_c8]) = rb[i];
     }
-    __syncthreads();
-    if (k0 + kBK < K) load(k0 + kBK);  // in flight while the matrix cores run
+  };
+
+  // One barrier per K step: step k+1 is stored into the other stage and step
+  // k+2's global loads are issued before the matrix cores run on stage k; the
+  // barrier then both publishes stage k+1 and retires the reads of stage k.
+  load(0);
+  store_stage(0);
+  if (kBK < K) load(kBK);
+  __syncthreads();
+  int st = 0;
+  for (uint32_t k0 = 0; k0 < K; k0 += kBK, st ^= 1) {
+    if (k0 + kBK < K) {
+      store_stage(st ^ 1);
+      if (k0 + 2 * kBK < K) load(k0 + 2 * kBK);
+    }
+    const uint16_t* A = sA[st];
+    const uint16_t* B = sB[st];
 #pragma unroll
     for (int kk = 0; kk < kBK; kk += 32) {
       bf16x8 af[4], bfr[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        af[i] = *reinterpret_cast<const bf16x8*>(&sA[(wm * 64 + 16 * i + frow) * kLdsRow + kk + fk]);
+        af[i] = *reinterpret_cast<const bf16x8*>(&A[(wm * 64 + 16 * i + frow) * kLdsRow + kk + fk]);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) bfr[j] = *reinterpret_cast<const bf16x8*>(&sB[(brow[j] + frow) * kLdsRow + kk + fk]);
+      for (int j = 0; j < 4; ++j) bfr[j] = *reinterpret_cast<const bf16x8*>(&B[(brow[j] + frow) * kLdsRow + kk + fk]);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
     }
+    __syncthreads();
   }
 
   // Epilogue: lane holds rows 4*(lane/16) + r, column lane%16 of each block.
