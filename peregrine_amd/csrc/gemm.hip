@@ -16,31 +16,6 @@ namespace {
 using namespace prg;
 
 constexpr int kBM = 128, kBN = 128, kBK = 64, kGemmThreads = 256;
-// Workgroups go to the 8 XCDs round-robin (workgroup b runs on XCD b % 8),
-// each XCD with its own 4 MB L2. Tiles are numbered in groups of kGroupM
-// M-tiles (M fastest inside a group, then N) and each XCD takes a contiguous
-// range of that order, so the blocks resident on one XCD share kGroupM
-// activation panels (128 x K bf16 each) in its L2 while they sweep N.
-constexpr int kXcds = 8;
-#ifndef PRG_GEMM_GROUP_M
-#define PRG_GEMM_GROUP_M 2
-#endif
-constexpr uint32_t kGroupM = PRG_GEMM_GROUP_M;
-
-// Launch slot -> tile index (the grid has kXcds * per_xcd slots; slots past
-// `tiles` have no tile).
-__device__ inline uint32_t tile_of_slot(uint32_t slot, uint32_t per_xcd) {
-  return (slot % kXcds) * per_xcd + slot / kXcds;
-}
-
-// Tile index -> (M-tile, N-tile) in the grouped order.
-__device__ inline void tile_coords(uint32_t t, uint32_t tiles_m, uint32_t tiles_n, uint32_t* tm, uint32_t* tn) {
-  const uint32_t per_group = kGroupM * tiles_n;
-  const uint32_t grp = t / per_group, r = t % per_group;
-  const uint32_t gm = min(kGroupM, tiles_m - grp * kGroupM);  // M-tiles in this (possibly last) group
-  *tm = grp * kGroupM + r % gm;
-  *tn = r / gm;
-}
 constexpr int kLdsRow = kBK + 8;  // bf16 per LDS row (144 bytes)
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -96,17 +71,14 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const GemmArgs g) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const uint32_t tiles_m = (g.M + kBM - 1) / kBM;
-  const uint32_t t = tile_of_slot(blockIdx.x, g.tiles_per_xcd);
-  if (t >= g.tiles) return;
-  uint32_t tm, tn;
-  tile_coords(t, tiles_m, g.tiles / tiles_m, &tm, &tn);
+  const uint32_t tn = blockIdx.x / tiles_m;
   uint32_t seg = 0;  // Q4 weight segment of this output tile
   if constexpr (Q4 && !kPair) {
 #pragma unroll
     for (int i = 1; i < kGemmMaxSegs; ++i)
       if (i < static_cast<int>(g.nq) && tn >= g.q[i].tile0) seg = i;
   }
-  const uint32_t m0 = tm * kBM;
+  const uint32_t m0 = (blockIdx.x % tiles_m) * kBM;
   const uint32_t n0 = (tn - (Q4 ? g.q[seg].tile0 : 0)) * kTileN;
   const uint32_t N = Q4 ? g.q[seg].n : g.N;
   const uint64_t z = blockIdx.z;
@@ -276,10 +248,8 @@ int launch_t(hipStream_t s, const GemmArgs& g, uint32_t batch, const char* name)
   uint32_t tiles_n = (g.N + kTileN - 1) / kTileN;
   if (Q4) tiles_n = (EPI == kGemmSiluPair) ? (g.q[0].n + kTileN - 1) / kTileN : g.q[g.nq - 1].tile0 +
                     (g.q[g.nq - 1].n + kTileN - 1) / kTileN;
-  GemmArgs a = g;
-  a.tiles = ((g.M + kBM - 1) / kBM) * tiles_n;
-  a.tiles_per_xcd = (a.tiles + kXcds - 1) / kXcds;
-  hipLaunchKernelGGL((gemm_kernel<Q4, EPI>), dim3(a.tiles_per_xcd * kXcds, 1, batch), dim3(kGemmThreads), 0, s, a);
+  const uint32_t tiles = ((g.M + kBM - 1) / kBM) * tiles_n;
+  hipLaunchKernelGGL((gemm_kernel<Q4, EPI>), dim3(tiles, 1, batch), dim3(kGemmThreads), 0, s, g);
   PRG_CHECK_LAUNCH(name);
   return PRG_OK;
 }

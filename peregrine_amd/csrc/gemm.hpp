@@ -64,8 +64,6 @@ struct GemmArgs {
   uint64_t ldc = 0, ldc_hi = 0, c_z = 0;
   uint32_t c_group = 0;
   uint32_t M = 0, N = 0, K = 0;
-  // set by the launcher: output tiles and launch slots per XCD
-  uint32_t tiles = 0, tiles_per_xcd = 0;
 };
 
 // Q4 weights in g.q[0..nq). K % 64 == 0; A rows 16-byte aligned (lda % 8 == 0).
