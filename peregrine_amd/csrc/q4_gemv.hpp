@@ -26,6 +26,8 @@
 //     one launch (e.g. in_proj qkv | z | a | b), cutting launches per layer.
 #pragma once
 
+#include <type_traits>
+
 #include "common.hpp"
 #include "norm.hpp"
 #include "gdn.hpp"
@@ -137,11 +139,15 @@ __device__ inline void unpack_q4_word(uint32_t word, uint32_t (&t)[4]) {
 }
 
 // Register buffer holding one group's weights for one wave: ROWS rows of each
-// of NMAT matrices, ITERS K-steps, plus the matching scale/bias halves.
+// of NMAT matrices, ITERS K-steps, plus the matching scale and bias bits.
+// Scale and bias stay in separate registers as loaded: combining them when
+// the loads are issued would make the wave wait for the prefetched group's
+// loads right away, i.e. one full memory latency per group.
 template <int NMAT, int ROWS, int ITERS>
 struct GemvBuf {
   u32x4 w[NMAT][ROWS][ITERS];
-  uint32_t sb[NMAT][ROWS][ITERS];  // scale bits | bias bits << 16
+  uint32_t sc[NMAT][ROWS][ITERS];  // bf16 scale bits (zero-extended)
+  uint32_t bi[NMAT][ROWS][ITERS];  // bf16 bias bits (zero-extended)
 };
 
 // Where group g of the launch lives: segment index and first row.
@@ -175,12 +181,12 @@ __device__ inline void gemv_load(const GemvParams& p, uint32_t g, int lane, bool
       for (int it = 0; it < ITERS; ++it) {
         if (!TAIL || it < ITERS - 1 || tail_active) {
           b.w[mat][r][it] = __builtin_nontemporal_load(wp + it * (kGemvKStep / 32));
-          const uint32_t sc = sg.s[mat][meta + it * (kGemvKStep / 64)];
-          const uint32_t bi = sg.b[mat][meta + it * (kGemvKStep / 64)];
-          b.sb[mat][r][it] = sc | (bi << 16);
+          b.sc[mat][r][it] = sg.s[mat][meta + it * (kGemvKStep / 64)];
+          b.bi[mat][r][it] = sg.b[mat][meta + it * (kGemvKStep / 64)];
         } else {
           b.w[mat][r][it] = u32x4{0u, 0u, 0u, 0u};
-          b.sb[mat][r][it] = 0u;
+          b.sc[mat][r][it] = 0u;
+          b.bi[mat][r][it] = 0u;
         }
       }
     }
@@ -242,8 +248,8 @@ __device__ inline void gemv_dot_step(const GemvBuf<NMAT, ROWS, ITERS>& b, int it
           for (int c = 0; c < 4; ++c) aq[m][c] = dot2_bf16(t[c], x.xp[m][4 * j + c], aq[m][c]);
         }
       }
-      const float sc = bf_lo(b.sb[mat][r][it]);
-      const float bi = bf_hi(b.sb[mat][r][it]);
+      const float sc = bf_lo(b.sc[mat][r][it]);
+      const float bi = bf_lo(b.bi[mat][r][it]);
 #pragma unroll
       for (int m = 0; m < M; ++m) {
         const float dq = (aq[m][0] + aq[m][1]) + (aq[m][2] + aq[m][3]);
@@ -461,18 +467,12 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(const GemvParams 
     }
   }
 
-  // 2) the first group's weights (the first three with kDeep).
+  // 2) the first group's weights. The wave handles n groups (wave-uniform).
   constexpr bool kRounds = (ROWS == 1 && EPI != kEpiArgmax);
-  // Measured on MI355X: three groups in flight per wave (four buffers) is
-  // slower than one (gate/up 17.9 vs 15.7 us), so the deep variant is off.
-  constexpr bool kDeep = false;
-  GemvBuf<NMAT, ROWS, ITERS> b0, b1, b2, b3;
+  GemvBuf<NMAT, ROWS, ITERS> b0, b1;
   uint32_t g = blockIdx.x * kGemvWaves + wid;
-  if (g < G) gemv_load<NMAT, ROWS, ITERS, TAIL>(p, g, lane, tail_active, b0);
-  if constexpr (kDeep) {
-    if (g + W < G) gemv_load<NMAT, ROWS, ITERS, TAIL>(p, g + W, lane, tail_active, b1);
-    if (g + 2 * W < G) gemv_load<NMAT, ROWS, ITERS, TAIL>(p, g + 2 * W, lane, tail_active, b2);
-  }
+  uint32_t n = g < G ? (G - 1 - g) / W + 1 : 0;
+  if (n > 0) gemv_load<NMAT, ROWS, ITERS, TAIL>(p, g, lane, tail_active, b0);
 
   // 3) stage x into LDS (normalised with NORM), then into registers.
 #pragma unroll
@@ -545,57 +545,59 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(const GemvParams 
     }
   };
 
+  // 4) The pipeline: group i + 1 streams into the other register buffer
+  // while group i is dequantised. Every prefetch load is issued on
+  // straight-line code whose continuation always uses it: a prefetch under a
+  // branch joins a path without it, and the compiler's wait counts at the
+  // join then cover the prefetched loads as well, i.e. the wave waits for the
+  // next group's loads before it dequantises the current one.
   if constexpr (kRounds) {
-    // 4) rounds of four groups g, g+W, g+2W, g+3W: the group `ahead` steps
-    // later streams into a free register buffer while the current one is
-    // dequantised (ahead = 3 with four buffers, else 1 with two); then one
-    // transposed reduction for the round and a one-lane-per-group epilogue.
+    // Rounds of up to four groups g + jW (j < NV); MORE says that another
+    // round follows, so the round's last group prefetches the next round's
+    // first. One transposed reduction per round, then a one-lane-per-group
+    // epilogue.
     constexpr int E = NMAT * M;
-    constexpr uint32_t ahead = kDeep ? 3 : 1;
-    auto step = [&](const GemvBuf<NMAT, 1, ITERS>& cur, GemvBuf<NMAT, 1, ITERS>& nxt, uint32_t gq,
-                    float (&vq)[E]) {
+    auto step = [&](const GemvBuf<NMAT, 1, ITERS>& cur, float (&vq)[E]) {
       float acc[NMAT][1][M];
-      if (gq < G) {
-        if (gq + ahead * W < G) gemv_load<NMAT, 1, ITERS, TAIL>(p, gq + ahead * W, lane, tail_active, nxt);
-        accumulate(cur, acc);
-      } else {
-#pragma unroll
-        for (int mat = 0; mat < NMAT; ++mat)
-#pragma unroll
-          for (int m = 0; m < M; ++m) acc[mat][0][m] = 0.0f;
-      }
+      accumulate(cur, acc);
 #pragma unroll
       for (int mat = 0; mat < NMAT; ++mat)
 #pragma unroll
         for (int m = 0; m < M; ++m) vq[mat * M + m] = acc[mat][0][m];
     };
-    while (g < G) {
+    auto round = [&](auto nv_c, auto more_c) {
+      constexpr int NV = decltype(nv_c)::value;
+      constexpr bool MORE = decltype(more_c)::value;
       float v[4][E];
-      if constexpr (kDeep) {
-        step(b0, b3, g, v[0]);
-        step(b1, b0, g + W, v[1]);
-        step(b2, b1, g + 2 * W, v[2]);
-        step(b3, b2, g + 3 * W, v[3]);
-      } else {
-        step(b0, b1, g, v[0]);
-        step(b1, b0, g + W, v[1]);
-        step(b0, b1, g + 2 * W, v[2]);
-        step(b1, b0, g + 3 * W, v[3]);
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int e = 0; e < E; ++e) v[q][e] = 0.0f;
+      if constexpr (NV > 1 || MORE) gemv_load<NMAT, 1, ITERS, TAIL>(p, g + W, lane, tail_active, b1);
+      step(b0, v[0]);
+      if constexpr (NV > 1) {
+        if constexpr (NV > 2 || MORE) gemv_load<NMAT, 1, ITERS, TAIL>(p, g + 2 * W, lane, tail_active, b0);
+        step(b1, v[1]);
+      }
+      if constexpr (NV > 2) {
+        if constexpr (NV > 3 || MORE) gemv_load<NMAT, 1, ITERS, TAIL>(p, g + 3 * W, lane, tail_active, b1);
+        step(b0, v[2]);
+      }
+      if constexpr (NV > 3) {
+        if constexpr (MORE) gemv_load<NMAT, 1, ITERS, TAIL>(p, g + 4 * W, lane, tail_active, b0);
+        step(b1, v[3]);
       }
       reduce4_rows<E>(v);
       // 16-lane row q now holds group g + qW; its first lane writes the row.
       GemvRowDst dst{};
       bool valid = false;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const uint32_t gq = g + q * W;
-        if (gq < G) {
-          const GemvLoc loc = gemv_locate<1>(p, gq);
-          const GemvRowDst dq = gemv_row_dst(p.seg[loc.seg], loc.row0);
-          if ((lane >> 4) == q) {
-            dst = dq;
-            valid = true;
-          }
+      for (int q = 0; q < NV; ++q) {
+        const GemvLoc loc = gemv_locate<1>(p, g + q * W);
+        const GemvRowDst dq = gemv_row_dst(p.seg[loc.seg], loc.row0);
+        if ((lane >> 4) == q) {
+          dst = dq;
+          valid = true;
         }
       }
       if (valid && (lane & 15) == 0) {
@@ -606,7 +608,22 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(const GemvParams 
           for (int m = 0; m < M; ++m) tot[mat][m] = v[0][mat * M + m];
         gemv_store_row<M, NMAT, EPI>(dst, tot);
       }
+    };
+    using C1 = std::integral_constant<int, 1>;
+    using C2 = std::integral_constant<int, 2>;
+    using C3 = std::integral_constant<int, 3>;
+    using C4 = std::integral_constant<int, 4>;
+    while (n > 4) {
+      round(C4{}, std::true_type{});
       g += 4 * W;
+      n -= 4;
+    }
+    switch (n) {
+      case 4: round(C4{}, std::false_type{}); break;
+      case 3: round(C3{}, std::false_type{}); break;
+      case 2: round(C2{}, std::false_type{}); break;
+      case 1: round(C1{}, std::false_type{}); break;
+      default: break;
     }
   } else {
     auto process = [&](const GemvBuf<NMAT, ROWS, ITERS>& b, uint32_t grp) {
@@ -614,15 +631,20 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(const GemvParams 
       accumulate(b, acc);
       gemv_epilogue<M, NMAT, ROWS, EPI>(p, gemv_locate<ROWS>(p, grp), lane, acc);
     };
-    // 4) two buffers: compute g while g+W streams in.
-    while (g < G) {
-      if (g + W < G) gemv_load<NMAT, ROWS, ITERS, TAIL>(p, g + W, lane, tail_active, b1);
+    while (n > 2) {
+      gemv_load<NMAT, ROWS, ITERS, TAIL>(p, g + W, lane, tail_active, b1);
       process(b0, g);
-      g += W;
-      if (g >= G) break;
-      if (g + W < G) gemv_load<NMAT, ROWS, ITERS, TAIL>(p, g + W, lane, tail_active, b0);
-      process(b1, g);
-      g += W;
+      gemv_load<NMAT, ROWS, ITERS, TAIL>(p, g + 2 * W, lane, tail_active, b0);
+      process(b1, g + W);
+      g += 2 * W;
+      n -= 2;
+    }
+    if (n == 2) {
+      gemv_load<NMAT, ROWS, ITERS, TAIL>(p, g + W, lane, tail_active, b1);
+      process(b0, g);
+      process(b1, g + W);
+    } else if (n == 1) {
+      process(b0, g);
     }
   }
 }
