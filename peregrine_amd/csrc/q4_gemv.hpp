@@ -14,7 +14,8 @@
 //   * Dequant stays in registers: v_perm_b32 places each nibble under the
 //     byte 0x43 (bf16 0x43qq == 128 + q exactly), two per dword, and
 //     v_dot2c_f32_bf16 multiplies them with the matching activation pair in
-//     fp32; the 128*sum(x) offset is removed once per half-group.
+//     fp32; one of the two dot2 chains of a half-group starts at -128*sum(x),
+//     which removes the offset.
 //   * x is staged once per block in LDS, pre-permuted so each activation pair
 //     lines up with the nibble pair the unpack produces.
 //     An optional fused RMSNorm prologue normalises x while staging it.
@@ -198,6 +199,7 @@ template <int M>
 struct XStep {
   uint32_t xp[M][16];
   float xsum[M];
+  float xoff[M];  // -128 * xsum, exact: the 128 + q offset of the unpacked nibbles
 };
 
 template <int M>
@@ -218,6 +220,7 @@ __device__ inline void gemv_read_x(const uint32_t* xs, uint32_t K, int it, int l
 #pragma unroll
     for (int j = 0; j < 16; ++j) s = dot2_bf16(x.xp[m][j], kOnes, s);
     x.xsum[m] = s;
+    x.xoff[m] = -128.0f * s;
   }
 }
 
@@ -231,13 +234,15 @@ __device__ inline void gemv_dot_step(const GemvBuf<NMAT, ROWS, ITERS>& b, int it
     for (int r = 0; r < ROWS; ++r) {
       const u32x4 w4 = b.w[mat][r][it];
       const uint32_t wd[4] = {w4[0], w4[1], w4[2], w4[3]};
-      // Four independent dot2 chains per activation row: the dependent
-      // v_dot2c latency would otherwise serialise the 16 dot2s of a step.
-      float aq[M][4];
+      // Two dot2 chains per activation row (the other matrices, rows and
+      // K-steps give the scheduler more independent chains); the first starts
+      // at -128 * sum(x), so the chains add up to sum(q * x) directly.
+      float aq[M][2];
 #pragma unroll
-      for (int m = 0; m < M; ++m)
-#pragma unroll
-        for (int c = 0; c < 4; ++c) aq[m][c] = 0.0f;
+      for (int m = 0; m < M; ++m) {
+        aq[m][0] = x.xoff[m];
+        aq[m][1] = 0.0f;
+      }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         uint32_t t[4];
@@ -245,15 +250,14 @@ __device__ inline void gemv_dot_step(const GemvBuf<NMAT, ROWS, ITERS>& b, int it
 #pragma unroll
         for (int m = 0; m < M; ++m) {
 #pragma unroll
-          for (int c = 0; c < 4; ++c) aq[m][c] = dot2_bf16(t[c], x.xp[m][4 * j + c], aq[m][c]);
+          for (int c = 0; c < 4; ++c) aq[m][c & 1] = dot2_bf16(t[c], x.xp[m][4 * j + c], aq[m][c & 1]);
         }
       }
       const float sc = bf_lo(b.sc[mat][r][it]);
       const float bi = bf_lo(b.bi[mat][r][it]);
 #pragma unroll
       for (int m = 0; m < M; ++m) {
-        const float dq = (aq[m][0] + aq[m][1]) + (aq[m][2] + aq[m][3]);
-        const float qx = dq - 128.0f * x.xsum[m];  // sum(q * x)
+        const float qx = aq[m][0] + aq[m][1];  // sum(q * x)
         acc[mat][r][m] += sc * qx + bi * x.xsum[m];
       }
     }
