@@ -158,6 +158,9 @@ def main() -> int:
     ap.add_argument("--eager", action="store_true",
                     help="launch each token's kernels directly instead of replaying the HIP graph "
                          "(for kernel tracers; slower)")
+    ap.add_argument("--configs", action="store_true",
+                    help="only the operator benchmarks of BASELINE configs 2-4 (Q4 GEMV sweep, 24 GDN layers, "
+                         "GQA decode attention at L = 4096 / 24576 / 65536), one JSON line")
     ap.add_argument("--roofline-only", action="store_true",
                     help="only the dominant-kernel loop and a 256 MiB copy-kernel reference (for PMC runs)")
     a = ap.parse_args()
@@ -172,6 +175,17 @@ def main() -> int:
 
     device.init(0)
     log("[bench]", device.device_name())
+    if a.configs:
+        from peregrine_amd.op_bench import configs_3_4
+
+        rows = gemv_sweep()
+        for r in rows:
+            r["config"] = 2
+        rows += configs_3_4()
+        for r in rows:
+            log(f"[bench] {r}")
+        print(json.dumps({"configs": rows, "device": device.device_name()}), flush=True)
+        return 0
     if a.roofline_only:
         import ctypes as C
 

@@ -21,6 +21,8 @@
 //   phase 3  P.V: 8 lanes x 16 B cover 64 consecutive tokens of one V row
 //            (128 B, coalesced); 8 rows per wave load; fp32 FMA with p from
 //            LDS; 8-lane DPP sum at the end.
+#include <stdlib.h>
+
 #include "attention.hpp"
 
 namespace {
@@ -178,7 +180,21 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnD
       if (4 * w + 16 * i < T) score(tt, kt[i][0], kt[i][1], tt < T);
     }
   } else {
-    for (uint32_t tt = 4 * w + r; tt < T; tt += 16) {
+    // Four tokens per lane per pass: all eight K loads are issued before the
+    // first dot product, so a wave keeps 8 KiB of K in flight.
+    uint32_t tt = 4 * w + r;
+    for (; tt + 48 < T; tt += 64) {
+      uint4 k4[4][2];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint4* kp = reinterpret_cast<const uint4*>(kbase + static_cast<size_t>(t0 + tt + 16 * i) * kAttnHeadDim);
+        k4[i][0] = kp[0];
+        k4[i][1] = kp[1];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) score(tt + 16 * i, k4[i][0], k4[i][1], true);
+    }
+    for (; tt < T; tt += 16) {
       const uint4* kp = reinterpret_cast<const uint4*>(kbase + static_cast<size_t>(t0 + tt) * kAttnHeadDim);
       score(tt, kp[0], kp[1], true);
     }
@@ -214,7 +230,44 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnD
   for (int p = 0; p < 8; ++p)
 #pragma unroll
     for (int g = 0; g < static_cast<int>(kAttnGroup); ++g) acc[p][g] = 0.0f;
-  for (uint32_t tb = 0; tb < T; tb += 64) {
+  uint32_t tb0 = 0;
+  if (!one_tile) {
+    // Two full 64-token tiles per pass: all sixteen V loads are issued before
+    // the first FMA, so a wave keeps 16 KiB of V in flight.
+    for (; tb0 + 128 <= T; tb0 += 128) {
+      uint4 v2[2][8];
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int p = 0; p < 8; ++p)
+          v2[h][p] = *reinterpret_cast<const uint4*>(vbase + static_cast<size_t>(8 * p) * a.stride + t0 + tb0 +
+                                                     64 * h + 8 * ts);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint32_t tl = tb0 + 64 * h + 8 * ts;
+        float pv[kAttnGroup][8];
+#pragma unroll
+        for (int g = 0; g < static_cast<int>(kAttnGroup); ++g)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) pv[g][i] = sc[g * ld + tl + i];
+#pragma unroll
+        for (int p = 0; p < 8; ++p) {
+          const uint32_t vd[4] = {v2[h][p].x, v2[h][p].y, v2[h][p].z, v2[h][p].w};
+          float v8[8];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            v8[2 * i] = bf_lo(vd[i]);
+            v8[2 * i + 1] = bf_hi(vd[i]);
+          }
+#pragma unroll
+          for (int g = 0; g < static_cast<int>(kAttnGroup); ++g)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[p][g] += pv[g][i] * v8[i];
+        }
+      }
+    }
+  }
+  for (uint32_t tb = tb0; tb < T; tb += 64) {
     const uint32_t tl = tb + 8 * ts;  // first of this lane's 8 tokens (block-local)
     if (tl >= T) continue;
     const uint32_t nvalid = min(8u, T - tl);
@@ -324,10 +377,22 @@ __global__ __launch_bounds__(kAttnThreads) void attn_reduce_kernel(const AttnDec
 
 namespace prg {
 
+// Most tokens one split may hold; PEREGRINE_ATTN_SPLIT_TOKENS overrides it
+// (a power of two from 64 to 4096) for tuning.
+static uint32_t attn_max_split_tokens() {
+  static const uint32_t v = [] {
+    const char* e = getenv("PEREGRINE_ATTN_SPLIT_TOKENS");
+    const long t = e ? atol(e) : 0;
+    return (t >= 64 && t <= 4096 && (t & (t - 1)) == 0) ? static_cast<uint32_t>(t) : 1024u;
+  }();
+  return v;
+}
+
 uint32_t attn_num_splits(uint32_t capacity) {
-  // >= 64 splits per kv head (256 blocks) and <= 1024 tokens per split.
+  // >= 64 splits per kv head (256 blocks) and <= attn_max_split_tokens() per split.
+  const uint32_t cap = attn_max_split_tokens();
   uint32_t n = 64;
-  while ((capacity + n - 1) / n > 1024 && n < kMaxSplits) n *= 2;
+  while ((capacity + n - 1) / n > cap && n < kMaxSplits) n *= 2;
   return n;
 }
 
