@@ -199,6 +199,19 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnD
       score(tt, kp[0], kp[1], true);
     }
   }
+  // The first two 64-token V tiles do not depend on the softmax: their loads
+  // are issued here, so they stream in while phase 2 runs.
+  const bool vpre = !one_tile && T >= 128;
+  uint4 v2[2][8];
+  auto load_v2 = [&](uint32_t tb) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int p = 0; p < 8; ++p)
+        v2[h][p] = *reinterpret_cast<const uint4*>(vbase + static_cast<size_t>(8 * p) * a.stride + t0 + tb +
+                                                   64 * h + 8 * ts);
+  };
+  if (vpre) load_v2(0);
   __syncthreads();
 
   // ---- phase 2: softmax statistics, wave g owns head g.
@@ -235,13 +248,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnD
     // Two full 64-token tiles per pass: all sixteen V loads are issued before
     // the first FMA, so a wave keeps 16 KiB of V in flight.
     for (; tb0 + 128 <= T; tb0 += 128) {
-      uint4 v2[2][8];
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int p = 0; p < 8; ++p)
-          v2[h][p] = *reinterpret_cast<const uint4*>(vbase + static_cast<size_t>(8 * p) * a.stride + t0 + tb0 +
-                                                     64 * h + 8 * ts);
+      if (tb0 > 0) load_v2(tb0);  // the first pair was loaded before phase 2
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const uint32_t tl = tb0 + 64 * h + 8 * ts;
