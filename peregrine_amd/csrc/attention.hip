@@ -65,26 +65,30 @@ __global__ __launch_bounds__(kAttnThreads) void attn_prepare_kernel(const AttnPr
   const uint32_t col = threadIdx.x;  // 256 threads == head_dim
   const size_t row_base = static_cast<size_t>(head) * kAttnHeadDim;
   const size_t packed_base = static_cast<size_t>(head) * 2 * kAttnHeadDim;
+  const uint16_t* w = use_q ? a.q_norm : a.k_norm;
+  constexpr uint32_t half = kAttnRotary / 2;
+  // Every input is loaded before the step scalars are read, so the loads do
+  // not wait for the step block's load.
+  const float v = bf2f(use_q ? a.packed_q[packed_base + col] : a.k_in[row_base + col]);
+  const uint16_t side = use_q ? a.packed_q[packed_base + kAttnHeadDim + col] : a.v_in[row_base + col];
+  const float v2 = col < half ? bf2f(use_q ? a.packed_q[packed_base + col + half] : a.k_in[row_base + col + half])
+                              : 0.0f;
   const uint32_t cache_pos = a.step ? a.step->cache_pos : a.cache_pos_host;
   const uint32_t rope_pos = a.step ? a.step->rope_pos : a.rope_pos_host;
-  const uint16_t* w = use_q ? a.q_norm : a.k_norm;
   if (cache_pos >= a.stride) return;  // never write outside the cache (host checks first)
 
-  const float v = bf2f(use_q ? a.packed_q[packed_base + col] : a.k_in[row_base + col]);
   if (use_q)
-    a.gate_out[row_base + col] = a.packed_q[packed_base + kAttnHeadDim + col];
+    a.gate_out[row_base + col] = side;
   else
-    a.value_cache[(row_base + col) * a.stride + cache_pos] = a.v_in[row_base + col];
+    a.value_cache[(row_base + col) * a.stride + cache_pos] = side;
   const float ss = block_sum<kAttnThreads>(v * v, red);
   const float inv_rms = rsqrtf(ss / static_cast<float>(kAttnHeadDim) + kAttnEps);
 
-  constexpr uint32_t half = kAttnRotary / 2;
   uint16_t* dst = use_q ? a.q_out + row_base
                         : a.key_cache + (static_cast<size_t>(head) * a.stride + cache_pos) * kAttnHeadDim;
   if (col < half) {
     // partial NeoX RoPE on dims [0, 64): pairs (i, i + 32); normed values are
     // rounded to bf16 before rotation (attention.metal:391-392).
-    const float v2 = bf2f(use_q ? a.packed_q[packed_base + col + half] : a.k_in[row_base + col + half]);
     const float x1 = round_bf(v * inv_rms * bf2f(w[col]));
     const float x2 = round_bf(v2 * inv_rms * bf2f(w[col + half]));
     const float inv_freq = powf(kAttnTheta, -(2.0f * static_cast<float>(col)) / static_cast<float>(kAttnRotary));

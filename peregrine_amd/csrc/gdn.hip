@@ -55,16 +55,20 @@ __global__ __launch_bounds__(NT) void gdn_decode_kernel(
   const int hw = tid >> 5;   // half-wave
   const int j = tid & 31;    // lane in half-wave
   const uint32_t row0 = (blockIdx.x % kBlocksPerHead) * kRowsPerBlock + hw * RPH;  // first dv row
-  const bool has_state = step ? (step->rope_pos != 0) : (has_state_host != 0);
-
-  // State rows for this half-wave, issued first.
+  // State rows for this half-wave, issued first and unconditionally: the
+  // step scalars decide only afterwards whether they are used, so the state
+  // loads do not wait for the step block's load.
   float4 S[RPH];
   const size_t row_off = (static_cast<size_t>(hv) * kGdnDv + row0) * kGdnDk;
   const float4* srow = reinterpret_cast<const float4*>(state + row_off) + j;
   float4* sout = reinterpret_cast<float4*>((IN_PLACE ? state : state_out) + row_off) + j;
 #pragma unroll
-  for (int r = 0; r < RPH; ++r)
-    S[r] = has_state ? srow[r * (kGdnDk / 4)] : make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int r = 0; r < RPH; ++r) S[r] = srow[r * (kGdnDk / 4)];
+  const bool has_state = step ? (step->rope_pos != 0) : (has_state_host != 0);
+  if (!has_state) {  // a fresh sequence: the stored state is ignored (may hold anything)
+#pragma unroll
+    for (int r = 0; r < RPH; ++r) S[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
 
   // Gates (gating_many_bf16 math, shaders/gated_norm.metal:247-268).
   const float gx = bf2f(a[hv]) + bf2f(dt_bias[hv]);
