@@ -148,12 +148,39 @@ def cpu_baseline(model, budget_s: float = 20.0) -> dict:
                       f"(C oracle, {threads} threads; weight readback {load_s:.1f}s excluded)"}
 
 
+def mtp_run(steps: int) -> dict:
+    """BASELINE configs[4]'s repeat with a 1-layer MTP draft head: the same
+    9B-shaped model plus a random-init drafter (fc 4096x8192 Q4, one attention
+    layer, shared lm_head). The device-resident speculative loop drafts one
+    token, verifies two rows through all 32 layers (M = 2 GEMVs), advances the
+    drafter and accepts or rejects, one captured graph per step. A random
+    drafter is almost never accepted, so this measures the cost of a
+    speculative step; emitted tokens equal plain greedy decoding (tested)."""
+    from dataclasses import replace
+
+    from peregrine_amd.model import QWEN35_9B, DeviceModel, ModelState
+
+    cfg = replace(QWEN35_9B, mtp_layers=1)
+    model = DeviceModel(cfg, seed=0)
+    st = ModelState(model, PROMPT_TOKENS + steps + 8)
+    rng = np.random.default_rng(0)
+    prompt = rng.integers(0, cfg.vocab, size=PROMPT_TOKENS).astype(np.uint32)
+    st.generate_speculative(prompt, 8)  # first call: prompt workspace and graph capture
+    toks, acc, att, ms = st.generate_speculative(prompt, steps)
+    st.close()
+    model.close()
+    return {"emitted_tokens": steps, "loop_ms": round(ms, 2), "tok_s": round(steps / (ms * 1e-3), 2),
+            "verify_steps": att, "accepted_drafts": acc, "ms_per_verify_step": round(ms / max(att, 1), 4),
+            "drafter": "random-init 1-layer MTP head (fc + attention layer + shared lm_head)"}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=512)
     ap.add_argument("--warmup", type=int, default=32)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--no-mtp", action="store_true", help="skip the MTP speculative run (BASELINE configs[4], repeat)")
     ap.add_argument("--sweep", action="store_true", help="also run the Q4 GEMV sweep (configs[1])")
     ap.add_argument("--eager", action="store_true",
                     help="launch each token's kernels directly instead of replaying the HIP graph "
@@ -237,6 +264,12 @@ def main() -> int:
         cpu = cpu_baseline(model)
         log(f"[bench] cpu baseline {cpu}")
     st.close()
+    weight_bytes = int(model.weight_bytes)
+    model.close()
+    mtp = None
+    if not a.no_mtp:
+        mtp = mtp_run(a.steps)
+        log(f"[bench] mtp speculative loop {mtp}")
 
     line = {
         "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": a.steps,
@@ -247,14 +280,14 @@ def main() -> int:
                    "layers": QWEN35_9B.num_layers, "gdn_layers": 24, "attention_layers": 8,
                    "hidden": QWEN35_9B.hidden, "ffn": QWEN35_9B.intermediate, "vocab": QWEN35_9B.vocab,
                    "prompt_tokens": PROMPT_TOKENS, "context_at_end": int(max_seq), "batch": 1,
-                   "weight_bytes": int(model.weight_bytes), "parallelism": "single GPU",
+                   "weight_bytes": weight_bytes, "parallelism": "single GPU",
                    "execution": "eager launches" if a.eager else "one HIP graph replay per token"},
         "roofline": roof,
         "cpu_baseline": cpu,
         "prefill": prefill,
+        "mtp": mtp,
         **extra,
     }
-    model.close()
     print(json.dumps(line), flush=True)
     return 0
 

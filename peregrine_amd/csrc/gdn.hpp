@@ -34,6 +34,35 @@ __device__ inline uint16_t conv1d_silu_step(const float* state, float* state_out
   return f2bf(acc / (1.0f + expf(-acc)));
 }
 
+// Two consecutive tokens of one channel (the two-token verify): x0 then x1
+// through the same arithmetic as two conv1d_silu_step calls. The state after
+// x0 goes to snap, the state after x1 to state_out; state is read once.
+__device__ inline void conv1d_silu_step2(const float* state, float* snap, float* state_out, const uint16_t* w,
+                                         uint32_t conv_dim, uint32_t c, float x0, float x1, uint16_t& o0,
+                                         uint16_t& o1) {
+  const float s0 = state[c], s1 = state[conv_dim + c], s2 = state[2 * conv_dim + c];
+  const uint2 wv = *reinterpret_cast<const uint2*>(w + static_cast<size_t>(c) * kGdnConvK);
+  const float w0 = bf_lo(wv.x), w1 = bf_hi(wv.x), w2 = bf_lo(wv.y), w3 = bf_hi(wv.y);
+  float a0 = 0.0f;
+  a0 = __fadd_rn(a0, __fmul_rn(w0, s0));
+  a0 = __fadd_rn(a0, __fmul_rn(w1, s1));
+  a0 = __fadd_rn(a0, __fmul_rn(w2, s2));
+  a0 = __fadd_rn(a0, __fmul_rn(w3, x0));
+  float a1 = 0.0f;
+  a1 = __fadd_rn(a1, __fmul_rn(w0, s1));
+  a1 = __fadd_rn(a1, __fmul_rn(w1, s2));
+  a1 = __fadd_rn(a1, __fmul_rn(w2, x0));
+  a1 = __fadd_rn(a1, __fmul_rn(w3, x1));
+  snap[c] = s1;
+  snap[conv_dim + c] = s2;
+  snap[2 * conv_dim + c] = x0;
+  state_out[c] = s2;
+  state_out[conv_dim + c] = x0;
+  state_out[2 * conv_dim + c] = x1;
+  o0 = f2bf(a0 / (1.0f + expf(-a0)));
+  o1 = f2bf(a1 / (1.0f + expf(-a1)));
+}
+
 // One block per v-head. With norm_w != nullptr the gated RMSNorm is fused and
 // y_out receives the normalised output. The state counts as present when
 // step_dev->rope_pos != 0 (decoder_layer.zig:564), or per has_state_host when

@@ -292,7 +292,7 @@ int encode_linear_attention(PrgModel* m, PrgModelState* st, const DecoderLayer& 
   p.seg[0].conv_w = b.conv_weight;
   p.seg[0].conv_dim = kGdnConvDim;
   add_seg(p, b.in_z, nullptr);
-  p.seg[1].silu_out = st->zsilu;
+  p.seg[1].silu_out[0] = st->zsilu;
   add_seg(p, b.in_a, st->abuf);
   add_seg(p, b.in_b, st->bbuf);
   if (int rc = run_gemv(s, p, kEpiPlain, kNormRms, "linear_attn.in_proj")) return rc;
@@ -308,6 +308,115 @@ int encode_linear_attention(PrgModel* m, PrgModelState* st, const DecoderLayer& 
   add_seg(o, b.out_proj, h);
   o.seg[0].res[0] = x;
   return run_gemv(s, o, kEpiResidual, kNormGated, "linear_attn.out_proj");
+}
+
+// Two consecutive tokens through one GDN layer (the verify rows, positions in
+// step[0] / step[1]): the normed in_proj for both rows in one M = 2 GEMV whose
+// epilogue runs both conv steps per channel (row 0's rolled conv state to
+// io.conv_out, row 1's back to io.conv_in), the recurrence for row 0
+// (io.recur_in -> io.recur_out) and then row 1 (io.recur_out -> io.recur_in),
+// and the gated-norm out_proj for both rows in one M = 2 GEMV. Every per-row
+// number equals two single-token layers: the M = 2 GEMVs do the M = 1
+// per-row arithmetic, and the conv epilogue repeats the single-step order.
+int encode_linear_attention2(PrgModel* m, PrgModelState* st, const DecoderLayer& L, const GdnIO& io,
+                             const uint16_t* const* x, uint16_t* const* h, const StepScalars* step) {
+  const LinearAttentionBlock& b = L.lin;
+  const PrgModelConfig& c = m->cfg;
+  hipStream_t s = st->stream;
+  uint16_t* conv_out[2] = {st->conv_out, st->conv_out + kGdnConvDim};
+  float* zsilu[2] = {st->zsilu, st->zsilu + kGdnValDim};
+  uint16_t* abuf[2] = {st->abuf, st->abuf + kGdnHv};
+  uint16_t* bbuf[2] = {st->bbuf, st->bbuf + kGdnHv};
+  uint16_t* gated[2] = {st->gated, st->gated + kGdnValDim};
+  GemvParams p = gemv_params(x[0], c.hidden);
+  p.x[1] = x[1];
+  p.norm_w = L.input_norm;
+  p.eps = c.rms_eps;
+  add_seg(p, b.in_qkv, conv_out[0]);
+  p.seg[0].out[1] = conv_out[1];
+  p.seg[0].conv_state = io.conv_in;
+  p.seg[0].conv_state_out = io.conv_out;
+  p.seg[0].conv_w = b.conv_weight;
+  p.seg[0].conv_dim = kGdnConvDim;
+  add_seg(p, b.in_z, nullptr);
+  p.seg[1].silu_out[0] = zsilu[0];
+  p.seg[1].silu_out[1] = zsilu[1];
+  add_seg(p, b.in_a, abuf[0]);
+  p.seg[2].out[1] = abuf[1];
+  add_seg(p, b.in_b, bbuf[0]);
+  p.seg[3].out[1] = bbuf[1];
+  if (int rc = run_gemv(s, p, kEpiPlain, kNormRms, "linear_attn.in_proj2")) return rc;
+  for (int r = 0; r < 2; ++r) {
+    float* rin = r == 0 ? io.recur_in : io.recur_out;
+    float* rout = r == 0 ? io.recur_out : io.recur_in;
+    if (int rc = launch_gdn_decode(s, rin, conv_out[r], abuf[r], bbuf[r], b.a_log, b.dt_bias, gated[r], &step[r], 0,
+                                   nullptr, nullptr, 0.0f, rout))
+      return rc;
+  }
+  GemvParams o = gemv_params(gated[0], kGdnValDim);
+  o.x[1] = gated[1];
+  o.norm_w = b.norm_weight;
+  o.eps = c.rms_eps;
+  o.gz[0] = zsilu[0];
+  o.gz[1] = zsilu[1];
+  add_seg(o, b.out_proj, h[0]);
+  o.seg[0].out[1] = h[1];
+  o.seg[0].res[0] = x[0];
+  o.seg[0].res[1] = x[1];
+  return run_gemv(s, o, kEpiResidual, kNormGated, "linear_attn.out_proj2");
+}
+
+// Two consecutive tokens through one attention layer: q/k/v for both rows in
+// one M = 2 GEMV, then prepare + append and the split decode for row 0 and
+// then row 1 (row 1 attends to row 0's appended K/V), and o_proj for both
+// rows in one M = 2 GEMV.
+int encode_full_attention2(PrgModel* m, PrgModelState* st, const DecoderLayer& L, LayerState& ls,
+                           const uint16_t* const* x, uint16_t* const* h, const StepScalars* step) {
+  const FullAttentionBlock& b = L.full;
+  const PrgModelConfig& c = m->cfg;
+  hipStream_t s = st->stream;
+  constexpr uint32_t kQp = 2 * kAttnQHeads * kAttnHeadDim, kKv = kAttnKvHeads * kAttnHeadDim;
+  constexpr uint32_t kCtx = kAttnQHeads * kAttnHeadDim;
+  uint16_t* qp[2] = {st->qp, st->qp + kQp};
+  uint16_t* kb[2] = {st->kbuf, st->kbuf + kKv};
+  uint16_t* vb[2] = {st->vbuf, st->vbuf + kKv};
+  uint16_t* ctx[2] = {st->ctx, st->ctx + kCtx};
+  GemvParams p = gemv_params(x[0], c.hidden);
+  p.x[1] = x[1];
+  p.norm_w = L.input_norm;
+  p.eps = c.rms_eps;
+  add_seg(p, b.q_proj, qp[0]);
+  p.seg[0].out[1] = qp[1];
+  add_seg(p, b.k_proj, kb[0]);
+  p.seg[1].out[1] = kb[1];
+  add_seg(p, b.v_proj, vb[0]);
+  p.seg[2].out[1] = vb[1];
+  if (int rc = run_gemv(s, p, kEpiPlain, kNormRms, "self_attn.qkv_proj2")) return rc;
+  for (int r = 0; r < 2; ++r) {
+    AttnPrepareArgs pa{qp[r], b.q_norm, kb[r], vb[r], b.k_norm, st->qbuf, st->gatebuf, ls.cache_k, ls.cache_v,
+                       st->stride, 0, 0, &step[r]};
+    if (int rc = launch_attn_prepare(s, pa)) return rc;
+    AttnDecodeArgs da{};
+    da.q = st->qbuf;
+    da.key_cache = ls.cache_k;
+    da.value_cache = ls.cache_v;
+    da.gate = st->gatebuf;
+    da.out = ctx[r];
+    da.partials = st->partials;
+    da.stride = st->stride;
+    da.nsplit = st->nsplit;
+    da.split_tokens = st->split_tokens;
+    da.step = &step[r];
+    da.scale = kAttnScale;
+    if (int rc = launch_attn_decode(s, da)) return rc;
+  }
+  GemvParams o = gemv_params(ctx[0], kCtx);
+  o.x[1] = ctx[1];
+  add_seg(o, b.o_proj, h[0]);
+  o.seg[0].out[1] = h[1];
+  o.seg[0].res[0] = x[0];
+  o.seg[0].res[1] = x[1];
+  return run_gemv(s, o, kEpiResidual, kNormNone, "self_attn.o_proj2");
 }
 
 // Attention layer: norm+q/k/v -> prepare/append -> flash decode -> o_proj + residual.
@@ -578,17 +687,17 @@ int prg_model_state_create(PrgModel* model, uint32_t max_seq, PrgModelState** ou
   const size_t state_items = items.size();
   items.push_back({"ws.hA", bf * c.hidden, reinterpret_cast<void**>(&st->hA)});
   items.push_back({"ws.hB", bf * c.hidden, reinterpret_cast<void**>(&st->hB)});
-  items.push_back({"ws.conv_out", bf * kGdnConvDim, reinterpret_cast<void**>(&st->conv_out)});
-  items.push_back({"ws.z_silu", sizeof(float) * kGdnValDim, reinterpret_cast<void**>(&st->zsilu)});
-  items.push_back({"ws.a", bf * kGdnHv, reinterpret_cast<void**>(&st->abuf)});
-  items.push_back({"ws.b", bf * kGdnHv, reinterpret_cast<void**>(&st->bbuf)});
-  items.push_back({"ws.gated", bf * kGdnValDim, reinterpret_cast<void**>(&st->gated)});
-  items.push_back({"ws.qp", bf * 2 * kAttnQHeads * kAttnHeadDim, reinterpret_cast<void**>(&st->qp)});
-  items.push_back({"ws.k", bf * kAttnKvHeads * kAttnHeadDim, reinterpret_cast<void**>(&st->kbuf)});
-  items.push_back({"ws.v", bf * kAttnKvHeads * kAttnHeadDim, reinterpret_cast<void**>(&st->vbuf)});
+  items.push_back({"ws.conv_out", 2 * bf * kGdnConvDim, reinterpret_cast<void**>(&st->conv_out)});
+  items.push_back({"ws.z_silu", 2 * sizeof(float) * kGdnValDim, reinterpret_cast<void**>(&st->zsilu)});
+  items.push_back({"ws.a", 2 * bf * kGdnHv, reinterpret_cast<void**>(&st->abuf)});
+  items.push_back({"ws.b", 2 * bf * kGdnHv, reinterpret_cast<void**>(&st->bbuf)});
+  items.push_back({"ws.gated", 2 * bf * kGdnValDim, reinterpret_cast<void**>(&st->gated)});
+  items.push_back({"ws.qp", 2 * bf * 2 * kAttnQHeads * kAttnHeadDim, reinterpret_cast<void**>(&st->qp)});
+  items.push_back({"ws.k", 2 * bf * kAttnKvHeads * kAttnHeadDim, reinterpret_cast<void**>(&st->kbuf)});
+  items.push_back({"ws.v", 2 * bf * kAttnKvHeads * kAttnHeadDim, reinterpret_cast<void**>(&st->vbuf)});
   items.push_back({"ws.q", bf * kAttnQHeads * kAttnHeadDim, reinterpret_cast<void**>(&st->qbuf)});
   items.push_back({"ws.gate", bf * kAttnQHeads * kAttnHeadDim, reinterpret_cast<void**>(&st->gatebuf)});
-  items.push_back({"ws.ctx", bf * kAttnQHeads * kAttnHeadDim, reinterpret_cast<void**>(&st->ctx)});
+  items.push_back({"ws.ctx", 2 * bf * kAttnQHeads * kAttnHeadDim, reinterpret_cast<void**>(&st->ctx)});
   items.push_back({"ws.partials", sizeof(float) * kAttnQHeads * st->nsplit * kAttnPartialStride,
                    reinterpret_cast<void**>(&st->partials)});
   items.push_back({"ws.inter", bf * c.intermediate, reinterpret_cast<void**>(&st->inter)});

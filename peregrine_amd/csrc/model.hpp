@@ -12,6 +12,8 @@
 //   ModelState / LayerState       src/model/state.zig:11-118
 #pragma once
 
+#include <stddef.h>
+
 #include <map>
 #include <string>
 #include <vector>
@@ -127,8 +129,9 @@ struct SpecCtl {
   uint32_t accepted, attempted;
   uint32_t capacity;   // positions must stay below it
   uint32_t stop;       // set when the next step would pass capacity
-  uint32_t discard;    // sink for the drafter's advance-step token
 };
+// The two verify rows' steps are read as an array (&v0)[0..1].
+static_assert(offsetof(SpecCtl, v1) == offsetof(SpecCtl, v0) + sizeof(StepScalars), "v1 must follow v0");
 
 bool is_linear_layer(const PrgModelConfig& c, uint32_t i);
 int validate_model_config(const PrgModelConfig& c);
@@ -222,6 +225,12 @@ int encode_linear_attention(PrgModel* m, PrgModelState* st, const DecoderLayer& 
                             const uint16_t* x, uint16_t* h, const StepScalars* step);
 int encode_full_attention(PrgModel* m, PrgModelState* st, const DecoderLayer& L, LayerState& ls, const uint16_t* x,
                           uint16_t* h, const StepScalars* step);
+// Two consecutive tokens through one layer with M = 2 projections; step[0]
+// and step[1] hold the two rows' positions (decoder_layer.zig:485-516).
+int encode_linear_attention2(PrgModel* m, PrgModelState* st, const DecoderLayer& L, const GdnIO& io,
+                             const uint16_t* const* x, uint16_t* const* h, const StepScalars* step);
+int encode_full_attention2(PrgModel* m, PrgModelState* st, const DecoderLayer& L, LayerState& ls,
+                           const uint16_t* const* x, uint16_t* const* h, const StepScalars* step);
 // out_r = h_r + mlp(norm(h_r)) for M = 1 or 2 rows (block_mlp.zig:260-311).
 int encode_mlp(PrgModel* m, PrgModelState* st, const DecoderLayer& L, int M, const uint16_t* const* h,
                uint16_t* const* inter, uint16_t* const* out);

@@ -94,6 +94,8 @@ T* snap_of(const PrgModelState* st, T* live) {
 // out_token.
 int encode_mtp_step(PrgModel* m, PrgModelState* st, const uint32_t* token_dev, const uint16_t* hidden,
                     const StepScalars* step, uint32_t* out_token) {
+  // out_token == nullptr: the step only advances the drafter's KV cache, so
+  // the final norm and the lm_head argmax are skipped.
   const MtpWeights& t = m->mtp;
   const PrgModelConfig& c = m->cfg;
   hipStream_t s = st->stream;
@@ -112,6 +114,7 @@ int encode_mtp_step(PrgModel* m, PrgModelState* st, const uint32_t* token_dev, c
   uint16_t* inter[1] = {st->inter};
   uint16_t* out[1] = {st->mtp_h};
   if (int rc = encode_mlp(m, st, t.layer, 1, h, inter, out)) return rc;
+  if (out_token == nullptr) return PRG_OK;
   // final norm, shared lm_head argmax (mtp.zig:230-233)
   GemvParams p = gemv_params(st->mtp_h, H);
   p.norm_w = t.norm;
@@ -143,18 +146,16 @@ int encode_verify(PrgModel* m, PrgModelState* st) {
     const DecoderLayer& L = m->layers[i];
     LayerState& ls = st->layers[i];
     int rc;
+    // v0 and v1 are consecutive in SpecCtl: &sc->v0 is the two rows' steps.
+    const uint16_t* xin[2] = {xa[0], xa[1]};
     if (L.linear) {
-      float* conv_snap = snap_of(st, ls.conv);
-      float* recur_snap = snap_of(st, ls.recur);
-      if ((rc = encode_linear_attention(m, st, L, GdnIO{ls.conv, conv_snap, ls.recur, recur_snap}, xa[0], xb[0],
-                                        &sc->v0)))
-        return rc;
-      if ((rc = encode_linear_attention(m, st, L, GdnIO{conv_snap, ls.conv, recur_snap, ls.recur}, xa[1], xb[1],
-                                        &sc->v1)))
+      // row 0's GDN update goes to the snapshot, row 1 continues from it
+      if ((rc = encode_linear_attention2(m, st, L,
+                                         GdnIO{ls.conv, snap_of(st, ls.conv), ls.recur, snap_of(st, ls.recur)}, xin,
+                                         xb, &sc->v0)))
         return rc;
     } else {
-      if ((rc = encode_full_attention(m, st, L, ls, xa[0], xb[0], &sc->v0))) return rc;
-      if ((rc = encode_full_attention(m, st, L, ls, xa[1], xb[1], &sc->v1))) return rc;
+      if ((rc = encode_full_attention2(m, st, L, ls, xin, xb, &sc->v0))) return rc;
     }
     const uint16_t* hin[2] = {xb[0], xb[1]};
     if ((rc = encode_mlp(m, st, L, 2, hin, inter, xa))) return rc;
@@ -179,8 +180,9 @@ int encode_spec_step(PrgModel* m, PrgModelState* st) {
   if (int rc = encode_mtp_step(m, st, &sc->v0.token, st->cur_hidden, &sc->d0, &sc->v1.token)) return rc;
   if (int rc = encode_verify(m, st)) return rc;
   // the drafter consumes (draft, hidden after the current token) whether or not
-  // the draft is accepted: on a reject the next draft step rewrites that slot
-  if (int rc = encode_mtp_step(m, st, &sc->v1.token, st->hnorm2, &sc->d1, &sc->discard)) return rc;
+  // the draft is accepted: on a reject the next draft step rewrites that slot.
+  // Only its KV cache matters here, so no lm_head.
+  if (int rc = encode_mtp_step(m, st, &sc->v1.token, st->hnorm2, &sc->d1, nullptr)) return rc;
   const uint32_t w8 = m->cfg.hidden / 8;
   hipLaunchKernelGGL(spec_decide_kernel, dim3(1), dim3(256), 0, s, sc, st->spec_out, st->drafts,
                      reinterpret_cast<const uint4*>(st->hnorm2), reinterpret_cast<uint4*>(st->cur_hidden), w8);

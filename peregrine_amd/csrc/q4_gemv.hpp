@@ -63,17 +63,21 @@ struct GemvSeg {
   const uint16_t* res[2];     // per activation row m (residual epilogue)
   float* pval[2];             // per activation row m (argmax epilogue)
   uint32_t* pidx[2];
-  // Optional conv1d+SiLU epilogue (plain epilogue, M == 1): the bf16 GEMV
-  // output x of row c feeds the depthwise causal conv of channel c, whose f32
-  // state [3, conv_dim] is rolled in place; out receives the conv output.
-  // This fuses in_proj_qkv with conv1d_silu_decode_bf16 (block_linear.zig:230-240).
+  // Optional conv1d+SiLU epilogue (plain epilogue): the bf16 GEMV output x
+  // of row c feeds the depthwise causal conv of channel c, whose f32 state
+  // [3, conv_dim] is rolled; out receives the conv output. This fuses
+  // in_proj_qkv with conv1d_silu_decode_bf16 (block_linear.zig:230-240).
+  // M == 1: the rolled state goes to conv_state_out (nullptr: in place).
+  // M == 2 (two consecutive tokens): the state after row 0 goes to
+  // conv_state_out and the state after row 1 back to conv_state.
   float* conv_state;
-  float* conv_state_out;      // rolled state destination (nullptr: in place)
+  float* conv_state_out;
   const uint16_t* conv_w;     // bf16 [conv_dim, 4]
   uint32_t conv_dim;
-  // Optional SiLU epilogue (plain epilogue, M == 1): row c writes
-  // silu(bf16(dot)) in f32 here instead of bf16 to out (the GDN z gate).
-  float* silu_out;
+  // Optional SiLU epilogue (plain epilogue): row c of activation row m
+  // writes silu(bf16(dot)) in f32 to silu_out[m] instead of bf16 to out (the
+  // GDN z gate).
+  float* silu_out[2];
   uint32_t rows;              // output rows of this segment
   uint32_t block_begin;       // first group index of this segment (set by the launcher)
 };
@@ -258,7 +262,9 @@ __device__ inline void gemv_dot_step(const GemvBuf<NMAT, ROWS, ITERS>& b, int it
 #pragma unroll
       for (int m = 0; m < M; ++m) {
         const float qx = aq[m][0] + aq[m][1];  // sum(q * x)
-        acc[mat][r][m] += sc * qx + bi * x.xsum[m];
+        // explicit fma order: every instantiation (M = 1 or 2, any rows per
+        // wave) rounds the same way, which the two-token verify relies on
+        acc[mat][r][m] = __fmaf_rn(bi, x.xsum[m], __fmaf_rn(sc, qx, acc[mat][r][m]));
       }
     }
   }
@@ -267,7 +273,7 @@ __device__ inline void gemv_dot_step(const GemvBuf<NMAT, ROWS, ITERS>& b, int it
 // Where one finished row goes (all epilogues but argmax), selected per lane.
 struct GemvRowDst {
   uint16_t* out[2];
-  float* silu_out;
+  float* silu_out[2];
   const uint16_t* res[2];
   float* conv_state;
   float* conv_state_out;
@@ -280,7 +286,8 @@ __device__ inline GemvRowDst gemv_row_dst(const GemvSeg& sg, uint32_t row) {
   GemvRowDst d;
   d.out[0] = sg.out[0];
   d.out[1] = sg.out[1];
-  d.silu_out = sg.silu_out;
+  d.silu_out[0] = sg.silu_out[0];
+  d.silu_out[1] = sg.silu_out[1];
   d.res[0] = sg.res[0];
   d.res[1] = sg.res[1];
   d.conv_state = sg.conv_state;
@@ -294,10 +301,25 @@ __device__ inline GemvRowDst gemv_row_dst(const GemvSeg& sg, uint32_t row) {
 // Epilogue of one row: tot[mat][m] are its finished dot products.
 template <int M, int NMAT, int EPI>
 __device__ inline void gemv_store_row(const GemvRowDst& d, const float (&tot)[NMAT][M]) {
-  if (EPI == kEpiPlain && M == 1 && d.silu_out != nullptr) {
-    const float zb = round_bf(tot[0][0]);
-    d.silu_out[d.row] = zb / (1.0f + expf(-zb));
-    return;
+  if constexpr (EPI == kEpiPlain) {
+    if (d.silu_out[0] != nullptr) {
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        const float zb = round_bf(tot[0][m]);
+        d.silu_out[m][d.row] = zb / (1.0f + expf(-zb));
+      }
+      return;
+    }
+    if constexpr (M == 2) {
+      if (d.conv_state != nullptr) {
+        uint16_t o0, o1;
+        conv1d_silu_step2(d.conv_state, d.conv_state_out, d.conv_state, d.conv_w, d.conv_dim, d.row,
+                          round_bf(tot[0][0]), round_bf(tot[0][1]), o0, o1);
+        d.out[0][d.row] = o0;
+        d.out[1][d.row] = o1;
+        return;
+      }
+    }
   }
 #pragma unroll
   for (int m = 0; m < M; ++m) {
@@ -393,13 +415,23 @@ __device__ inline void gemv_epilogue(const GemvParams& p, const GemvLoc& loc, in
     for (int r = 0; r < ROWS; ++r) {
       const uint32_t row = row0 + r;
       if (row >= sg.rows) break;
+      if constexpr (EPI == kEpiPlain && M == 2) {
+        if (sg.silu_out[0] == nullptr && sg.conv_state != nullptr) {
+          uint16_t o0, o1;
+          conv1d_silu_step2(sg.conv_state, sg.conv_state_out, sg.conv_state, sg.conv_w, sg.conv_dim, row,
+                            round_bf(tot[0][r][0]), round_bf(tot[0][r][1]), o0, o1);
+          sg.out[0][row] = o0;
+          sg.out[1][row] = o1;
+          continue;
+        }
+      }
 #pragma unroll
       for (int m = 0; m < M; ++m) {
         uint16_t o;
         if constexpr (EPI == kEpiPlain) {
-          if (M == 1 && sg.silu_out != nullptr) {
+          if (sg.silu_out[0] != nullptr) {
             const float zb = round_bf(tot[0][r][m]);
-            sg.silu_out[row] = zb / (1.0f + expf(-zb));
+            sg.silu_out[m][row] = zb / (1.0f + expf(-zb));
             continue;
           }
           if (M == 1 && sg.conv_state != nullptr)
@@ -490,12 +522,12 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(const GemvParams 
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const float a = bf_lo(d[i]), b = bf_hi(d[i]);
-          ss += a * a;
-          ss += b * b;
+          ss = __fmaf_rn(a, a, ss);
+          ss = __fmaf_rn(b, b, ss);
         }
       }
       const float total = block_sum<kGemvThreads>(ss, red);
-      scale = 1.0f / sqrtf(total / static_cast<float>(p.K) + p.eps);
+      scale = 1.0f / sqrtf(__fadd_rn(total / static_cast<float>(p.K), p.eps));
     }
     uint4* dst = reinterpret_cast<uint4*>(xs + m * (p.K / 2));
 #pragma unroll
@@ -508,10 +540,10 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(const GemvParams 
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const float a = bf_lo(d[i]), b = bf_hi(d[i]);
-          ss += a * a;
-          ss += b * b;
+          ss = __fmaf_rn(a, a, ss);
+          ss = __fmaf_rn(b, b, ss);
         }
-        const float hscale = rsqrtf(row16_sum(ss) / static_cast<float>(kGdnDv) + p.eps);
+        const float hscale = rsqrtf(__fadd_rn(__fmul_rn(row16_sum(ss), 1.0f / kGdnDv), p.eps));
         if (gi < n8) dst[gi] = permute_pairs(gated_rms_apply(xv[m][it], nw[it], zv[m][it][0], zv[m][it][1], hscale));
       } else if (gi < n8) {
         if constexpr (NORM == kNormRms)
