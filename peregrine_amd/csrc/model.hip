@@ -520,12 +520,12 @@ int capture(PrgModel* m, PrgModelState* st, bool with_head, hipGraphExec_t* out)
   const int rc = encode_token(m, st, with_head);
   hipError_t e = hipStreamEndCapture(st->stream, &g);
   if (rc) {
-    if (g) hipGraphDestroy(g);
+    if (g) (void)hipGraphDestroy(g);
     return rc;
   }
   if (e != hipSuccess) return set_error(PRG_ERR_HIP, "hipStreamEndCapture: %s", hipGetErrorString(e));
   e = hipGraphInstantiate(out, g, nullptr, nullptr, 0);
-  hipGraphDestroy(g);
+  (void)hipGraphDestroy(g);
   if (e != hipSuccess) return set_error(PRG_ERR_HIP, "hipGraphInstantiate: %s", hipGetErrorString(e));
   return PRG_OK;
 }
@@ -588,7 +588,7 @@ int prg_model_create_random(const PrgModelConfig* cfg, uint64_t seed, PrgModel**
   }
   e = hipDeviceSynchronize();
   if (e != hipSuccess) {
-    hipFree(m->arena);
+    (void)hipFree(m->arena);
     delete m;
     return set_error(PRG_ERR_HIP, "model init: %s", hipGetErrorString(e));
   }
@@ -598,7 +598,7 @@ int prg_model_create_random(const PrgModelConfig* cfg, uint64_t seed, PrgModel**
 
 void prg_model_destroy(PrgModel* model) {
   if (!model) return;
-  hipFree(model->arena);
+  (void)hipFree(model->arena);
   delete model;
 }
 
@@ -738,15 +738,15 @@ int prg_model_state_create(PrgModel* model, uint32_t max_seq, PrgModelState** ou
 
 void prg_model_state_destroy(PrgModelState* st) {
   if (!st) return;
-  if (st->graph_decode) hipGraphExecDestroy(st->graph_decode);
-  if (st->graph_prompt) hipGraphExecDestroy(st->graph_prompt);
-  if (st->ev0) hipEventDestroy(st->ev0);
-  if (st->ev1) hipEventDestroy(st->ev1);
-  if (st->graph_spec) hipGraphExecDestroy(st->graph_spec);
-  if (st->stream) hipStreamDestroy(st->stream);
-  hipFree(st->arena);
-  if (st->pf.arena) hipFree(st->pf.arena);
-  if (st->spec_arena) hipFree(st->spec_arena);
+  if (st->graph_decode) (void)hipGraphExecDestroy(st->graph_decode);
+  if (st->graph_prompt) (void)hipGraphExecDestroy(st->graph_prompt);
+  if (st->ev0) (void)hipEventDestroy(st->ev0);
+  if (st->ev1) (void)hipEventDestroy(st->ev1);
+  if (st->graph_spec) (void)hipGraphExecDestroy(st->graph_spec);
+  if (st->stream) (void)hipStreamDestroy(st->stream);
+  (void)hipFree(st->arena);
+  if (st->pf.arena) (void)hipFree(st->pf.arena);
+  if (st->spec_arena) (void)hipFree(st->spec_arena);
   delete st;
 }
 

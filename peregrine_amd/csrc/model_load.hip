@@ -46,12 +46,12 @@ class Staging {
   static constexpr size_t kChunk = size_t(64) << 20;
 
   ~Staging() {
-    if (stream_) hipStreamSynchronize(stream_);
+    if (stream_) (void)hipStreamSynchronize(stream_);
     for (int k = 0; k < 2; ++k) {
-      if (ev_[k]) hipEventDestroy(ev_[k]);
-      if (buf_[k]) hipHostFree(buf_[k]);
+      if (ev_[k]) (void)hipEventDestroy(ev_[k]);
+      if (buf_[k]) (void)hipHostFree(buf_[k]);
     }
-    if (stream_) hipStreamDestroy(stream_);
+    if (stream_) (void)hipStreamDestroy(stream_);
   }
 
   int init() {

@@ -202,12 +202,12 @@ int run_spec_step(PrgModel* m, PrgModelState* st) {
     const int rc = encode_spec_step(m, st);
     hipError_t e = hipStreamEndCapture(st->stream, &g);
     if (rc) {
-      if (g) hipGraphDestroy(g);
+      if (g) (void)hipGraphDestroy(g);
       return rc;
     }
     if (e != hipSuccess) return set_error(PRG_ERR_HIP, "hipStreamEndCapture: %s", hipGetErrorString(e));
     e = hipGraphInstantiate(&st->graph_spec, g, nullptr, nullptr, 0);
-    hipGraphDestroy(g);
+    (void)hipGraphDestroy(g);
     if (e != hipSuccess) return set_error(PRG_ERR_HIP, "hipGraphInstantiate: %s", hipGetErrorString(e));
   }
   PRG_HIP(hipGraphLaunch(st->graph_spec, st->stream));

@@ -202,7 +202,7 @@ int prg_hip_graph_end(void* stream, void** graph) {
   PRG_HIP(hipStreamEndCapture(prg::as_stream(stream), &g));
   hipGraphExec_t exec = nullptr;
   const hipError_t e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
-  hipGraphDestroy(g);
+  (void)hipGraphDestroy(g);
   if (e != hipSuccess) return prg::set_error(PRG_ERR_HIP, "prg_hip_graph_end: instantiate: %s", hipGetErrorString(e));
   *graph = exec;
   return PRG_OK;
