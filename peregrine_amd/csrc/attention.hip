@@ -57,8 +57,17 @@ __device__ inline float dot2(uint32_t a, uint32_t b, float c) {
 }
 
 // ------------------------------------------------------------------ prepare --
-__global__ __launch_bounds__(kAttnThreads) void attn_prepare_kernel(const AttnPrepareArgs a) {
+__global__ __launch_bounds__(kAttnThreads) void attn_prepare_kernel(const AttnPrepareArgs a0) {
   __shared__ float red[kAttnThreads / kWave];
+  AttnPrepareArgs a = a0;  // token blockIdx.y's slices
+  if (const uint32_t r = blockIdx.y) {
+    a.packed_q += r * (2 * kAttnQHeads * kAttnHeadDim);
+    a.k_in += r * (kAttnKvHeads * kAttnHeadDim);
+    a.v_in += r * (kAttnKvHeads * kAttnHeadDim);
+    a.q_out += r * (kAttnQHeads * kAttnHeadDim);
+    a.gate_out += r * (kAttnQHeads * kAttnHeadDim);
+    a.step += r;
+  }
   const uint32_t tg = blockIdx.x;
   const bool use_q = tg < kAttnQHeads;
   const uint32_t head = use_q ? tg : tg - kAttnQHeads;
@@ -102,9 +111,24 @@ __global__ __launch_bounds__(kAttnThreads) void attn_prepare_kernel(const AttnPr
 }
 
 // ----------------------------------------------------------------- partials --
-__global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnDecodeArgs a) {
+// Query token r = blockIdx.z (or blockIdx.y for the merge) of a launch:
+// its q / gate / output rows, its partials and its step scalars.
+__device__ inline AttnDecodeArgs attn_row_args(const AttnDecodeArgs& a0, uint32_t r) {
+  AttnDecodeArgs a = a0;
+  if (r) {
+    a.q += r * (kAttnQHeads * kAttnHeadDim);
+    a.gate += r * (kAttnQHeads * kAttnHeadDim);
+    a.out += r * (kAttnQHeads * kAttnHeadDim);
+    a.partials += static_cast<size_t>(r) * kAttnQHeads * a.nsplit * kAttnPartialStride;
+    a.step += r;
+  }
+  return a;
+}
+
+__global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnDecodeArgs a0) {
   extern __shared__ float sc[];  // [4][split_tokens] scores, then probabilities
   __shared__ float mh[kAttnGroup], lh[kAttnGroup];
+  const AttnDecodeArgs a = attn_row_args(a0, blockIdx.z);
 
   const uint32_t kvh = blockIdx.y;
   const uint32_t split = blockIdx.x;
@@ -338,9 +362,10 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnD
 // dim over the splits with independent loads.
 constexpr uint32_t kMaxSplits = 1024;
 
-__global__ __launch_bounds__(kAttnThreads) void attn_reduce_kernel(const AttnDecodeArgs a) {
+__global__ __launch_bounds__(kAttnThreads) void attn_reduce_kernel(const AttnDecodeArgs a0) {
   __shared__ float wsh[kMaxSplits];
   __shared__ float red[kAttnThreads / kWave];
+  const AttnDecodeArgs a = attn_row_args(a0, blockIdx.y);
   const uint32_t h = blockIdx.x;  // q head
   const uint32_t t = threadIdx.x;
   const float* base = a.partials + static_cast<size_t>(h) * a.nsplit * kAttnPartialStride;
@@ -413,16 +438,20 @@ uint32_t attn_split_tokens(uint32_t capacity, uint32_t nsplit) {
 }
 
 int launch_attn_prepare(hipStream_t s, const AttnPrepareArgs& a) {
-  hipLaunchKernelGGL(attn_prepare_kernel, dim3(kAttnQHeads + kAttnKvHeads), dim3(kAttnThreads), 0, s, a);
+  if (a.rows < 1 || a.rows > 2 || (a.rows == 2 && a.step == nullptr))
+    return set_error(PRG_ERR_INVALID_ARG, "attn_prepare: rows %u (two rows need device step scalars)", a.rows);
+  hipLaunchKernelGGL(attn_prepare_kernel, dim3(kAttnQHeads + kAttnKvHeads, a.rows), dim3(kAttnThreads), 0, s, a);
   PRG_CHECK_LAUNCH("attn_prepare");
   return PRG_OK;
 }
 
 int launch_attn_decode(hipStream_t s, const AttnDecodeArgs& a) {
+  if (a.rows < 1 || a.rows > 2 || (a.rows == 2 && a.step == nullptr))
+    return set_error(PRG_ERR_INVALID_ARG, "attn_decode: rows %u (two rows need device step scalars)", a.rows);
   const size_t lds = static_cast<size_t>(kAttnGroup) * a.split_tokens * sizeof(float);
-  hipLaunchKernelGGL(attn_partials_kernel, dim3(a.nsplit, kAttnKvHeads), dim3(kAttnThreads), lds, s, a);
+  hipLaunchKernelGGL(attn_partials_kernel, dim3(a.nsplit, kAttnKvHeads, a.rows), dim3(kAttnThreads), lds, s, a);
   PRG_CHECK_LAUNCH("attn_partials");
-  hipLaunchKernelGGL(attn_reduce_kernel, dim3(kAttnQHeads), dim3(kAttnHeadDim), 0, s, a);
+  hipLaunchKernelGGL(attn_reduce_kernel, dim3(kAttnQHeads, a.rows), dim3(kAttnHeadDim), 0, s, a);
   PRG_CHECK_LAUNCH("attn_reduce");
   return PRG_OK;
 }

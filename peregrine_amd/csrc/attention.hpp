@@ -37,6 +37,10 @@ struct AttnPrepareArgs {
   uint32_t cache_pos_host;   // used when step == nullptr
   uint32_t rope_pos_host;
   const StepScalars* step;   // device scalars (graph replay) or nullptr
+  // Consecutive tokens handled by one launch (1 or 2; 2 needs step). Token r
+  // reads and writes the row-r slices (packed_q + r*8192, k_in / v_in +
+  // r*1024, q_out / gate_out + r*4096) and uses step[r].
+  uint32_t rows = 1;
 };
 
 int launch_attn_prepare(hipStream_t s, const AttnPrepareArgs& a);
@@ -54,6 +58,9 @@ struct AttnDecodeArgs {
   uint32_t seq_len_host;      // used when step == nullptr
   const StepScalars* step;
   float scale;
+  // Consecutive tokens handled by one launch (1 or 2; 2 needs step). Query r
+  // uses q / gate / out + r*4096, partials + r*16*nsplit*258 and step[r].
+  uint32_t rows = 1;
 };
 
 int launch_attn_decode(hipStream_t s, const AttnDecodeArgs& a);

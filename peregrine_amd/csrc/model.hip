@@ -367,9 +367,9 @@ int encode_linear_attention2(PrgModel* m, PrgModelState* st, const DecoderLayer&
 }
 
 // Two consecutive tokens through one attention layer: q/k/v for both rows in
-// one M = 2 GEMV, then prepare + append and the split decode for row 0 and
-// then row 1 (row 1 attends to row 0's appended K/V), and o_proj for both
-// rows in one M = 2 GEMV.
+// one M = 2 GEMV, one prepare + append launch and one split decode for both
+// rows (row 1 attends to row 0's appended K/V), and o_proj for both rows in
+// one M = 2 GEMV.
 int encode_full_attention2(PrgModel* m, PrgModelState* st, const DecoderLayer& L, LayerState& ls,
                            const uint16_t* const* x, uint16_t* const* h, const StepScalars* step) {
   const FullAttentionBlock& b = L.full;
@@ -392,24 +392,26 @@ int encode_full_attention2(PrgModel* m, PrgModelState* st, const DecoderLayer& L
   add_seg(p, b.v_proj, vb[0]);
   p.seg[2].out[1] = vb[1];
   if (int rc = run_gemv(s, p, kEpiPlain, kNormRms, "self_attn.qkv_proj2")) return rc;
-  for (int r = 0; r < 2; ++r) {
-    AttnPrepareArgs pa{qp[r], b.q_norm, kb[r], vb[r], b.k_norm, st->qbuf, st->gatebuf, ls.cache_k, ls.cache_v,
-                       st->stride, 0, 0, &step[r]};
-    if (int rc = launch_attn_prepare(s, pa)) return rc;
-    AttnDecodeArgs da{};
-    da.q = st->qbuf;
-    da.key_cache = ls.cache_k;
-    da.value_cache = ls.cache_v;
-    da.gate = st->gatebuf;
-    da.out = ctx[r];
-    da.partials = st->partials;
-    da.stride = st->stride;
-    da.nsplit = st->nsplit;
-    da.split_tokens = st->split_tokens;
-    da.step = &step[r];
-    da.scale = kAttnScale;
-    if (int rc = launch_attn_decode(s, da)) return rc;
-  }
+  // Both rows' K/V are appended first; row 0 attends to seq_len = pos + 1, so
+  // row 1's slot is outside its range.
+  AttnPrepareArgs pa{qp[0], b.q_norm, kb[0], vb[0], b.k_norm, st->qbuf, st->gatebuf, ls.cache_k, ls.cache_v,
+                     st->stride, 0, 0, step};
+  pa.rows = 2;
+  if (int rc = launch_attn_prepare(s, pa)) return rc;
+  AttnDecodeArgs da{};
+  da.q = st->qbuf;
+  da.key_cache = ls.cache_k;
+  da.value_cache = ls.cache_v;
+  da.gate = st->gatebuf;
+  da.out = ctx[0];
+  da.partials = st->partials;
+  da.stride = st->stride;
+  da.nsplit = st->nsplit;
+  da.split_tokens = st->split_tokens;
+  da.step = step;
+  da.scale = kAttnScale;
+  da.rows = 2;
+  if (int rc = launch_attn_decode(s, da)) return rc;
   GemvParams o = gemv_params(ctx[0], kCtx);
   o.x[1] = ctx[1];
   add_seg(o, b.o_proj, h[0]);
@@ -695,10 +697,10 @@ int prg_model_state_create(PrgModel* model, uint32_t max_seq, PrgModelState** ou
   items.push_back({"ws.qp", 2 * bf * 2 * kAttnQHeads * kAttnHeadDim, reinterpret_cast<void**>(&st->qp)});
   items.push_back({"ws.k", 2 * bf * kAttnKvHeads * kAttnHeadDim, reinterpret_cast<void**>(&st->kbuf)});
   items.push_back({"ws.v", 2 * bf * kAttnKvHeads * kAttnHeadDim, reinterpret_cast<void**>(&st->vbuf)});
-  items.push_back({"ws.q", bf * kAttnQHeads * kAttnHeadDim, reinterpret_cast<void**>(&st->qbuf)});
-  items.push_back({"ws.gate", bf * kAttnQHeads * kAttnHeadDim, reinterpret_cast<void**>(&st->gatebuf)});
+  items.push_back({"ws.q", 2 * bf * kAttnQHeads * kAttnHeadDim, reinterpret_cast<void**>(&st->qbuf)});
+  items.push_back({"ws.gate", 2 * bf * kAttnQHeads * kAttnHeadDim, reinterpret_cast<void**>(&st->gatebuf)});
   items.push_back({"ws.ctx", 2 * bf * kAttnQHeads * kAttnHeadDim, reinterpret_cast<void**>(&st->ctx)});
-  items.push_back({"ws.partials", sizeof(float) * kAttnQHeads * st->nsplit * kAttnPartialStride,
+  items.push_back({"ws.partials", 2 * sizeof(float) * kAttnQHeads * st->nsplit * kAttnPartialStride,
                    reinterpret_cast<void**>(&st->partials)});
   items.push_back({"ws.inter", bf * c.intermediate, reinterpret_cast<void**>(&st->inter)});
   items.push_back({"ws.pval", sizeof(float) * (c.vocab / 8), reinterpret_cast<void**>(&st->pval)});
