@@ -33,6 +33,70 @@ constexpr int kGdnSplitThreads = 256;  // unfused: 8 half-waves x 2 rows = 16 ro
 
 __device__ inline float hsum32(float v) { return group_sum<32>(v); }
 
+// The per-token math, shared by the one- and two-token kernels. Every
+// multiply-add is an explicit __fmaf_rn / __fmul_rn / __fadd_rn, so both
+// kernels round identically (the two-token verify must equal two single
+// steps bit for bit).
+struct GdnGates {
+  float decay, beta;
+};
+// gating_many_bf16 math (shaders/gated_norm.metal:247-268).
+__device__ inline GdnGates gdn_gates(const uint16_t* a, const uint16_t* bgate, const float* A_log,
+                                     const uint16_t* dt_bias, uint32_t hv) {
+  const float gx = __fadd_rn(bf2f(a[hv]), bf2f(dt_bias[hv]));
+  const float softplus = __fadd_rn(fmaxf(gx, 0.0f), logf(__fadd_rn(1.0f, expf(-fabsf(gx)))));
+  return GdnGates{expf(-__fmul_rn(expf(A_log[hv]), softplus)), 1.0f / __fadd_rn(1.0f, expf(-bf2f(bgate[hv])))};
+}
+
+// q/k L2 norms (qk_l2norm_prefill_bf16 math, shaders/gated_norm.metal:191-245)
+// for lane j of a half-wave (dk = 4j..4j+3), and k.q over the head.
+struct GdnQK {
+  float qn[4], kn[4], kq;
+};
+__device__ inline GdnQK gdn_qk(const uint16_t* conv_out, uint32_t hk, int j) {
+  const uint2 qv = *reinterpret_cast<const uint2*>(conv_out + hk * kGdnDk + 4 * j);
+  const uint2 kv = *reinterpret_cast<const uint2*>(conv_out + kGdnKeyDim + hk * kGdnDk + 4 * j);
+  const float q[4] = {bf_lo(qv.x), bf_hi(qv.x), bf_lo(qv.y), bf_hi(qv.y)};
+  const float k[4] = {bf_lo(kv.x), bf_hi(kv.x), bf_lo(kv.y), bf_hi(kv.y)};
+  float qss = 0.f, kss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    qss = __fmaf_rn(q[i], q[i], qss);
+    kss = __fmaf_rn(k[i], k[i], kss);
+  }
+  const float q_inv = __fmul_rn(rsqrtf(__fadd_rn(hsum32(qss), 1.0e-6f)), rsqrtf(static_cast<float>(kGdnDk)));
+  const float k_inv = rsqrtf(__fadd_rn(hsum32(kss), 1.0e-6f));
+  GdnQK r;
+  float kq = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    r.qn[i] = __fmul_rn(q[i], q_inv);
+    r.kn[i] = __fmul_rn(k[i], k_inv);
+    kq = __fmaf_rn(r.kn[i], r.qn[i], kq);
+  }
+  r.kq = hsum32(kq);
+  return r;
+}
+
+// One state row (this lane's 4 of its 128 dk): d = S*decay; kv = d.k;
+// ob = d.q; delta = (v - kv)*beta; S <- d + k*delta; returns bf16(ob + delta*(k.q)).
+__device__ inline uint16_t gdn_row(float4& S, const GdnQK& qk, const GdnGates& g, float v) {
+  const float d[4] = {__fmul_rn(S.x, g.decay), __fmul_rn(S.y, g.decay), __fmul_rn(S.z, g.decay),
+                      __fmul_rn(S.w, g.decay)};
+  float kvm = 0.f, ob = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    kvm = __fmaf_rn(d[i], qk.kn[i], kvm);
+    ob = __fmaf_rn(d[i], qk.qn[i], ob);
+  }
+  kvm = hsum32(kvm);
+  ob = hsum32(ob);
+  const float delta = __fmul_rn(__fsub_rn(v, kvm), g.beta);
+  S = make_float4(__fmaf_rn(qk.kn[0], delta, d[0]), __fmaf_rn(qk.kn[1], delta, d[1]),
+                  __fmaf_rn(qk.kn[2], delta, d[2]), __fmaf_rn(qk.kn[3], delta, d[3]));
+  return f2bf(__fmaf_rn(delta, qk.kq, ob));
+}
+
 // IN_PLACE: state_out is state (each thread reads its rows before writing
 // them); otherwise the two buffers are distinct. NT threads, RPH rows per
 // half-wave; FUSE_NORM needs the whole head in one block.
@@ -70,50 +134,13 @@ __global__ __launch_bounds__(NT) void gdn_decode_kernel(
     for (int r = 0; r < RPH; ++r) S[r] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
 
-  // Gates (gating_many_bf16 math, shaders/gated_norm.metal:247-268).
-  const float gx = bf2f(a[hv]) + bf2f(dt_bias[hv]);
-  const float softplus = fmaxf(gx, 0.0f) + logf(1.0f + expf(-fabsf(gx)));
-  const float decay = expf(-expf(A_log[hv]) * softplus);
-  const float beta = 1.0f / (1.0f + expf(-bf2f(bgate[hv])));
-
-  // q/k L2 norms (qk_l2norm_prefill_bf16 math, shaders/gated_norm.metal:191-245).
-  const uint2 qv = *reinterpret_cast<const uint2*>(conv_out + hk * kGdnDk + 4 * j);
-  const uint2 kv = *reinterpret_cast<const uint2*>(conv_out + kGdnKeyDim + hk * kGdnDk + 4 * j);
-  const float q[4] = {bf_lo(qv.x), bf_hi(qv.x), bf_lo(qv.y), bf_hi(qv.y)};
-  const float k[4] = {bf_lo(kv.x), bf_hi(kv.x), bf_lo(kv.y), bf_hi(kv.y)};
-  float qss = 0.f, kss = 0.f;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    qss += q[i] * q[i];
-    kss += k[i] * k[i];
-  }
-  const float q_inv = rsqrtf(hsum32(qss) + 1.0e-6f) * rsqrtf(static_cast<float>(kGdnDk));
-  const float k_inv = rsqrtf(hsum32(kss) + 1.0e-6f);
-  float qn[4], kn[4], kq = 0.f;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    qn[i] = q[i] * q_inv;
-    kn[i] = k[i] * k_inv;
-    kq += kn[i] * qn[i];
-  }
-  kq = hsum32(kq);
-
+  const GdnGates gates = gdn_gates(a, bgate, A_log, dt_bias, hv);
+  const GdnQK qk = gdn_qk(conv_out, hk, j);
   const uint16_t* vsrc = conv_out + 2 * kGdnKeyDim + hv * kGdnDv + row0;
 #pragma unroll
   for (int r = 0; r < RPH; ++r) {
-    const float d[4] = {S[r].x * decay, S[r].y * decay, S[r].z * decay, S[r].w * decay};
-    float kvm = 0.f, ob = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      kvm += d[i] * kn[i];
-      ob += d[i] * qn[i];
-    }
-    kvm = hsum32(kvm);
-    ob = hsum32(ob);
-    const float delta = (bf2f(vsrc[r]) - kvm) * beta;
-    sout[r * (kGdnDk / 4)] = make_float4(d[0] + kn[0] * delta, d[1] + kn[1] * delta,
-                                         d[2] + kn[2] * delta, d[3] + kn[3] * delta);
-    const uint16_t yb = f2bf(ob + delta * kq);
+    const uint16_t yb = gdn_row(S[r], qk, gates, bf2f(vsrc[r]));
+    sout[r * (kGdnDk / 4)] = S[r];
     if (j == 0) {
       if constexpr (FUSE_NORM)
         ysh[row0 + r] = bf2f(yb);
@@ -133,6 +160,48 @@ __global__ __launch_bounds__(NT) void gdn_decode_kernel(
     const float n = yv * scale * bf2f(norm_w[tid]);
     const float g = bf2f(z[hv * kGdnDv + tid]);
     y_out[hv * kGdnDv + tid] = f2bf(n * (g / (1.0f + expf(-g))));
+  }
+}
+
+// Two consecutive tokens (the verify rows) in one launch: token 0 updates the
+// state read from `state` and writes it to `snap`, token 1 continues from
+// it in registers and writes `state_out` (may equal state). Inputs per token
+// r: conv_out + r*8192, a / b + r*32, y_out + r*4096, step[r]. The per-token
+// math is the single-token kernel's (gdn_gates, gdn_qk, gdn_row).
+template <int NT, int RPH>
+__global__ __launch_bounds__(NT) void gdn_decode2_kernel(
+    const float* state, float* __restrict__ snap, float* state_out, const uint16_t* __restrict__ conv_out,
+    const uint16_t* __restrict__ a, const uint16_t* __restrict__ bgate, const float* __restrict__ A_log,
+    const uint16_t* __restrict__ dt_bias, uint16_t* __restrict__ y_out, const StepScalars* __restrict__ step) {
+  constexpr int kRowsPerBlock = (NT / 32) * RPH;
+  constexpr int kBlocksPerHead = kGdnDv / kRowsPerBlock;
+  const uint32_t hv = blockIdx.x / kBlocksPerHead;
+  const uint32_t hk = hv / (kGdnHv / kGdnHk);
+  const int tid = threadIdx.x;
+  const int hw = tid >> 5;
+  const int j = tid & 31;
+  const uint32_t row0 = (blockIdx.x % kBlocksPerHead) * kRowsPerBlock + hw * RPH;
+  const size_t row_off = (static_cast<size_t>(hv) * kGdnDv + row0) * kGdnDk;
+  float4 S[RPH];
+#pragma unroll
+  for (int r = 0; r < RPH; ++r) S[r] = reinterpret_cast<const float4*>(state + row_off)[j + r * (kGdnDk / 4)];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    if (step[t].rope_pos == 0) {  // a fresh sequence: the incoming state is ignored
+#pragma unroll
+      for (int r = 0; r < RPH; ++r) S[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    const uint16_t* co = conv_out + t * kGdnConvDim;
+    const GdnGates gates = gdn_gates(a + t * kGdnHv, bgate + t * kGdnHv, A_log, dt_bias, hv);
+    const GdnQK qk = gdn_qk(co, hk, j);
+    const uint16_t* vsrc = co + 2 * kGdnKeyDim + hv * kGdnDv + row0;
+    float4* dst = reinterpret_cast<float4*>((t == 0 ? snap : state_out) + row_off) + j;
+#pragma unroll
+    for (int r = 0; r < RPH; ++r) {
+      const uint16_t yb = gdn_row(S[r], qk, gates, bf2f(vsrc[r]));
+      dst[r * (kGdnDk / 4)] = S[r];
+      if (j == 0) y_out[t * kGdnValDim + hv * kGdnDv + row0 + r] = yb;
+    }
   }
 }
 
@@ -193,6 +262,19 @@ int launch_gdn_decode(hipStream_t s, float* state, const uint16_t* conv_out, con
                          0.0f, state_out);
   }
   PRG_CHECK_LAUNCH("gated_delta_decode");
+  return PRG_OK;
+}
+
+int launch_gdn_decode2(hipStream_t s, const float* state, float* snap, float* state_out, const uint16_t* conv_out,
+                       const uint16_t* a, const uint16_t* b, const float* A_log, const uint16_t* dt_bias,
+                       uint16_t* y_out, const StepScalars* step_dev) {
+  if (!state || !snap || !state_out || !step_dev || snap == state || snap == state_out)
+    return set_error(PRG_ERR_INVALID_ARG, "gated_delta_decode2: needs state, a distinct snapshot and step scalars");
+  constexpr int kRph = 2;
+  const dim3 grid(kGdnHv * (kGdnDv / ((kGdnSplitThreads / 32) * kRph)));
+  hipLaunchKernelGGL((gdn_decode2_kernel<kGdnSplitThreads, kRph>), grid, dim3(kGdnSplitThreads), 0, s, state, snap,
+                     state_out, conv_out, a, b, A_log, dt_bias, y_out, step_dev);
+  PRG_CHECK_LAUNCH("gated_delta_decode2");
   return PRG_OK;
 }
 

@@ -73,4 +73,12 @@ int launch_gdn_decode(hipStream_t s, float* state, const uint16_t* conv_out, con
                       uint16_t* y_out, const StepScalars* step_dev, uint32_t has_state_host,
                       const uint16_t* norm_w, const uint16_t* z, float eps, float* state_out = nullptr);
 
+// Two consecutive tokens (the two-token verify): token 0 reads `state` and
+// writes `snap`, token 1 continues and writes `state_out` (may equal state).
+// conv_out, a, b and y_out hold the two tokens' rows back to back
+// (8192 / 32 / 32 / 4096 values apart); step_dev[0..1] are their steps.
+int launch_gdn_decode2(hipStream_t s, const float* state, float* snap, float* state_out, const uint16_t* conv_out,
+                       const uint16_t* a, const uint16_t* b, const float* A_log, const uint16_t* dt_bias,
+                       uint16_t* y_out, const StepScalars* step_dev);
+
 }  // namespace prg

@@ -313,8 +313,8 @@ int encode_linear_attention(PrgModel* m, PrgModelState* st, const DecoderLayer& 
 // Two consecutive tokens through one GDN layer (the verify rows, positions in
 // step[0] / step[1]): the normed in_proj for both rows in one M = 2 GEMV whose
 // epilogue runs both conv steps per channel (row 0's rolled conv state to
-// io.conv_out, row 1's back to io.conv_in), the recurrence for row 0
-// (io.recur_in -> io.recur_out) and then row 1 (io.recur_out -> io.recur_in),
+// io.conv_out, row 1's back to io.conv_in), both recurrence steps in one
+// launch (row 0: io.recur_in -> io.recur_out, row 1: on to io.recur_in),
 // and the gated-norm out_proj for both rows in one M = 2 GEMV. Every per-row
 // number equals two single-token layers: the M = 2 GEMVs do the M = 1
 // per-row arithmetic, and the conv epilogue repeats the single-step order.
@@ -346,13 +346,11 @@ int encode_linear_attention2(PrgModel* m, PrgModelState* st, const DecoderLayer&
   add_seg(p, b.in_b, bbuf[0]);
   p.seg[3].out[1] = bbuf[1];
   if (int rc = run_gemv(s, p, kEpiPlain, kNormRms, "linear_attn.in_proj2")) return rc;
-  for (int r = 0; r < 2; ++r) {
-    float* rin = r == 0 ? io.recur_in : io.recur_out;
-    float* rout = r == 0 ? io.recur_out : io.recur_in;
-    if (int rc = launch_gdn_decode(s, rin, conv_out[r], abuf[r], bbuf[r], b.a_log, b.dt_bias, gated[r], &step[r], 0,
-                                   nullptr, nullptr, 0.0f, rout))
-      return rc;
-  }
+  // both recurrence steps in one launch: row 0's state to io.recur_out (the
+  // snapshot), row 1's back to io.recur_in
+  if (int rc = launch_gdn_decode2(s, io.recur_in, io.recur_out, io.recur_in, conv_out[0], abuf[0], bbuf[0], b.a_log,
+                                  b.dt_bias, gated[0], step))
+    return rc;
   GemvParams o = gemv_params(gated[0], kGdnValDim);
   o.x[1] = gated[1];
   o.norm_w = b.norm_weight;
