@@ -87,15 +87,43 @@ def dominant_kernel_roofline(iters: int = 100) -> dict:
     launches = reps * copies
     avg_us = a.elapsed_ms(b) * 1e3 / launches
     graph.close()
-    stream.close()
-    synchronize()
+    del ring
     algo = 2 * q4_bytes(N, K) + 2 * K * 2 + N * 2  # gate+up weights, x + norm weight, out
     gbs = algo / (avg_us * 1e-6) / 1e9
+
+    # The single-launch read floor: a streaming read of the same number of
+    # bytes (prg_hip_read_kernel), over a ring of the same size, timed the same way.
+    nbytes = (algo + 15) // 16 * 16
+    bufs = [DeviceArray((nbytes,), np.uint8) for _ in range(copies)]
+    sink = DeviceArray((1,), np.uint32)
+    for buf in bufs:
+        call("prg_hip_read_kernel", C.c_void_p(buf.ptr), C.c_size_t(nbytes), C.c_void_p(sink.ptr),
+             C.c_void_p(stream.handle))
+    stream.synchronize()
+    with Graph.capture(stream) as rgraph:
+        for buf in bufs:
+            call("prg_hip_read_kernel", C.c_void_p(buf.ptr), C.c_size_t(nbytes), C.c_void_p(sink.ptr),
+                 C.c_void_p(stream.handle))
+    rgraph.launch()
+    stream.synchronize()
+    a.record(C.c_void_p(stream.handle))
+    for _ in range(reps):
+        rgraph.launch()
+    b.record(C.c_void_p(stream.handle))
+    stream.synchronize()
+    read_us = a.elapsed_ms(b) * 1e3 / launches
+    rgraph.close()
+    for buf in bufs:
+        buf.close()
+    stream.close()
+    synchronize()
     return {"kernel": "q4_gemv_kernel<M=1,ROWS=1,ITERS=2,EPI=silu_gate,NORM=rms> (mlp.gate_up, 2x12288x4096 Q4)",
             "bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": DOMINANT_TRAFFIC_BYTES,
             "traffic_unit": "bytes/launch (PMC, calibrated)",
             "avg_us": round(avg_us, 3), "timing": "HIP events around graph replays (no host launch overhead)",
+            "read_floor_us": round(read_us, 3), "read_floor_GBps": round(nbytes / (read_us * 1e-6) / 1e9, 1),
+            "frac_of_read_floor": round(read_us / avg_us, 4),
             "algo_bytes_per_launch": int(algo), "launches": launches, "ring_copies": copies}
 
 
@@ -255,7 +283,8 @@ def main() -> int:
     log(f"[bench] decode {a.steps} steps {ms:.1f} ms -> {tok_s:.1f} tok/s; last tokens {toks[-4:].tolist()}")
 
     roof = dominant_kernel_roofline()
-    log(f"[bench] dominant kernel {roof['avg_us']} us, {roof['achieved']} GB/s ({roof['frac'] * 100:.1f}% of peak)")
+    log(f"[bench] dominant kernel {roof['avg_us']} us, {roof['achieved']} GB/s ({roof['frac'] * 100:.1f}% of peak); "
+        f"a streaming read of the same bytes takes {roof['read_floor_us']} us ({roof['read_floor_GBps']} GB/s)")
     extra = {}
     if a.sweep:
         extra["gemv_sweep"] = gemv_sweep()

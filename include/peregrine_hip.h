@@ -97,6 +97,11 @@ int prg_hip_graph_destroy(void *graph);
 /* Plain device-to-device copy kernel (bytes % 16 == 0); the reference dispatch
  * for calibrating HBM byte counters. */
 int prg_hip_copy_kernel(void *dst, const void *src, size_t bytes, void *stream);
+/* Streaming read of `bytes` (% 16 == 0) with non-temporal 16-byte loads, four
+ * in flight per thread over a 4096-block grid; writes at most one word of
+ * sink. The single-launch HBM read floor the GEMVs are compared with. No
+ * counterpart in the reference (measurement only). */
+int prg_hip_read_kernel(const void *src, size_t bytes, uint32_t *sink, void *stream);
 
 /* ======================================================================
  * Q4 linear ops — MLX affine 4-bit, group 64, bf16 scale + bias.
