@@ -30,6 +30,12 @@ namespace {
 using namespace prg;
 
 constexpr int kAttnThreads = 256;
+// Split ranges are multiples of 32 tokens: at a 2k-token context the 64
+// splits of each kv head then all hold tokens (256 blocks), where 64-token
+// ranges would leave half of them empty. A lane reads V in 8-token pieces, so
+// every read stays inside the split's 32-token-aligned range (and the cache
+// stride, a multiple of 64).
+constexpr uint32_t kAttnChunkAlign = 32;
 
 template <int CTRL>
 __device__ inline float dpp_add(float v) {
@@ -134,7 +140,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnD
   const uint32_t split = blockIdx.x;
   const uint32_t L = min(a.step ? a.step->seq_len : a.seq_len_host, a.stride);
   uint32_t chunk = (L + a.nsplit - 1) / a.nsplit;
-  chunk = (chunk + 63u) & ~63u;
+  chunk = (chunk + kAttnChunkAlign - 1) & ~(kAttnChunkAlign - 1);
   const uint32_t t0 = split * chunk;
   const uint32_t t1 = min(t0 + chunk, L);
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -374,7 +380,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_reduce_kernel(const AttnDec
   // the statistics: one memory round trip.
   const uint32_t L = min(a.step ? a.step->seq_len : a.seq_len_host, a.stride);
   uint32_t chunk = (L + a.nsplit - 1) / a.nsplit;
-  chunk = (chunk + 63u) & ~63u;
+  chunk = (chunk + kAttnChunkAlign - 1) & ~(kAttnChunkAlign - 1);
   const uint32_t nact = min(a.nsplit, (L + chunk - 1) / chunk);
   const uint32_t d = t;
   constexpr uint32_t kPre = 64;
@@ -434,7 +440,7 @@ uint32_t attn_num_splits(uint32_t capacity) {
 
 uint32_t attn_split_tokens(uint32_t capacity, uint32_t nsplit) {
   const uint32_t c = (capacity + nsplit - 1) / nsplit;
-  return (c + 63u) & ~63u;
+  return (c + kAttnChunkAlign - 1) & ~(kAttnChunkAlign - 1);
 }
 
 int launch_attn_prepare(hipStream_t s, const AttnPrepareArgs& a) {

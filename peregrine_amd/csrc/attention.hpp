@@ -54,7 +54,7 @@ struct AttnDecodeArgs {
   float* partials;            // [16, nsplit, 258]
   uint32_t stride;
   uint32_t nsplit;
-  uint32_t split_tokens;      // LDS sizing bound (>= ceil(seq_len/nsplit) rounded to 64)
+  uint32_t split_tokens;      // LDS sizing bound (>= ceil(seq_len/nsplit) rounded to 32)
   uint32_t seq_len_host;      // used when step == nullptr
   const StepScalars* step;
   float scale;
