@@ -12,7 +12,8 @@
  * the reference leaves to hardware (Metal simd_sum over 32 lanes, threadgroup
  * trees) are restated as butterfly / strided trees in the order noted at each
  * function; the hardware's own order is not observable here, so last-ulp
- * agreement with Apple GPUs is "parity unpinned" (see DESIGN.md).
+ * agreement with Apple GPUs is "parity unpinned": no test can pin it without
+ * the reference's Metal build, which needs macOS.
  *
  * Parallelism: only across independent output rows (pthreads), so results do
  * not depend on the thread count (orc_set_threads).
