@@ -30,7 +30,7 @@ inline int gemv_blocks_per_cu() {
   static int bpc = [] {
     const char* e = getenv("PEREGRINE_GEMV_BPC");
     const int v = e ? atoi(e) : 0;
-    return v > 0 ? v : 4;
+    return v > 0 ? v : 3;
   }();
   return bpc;
 }
@@ -66,9 +66,11 @@ int launch_one_t(hipStream_t s, const GemvParams& p, size_t lds) {
   // A grid of a few blocks per CU (not the occupancy maximum) gives every
   // wave several groups, so its next group's loads overlap the dequant. For
   // small matrices more waves with partly empty rounds beat fewer full ones
-  // (measured: 4096 x 4096 takes 5.5 us at 3 blocks/CU, 6.4 us at 1); decode
-  // runs at 532 / 550 / 564 / 561 tok/s with 2 / 3 / 4 / 5 blocks per CU. One
-  // 768-thread block per CU (x staged once per CU) spills at K = 12288.
+  // (measured: 4096 x 4096 takes 5.5 us at 3 blocks/CU, 6.4 us at 1). With
+  // the current kernels decode runs at 621 / 612 / 612 / 611 tok/s with 3 / 4
+  // / 5 / 6 blocks per CU (the gate/up kernel's registers cap it at 3 in any
+  // case). One 768-thread block per CU (x staged once per CU) spills at
+  // K = 12288.
   const uint32_t want = (p.total_groups + kGemvWaves - 1) / kGemvWaves;
   const uint32_t cap = std::min<uint32_t>(resident, static_cast<uint32_t>(device_cus() * gemv_blocks_per_cu()));
   const uint32_t blocks = std::max<uint32_t>(1, std::min<uint32_t>(want, cap));
