@@ -255,14 +255,17 @@ void prg_model_state_destroy(PrgModelState *state);
 /* Zero the GDN states (ModelState.resetForNewSequence, state.zig:110-118). */
 int prg_model_state_reset(PrgModelState *state);
 /* Device pointer of a state tensor: "layers.<i>.conv", "layers.<i>.recur",
- * "layers.<i>.cache_k", "layers.<i>.cache_v"; or of a workspace buffer. */
+ * "layers.<i>.cache_k", "layers.<i>.cache_v", the drafter's "mtp.cache_k" /
+ * "mtp.cache_v" (once a drafter call has run); or of a workspace buffer. */
 int prg_model_state_tensor(const PrgModelState *state, const char *name, void **ptr, size_t *bytes);
 uint32_t prg_model_state_stride(const PrgModelState *state);
 
 /* One token through the whole stack and the greedy argmax tail, synchronous.
  * cache_pos: KV slot written; rope_pos: RoPE position (GDN state is used iff
  * rope_pos != 0); seq_len: tokens attended (must be cache_pos + 1: prefix
- * caches are not supported). Errors: SEQUENCE_TOO_LONG, INVALID_TOKEN.
+ * caches are not supported). Afterwards prg_model_decode continues at
+ * cache_pos + 1 with *next_token as its input (positions then advance with
+ * rope_pos == cache_pos). Errors: SEQUENCE_TOO_LONG, INVALID_TOKEN.
  * Replaces DeviceModel.forwardNextTokenBf16WithPrefix (model.zig:1564-1578). */
 int prg_model_forward_next_token(PrgModel *model, PrgModelState *state, uint32_t token,
                                  uint32_t cache_pos, uint32_t rope_pos, uint32_t seq_len,
@@ -279,7 +282,9 @@ int prg_model_forward_next_token(PrgModel *model, PrgModelState *state, uint32_t
 int prg_model_prefill(PrgModel *model, PrgModelState *state, const uint32_t *prompt,
                       uint32_t prompt_len, uint32_t *next_token);
 
-/* Continue the greedy loop for n_steps tokens from the current state,
+/* Continue the greedy loop for n_steps tokens from the current state (after
+ * prg_model_prefill, prg_model_generate, prg_model_forward_next_token,
+ * prg_model_forward_two_tokens or an earlier prg_model_decode),
  * device-resident (graph replay, no host sync between tokens). tokens_out (host,
  * n_steps) receives the greedy token produced by each step; gpu_ms (optional)
  * the GPU time of the n_steps steps from HIP events on the decode stream.
@@ -314,7 +319,9 @@ int prg_model_generate(PrgModel *model, PrgModelState *state, const uint32_t *pr
  * (rope_pos, rope_pos + 1; seq_len must be cache_pos + 1): the state advances
  * by both. verify_token = argmax after token0, bonus_token = argmax after
  * token1; hidden_out (device bf16 [2, hidden], may be NULL) receives the two
- * final-normed hidden rows. Errors: SEQUENCE_TOO_LONG, INVALID_TOKEN.
+ * final-normed hidden rows. Afterwards prg_model_decode continues at
+ * cache_pos + 2 with bonus_token as its input. Errors: SEQUENCE_TOO_LONG,
+ * INVALID_TOKEN.
  * Replaces DeviceModel.forwardTwoTokenDecodeVerifierBf16WithPrefixProfiled
  * (model.zig:1627-1659; encodeStack2Bf16 :719-760, decodeStep2Bf16
  * decoder_layer.zig:485-516). */

@@ -148,6 +148,18 @@ class OracleModel:
         tok, logits = self._head(normed, want_logits)
         return (tok, logits, normed) if want_hidden else (tok, logits)
 
+    def verify2(self, t0: int, t1: int, pos: int, want_logits: bool = False):
+        """forwardTwoTokenDecodeVerifierBf16 (model.zig:1627-1659): rows t0 at
+        pos and t1 at pos + 1 through encodeStack2Bf16 / decodeStep2Bf16
+        (model.zig:719-760, decoder_layer.zig:485-516). The reference runs
+        the attention-side projections once per row and the M = 2 GEMVs
+        (linear_decode.metal:76-159, 233-309, 484-580) with per-row
+        arithmetic identical to M = 1, so each row is one decode step.
+        Returns (verify, bonus, logits0|None, logits1|None, hidden rows)."""
+        v, lg0, h0 = self.step(t0, pos, want_logits, want_hidden=True)
+        b, lg1, h1 = self.step(t1, pos + 1, want_logits, want_hidden=True)
+        return v, b, lg0, lg1, np.stack([h0, h1])
+
     def _head(self, normed, want_logits: bool):
         o = self.o
         pv, pi = o.q4_argmax_partial(normed, self.lm_head)          # model.zig:1386

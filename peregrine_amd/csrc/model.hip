@@ -781,14 +781,18 @@ int prg_model_forward_next_token(PrgModel* model, PrgModelState* st, uint32_t to
   if (seq_len != cache_pos + 1)
     return set_error(PRG_ERR_INVALID_ARG, "seq_len %u != cache_pos + 1 (prefix caches are not supported)", seq_len);
   if (int rc = ensure_graphs(st)) return rc;
+  // Step n = cache_pos: the argmax records predictions[cache_pos] and leaves
+  // the loop at cache_pos + 1 with the prediction as its input, so a later
+  // prg_model_decode continues from here.
   DecodeCtl ctl{};
   ctl.s = StepScalars{token, cache_pos, rope_pos, seq_len};
-  ctl.n = 0;
+  ctl.n = cache_pos;
   ctl.prompt_len = 0;
   ctl.capacity = st->max_seq;
   PRG_HIP(hipMemcpyAsync(st->ctl, &ctl, sizeof(ctl), hipMemcpyHostToDevice, st->stream));
   if (int rc = run_step(st, true)) return rc;
-  PRG_HIP(hipMemcpyAsync(next_token, st->predictions, sizeof(uint32_t), hipMemcpyDeviceToHost, st->stream));
+  PRG_HIP(hipMemcpyAsync(next_token, st->predictions + cache_pos, sizeof(uint32_t), hipMemcpyDeviceToHost,
+                         st->stream));
   PRG_HIP(hipStreamSynchronize(st->stream));
   return PRG_OK;
 }
@@ -800,6 +804,8 @@ int prg_model_decode(PrgModel* model, PrgModelState* st, uint32_t n_steps, uint3
   DecodeCtl ctl{};
   PRG_HIP(hipMemcpyAsync(&ctl, st->ctl, sizeof(ctl), hipMemcpyDeviceToHost, st->stream));
   PRG_HIP(hipStreamSynchronize(st->stream));
+  if (ctl.overflow)
+    return set_error(PRG_ERR_SEQUENCE_TOO_LONG, "the state is at max_seq %u; nothing left to decode", st->max_seq);
   if (ctl.n + n_steps > st->max_seq)
     return set_error(PRG_ERR_SEQUENCE_TOO_LONG, "position %u + %u steps exceeds max_seq %u", ctl.n, n_steps,
                      st->max_seq);

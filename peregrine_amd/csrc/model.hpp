@@ -128,7 +128,8 @@ struct SpecCtl {
   uint32_t reject;     // this step rejected its draft: GDN states roll back
   uint32_t accepted, attempted;
   uint32_t capacity;   // positions must stay below it
-  uint32_t stop;       // set when the next step would pass capacity
+  uint32_t stop;       // set when the next step would pass capacity or `target` tokens are out
+  uint32_t target;     // tokens the loop was asked for
 };
 // The two verify rows' steps are read as an array (&v0)[0..1].
 static_assert(offsetof(SpecCtl, v1) == offsetof(SpecCtl, v0) + sizeof(StepScalars), "v1 must follow v0");
@@ -237,6 +238,9 @@ int encode_mlp(PrgModel* m, PrgModelState* st, const DecoderLayer& L, int M, con
 
 // ------------------------------------------------------------ prompt path ---
 int ensure_prefill_ws(PrgModelState* st);
+// Tokens of the next prefill chunk at `start`: at most the workspace rows, and
+// halved until the attention score block of the chunk fits the workspace.
+uint32_t prefill_chunk_tokens(const PrgModelState* st, uint32_t start, uint32_t remaining);
 int prefill_layer(PrgModel* m, PrgModelState* st, const DecoderLayer& L, LayerState& ls, const uint16_t* x,
                   uint16_t* out, uint32_t T, uint32_t start);
 // Ingest st->prompt[from, len) on top of positions [0, from); with_mtp also

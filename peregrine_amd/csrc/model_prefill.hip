@@ -75,14 +75,14 @@ int ensure_prefill_ws(PrgModelState* st) {
   return PRG_OK;
 }
 
-namespace {
-
 // Largest chunk (<= the workspace rows) whose attention scores fit.
 uint32_t prefill_chunk_tokens(const PrgModelState* st, uint32_t start, uint32_t remaining) {
   uint32_t T = std::min(remaining, st->pf.rows);
   while (T > 1 && attn_prefill_scores_elems(T, start) > st->pf.scores_elems) T = (T + 1) / 2;
   return T;
 }
+
+namespace {
 
 // x [T, in] -> out [T, out_dim] on the matrix cores (Q4Linear.encodePrefillQmm*,
 // linear_q4.zig:197-233). `up` selects the gate/up SiLU pair.
@@ -153,8 +153,8 @@ int prefill_layer(PrgModel* m, PrgModelState* st, const DecoderLayer& L, LayerSt
     if (int rc = launch_attn_prefill_prepare(s, w.qp, b.q_norm, w.k, b.k_norm, w.v, w.q, w.gate, ls.cache_k,
                                              ls.cache_v, T, start, start, st->stride))
       return rc;
-    if (int rc = launch_attn_prefill(s, w.q, ls.cache_k, ls.cache_v, w.gate, w.ctx, w.scores, T, start, st->stride,
-                                     kAttnScale))
+    if (int rc = launch_attn_prefill(s, w.q, ls.cache_k, ls.cache_v, w.gate, w.ctx, w.scores, w.scores_elems, T,
+                                     start, st->stride, kAttnScale))
       return rc;
     if (int rc = qmm(s, w.ctx, b.o_proj, w.attn, T, kGemmStore, nullptr, nullptr, "prefill.o_proj")) return rc;
   }

@@ -64,7 +64,7 @@ __global__ void spec_decide_kernel(SpecCtl* __restrict__ c, uint32_t* __restrict
       c->v1 = StepScalars{0u, np + 1, np + 1, np + 2};
       c->d0 = StepScalars{cur, np - 1, np - 1, np};
       c->d1 = StepScalars{0u, np, np, np + 1};
-      if (np + 2 > c->capacity) c->stop = 1;
+      if (np + 2 > c->capacity || c->n >= c->target) c->stop = 1;
     } else {
       c->reject = 0;
     }
@@ -264,6 +264,10 @@ int ensure_spec_ws(PrgModelState* st) {
   }
   if ((e = hipMemsetAsync(st->spec_arena, 0, total, st->stream)) != hipSuccess)
     return set_error(PRG_ERR_HIP, "speculative workspace: %s", hipGetErrorString(e));
+  if (m->mtp.present) {  // the drafter's KV cache, readable by name like the target's
+    st->tensors["mtp.cache_k"] = TensorRef{reinterpret_cast<uint8_t*>(st->mtp.cache_k), kv};
+    st->tensors["mtp.cache_v"] = TensorRef{reinterpret_cast<uint8_t*>(st->mtp.cache_v), kv};
+  }
   return PRG_OK;
 }
 
@@ -298,6 +302,17 @@ int prg_model_forward_two_tokens(PrgModel* model, PrgModelState* st, uint32_t to
   PRG_HIP(hipStreamSynchronize(st->stream));
   *verify_token = c.verify;
   *bonus_token = c.bonus;
+  // Both tokens are now in the state: a later prg_model_decode continues at
+  // cache_pos + 2 with the bonus token, as after two single steps.
+  const uint32_t preds[2] = {c.verify, c.bonus};
+  DecodeCtl ctl{};
+  ctl.s = StepScalars{c.bonus, cache_pos + 2, cache_pos + 2, cache_pos + 3};
+  ctl.n = cache_pos + 2;
+  ctl.capacity = st->max_seq;
+  ctl.overflow = cache_pos + 2 >= st->max_seq;
+  PRG_HIP(hipMemcpyAsync(st->predictions + cache_pos, preds, sizeof(preds), hipMemcpyHostToDevice, st->stream));
+  PRG_HIP(hipMemcpyAsync(st->ctl, &ctl, sizeof(ctl), hipMemcpyHostToDevice, st->stream));
+  PRG_HIP(hipStreamSynchronize(st->stream));
   return PRG_OK;
 }
 
@@ -341,7 +356,7 @@ int prg_model_mtp_prefill(PrgModel* model, PrgModelState* st, const uint32_t* to
   PRG_HIP(hipMemcpyAsync(st->spec_out, tokens, sizeof(uint32_t) * token_count, hipMemcpyHostToDevice, st->stream));
   const size_t H = model->cfg.hidden;
   for (uint32_t off = 0; off < token_count;) {
-    const uint32_t T = std::min(token_count - off, st->pf.rows);
+    const uint32_t T = prefill_chunk_tokens(st, start_pos + off, token_count - off);
     if (int rc = mtp_prefill_rows(model, st, st->spec_out + off, hidden_rows + off * H, T, start_pos + off)) return rc;
     off += T;
   }
@@ -384,12 +399,15 @@ int prg_model_generate_speculative(PrgModel* model, PrgModelState* st, const uin
   c.d1 = StepScalars{0u, L, L, L + 1};
   c.pos = L;
   c.capacity = st->max_seq;
+  c.target = n_new;
   PRG_HIP(hipMemcpyAsync(st->spec, &c, sizeof(c), hipMemcpyHostToDevice, st->stream));
   PRG_HIP(hipEventRecord(st->ev0, st->stream));
   uint32_t n = 0;
   while (n < n_new) {
-    // each step emits 1 or 2 tokens: never more than n_new + 1 in total
-    const uint32_t batch = std::min<uint32_t>(8, n_new - n);
+    // Each step emits 1 or 2 tokens, so ceil(remaining / 2) steps never run
+    // past the request: at most n_new + 1 tokens, and no step after the one
+    // that reaches n_new (the decide kernel also stops there).
+    const uint32_t batch = std::min<uint32_t>(8, (n_new - n + 1) / 2);
     for (uint32_t i = 0; i < batch; ++i)
       if (int rc = run_spec_step(model, st)) return rc;
     PRG_HIP(hipMemcpyAsync(&c, st->spec, sizeof(c), hipMemcpyDeviceToHost, st->stream));

@@ -393,8 +393,12 @@ int launch_attn_prefill_prepare(hipStream_t s, const uint16_t* qp, const uint16_
 }
 
 int launch_attn_prefill(hipStream_t s, const uint16_t* q, const uint16_t* cache_k, const uint16_t* cache_v,
-                        const uint16_t* gate, uint16_t* out, uint16_t* scores, uint32_t T, uint32_t prefix,
-                        uint32_t stride, float scale) {
+                        const uint16_t* gate, uint16_t* out, uint16_t* scores, size_t scores_cap, uint32_t T,
+                        uint32_t prefix, uint32_t stride, float scale) {
+  // scores_cap: bf16 elements the score block holds
+  if (attn_prefill_scores_elems(T, prefix) > scores_cap)
+    return set_error(PRG_ERR_INVALID_ARG, "attention prefill: %u tokens after %u need %zu score elements, %zu held",
+                     T, prefix, attn_prefill_scores_elems(T, prefix), scores_cap);
   const uint32_t L = prefix + T, ld = (L + 63) / 64 * 64;
   const uint32_t rows = kAttnGroup * T;  // per kv head: q head in group x token
   GemmArgs sc;
@@ -510,8 +514,10 @@ int prg_attn_prefill_bf16(void* stream, const uint16_t* q, const uint16_t* key_c
                 cache_stride_tokens);
   PRG_CHECK_ARG(static_cast<uint64_t>(kAttnQHeads) * token_count < (1ull << 31),
                 "prg_attn_prefill_bf16: token_count %u too large", token_count);
-  return prg::launch_attn_prefill(as_stream(stream), q, key_cache, value_cache, gate, out, scores, token_count,
-                                  prefix_len, cache_stride_tokens, scale);
+  // the caller sized scores with prg_attn_prefill_scores_bytes (op contract)
+  return prg::launch_attn_prefill(as_stream(stream), q, key_cache, value_cache, gate, out, scores,
+                                  prg::attn_prefill_scores_elems(token_count, prefix_len), token_count, prefix_len,
+                                  cache_stride_tokens, scale);
 }
 
 int prg_conv1d_silu_prefill_bf16(void* stream, float* state, const uint16_t* qkv, const uint16_t* weight,

@@ -19,8 +19,8 @@ int launch_attn_prefill_prepare(hipStream_t s, const uint16_t* qp, const uint16_
 // Causal attention of T queries [T, 16, 256] over cache slots [0, prefix + T),
 // gated: out = bf16(bf16(P V) * sigmoid(gate)).
 int launch_attn_prefill(hipStream_t s, const uint16_t* q, const uint16_t* cache_k, const uint16_t* cache_v,
-                        const uint16_t* gate, uint16_t* out, uint16_t* scores, uint32_t T, uint32_t prefix,
-                        uint32_t stride, float scale);
+                        const uint16_t* gate, uint16_t* out, uint16_t* scores, size_t scores_cap, uint32_t T,
+                        uint32_t prefix, uint32_t stride, float scale);
 
 // conv1d + SiLU over T tokens [T, 8192], then the f32 state [3, 8192] takes the
 // last three inputs.

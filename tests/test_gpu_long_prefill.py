@@ -1,0 +1,90 @@
+"""Long prompts through the layer-major chunked prefill at the full 9B shape
+(DeviceModel.prefillLayerMajor*, src/model/model.zig:829-1093;
+prefill.zig:38-196; KV stride rule state.zig:11-32).
+
+Chunking must not change a single bit: every projection is row-independent,
+the attention of chunk c reads the cache that chunks < c wrote (masked
+columns contribute exact zeros), and the GDN / conv states carry across
+chunk boundaries with the same arithmetic. So prompts ingested with
+different chunk sizes must leave identical tokens and states. The chunk size
+is capped per state through PEREGRINE_PREFILL_CHUNK (read when the state's
+prefill workspace is created).
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def m9b(gpu):
+    from peregrine_amd.model import QWEN35_9B, DeviceModel
+
+    m = DeviceModel(QWEN35_9B, seed=7)
+    yield m
+    m.close()
+
+
+def _state(m, max_seq, chunk, monkeypatch):
+    from peregrine_amd.model import ModelState
+
+    if chunk is None:
+        monkeypatch.delenv("PEREGRINE_PREFILL_CHUNK", raising=False)
+    else:
+        monkeypatch.setenv("PEREGRINE_PREFILL_CHUNK", str(chunk))
+    return ModelState(m, max_seq=max_seq)
+
+
+def _same_states(a, b, m, upto):
+    cfg = m.cfg
+    for i in range(cfg.num_layers):
+        if cfg.is_linear(i):
+            for n in ("recur", "conv"):
+                assert np.array_equal(a.read(f"layers.{i}.{n}", np.uint32), b.read(f"layers.{i}.{n}", np.uint32)), \
+                    f"layer {i} {n}"
+        else:
+            for n in ("cache_k", "cache_v"):
+                ga = a.read(f"layers.{i}.{n}", np.uint16).reshape(4, -1)
+                gb = b.read(f"layers.{i}.{n}", np.uint16).reshape(4, -1)
+                assert np.array_equal(ga, gb), f"layer {i} {n}"
+
+
+def _compare(m, prompt, max_seq, chunks, monkeypatch, decode_steps=4):
+    states = [_state(m, max_seq, c, monkeypatch) for c in chunks]
+    firsts = []
+    for c, st in zip(chunks, states):
+        print(f"[long-prefill] {len(prompt)} tokens, chunk cap {c}, stride {st.stride}", flush=True)
+        firsts.append(st.prefill(prompt))
+    assert len(set(firsts)) == 1, firsts
+    for st in states[1:]:
+        _same_states(states[0], st, m, len(prompt))
+    toks = [st.decode(decode_steps)[0] for st in states]
+    for t in toks[1:]:
+        np.testing.assert_array_equal(toks[0], t)
+    for st in states:
+        st.close()
+
+
+def test_1600_tokens_one_chunk_equals_two(m9b, monkeypatch):
+    prompt = np.random.default_rng(0).integers(0, 248320, size=1600).astype(np.uint32)
+    _compare(m9b, prompt, 2048, [None, 800], monkeypatch)
+
+
+def test_4096_tokens_default_chunks_equal_1024(m9b, monkeypatch):
+    prompt = np.random.default_rng(1).integers(0, 248320, size=4096).astype(np.uint32)
+    _compare(m9b, prompt, 4200, [None, 1024], monkeypatch)
+
+
+def test_long_context_stride_and_score_block_shrink(m9b, monkeypatch):
+    """max_seq 16000: the KV stride is aligned to 64 rather than 256
+    (state.zig:11-32), and the 2048-token chunk at position 8192 needs
+    16 * 2048 * 10240 bf16 scores, more than the 512 MiB score block, so it
+    is halved. Same tokens and states as 512-token chunks."""
+    from peregrine_amd.model import ModelState
+
+    st = ModelState(m9b, max_seq=16000)
+    assert st.stride == 16000
+    st.close()
+    assert ModelState(m9b, max_seq=15000).stride == 15104  # below 16000: aligned to 256
+    prompt = np.random.default_rng(2).integers(0, 248320, size=9000).astype(np.uint32)
+    _compare(m9b, prompt, 16000, [None, 512], monkeypatch)

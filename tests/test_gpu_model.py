@@ -214,3 +214,34 @@ def test_qwen35_9b_shape_first_steps(gpu):
     _compare([first], [ref_first], [lg], min_checked=0.0, what="9B shape prefill")
     st.close()
     m.close()
+
+
+def test_decode_continues_after_forward_next_token(small):
+    """prefill, one forward_next_token step, then prg_model_decode: the tokens
+    equal plain greedy generation (the step leaves the device loop at the
+    next position with its prediction as input)."""
+    m, st, om = small
+    rng = np.random.default_rng(6)
+    prompt = rng.integers(0, SMALL["vocab"], size=10).astype(np.uint32)
+    ref, _ = st.generate(prompt, 8)
+    ref = ref[9:]
+    first = st.prefill(prompt)
+    second = st.forward_next_token(first, 10)
+    rest, _ = st.decode(6)
+    np.testing.assert_array_equal(np.concatenate([[first, second], rest]).astype(np.uint32), ref)
+
+
+def test_decode_refuses_a_full_state(gpu):
+    """A step at the last slot leaves nothing to decode: SequenceTooLong."""
+    from peregrine_amd._lib import PrgError
+    from peregrine_amd.model import DeviceModel, ModelConfig, ModelState
+
+    m = DeviceModel(ModelConfig(**SMALL), seed=1)
+    st = ModelState(m, max_seq=16)
+    st.prefill(np.arange(15, dtype=np.uint32))
+    st.forward_next_token(3, 15)
+    with pytest.raises(PrgError) as e:
+        st.decode(1)
+    assert e.value.code == 5
+    st.close()
+    m.close()
