@@ -304,6 +304,21 @@ int prg_attn_decode_bf16(void *stream, const uint16_t *q, const uint16_t *key_ca
                          float scale);
 size_t prg_attn_decode_partials_bytes(uint32_t cache_stride_tokens);
 
+/* prg_attn_decode_bf16 without the partials argument, for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). No counterpart in the reference. It allocates nothing:
+ * the partials live in a library-owned device array (one per GPU, 4,227,072
+ * bytes, held until the process ends) whose address is looked up once per
+ * device by prg_hip_device_init or the first call on a device. Holds caches of
+ * up to 256 splits, i.e. cache_stride_tokens <= 262144 at the default 1024
+ * tokens per split; larger caches are rejected with PRG_ERR_INVALID_ARG.
+ * Calls that overlap on one GPU (different streams, or threads) share the
+ * array and race: serialise them. Output is bit-identical to
+ * prg_attn_decode_bf16 on the same inputs. */
+int prg_attn_decode_noalloc_bf16(void *stream, const uint16_t *q, const uint16_t *key_cache,
+                                 const uint16_t *value_cache, const uint16_t *gate, uint16_t *out,
+                                 uint32_t cache_stride_tokens, uint32_t seq_len, float scale);
+
 /* ======================================================================
  * Prompt (prefill) path: T tokens at once through MFMA GEMMs.
  * Row-major [T, dim] activations; the same shape rules as above.

@@ -23,6 +23,8 @@
 //            LDS; 8-lane DPP sum at the end.
 #include <stdlib.h>
 
+#include <mutex>
+
 #include "attention.hpp"
 
 namespace {
@@ -462,6 +464,72 @@ int launch_attn_decode(hipStream_t s, const AttnDecodeArgs& a) {
   return PRG_OK;
 }
 
+// ------------------------------------------------------- allocation-free --
+// Partials of prg_attn_decode_noalloc_bf16 live in this file-scope device
+// array: each GPU holds its own copy (4,227,072 bytes: 16 q heads x 256
+// splits x 258 floats, i.e. caches of up to 256 splits, 262144 tokens at the
+// default 1024 tokens per split) until the process ends. Host code must not
+// pass `scratch` itself to a kernel: its device address is looked up once
+// per device (attn_noalloc_setup) and kept in g_scratch.
+constexpr uint32_t kNoAllocMaxSplits = 256;
+constexpr size_t kNoAllocFloats = static_cast<size_t>(kAttnQHeads) * kNoAllocMaxSplits * kAttnPartialStride;
+static __device__ __align__(256) float scratch[kNoAllocFloats];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device (set up on first use).
+int noalloc_scratch(float** out) {
+  int dev = 0;
+  PRG_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices)
+    return set_error(PRG_ERR_INVALID_ARG, "allocation-free attention: device %d >= %d", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return set_error(PRG_ERR_HIP, "allocation-free attention: hipGetSymbolAddress: %s", hipGetErrorString(e));
+    g_scratch[dev] = static_cast<float*>(p);
+  }
+  *out = g_scratch[dev];
+  return PRG_OK;
+}
+}  // namespace
+
+int attn_noalloc_setup() {
+  float* p = nullptr;
+  return noalloc_scratch(&p);
+}
+
+// Shared by the decode-attention entry points: argument checks, then the
+// partials + merge launches with `partials` as the workspace.
+static int attn_decode_entry(const char* name, void* stream, const uint16_t* q, const uint16_t* key_cache,
+                             const uint16_t* value_cache, const uint16_t* gate, uint16_t* out, float* partials,
+                             uint32_t cache_stride_tokens, uint32_t seq_len, float scale) {
+  PRG_CHECK_ARG(q && key_cache && value_cache && gate && out && partials, "%s: null pointer", name);
+  PRG_CHECK_ARG(cache_stride_tokens % 64 == 0, "%s: stride %u must be a multiple of 64", name, cache_stride_tokens);
+  if (seq_len == 0 || seq_len > cache_stride_tokens)
+    return set_error(PRG_ERR_SEQUENCE_TOO_LONG, "%s: seq_len %u outside (0, %u]", name, seq_len,
+                     cache_stride_tokens);
+  AttnDecodeArgs a{};
+  a.q = q;
+  a.key_cache = key_cache;
+  a.value_cache = value_cache;
+  a.gate = gate;
+  a.out = out;
+  a.partials = partials;
+  a.stride = cache_stride_tokens;
+  a.nsplit = attn_num_splits(cache_stride_tokens);
+  a.split_tokens = attn_split_tokens(cache_stride_tokens, a.nsplit);
+  a.seq_len_host = seq_len;
+  a.step = nullptr;
+  a.scale = scale;
+  return launch_attn_decode(as_stream(stream), a);
+}
+
 }  // namespace prg
 
 extern "C" {
@@ -486,26 +554,26 @@ int prg_attn_decode_bf16(void* stream, const uint16_t* q, const uint16_t* key_ca
                          const uint16_t* value_cache, const uint16_t* gate, uint16_t* out,
                          float* partials, uint32_t cache_stride_tokens, uint32_t seq_len,
                          float scale) {
-  PRG_CHECK_ARG(q && key_cache && value_cache && gate && out && partials, "prg_attn_decode_bf16: null pointer");
-  PRG_CHECK_ARG(cache_stride_tokens % 64 == 0, "prg_attn_decode_bf16: stride %u must be a multiple of 64",
-                cache_stride_tokens);
-  if (seq_len == 0 || seq_len > cache_stride_tokens)
-    return prg::set_error(PRG_ERR_SEQUENCE_TOO_LONG, "prg_attn_decode_bf16: seq_len %u outside (0, %u]", seq_len,
-                          cache_stride_tokens);
-  prg::AttnDecodeArgs a{};
-  a.q = q;
-  a.key_cache = key_cache;
-  a.value_cache = value_cache;
-  a.gate = gate;
-  a.out = out;
-  a.partials = partials;
-  a.stride = cache_stride_tokens;
-  a.nsplit = prg::attn_num_splits(cache_stride_tokens);
-  a.split_tokens = prg::attn_split_tokens(cache_stride_tokens, a.nsplit);
-  a.seq_len_host = seq_len;
-  a.step = nullptr;
-  a.scale = scale;
-  return prg::launch_attn_decode(prg::as_stream(stream), a);
+  return prg::attn_decode_entry("prg_attn_decode_bf16", stream, q, key_cache, value_cache, gate, out, partials,
+                                cache_stride_tokens, seq_len, scale);
+}
+
+int prg_attn_decode_noalloc_bf16(void* stream, const uint16_t* q, const uint16_t* key_cache,
+                                 const uint16_t* value_cache, const uint16_t* gate, uint16_t* out,
+                                 uint32_t cache_stride_tokens, uint32_t seq_len, float scale) {
+  const char* name = "prg_attn_decode_noalloc_bf16";
+  PRG_CHECK_ARG(cache_stride_tokens > 0, "%s: stride 0", name);
+  const uint32_t nsplit = prg::attn_num_splits(cache_stride_tokens);
+  if (nsplit > prg::kNoAllocMaxSplits)
+    return prg::set_error(PRG_ERR_INVALID_ARG,
+                          "%s: a cache of %u tokens needs %u splits (%zu partial bytes); this entry holds %u splits "
+                          "(%zu bytes)",
+                          name, cache_stride_tokens, nsplit, prg_attn_decode_partials_bytes(cache_stride_tokens),
+                          prg::kNoAllocMaxSplits, prg::kNoAllocFloats * sizeof(float));
+  float* partials = nullptr;
+  if (int rc = prg::noalloc_scratch(&partials)) return rc;
+  return prg::attn_decode_entry(name, stream, q, key_cache, value_cache, gate, out, partials, cache_stride_tokens,
+                                seq_len, scale);
 }
 
 size_t prg_attn_decode_partials_bytes(uint32_t cache_stride_tokens) {

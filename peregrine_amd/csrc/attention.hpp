@@ -16,6 +16,10 @@ constexpr float kAttnEps = 1.0e-6f;
 constexpr float kAttnScale = 1.0f / 16.0f;
 constexpr uint32_t kAttnPartialStride = kAttnHeadDim + 2;  // [m, denom, acc[256]]
 
+// Look up the device address of the allocation-free decode attention's
+// partials on the current device (once per device; later calls are free).
+int attn_noalloc_setup();
+
 // Split-context count for a cache of `capacity` tokens: every kv head is split
 // into this many contiguous token ranges (one block each), fixed per cache so a
 // captured graph stays valid as seq_len grows.

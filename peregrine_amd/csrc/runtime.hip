@@ -7,6 +7,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include "attention.hpp"
 #include "common.hpp"
 
 namespace prg {
@@ -100,7 +101,7 @@ int prg_hip_device_init(int ordinal) {
     return set_error(PRG_ERR_NO_DEVICE, "no HIP device visible");
   PRG_CHECK_ARG(ordinal >= 0 && ordinal < n, "device ordinal %d out of range [0,%d)", ordinal, n);
   PRG_HIP(hipSetDevice(ordinal));
-  return PRG_OK;
+  return prg::attn_noalloc_setup();
 }
 
 int prg_hip_device_name(char* buf, size_t len) {

@@ -157,6 +157,12 @@ def attn_decode(q, key_cache, value_cache, gate, out, partials, stride: int, seq
          ptr(partials), stride, seq_len, scale)
 
 
+def attn_decode_noalloc(q, key_cache, value_cache, gate, out, stride: int, seq_len: int,
+                        scale: float = 1.0 / 16.0, stream=None) -> None:
+    call("prg_attn_decode_noalloc_bf16", _s(stream), ptr(q), ptr(key_cache), ptr(value_cache), ptr(gate),
+         ptr(out), stride, seq_len, scale)
+
+
 # ------------------------------------------------------------- prefill ops
 def attn_prefill_prepare(packed_q, q_w, k_in, k_w, v_in, q_out, gate_out, key_cache, value_cache,
                          token_count: int, start_rope: int, start_cache: int, stride: int, stream=None) -> None:
