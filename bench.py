@@ -146,34 +146,179 @@ def prefill_flops(cfg, T: int) -> float:
 def gemv_sweep() -> list[dict]:
     from peregrine_amd.gemv_bench import sweep
 
-    return [{k: (round(v, 3) if isinstance(v, float) else v) for k, v in r.items()} for r in sweep(iters=60)]
+    return [{k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()} for r in sweep()]
 
 
-def cpu_baseline(model, budget_s: float = 20.0) -> dict:
-    """The C oracle (scalar restatement of the reference shaders) running the
-    same 9B-shaped decode step on the host cores, row-parallel. Bounded
-    sample: teacher-forced decode steps from an empty state until ~budget_s."""
+def host_info() -> dict:
+    """Host CPUs of this box: nproc, the CPU model name, and the threads the
+    CPU baselines use (the box's CPU share is 16 threads for one GPU)."""
+    name = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                name = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    nproc = os.cpu_count() or 1
+    return {"nproc": nproc, "cpu_model": name, "threads": max(1, min(16, nproc))}
+
+
+def _timed(fn, min_s: float = 0.3, max_reps: int = 20) -> float:
+    """Seconds per call of fn(): at least one call, repeated until min_s."""
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        dt = time.perf_counter() - t0
+        if dt >= min_s or n >= max_reps:
+            return dt / n
+
+
+def cpu_configs(threads: int) -> list[dict]:
+    """The C oracle (scalar restatement of the reference shaders) on BASELINE
+    configs 1-4, on this box's host cores: single-threaded and row-parallel
+    on `threads` threads (the row split keeps every output's arithmetic, so
+    results do not depend on the thread count). Same seeded distributions as
+    the GPU runs; per call, with the algorithmic bytes of the call."""
+    from oracle import oracle
+    from peregrine_amd.gemv_bench import q4_bytes
+    from peregrine_amd.synth import random_bf16, random_q4
+
+    o = oracle()
+    rows = []
+
+    def both(case, config, algo, fn, parallel=True):
+        r = {"config": config, "case": case, "algo_bytes": int(algo)}
+        for t in ((1, threads) if parallel else (1,)):
+            o.set_threads(t)
+            sec = _timed(fn)
+            r[f"ms_{t}t"] = round(sec * 1e3, 3)
+            r[f"GBps_{t}t"] = round(algo / sec / 1e9, 3)
+        if not parallel:
+            r["note"] = "the oracle's decode recurrence runs on one thread"
+        rows.append(r)
+
+    rng = np.random.default_rng(0)  # config 1: seed 0, the BASELINE distributions
+    wt = random_q4(rng, 12288, 4096)
+    x = random_bf16(rng, (1, 4096))
+    both("q4 gemv 12288x4096 (seed 0)", 1, q4_bytes(12288, 4096) + 4096 * 2 + 12288 * 2, lambda: o.q4_gemv(x, wt))
+    rng = np.random.default_rng(1)
+    for N, K in ((4096, 12288), (4096, 4096)):
+        w2, x2 = random_q4(rng, N, K), random_bf16(rng, (1, K))
+        both(f"q4 gemv {N}x{K}", 2, q4_bytes(N, K) + K * 2 + N * 2, lambda: o.q4_gemv(x2, w2))
+    wl, xl = random_q4(rng, 248320, 4096, zero_mean=True), random_bf16(rng, (4096,))
+
+    def lm_head():
+        pv, pi = o.q4_argmax_partial(xl, wl)
+        o.argmax_pairs(pv[0], pi[0])
+
+    both("lm_head 248320x4096 + argmax", 2, q4_bytes(248320, 4096) + 4096 * 2 + 31040 * 8, lm_head)
+    del wl
+
+    # config 3: one Gated DeltaNet decode layer (conv, recurrence, gated norm)
+    rng = np.random.default_rng(3)
+    cs = rng.normal(0, 1.0, size=(3, 8192)).astype(np.float32)
+    cw = random_bf16(rng, (8192, 4), std=0.5)
+    qkv = random_bf16(rng, (8192,))
+    S = rng.normal(0, 0.1, size=(32, 128, 128)).astype(np.float32)
+    a, b = random_bf16(rng, (32,)), random_bf16(rng, (32,))
+    A_log = np.zeros(32, np.float32)
+    dt = np.zeros(32, np.uint16)
+    nw, z = random_bf16(rng, (128,), std=0.1, mean=1.0), random_bf16(rng, (4096,))
+
+    def gdn_layer():
+        c, _ = o.conv1d_decode(cs, qkv, cw)
+        y, _ = o.gated_delta_decode(S, c, a, b, A_log, dt)
+        o.rmsnorm_gated(y, nw, z, 128)
+
+    both("gdn decode layer (conv + recurrence + gated norm)", 3,
+         2 * S.nbytes + 2 * cs.nbytes + cw.nbytes + qkv.nbytes + z.nbytes + 4096 * 2, gdn_layer, parallel=False)
+
+    # config 4: one GQA decode attention layer (prepare + attention) at L
+    for L in (4096, 24576, 65536):
+        rng = np.random.default_rng(4 + L)
+        kc, vc = random_bf16(rng, (4, L, 256)), random_bf16(rng, (4, 256, L))
+        pq, kin, vin = random_bf16(rng, (16 * 512,)), random_bf16(rng, (1024,)), random_bf16(rng, (1024,))
+        qw, kw = random_bf16(rng, (256,), std=0.1, mean=1.0), random_bf16(rng, (256,), std=0.1, mean=1.0)
+
+        # the q/k norm + RoPE + append (~40 KB of work) runs once, untimed: the
+        # numpy binding copies both caches around it
+        q, g, kc, vc = o.attn_prepare(pq, qw, kin, vin, kw, kc, vc, L, L - 1, L - 1)
+        both(f"gqa decode attention L={L} (split-context attention + gated merge)", 4,
+             4096 * L + 16 * 256 * 2 * 3, lambda: o.attn_decode(q, kc, vc, g, L, L))
+    o.set_threads(threads)
+    return rows
+
+
+def cpu_baseline(model, snapshot: dict, tokens, start: int, info: dict, budget_s: float = 15.0) -> dict:
+    """The C oracle running the same 9B-shaped decode step on the host cores,
+    row-parallel, at the GPU's context: its state is the GPU's state after
+    the prompt (KV caches and GDN states copied from the device), and it is
+    teacher-forced on the GPU's greedy tokens from position `start`, until
+    ~budget_s. Also reports how many of those steps predict the GPU's next
+    token."""
     from oracle import oracle
     from oracle.model import OracleModel
 
-    threads = max(1, min(16, os.cpu_count() or 1))
+    threads = info["threads"]
     o = oracle()
     o.set_threads(threads)
     t0 = time.time()
-    om = OracleModel(model, 64)
+    om = OracleModel(model, snapshot["max_seq"])
     load_s = time.time() - t0
-    om.reset()
-    toks = [11, 248319, 4096, 77, 5, 6, 7, 8]
-    n, t0 = 0, time.time()
-    while n < len(toks):
-        om.step(toks[n], n)
+    assert om.stride == snapshot["stride"], (om.stride, snapshot["stride"])
+    for i, L in enumerate(om.layers):
+        if L["linear"]:
+            om.state[i]["conv"] = snapshot[f"layers.{i}.conv"].reshape(3, 8192).copy()
+            om.state[i]["recur"] = snapshot[f"layers.{i}.recur"].reshape(32, 128, 128).copy()
+        else:
+            om.state[i]["k"] = snapshot[f"layers.{i}.cache_k"].reshape(4, om.stride, 256).copy()
+            om.state[i]["v"] = snapshot[f"layers.{i}.cache_v"].reshape(4, 256, om.stride).copy()
+    n = same = 0
+    t0 = time.time()
+    while n + 1 < len(tokens):
+        pred, _ = om.step(int(tokens[n]), start + n)
+        same += int(pred == int(tokens[n + 1]))
         n += 1
         if time.time() - t0 > budget_s:
             break
     dt = time.time() - t0
     return {"value": round(n / dt, 4), "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"{n} decode steps of the same 9B-shaped model at positions 0..{n - 1} "
-                      f"(C oracle, {threads} threads; weight readback {load_s:.1f}s excluded)"}
+            "nproc": info["nproc"], "cpu_model": info["cpu_model"],
+            "sample": f"{n} decode steps of the same 9B-shaped model at positions {start}..{start + n - 1}, "
+                      f"on the GPU's state after the {start}-token prompt, teacher-forced on the GPU's tokens "
+                      f"(C oracle, {threads} threads; weight readback {load_s:.1f}s excluded)",
+            "predicts_gpu_token": f"{same}/{n}"}
+
+
+def snapshot_state(st) -> dict:
+    """Host copy of a ModelState's GDN states and KV caches."""
+    snap = {"max_seq": st.max_seq, "stride": st.stride}
+    cfg = st.model.cfg
+    for i in range(cfg.num_layers):
+        names = ("conv", "recur") if cfg.is_linear(i) else ("cache_k", "cache_v")
+        for nm in names:
+            snap[f"layers.{i}.{nm}"] = st.read(f"layers.{i}.{nm}", np.float32 if cfg.is_linear(i) else np.uint16)
+    return snap
+
+
+def long_prefill(model, tokens: int = 16384) -> dict:
+    """Cold prefill of a `tokens`-token random prompt (no cached prefix) on a
+    fresh state: the reference's reason for chunked prefill is 16k-token agent
+    prefixes. The prompt workspace is allocated by a 1-token prefill first;
+    the timed call is the whole multi-chunk ingestion to the first token."""
+    from peregrine_amd.model import ModelState
+
+    st = ModelState(model, tokens + 64)
+    prompt = np.random.default_rng(5).integers(0, model.cfg.vocab, size=tokens).astype(np.uint32)
+    st.prefill(prompt[:1])
+    t0 = time.time()
+    st.prefill(prompt)
+    sec = time.time() - t0
+    st.close()
+    return {"tokens": tokens, "ms": round(sec * 1e3, 1), "tok_s": round(tokens / sec, 1),
+            "tflops": round(prefill_flops(model.cfg, tokens) / sec / 1e12, 2), "max_seq": tokens + 64}
 
 
 def mtp_run(steps: int) -> dict:
@@ -209,7 +354,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=32)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--no-mtp", action="store_true", help="skip the MTP speculative run (BASELINE configs[4], repeat)")
-    ap.add_argument("--sweep", action="store_true", help="also run the Q4 GEMV sweep (configs[1])")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the operator benchmarks of BASELINE configs 2-4 (graph-replayed)")
+    ap.add_argument("--no-long-prefill", action="store_true", help="skip the 16k-token cold prefill")
     ap.add_argument("--eager", action="store_true",
                     help="launch each token's kernels directly instead of replaying the HIP graph "
                          "(for kernel tracers; slower)")
@@ -274,8 +421,8 @@ def main() -> int:
                "first_call_ms": round(cold_s * 1e3, 2)}
     log(f"[bench] prompt ingest {PROMPT_TOKENS} tokens {prefill_s * 1e3:.1f} ms "
         f"({prefill['tok_s']} tok/s, {prefill['tflops']} TFLOP/s), first token {first}")
-    if a.warmup:
-        st.decode(a.warmup)
+    snap = None if a.no_cpu else snapshot_state(st)
+    wtoks = st.decode(a.warmup)[0] if a.warmup else np.zeros(0, np.uint32)
     device.synchronize()
     toks, ms = st.decode(a.steps)
     device.synchronize()
@@ -286,11 +433,15 @@ def main() -> int:
     log(f"[bench] dominant kernel {roof['avg_us']} us, {roof['achieved']} GB/s ({roof['frac'] * 100:.1f}% of peak); "
         f"a streaming read of the same bytes takes {roof['read_floor_us']} us ({roof['read_floor_GBps']} GB/s)")
     extra = {}
-    if a.sweep:
-        extra["gemv_sweep"] = gemv_sweep()
+    if not a.no_long_prefill:
+        extra["prefill_16k"] = long_prefill(model)
+        log(f"[bench] 16k cold prefill {extra['prefill_16k']}")
     cpu = None
+    info = host_info()
     if not a.no_cpu:
-        cpu = cpu_baseline(model)
+        # the GPU's tokens from position PROMPT_TOKENS: the prompt's next token, then every decode step's
+        gpu_toks = np.concatenate([[first], wtoks, toks]).astype(np.uint32)
+        cpu = cpu_baseline(model, snap, gpu_toks, PROMPT_TOKENS, info)
         log(f"[bench] cpu baseline {cpu}")
     st.close()
     weight_bytes = int(model.weight_bytes)
@@ -299,6 +450,19 @@ def main() -> int:
     if not a.no_mtp:
         mtp = mtp_run(a.steps)
         log(f"[bench] mtp speculative loop {mtp}")
+    if not a.no_configs:
+        from peregrine_amd.op_bench import configs_3_4
+
+        rows = gemv_sweep()
+        for r in rows:
+            r["config"] = 2
+        extra["configs_2_4"] = rows + configs_3_4()
+        for r in extra["configs_2_4"]:
+            log(f"[bench] {r}")
+    if not a.no_cpu:
+        extra["cpu_configs_1_4"] = {"host": info, "rows": cpu_configs(info["threads"])}
+        for r in extra["cpu_configs_1_4"]["rows"]:
+            log(f"[bench] cpu {r}")
 
     line = {
         "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": a.steps,

@@ -1,16 +1,21 @@
 // Prompt-prefix state cache and its PRGPFXS1 v3 persistence file (host code;
 // the device work is copies between ModelStates).
 //
-// Reference:
-//   PrefixIndex, Entry, Cache   src/server/prefix_state_cache.zig:21-795
-//   save / load / fingerprint   src/server/prefix_persist.zig:31-412
+// Observable rules kept from the reference (src/server/prefix_state_cache.zig):
+// an entry per exact token prefix; the longest cached prefix of a prompt is
+// reused; storing a longer prefix that continues a reused entry re-keys that
+// entry; every entry reserves max(tokens, prefill chunk) state slots and the
+// reserved total stays within the token budget by evicting the least recently
+// used unpinned entry; entries are numbered in creation order. The file format,
+// its validation and the model fingerprint follow src/server/prefix_persist.zig:31-412.
 //
-// Entries own a PrgModelState sized to their tokens (at least the prefill
-// chunk), keyed in a token trie; the reserved-token budget evicts the least
-// recently used unpinned entry. A working state reuses a cached prefix by
-// copying it in (prg_prefix_cache_restore), so positions stay absolute (see
-// model_prefix.hip). Created without a model, the cache keeps tokens and
-// accounting only (no device state), which is all the index needs.
+// The store itself is this file's own: entries live in a table keyed by
+// stable ids and are found through a hash of their whole token key with a
+// per-length probe for the longest match (no trie), and the budget totals are
+// summed from the entries when needed. A working state reuses a cached
+// prefix by copying it in (prg_prefix_cache_restore), so positions stay
+// absolute (see model_prefix.hip). Created without a model, the cache keeps
+// tokens and accounting only (no device state).
 #include <dirent.h>
 #include <fcntl.h>
 #include <stdio.h>
@@ -21,7 +26,10 @@
 
 #include <algorithm>
 #include <cerrno>
+#include <iterator>
+#include <map>
 #include <string>
+#include <unordered_map>
 #include <vector>
 
 #include "model.hpp"
@@ -134,164 +142,172 @@ class Wyhash {
 };
 constexpr uint64_t Wyhash::kSecret[4];
 
-// ------------------------------------------------------------ the index -----
-// Token trie: node 0 is the root; an entry is registered at the node of its
-// full token sequence (prefix_state_cache.zig:21-210).
-class PrefixIndex {
- public:
-  void clear() {
-    nodes_.clear();
-    free_.clear();
-  }
-
-  void insert(const uint32_t* t, size_t n, int entry) {
-    if (n == 0) return;
-    if (nodes_.empty()) nodes_.push_back(root());
-    int node = 0;
-    for (size_t i = 0; i < n; ++i) {
-      int c = child(node, t[i]);
-      if (c < 0) {
-        c = alloc(node, t[i]);
-        nodes_[node].children.push_back({t[i], c});
-      }
-      node = c;
-    }
-    nodes_[node].entry = entry;
-  }
-
-  void remove(const uint32_t* t, size_t n) {
-    const int node = find_node(t, n);
-    if (node < 0) return;
-    nodes_[node].entry = -1;
-    prune(node);
-  }
-
-  // Longest registered prefix of p: entry index and length, or false.
-  bool find_longest(const uint32_t* p, size_t n, int* entry, size_t* len) const {
-    if (nodes_.empty()) return false;
-    int node = 0;
-    bool found = false;
-    for (size_t i = 0; i < n; ++i) {
-      node = child(node, p[i]);
-      if (node < 0) break;
-      if (nodes_[node].entry >= 0) {
-        *entry = nodes_[node].entry;
-        *len = i + 1;
-        found = true;
-      }
-    }
-    return found;
-  }
-
-  int find_exact(const uint32_t* t, size_t n) const {
-    const int node = find_node(t, n);
-    return node < 0 ? -1 : nodes_[node].entry;
-  }
-
-  bool contains_prefix(const uint32_t* p, size_t n, size_t prefix_len) const {
-    if (prefix_len == 0) return true;
-    if (prefix_len > n || nodes_.empty()) return false;
-    const int node = find_node(p, prefix_len);
-    return node >= 0 && nodes_[node].entry >= 0;
-  }
-
-  // Entry `removed` left the entry list: later indexes shift down by one.
-  void decrement_after(int removed) {
-    for (Node& nd : nodes_) {
-      if (!nd.alive || nd.entry < 0) continue;
-      if (nd.entry == removed)
-        nd.entry = -1;
-      else if (nd.entry > removed)
-        nd.entry -= 1;
-    }
-  }
-
- private:
-  struct Node {
-    int parent = -1;
-    uint32_t parent_token = 0;
-    std::vector<std::pair<uint32_t, int>> children;
-    int entry = -1;
-    bool alive = false;
-  };
-  std::vector<Node> nodes_;
-  std::vector<int> free_;
-
-  static Node root() {
-    Node r;
-    r.alive = true;
-    return r;
-  }
-  int alloc(int parent, uint32_t token) {
-    Node nd;
-    nd.parent = parent;
-    nd.parent_token = token;
-    nd.alive = true;
-    if (!free_.empty()) {
-      const int i = free_.back();
-      free_.pop_back();
-      nodes_[i] = std::move(nd);
-      return i;
-    }
-    nodes_.push_back(std::move(nd));
-    return static_cast<int>(nodes_.size()) - 1;
-  }
-  int child(int node, uint32_t token) const {
-    const Node& nd = nodes_[node];
-    if (!nd.alive) return -1;
-    for (const auto& c : nd.children)
-      if (c.first == token) return c.second;
-    return -1;
-  }
-  int find_node(const uint32_t* t, size_t n) const {
-    if (nodes_.empty()) return -1;
-    int node = 0;
-    for (size_t i = 0; i < n && node >= 0; ++i) node = child(node, t[i]);
-    return node;
-  }
-  // Drop childless nodes without an entry, walking up towards the root.
-  void prune(int node) {
-    while (node != 0) {
-      Node& nd = nodes_[node];
-      if (nd.entry >= 0 || !nd.children.empty()) return;
-      const int parent = nd.parent;
-      auto& sib = nodes_[parent].children;
-      for (size_t k = 0; k < sib.size(); ++k) {
-        if (sib[k].first == nd.parent_token && sib[k].second == node) {
-          sib.erase(sib.begin() + static_cast<long>(k));
-          break;
-        }
-      }
-      nd = Node{};
-      free_.push_back(node);
-      node = parent;
-    }
-  }
-};
-
-struct PrefixEntry {
-  PrgModelState* state = nullptr;  // nullptr without a model
-  uint32_t capacity = 0;           // token capacity of `state` (the reserved tokens)
-  uint16_t* hidden = nullptr;      // device bf16 [hidden_rows, hidden] when tracking
-  uint32_t hidden_rows = 0;
+// ------------------------------------------------------------ the store -----
+// Cached prefixes live in a table keyed by a stable id that is never reused;
+// ids grow with creation, so the table's order is creation order and the
+// C ABI's entry index is an entry's rank in it. Lookups go through a hash of
+// the whole token key (verified against the tokens, so a collision can only
+// cost a comparison): the longest cached prefix of a prompt is found by
+// hashing the prompt's prefixes once and probing only the key lengths that
+// exist, longest first.
+struct CachedPrefix {
+  std::vector<uint32_t> tokens;    // the key
+  uint64_t key_hash = 0;
+  uint32_t reserved = 0;           // token capacity of `state`; counts against the budget
+  PrgModelState* state = nullptr;  // nullptr for a cache without a model
+  uint16_t* hidden = nullptr;      // device bf16 rows [reserved, hidden] once tracked
   bool hidden_valid = false;
   uint32_t next_token = 0;
   bool next_valid = false;
-  std::vector<uint32_t> tokens;
   bool pinned = false;
-  uint64_t last_access = 0;
+  uint64_t stamp = 0;  // last use (logical clock)
   uint64_t hits = 0;
+};
+
+// Polynomial hash of a token key, extended one token at a time.
+inline uint64_t key_step(uint64_t h, uint32_t t) { return (h ^ (t + 0x9e3779b97f4a7c15ull)) * 0x100000001b3ull; }
+inline uint64_t key_hash(const uint32_t* t, size_t n) {
+  uint64_t h = 0xcbf29ce484222325ull;
+  for (size_t i = 0; i < n; ++i) h = key_step(h, t[i]);
+  return h;
+}
+
+class PrefixStore {
+ public:
+  using Table = std::map<uint64_t, CachedPrefix>;
+
+  Table& table() { return table_; }
+  const Table& table() const { return table_; }
+  size_t size() const { return table_.size(); }
+
+  CachedPrefix* get(uint64_t id) {
+    auto it = table_.find(id);
+    return it == table_.end() ? nullptr : &it->second;
+  }
+  const CachedPrefix* get(uint64_t id) const {
+    auto it = table_.find(id);
+    return it == table_.end() ? nullptr : &it->second;
+  }
+  // Id at C-ABI index `rank`, or 0.
+  uint64_t id_at(size_t rank) const {
+    if (rank >= table_.size()) return 0;
+    return std::next(table_.begin(), static_cast<long>(rank))->first;
+  }
+  uint32_t rank_of(uint64_t id) const {
+    return static_cast<uint32_t>(std::distance(table_.begin(), table_.find(id)));
+  }
+
+  uint64_t add(CachedPrefix&& e) {
+    const uint64_t id = ++last_id_;
+    e.key_hash = key_hash(e.tokens.data(), e.tokens.size());
+    link(id, e);
+    table_.emplace(id, std::move(e));
+    return id;
+  }
+  // Re-key entry `id` to a new token sequence.
+  void rekey(uint64_t id, const uint32_t* t, size_t n) {
+    CachedPrefix& e = table_.at(id);
+    unlink(id, e);
+    e.tokens.assign(t, t + n);
+    e.key_hash = key_hash(t, n);
+    link(id, e);
+  }
+  // Remove entry `id` from the table; the caller releases its resources.
+  CachedPrefix take(uint64_t id) {
+    auto it = table_.find(id);
+    unlink(id, it->second);
+    CachedPrefix e = std::move(it->second);
+    table_.erase(it);
+    return e;
+  }
+  void reset() {
+    table_.clear();
+    by_hash_.clear();
+    lengths_.clear();
+  }
+
+  uint64_t exact(const uint32_t* t, size_t n) const {
+    if (n == 0 || lengths_.find(static_cast<uint32_t>(n)) == lengths_.end()) return 0;
+    return probe(key_hash(t, n), t, n);
+  }
+  // Longest cached key that is a prefix of p[0, n): its id and length.
+  uint64_t longest(const uint32_t* p, size_t n, size_t* len) const {
+    if (lengths_.empty() || n == 0) return 0;
+    const size_t top = std::min<size_t>(n, lengths_.rbegin()->first);
+    std::vector<uint64_t> h(top + 1);
+    h[0] = 0xcbf29ce484222325ull;
+    for (size_t i = 0; i < top; ++i) h[i + 1] = key_step(h[i], p[i]);
+    for (auto it = lengths_.rbegin(); it != lengths_.rend(); ++it) {
+      const size_t L = it->first;
+      if (L > top) continue;
+      if (const uint64_t id = probe(h[L], p, L)) {
+        *len = L;
+        return id;
+      }
+    }
+    return 0;
+  }
+
+  uint64_t reserved_total() const {
+    uint64_t s = 0;
+    for (const auto& kv : table_) s += kv.second.reserved;
+    return s;
+  }
+  uint64_t resident_total() const {
+    uint64_t s = 0;
+    for (const auto& kv : table_) s += kv.second.tokens.size();
+    return s;
+  }
+  // The unpinned entry other than `keep` used longest ago, or 0.
+  uint64_t coldest(uint64_t keep) const {
+    uint64_t best = 0, best_stamp = 0;
+    for (const auto& kv : table_) {
+      if (kv.first == keep || kv.second.pinned) continue;
+      if (best == 0 || kv.second.stamp < best_stamp) {
+        best = kv.first;
+        best_stamp = kv.second.stamp;
+      }
+    }
+    return best;
+  }
+
+ private:
+  Table table_;
+  std::unordered_multimap<uint64_t, uint64_t> by_hash_;  // key hash -> id
+  std::map<uint32_t, uint32_t> lengths_;                  // key length -> entries with it
+  uint64_t last_id_ = 0;
+
+  void link(uint64_t id, const CachedPrefix& e) {
+    by_hash_.emplace(e.key_hash, id);
+    lengths_[static_cast<uint32_t>(e.tokens.size())] += 1;
+  }
+  void unlink(uint64_t id, const CachedPrefix& e) {
+    auto range = by_hash_.equal_range(e.key_hash);
+    for (auto it = range.first; it != range.second; ++it)
+      if (it->second == id) {
+        by_hash_.erase(it);
+        break;
+      }
+    auto l = lengths_.find(static_cast<uint32_t>(e.tokens.size()));
+    if (l != lengths_.end() && --l->second == 0) lengths_.erase(l);
+  }
+  uint64_t probe(uint64_t h, const uint32_t* t, size_t n) const {
+    auto range = by_hash_.equal_range(h);
+    for (auto it = range.first; it != range.second; ++it) {
+      const CachedPrefix& e = table_.at(it->second);
+      if (e.tokens.size() == n && std::equal(e.tokens.begin(), e.tokens.end(), t)) return it->second;
+    }
+    return 0;
+  }
 };
 
 }  // namespace prg
 
 struct PrgPrefixCache {
   PrgModel* model = nullptr;
-  std::vector<prg::PrefixEntry> entries;
-  prg::PrefixIndex index;
+  prg::PrefixStore store;
   uint64_t max_tokens = 0, initial_state_tokens = 0;
-  uint64_t resident_tokens = 0, reserved_tokens = 0;
-  int active = -1;
+  uint64_t active = 0;  // id of the entry last used, 0 = none
   uint64_t clock = 0;
   uint64_t hits = 0, misses = 0, hit_tokens = 0, computed_tokens = 0, evictions = 0;
   bool track_hidden = false;
@@ -305,186 +321,149 @@ using Cache = PrgPrefixCache;
 
 size_t hidden_row_bytes(const Cache* c) { return sizeof(uint16_t) * c->model->cfg.hidden; }
 
-void free_entry(PrefixEntry& e) {
+void release(CachedPrefix& e) {
   if (e.state) prg_model_state_destroy(e.state);
-  if (e.hidden) hipFree(e.hidden);
+  if (e.hidden) (void)hipFree(e.hidden);
   e.state = nullptr;
   e.hidden = nullptr;
 }
 
-int new_entry(Cache* c, uint32_t capacity, bool pinned, PrefixEntry* out) {
-  PrefixEntry e;
-  e.capacity = capacity;
-  e.pinned = pinned;
-  if (c->model) {
-    if (int rc = prg_model_state_create(c->model, capacity, &e.state)) return rc;
-  }
-  *out = std::move(e);
-  return PRG_OK;
+void drop(Cache* c, uint64_t id) {
+  CachedPrefix e = c->store.take(id);
+  release(e);
+  if (c->active == id) c->active = 0;
 }
 
-uint64_t next_access(Cache* c) { return ++c->clock; }
-
-void clear_all(Cache* c) {
-  for (PrefixEntry& e : c->entries) free_entry(e);
-  c->entries.clear();
-  c->index.clear();
-  c->resident_tokens = c->reserved_tokens = 0;
-  c->active = -1;
+void drop_all(Cache* c) {
+  for (auto& kv : c->store.table()) release(kv.second);
+  c->store.reset();
+  c->active = 0;
 }
 
-void remove_entry(Cache* c, size_t i) {
-  if (i >= c->entries.size()) return;
-  PrefixEntry& e = c->entries[i];
-  c->index.remove(e.tokens.data(), e.tokens.size());
-  c->resident_tokens -= std::min<uint64_t>(c->resident_tokens, e.tokens.size());
-  c->reserved_tokens -= std::min<uint64_t>(c->reserved_tokens, e.capacity);
-  free_entry(e);
-  c->entries.erase(c->entries.begin() + static_cast<long>(i));
-  c->index.decrement_after(static_cast<int>(i));
-  if (c->active == static_cast<int>(i))
-    c->active = -1;
-  else if (c->active > static_cast<int>(i))
-    c->active -= 1;
+void mark_used(Cache* c, uint64_t id) {
+  CachedPrefix* e = c->store.get(id);
+  if (!e) return;
+  e->stamp = ++c->clock;
+  e->hits += 1;
+  c->active = id;
 }
 
-void touch(Cache* c, size_t i) {
-  if (i >= c->entries.size()) return;
-  c->entries[i].last_access = next_access(c);
-  c->entries[i].hits += 1;
-  c->active = static_cast<int>(i);
-}
-
-int evictable(const Cache* c, int preserve) {
-  int victim = -1;
-  for (size_t i = 0; i < c->entries.size(); ++i) {
-    if (static_cast<int>(i) == preserve || c->entries[i].pinned) continue;
-    if (victim < 0 || c->entries[i].last_access < c->entries[victim].last_access) victim = static_cast<int>(i);
-  }
-  return victim;
-}
-
-// ensureReservedTokenBudget (prefix_state_cache.zig:760-774).
-int ensure_budget(Cache* c, int* preserve, uint64_t additional) {
-  if (additional > c->max_tokens)
+// Evict least recently used unpinned entries (never `keep`) until `extra`
+// more reserved tokens fit the budget.
+int make_room(Cache* c, uint64_t extra, uint64_t keep) {
+  if (extra > c->max_tokens)
     return set_error(PRG_ERR_SEQUENCE_TOO_LONG, "prefix cache: %llu tokens exceed the budget %llu",
-                     (unsigned long long)additional, (unsigned long long)c->max_tokens);
-  while (c->reserved_tokens + additional > c->max_tokens) {
-    const int victim = evictable(c, *preserve);
-    if (victim < 0)
+                     (unsigned long long)extra, (unsigned long long)c->max_tokens);
+  while (c->store.reserved_total() + extra > c->max_tokens) {
+    const uint64_t victim = c->store.coldest(keep);
+    if (victim == 0)
       return set_error(PRG_ERR_SEQUENCE_TOO_LONG, "prefix cache: budget %llu exhausted by pinned entries",
                        (unsigned long long)c->max_tokens);
-    remove_entry(c, static_cast<size_t>(victim));
-    if (*preserve >= 0 && victim < *preserve) *preserve -= 1;
+    drop(c, victim);
     c->evictions += 1;
   }
   return PRG_OK;
 }
 
-// Entry.ensureStateCapacity (prefix_state_cache.zig:246-258).
-int ensure_state_capacity(Cache* c, PrefixEntry& e, uint32_t n) {
-  if (n == 0 || n <= e.capacity) return PRG_OK;
-  PrefixEntry grown;
-  if (int rc = new_entry(c, n, e.pinned, &grown)) return rc;
-  if (e.state && !e.tokens.empty()) {
-    const uint32_t keep = static_cast<uint32_t>(e.tokens.size());
-    int rc = copy_attention_range(grown.state, 0, e.state, 0, keep);
-    if (rc == PRG_OK) rc = copy_linear_state(grown.state, e.state);
+// Device buffers of an entry with `capacity` token slots: a model state, and
+// hidden rows when the cache tracks them. Existing contents (the entry's
+// first `keep` positions and its GDN state, its first `keep` hidden rows)
+// move into the new buffers.
+int resize_buffers(Cache* c, CachedPrefix& e, uint32_t capacity, uint32_t keep) {
+  if (!c->model) {
+    e.reserved = capacity;
+    return PRG_OK;
+  }
+  PrgModelState* st = nullptr;
+  if (int rc = prg_model_state_create(c->model, capacity, &st)) return rc;
+  if (e.state && keep) {
+    int rc = copy_attention_range(st, 0, e.state, 0, keep);
+    if (rc == PRG_OK) rc = copy_linear_state(st, e.state);
     if (rc) {
-      free_entry(grown);
+      prg_model_state_destroy(st);
       return rc;
+    }
+  }
+  uint16_t* rows = nullptr;
+  if (c->track_hidden || e.hidden) {
+    const size_t rb = hidden_row_bytes(c);
+    hipError_t err = hipMalloc(reinterpret_cast<void**>(&rows), rb * capacity);
+    if (err == hipSuccess) err = hipMemsetAsync(rows, 0, rb * capacity, c->stream);
+    if (err == hipSuccess && e.hidden && keep)
+      err = hipMemcpyAsync(rows, e.hidden, rb * keep, hipMemcpyDeviceToDevice, c->stream);
+    if (err == hipSuccess) err = hipStreamSynchronize(c->stream);
+    if (err != hipSuccess) {
+      if (rows) (void)hipFree(rows);
+      prg_model_state_destroy(st);
+      return set_error(PRG_ERR_HIP, "prefix cache hidden rows: %s", hipGetErrorString(err));
     }
   }
   if (e.state) prg_model_state_destroy(e.state);
-  e.state = grown.state;
-  e.capacity = n;
+  if (e.hidden) (void)hipFree(e.hidden);
+  e.state = st;
+  e.hidden = rows;
+  e.reserved = capacity;
   return PRG_OK;
 }
 
-// Entry.ensureHiddenCapacity (prefix_state_cache.zig:262-290): the old rows
-// are kept, new rows are zero.
-int ensure_hidden_capacity(Cache* c, PrefixEntry& e, uint32_t n) {
-  const uint32_t rows = std::max(n, e.capacity);
-  if (e.hidden && e.hidden_rows >= rows) return PRG_OK;
+// Hidden rows for an entry created before tracking was switched on.
+int ensure_hidden_rows(Cache* c, CachedPrefix& e) {
+  if (e.hidden) return PRG_OK;
   const size_t rb = hidden_row_bytes(c);
-  uint16_t* buf = nullptr;
-  PRG_HIP(hipMalloc(reinterpret_cast<void**>(&buf), rb * rows));
-  hipError_t err = hipMemsetAsync(buf, 0, rb * rows, c->stream);
-  if (err == hipSuccess && e.hidden) {
-    const size_t keep = std::min<size_t>(e.tokens.size(), e.hidden_rows);
-    if (keep) err = hipMemcpyAsync(buf, e.hidden, rb * keep, hipMemcpyDeviceToDevice, c->stream);
-  }
-  if (err == hipSuccess) err = hipStreamSynchronize(c->stream);
-  if (err != hipSuccess) {
-    hipFree(buf);
-    return set_error(PRG_ERR_HIP, "prefix cache hidden rows: %s", hipGetErrorString(err));
-  }
-  if (e.hidden) hipFree(e.hidden);
-  e.hidden = buf;
-  e.hidden_rows = rows;
+  PRG_HIP(hipMalloc(reinterpret_cast<void**>(&e.hidden), rb * e.reserved));
+  PRG_HIP(hipMemsetAsync(e.hidden, 0, rb * e.reserved, c->stream));
+  PRG_HIP(hipStreamSynchronize(c->stream));
   return PRG_OK;
 }
 
-// replaceEntryPrefix (prefix_state_cache.zig:736-756).
-int replace_entry_prefix(Cache* c, int* preserve, const uint32_t* ids, uint32_t n, bool pinned) {
-  PrefixEntry* e = &c->entries[*preserve];
-  const uint64_t old_len = e->tokens.size(), old_capacity = e->capacity;
-  if (n > old_capacity)
-    if (int rc = ensure_budget(c, preserve, n - old_capacity)) return rc;
-  e = &c->entries[*preserve];
-  if (int rc = ensure_state_capacity(c, *e, n)) return rc;
-  c->reserved_tokens = c->reserved_tokens - old_capacity + e->capacity;
-  e->tokens.assign(ids, ids + n);
-  e->pinned = e->pinned || pinned;
-  c->resident_tokens = c->resident_tokens - old_len + n;
-  return PRG_OK;
-}
-
-// prepareEntry (prefix_state_cache.zig:693-734): the exact entry, the reused
-// entry re-keyed to the longer prefix, or a new entry within the budget.
-int prepare_entry(Cache* c, const uint32_t* ids, uint32_t n, int reuse, bool pinned, int* out) {
+// Make the entry that will hold ids[0, n): the entry already keyed by exactly
+// these tokens; else `reuse` re-keyed to them (a longer prefix continuing
+// it); else a new entry of max(n, initial_state_tokens) slots. Growing an
+// entry or adding one evicts least recently used unpinned entries first.
+int admit(Cache* c, const uint32_t* ids, uint32_t n, uint64_t reuse, bool pinned, uint64_t* out) {
   if (n == 0 || n > c->max_tokens)
     return set_error(PRG_ERR_SEQUENCE_TOO_LONG, "prefix cache: prefix of %u tokens (budget %llu)", n,
                      (unsigned long long)c->max_tokens);
-  const int exact = c->index.find_exact(ids, n);
-  if (exact >= 0) {
-    int keep = exact;
-    if (int rc = replace_entry_prefix(c, &keep, ids, n, pinned)) return rc;
-    *out = keep;
-    return PRG_OK;
-  }
-  if (reuse >= 0) {
-    int keep = reuse;
-    const std::vector<uint32_t> old_tokens = c->entries[keep].tokens;
-    c->index.insert(ids, n, keep);
-    if (int rc = replace_entry_prefix(c, &keep, ids, n, pinned)) {
-      c->index.remove(ids, n);
-      return rc;
+  uint64_t id = c->store.exact(ids, n);
+  if (id == 0) id = reuse;
+  if (id != 0) {
+    CachedPrefix& e = *c->store.get(id);
+    if (n > e.reserved) {
+      if (int rc = make_room(c, n - e.reserved, id)) return rc;
+      CachedPrefix& grown = *c->store.get(id);
+      if (int rc = resize_buffers(c, grown, n, static_cast<uint32_t>(grown.tokens.size()))) return rc;
     }
-    c->index.remove(old_tokens.data(), old_tokens.size());
-    *out = keep;
+    CachedPrefix& ent = *c->store.get(id);
+    if (ent.tokens.size() != n || !std::equal(ent.tokens.begin(), ent.tokens.end(), ids)) c->store.rekey(id, ids, n);
+    ent.pinned = ent.pinned || pinned;
+    *out = id;
     return PRG_OK;
   }
-  int none = -1;
   const uint32_t capacity = static_cast<uint32_t>(std::max<uint64_t>(n, c->initial_state_tokens));
-  if (int rc = ensure_budget(c, &none, capacity)) return rc;
-  PrefixEntry e;
-  if (int rc = new_entry(c, capacity, pinned, &e)) return rc;
+  if (int rc = make_room(c, capacity, 0)) return rc;
+  CachedPrefix e;
   e.tokens.assign(ids, ids + n);
-  e.last_access = next_access(c);
-  c->entries.push_back(std::move(e));
-  const int idx = static_cast<int>(c->entries.size()) - 1;
-  c->index.insert(ids, n, idx);
-  c->resident_tokens += n;
-  c->reserved_tokens += capacity;
-  *out = idx;
+  e.pinned = pinned;
+  e.stamp = ++c->clock;
+  if (int rc = resize_buffers(c, e, capacity, 0)) {
+    release(e);
+    return rc;
+  }
+  *out = c->store.add(std::move(e));
   return PRG_OK;
 }
 
-int check_match(const Cache* c, const PrgPrefixMatch& m) {
-  PRG_CHECK_ARG(m.index < c->entries.size(), "prefix cache: match index %u of %zu entries", m.index,
-                c->entries.size());
+int match_id(const Cache* c, const PrgPrefixMatch& m, uint64_t* id) {
+  *id = c->store.id_at(m.index);
+  PRG_CHECK_ARG(*id != 0, "prefix cache: match index %u of %zu entries", m.index, c->store.size());
   return PRG_OK;
+}
+
+PrgPrefixMatch match_of(const Cache* c, uint64_t id, uint32_t len) {
+  PrgPrefixMatch m;
+  m.index = c->store.rank_of(id);
+  m.len = len;
+  return m;
 }
 
 // ------------------------------------------------------- persistence --------
@@ -582,13 +561,13 @@ int make_parent_dirs(const std::string& path) {
   return PRG_OK;
 }
 
-// The entry a save persists: the active one, else the most recently used
+// The entry a save persists: the one last used, else the most recently used
 // non-empty one (persistedEntryConst, prefix_state_cache.zig:380-391).
-const PrefixEntry* persisted_entry(const Cache* c) {
-  if (c->active >= 0 && c->active < static_cast<int>(c->entries.size())) return &c->entries[c->active];
-  const PrefixEntry* best = nullptr;
-  for (const PrefixEntry& e : c->entries)
-    if (!e.tokens.empty() && (!best || e.last_access > best->last_access)) best = &e;
+const CachedPrefix* persisted_entry(const Cache* c) {
+  if (const CachedPrefix* e = c->store.get(c->active)) return e;
+  const CachedPrefix* best = nullptr;
+  for (const auto& kv : c->store.table())
+    if (!kv.second.tokens.empty() && (!best || kv.second.stamp > best->stamp)) best = &kv.second;
   return best;
 }
 
@@ -749,31 +728,31 @@ int prg_prefix_cache_create(PrgModel* model, uint32_t max_cache_tokens, uint32_t
 
 void prg_prefix_cache_destroy(PrgPrefixCache* c) {
   if (!c) return;
-  clear_all(c);
-  if (c->stream) hipStreamDestroy(c->stream);
+  drop_all(c);
+  if (c->stream) (void)hipStreamDestroy(c->stream);
   delete c;
 }
 
 int prg_prefix_cache_clear(PrgPrefixCache* c) {
   PRG_CHECK_ARG(c, "prg_prefix_cache_clear: null cache");
-  clear_all(c);
+  drop_all(c);
   return PRG_OK;
 }
 
 uint32_t prg_prefix_cache_entry_count(const PrgPrefixCache* c) {
-  return c ? static_cast<uint32_t>(c->entries.size()) : 0u;
+  return c ? static_cast<uint32_t>(c->store.size()) : 0u;
 }
 
 uint32_t prg_prefix_cache_pinned_count(const PrgPrefixCache* c) {
   if (!c) return 0;
   uint32_t n = 0;
-  for (const PrefixEntry& e : c->entries) n += e.pinned ? 1 : 0;
+  for (const auto& kv : c->store.table()) n += kv.second.pinned ? 1 : 0;
   return n;
 }
 
 uint32_t prg_prefix_cache_active_tokens(const PrgPrefixCache* c) {
-  if (!c || c->active < 0 || c->active >= static_cast<int>(c->entries.size())) return 0;
-  return static_cast<uint32_t>(c->entries[c->active].tokens.size());
+  const CachedPrefix* e = c ? c->store.get(c->active) : nullptr;
+  return e ? static_cast<uint32_t>(e->tokens.size()) : 0u;
 }
 
 int prg_prefix_cache_stats(const PrgPrefixCache* c, PrgPrefixCacheStats* s) {
@@ -782,10 +761,10 @@ int prg_prefix_cache_stats(const PrgPrefixCache* c, PrgPrefixCacheStats* s) {
   s->misses = c->misses;
   s->hit_tokens = c->hit_tokens;
   s->computed_tokens = c->computed_tokens;
-  s->reserved_tokens = c->reserved_tokens;
-  s->resident_tokens = c->resident_tokens;
+  s->reserved_tokens = c->store.reserved_total();
+  s->resident_tokens = c->store.resident_total();
   s->max_tokens = c->max_tokens;
-  s->entry_count = c->entries.size();
+  s->entry_count = c->store.size();
   s->evictions = c->evictions;
   return PRG_OK;
 }
@@ -807,93 +786,94 @@ void prg_prefix_cache_record_computed(PrgPrefixCache* c, uint32_t token_count) {
 int prg_prefix_cache_find(const PrgPrefixCache* c, const uint32_t* prompt, uint32_t prompt_len,
                           PrgPrefixMatch* match) {
   PRG_CHECK_ARG(c && match && (prompt || prompt_len == 0), "prg_prefix_cache_find: null argument");
-  int entry = -1;
   size_t len = 0;
-  if (c->index.find_longest(prompt, prompt_len, &entry, &len)) {
-    match->index = static_cast<uint32_t>(entry);
-    match->len = static_cast<uint32_t>(len);
-  } else {
-    match->index = 0;
-    match->len = 0;
-  }
+  const uint64_t id = c->store.longest(prompt, prompt_len, &len);
+  *match = id ? match_of(c, id, static_cast<uint32_t>(len)) : PrgPrefixMatch{0, 0};
   return PRG_OK;
 }
 
 int prg_prefix_cache_contains(const PrgPrefixCache* c, const uint32_t* prompt, uint32_t prompt_len,
                               uint32_t prefix_len) {
   if (!c || (!prompt && prompt_len)) return 0;
-  return c->index.contains_prefix(prompt, prompt_len, prefix_len) ? 1 : 0;
+  if (prefix_len == 0) return 1;
+  if (prefix_len > prompt_len) return 0;
+  return c->store.exact(prompt, prefix_len) != 0 ? 1 : 0;
 }
 
 int prg_prefix_cache_touch(PrgPrefixCache* c, PrgPrefixMatch match) {
   PRG_CHECK_ARG(c, "prg_prefix_cache_touch: null cache");
-  if (int rc = check_match(c, match)) return rc;
-  touch(c, match.index);
+  uint64_t id = 0;
+  if (int rc = match_id(c, match, &id)) return rc;
+  mark_used(c, id);
   return PRG_OK;
 }
 
 int prg_prefix_cache_remove(PrgPrefixCache* c, uint32_t index) {
-  PRG_CHECK_ARG(c && index < c->entries.size(), "prg_prefix_cache_remove: bad index");
-  remove_entry(c, index);
+  const uint64_t id = c ? c->store.id_at(index) : 0;
+  PRG_CHECK_ARG(id != 0, "prg_prefix_cache_remove: bad index");
+  drop(c, id);
   return PRG_OK;
 }
 
 int prg_prefix_cache_entry_info(const PrgPrefixCache* c, uint32_t index, uint32_t* token_count, uint32_t* capacity,
                                 int* pinned, uint64_t* hits) {
-  PRG_CHECK_ARG(c && index < c->entries.size(), "prg_prefix_cache_entry_info: bad index");
-  const PrefixEntry& e = c->entries[index];
-  if (token_count) *token_count = static_cast<uint32_t>(e.tokens.size());
-  if (capacity) *capacity = e.capacity;
-  if (pinned) *pinned = e.pinned ? 1 : 0;
-  if (hits) *hits = e.hits;
+  const CachedPrefix* e = c ? c->store.get(c->store.id_at(index)) : nullptr;
+  PRG_CHECK_ARG(e, "prg_prefix_cache_entry_info: bad index");
+  if (token_count) *token_count = static_cast<uint32_t>(e->tokens.size());
+  if (capacity) *capacity = e->reserved;
+  if (pinned) *pinned = e->pinned ? 1 : 0;
+  if (hits) *hits = e->hits;
   return PRG_OK;
 }
 
 int prg_prefix_cache_entry_tokens(const PrgPrefixCache* c, uint32_t index, uint32_t* tokens, uint32_t capacity) {
-  PRG_CHECK_ARG(c && tokens && index < c->entries.size(), "prg_prefix_cache_entry_tokens: bad argument");
-  const PrefixEntry& e = c->entries[index];
-  PRG_CHECK_ARG(capacity >= e.tokens.size(), "prg_prefix_cache_entry_tokens: buffer of %u < %zu", capacity,
-                e.tokens.size());
-  std::copy(e.tokens.begin(), e.tokens.end(), tokens);
+  const CachedPrefix* e = c && tokens ? c->store.get(c->store.id_at(index)) : nullptr;
+  PRG_CHECK_ARG(e, "prg_prefix_cache_entry_tokens: bad argument");
+  PRG_CHECK_ARG(capacity >= e->tokens.size(), "prg_prefix_cache_entry_tokens: buffer of %u < %zu", capacity,
+                e->tokens.size());
+  std::copy(e->tokens.begin(), e->tokens.end(), tokens);
   return PRG_OK;
 }
 
 int prg_prefix_cache_entry_state(PrgPrefixCache* c, uint32_t index, PrgModelState** state) {
-  PRG_CHECK_ARG(c && state && index < c->entries.size(), "prg_prefix_cache_entry_state: bad argument");
+  const CachedPrefix* e = c && state ? c->store.get(c->store.id_at(index)) : nullptr;
+  PRG_CHECK_ARG(e, "prg_prefix_cache_entry_state: bad argument");
   PRG_CHECK_ARG(c->model, "prg_prefix_cache_entry_state: the cache was created without a model");
-  *state = c->entries[index].state;
+  *state = e->state;
   return PRG_OK;
 }
 
 int prg_prefix_cache_cached_next_token(const PrgPrefixCache* c, PrgPrefixMatch match, uint32_t* token, int* valid) {
   PRG_CHECK_ARG(c && token && valid, "prg_prefix_cache_cached_next_token: null argument");
-  if (int rc = check_match(c, match)) return rc;
-  *token = c->entries[match.index].next_token;
-  *valid = c->entries[match.index].next_valid ? 1 : 0;
+  uint64_t id = 0;
+  if (int rc = match_id(c, match, &id)) return rc;
+  const CachedPrefix& e = *c->store.get(id);
+  *token = e.next_token;
+  *valid = e.next_valid ? 1 : 0;
   return PRG_OK;
 }
 
 int prg_prefix_cache_start_direct(PrgPrefixCache* c, const uint32_t* ids, uint32_t n, int pinned,
                                   PrgPrefixMatch* out) {
   PRG_CHECK_ARG(c && out && (ids || n == 0), "prg_prefix_cache_start_direct: null argument");
-  int idx = -1;
-  if (int rc = prepare_entry(c, ids, n, -1, pinned != 0, &idx)) return rc;
-  PrefixEntry& e = c->entries[idx];
+  uint64_t id = 0;
+  if (int rc = admit(c, ids, n, 0, pinned != 0, &id)) return rc;
+  CachedPrefix& e = *c->store.get(id);
   if (e.state)
     if (int rc = prg_model_state_reset(e.state)) return rc;
   e.next_valid = false;
-  out->index = static_cast<uint32_t>(idx);
-  out->len = n;
+  *out = match_of(c, id, n);
   return PRG_OK;
 }
 
 int prg_prefix_cache_finish_direct(PrgPrefixCache* c, PrgPrefixMatch match, uint32_t next_token) {
   PRG_CHECK_ARG(c, "prg_prefix_cache_finish_direct: null cache");
-  if (int rc = check_match(c, match)) return rc;
-  PrefixEntry& e = c->entries[match.index];
+  uint64_t id = 0;
+  if (int rc = match_id(c, match, &id)) return rc;
+  CachedPrefix& e = *c->store.get(id);
   e.next_token = next_token;
   e.next_valid = true;
-  touch(c, match.index);
+  mark_used(c, id);
   return PRG_OK;
 }
 
@@ -902,58 +882,56 @@ int prg_prefix_cache_store(PrgPrefixCache* c, const uint32_t* ids, uint32_t n, c
                            const uint32_t* next_token, int pinned, PrgPrefixMatch* out) {
   PRG_CHECK_ARG(c && out && (ids || n == 0), "prg_prefix_cache_store: null argument");
   PRG_CHECK_ARG(!c->model || (work && work->model == c->model), "prg_prefix_cache_store: work state of another model");
+  uint64_t reuse_id = 0;
   if (reuse)
-    if (int rc = check_match(c, *reuse)) return rc;
+    if (int rc = match_id(c, *reuse, &reuse_id)) return rc;
   if (n == 0 || n > c->max_tokens)
     return set_error(PRG_ERR_SEQUENCE_TOO_LONG, "prefix cache: prefix of %u tokens (budget %llu)", n,
                      (unsigned long long)c->max_tokens);
   if (work) PRG_CHECK_ARG(n <= work->max_seq, "prg_prefix_cache_store: %u tokens > work capacity %u", n, work->max_seq);
-  const bool had_exact = c->index.find_exact(ids, n) >= 0;
-  int idx = -1;
-  if (int rc = prepare_entry(c, ids, n, reuse ? static_cast<int>(reuse->index) : -1, pinned != 0, &idx)) return rc;
-  PrefixEntry& e = c->entries[idx];
+  const bool already_cached = c->store.exact(ids, n) != 0;
+  uint64_t id = 0;
+  if (int rc = admit(c, ids, n, reuse_id, pinned != 0, &id)) return rc;
+  CachedPrefix& e = *c->store.get(id);
+  // The working state holds absolute positions [0, n) (a reused prefix was
+  // copied into it first), so an entry continuing `reuse` only needs
+  // positions [reuse_len, n) and the GDN state after token n.
   const uint32_t reuse_len = reuse ? std::min(reuse->len, n) : 0;
-  // storePrefixFromWork (prefix_state_cache.zig:563-648). The working state
-  // holds absolute positions [0, n) (the reused prefix was copied into it), so
-  // a re-keyed entry takes positions [reuse_len, n) plus the GDN state.
-  if (!had_exact && e.state) {
+  if (!already_cached && e.state) {
     int rc = copy_attention_range(e.state, reuse_len, work, reuse_len, n - reuse_len);
     if (rc == PRG_OK) rc = copy_linear_state(e.state, work);
     if (rc) return rc;
   }
   if (c->track_hidden && c->model) {
-    const bool reuse_hidden_valid = reuse_len != 0 ? e.hidden_valid : false;
-    if (int rc = ensure_hidden_capacity(c, e, n)) return rc;
-    const uint32_t suffix = n - reuse_len;
+    // rows [0, reuse_len) stay; rows [reuse_len, n) come from work_hidden
+    const bool prefix_rows_valid = reuse_len == 0 || e.hidden_valid;
+    if (int rc = ensure_hidden_rows(c, e)) return rc;
+    const uint32_t fresh = n - reuse_len;
     const size_t rb = hidden_row_bytes(c);
-    if (suffix) {
-      uint16_t* dst = e.hidden + static_cast<size_t>(reuse_len) * (rb / 2);
+    if (fresh) {
+      char* dst = reinterpret_cast<char*>(e.hidden) + static_cast<size_t>(reuse_len) * rb;
       if (work_hidden)
-        PRG_HIP(hipMemcpyAsync(dst, work_hidden + static_cast<size_t>(work_hidden_base_rows) * (rb / 2), suffix * rb,
-                               hipMemcpyDeviceToDevice, c->stream));
+        PRG_HIP(hipMemcpyAsync(dst, reinterpret_cast<const char*>(work_hidden) + work_hidden_base_rows * rb,
+                               fresh * rb, hipMemcpyDeviceToDevice, c->stream));
       else
-        PRG_HIP(hipMemsetAsync(dst, 0, suffix * rb, c->stream));
+        PRG_HIP(hipMemsetAsync(dst, 0, fresh * rb, c->stream));
       PRG_HIP(hipStreamSynchronize(c->stream));
     }
-    e.hidden_valid = (reuse_len == 0 || reuse_hidden_valid) && (suffix == 0 || work_hidden != nullptr);
+    e.hidden_valid = prefix_rows_valid && (fresh == 0 || work_hidden != nullptr);
   }
-  if (next_token) {
-    e.next_token = *next_token;
-    e.next_valid = true;
-  } else {
-    e.next_valid = false;
-  }
-  touch(c, idx);
-  out->index = static_cast<uint32_t>(idx);
-  out->len = n;
+  e.next_valid = next_token != nullptr;
+  if (next_token) e.next_token = *next_token;
+  mark_used(c, id);
+  *out = match_of(c, id, n);
   return PRG_OK;
 }
 
 int prg_prefix_cache_restore(const PrgPrefixCache* c, PrgPrefixMatch match, PrgModelState* work) {
   PRG_CHECK_ARG(c && work, "prg_prefix_cache_restore: null argument");
   PRG_CHECK_ARG(c->model && work->model == c->model, "prg_prefix_cache_restore: work state of another model");
-  if (int rc = check_match(c, match)) return rc;
-  const PrefixEntry& e = c->entries[match.index];
+  uint64_t id = 0;
+  if (int rc = match_id(c, match, &id)) return rc;
+  const CachedPrefix& e = *c->store.get(id);
   // The GDN state exists only after the entry's last token.
   PRG_CHECK_ARG(match.len == e.tokens.size(), "prg_prefix_cache_restore: match of %u tokens on an entry of %zu",
                 match.len, e.tokens.size());
@@ -971,17 +949,22 @@ int prg_prefix_cache_enable_hidden(PrgPrefixCache* c) {
 
 int prg_prefix_cache_entry_hidden(const PrgPrefixCache* c, PrgPrefixMatch match, uint16_t** rows, int* valid) {
   PRG_CHECK_ARG(c && rows && valid, "prg_prefix_cache_entry_hidden: null argument");
-  if (int rc = check_match(c, match)) return rc;
-  *rows = c->entries[match.index].hidden;
-  *valid = c->entries[match.index].hidden_valid ? 1 : 0;
+  uint64_t id = 0;
+  if (int rc = match_id(c, match, &id)) return rc;
+  const CachedPrefix& e = *c->store.get(id);
+  *rows = e.hidden;
+  *valid = e.hidden_valid ? 1 : 0;
   return PRG_OK;
 }
 
 int prg_prefix_cache_set_entry_hidden(PrgPrefixCache* c, PrgPrefixMatch match, const uint16_t* rows) {
   PRG_CHECK_ARG(c && rows && c->model, "prg_prefix_cache_set_entry_hidden: bad argument");
-  if (int rc = check_match(c, match)) return rc;
-  PrefixEntry& e = c->entries[match.index];
-  if (int rc = ensure_hidden_capacity(c, e, match.len)) return rc;
+  uint64_t id = 0;
+  if (int rc = match_id(c, match, &id)) return rc;
+  CachedPrefix& e = *c->store.get(id);
+  PRG_CHECK_ARG(match.len <= e.reserved, "prg_prefix_cache_set_entry_hidden: %u rows > capacity %u", match.len,
+                e.reserved);
+  if (int rc = ensure_hidden_rows(c, e)) return rc;
   PRG_HIP(hipMemcpyAsync(e.hidden, rows, match.len * hidden_row_bytes(c), hipMemcpyDeviceToDevice, c->stream));
   PRG_HIP(hipStreamSynchronize(c->stream));
   e.hidden_valid = true;
@@ -991,10 +974,9 @@ int prg_prefix_cache_set_entry_hidden(PrgPrefixCache* c, PrgPrefixMatch match, c
 // save (prefix_persist.zig:253-328): temp file + rename.
 int prg_prefix_cache_save(const PrgPrefixCache* c, const char* path, uint64_t model_fingerprint) {
   PRG_CHECK_ARG(c && path && c->model, "prg_prefix_cache_save: bad argument");
-  const PrefixEntry* e = persisted_entry(c);
+  const CachedPrefix* e = persisted_entry(c);
   if (!e || e->tokens.empty()) return set_error(PRG_ERR_EMPTY_INPUT, "EmptyPrefix: nothing cached");
   const uint32_t T = static_cast<uint32_t>(e->tokens.size());
-  if (T > e->capacity) return set_error(PRG_ERR_SEQUENCE_TOO_LONG, "SequenceTooLong: %u > %u", T, e->capacity);
   const std::string final_path = path;
   if (int rc = make_parent_dirs(final_path)) return rc;
   const std::string tmp = final_path + ".tmp." + std::to_string(getpid());
@@ -1032,9 +1014,10 @@ int prg_prefix_cache_save(const PrgPrefixCache* c, const char* path, uint64_t mo
   return rc;
 }
 
-// load (prefix_persist.zig:334-412). A missing or invalid file leaves the
-// cache unchanged and reports *loaded_tokens = 0 (the reference returns null;
-// prg_last_error() says why); a failure while reading clears the cache.
+// load (prefix_persist.zig:334-412). A missing or invalid file (header,
+// length or tokens) leaves the cache unchanged and reports *loaded_tokens = 0
+// (the reference returns null; prg_last_error() says why); a failure while
+// reading the state sections clears the cache.
 int prg_prefix_cache_load(PrgPrefixCache* c, const char* path, uint64_t model_fingerprint, uint32_t* loaded_tokens) {
   PRG_CHECK_ARG(c && path && loaded_tokens && c->model, "prg_prefix_cache_load: bad argument");
   *loaded_tokens = 0;
@@ -1062,41 +1045,37 @@ int prg_prefix_cache_load(PrgPrefixCache* c, const char* path, uint64_t model_fi
   const uint32_t T = static_cast<uint32_t>(h.token_count);
   if (size != expected_file_bytes(c->model->cfg, T)) return ignore("file length");
 
-  // loadEntrySlot + finishLoadedEntry (prefix_state_cache.zig:663-690).
-  clear_all(c);
-  PrefixEntry e;
-  int rc = new_entry(c, static_cast<uint32_t>(std::max<uint64_t>(T, c->initial_state_tokens)), true, &e);
-  if (rc) return rc;
-  e.tokens.resize(T);
-  e.last_access = next_access(c);
-  c->entries.push_back(std::move(e));
-  PrefixEntry& ent = c->entries.back();
-  c->resident_tokens = T;
-  c->reserved_tokens = ent.capacity;
-  c->active = static_cast<int>(c->entries.size()) - 1;
-  if (c->track_hidden) rc = ensure_hidden_capacity(c, ent, T);
+  std::vector<uint32_t> tokens(T);
+  if (f.read_all(tokens.data(), sizeof(uint32_t) * T) != PRG_OK) return ignore("short token list");
+  for (uint32_t t : tokens)
+    if (t >= c->model->cfg.vocab) return ignore("token outside the vocab");
+
+  // The file replaces the cache's contents with one pinned entry
+  // (prefix_state_cache.zig:663-690), which becomes the active one.
+  drop_all(c);
+  uint64_t id = 0;
+  int rc = admit(c, tokens.data(), T, 0, true, &id);
   std::vector<uint8_t> host;
-  if (!rc) rc = f.read_all(ent.tokens.data(), sizeof(uint32_t) * T);
+  if (!rc) rc = read_state(f, c->store.get(id)->state, T, host);
   if (!rc) {
-    for (uint32_t t : ent.tokens)
-      if (t >= c->model->cfg.vocab) rc = set_error(PRG_ERR_INVALID_TOKEN, "persisted token %u >= vocab", t);
-  }
-  if (!rc) c->index.insert(ent.tokens.data(), T, c->active);
-  if (!rc) rc = read_state(f, ent.state, T, host);
-  if (!rc) {
+    CachedPrefix& ent = *c->store.get(id);
     ent.next_token = h.next_token;
     ent.next_valid = h.next_token_valid == 1;
     const size_t hb = static_cast<size_t>(T) * hidden_row_bytes(c);
     host.resize(hb);
     rc = f.read_all(host.data(), hb);
-    if (!rc && ent.hidden) {
-      const hipError_t err = hipMemcpy(ent.hidden, host.data(), hb, hipMemcpyHostToDevice);
-      if (err != hipSuccess) rc = set_error(PRG_ERR_HIP, "hidden rows: %s", hipGetErrorString(err));
+    if (!rc && c->track_hidden) {
+      rc = ensure_hidden_rows(c, ent);
+      if (!rc) {
+        const hipError_t err = hipMemcpy(ent.hidden, host.data(), hb, hipMemcpyHostToDevice);
+        if (err != hipSuccess) rc = set_error(PRG_ERR_HIP, "hidden rows: %s", hipGetErrorString(err));
+      }
       ent.hidden_valid = h.hidden_valid == 1;
     }
+    c->active = id;
   }
   if (rc) {
-    clear_all(c);
+    drop_all(c);
     return rc;
   }
   *loaded_tokens = T;

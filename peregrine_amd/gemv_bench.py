@@ -2,15 +2,18 @@
 
 Each shape is timed over a ring of distinct weight copies totalling >= 512 MiB
 (MI355X's Infinity Cache is 256 MiB), so every launch streams its weights from
-HBM. Per-launch kernel time comes from a HIP event pair around each launch;
-the median over >= 50 rotated launches is reported together with the
-algorithmic bytes (weights + scales + biases + x + outputs) and GB/s.
+HBM. One launch per ring copy is captured into a HIP graph and the graph is
+replayed; the per-launch time is the median over replays (each bracketed by
+HIP events on the graph's stream) divided by the ring length, so no host
+launch overhead enters, as in the decode loop. Reported with the algorithmic
+bytes (weights + scales + biases + x + outputs) and GB/s.
 """
 from __future__ import annotations
 
 import numpy as np
 
-from .device import DeviceArray, Event, synchronize
+from .device import DeviceArray, Stream, synchronize
+from .op_bench import time_graph
 from .ops import Q4Linear, argmax_pairs, gate_up_silu
 from .synth import random_bf16, random_q4
 
@@ -32,25 +35,17 @@ def _ring(rng, N: int, K: int, **kw) -> list[Q4Linear]:
     return ring
 
 
-def time_launches(fn, ring, iters: int = 60, warmup: int = 5) -> float:
-    """Median per-launch milliseconds of fn(lin) over the rotated ring."""
-    evs = [(Event(), Event()) for _ in range(iters)]
-    for i in range(warmup):
-        fn(ring[i % len(ring)])
-    synchronize()
-    for i, (a, b) in enumerate(evs):
-        a.record()
-        fn(ring[i % len(ring)])
-        b.record()
-    synchronize()
-    ms = [a.elapsed_ms(b) for a, b in evs]
-    for a, b in evs:
-        a.close()
-        b.close()
-    return float(np.median(ms))
+def time_launches(fn, ring, reps: int = 10) -> float:
+    """Milliseconds per launch of fn(item, stream) over the rotated ring, from
+    graph replays (at least 50 launches in total)."""
+    st = Stream()
+    reps = max(reps, -(-50 // len(ring)))
+    ms = time_graph(st, lambda: [fn(item, st.handle) for item in ring], reps) / len(ring)
+    st.close()
+    return ms
 
 
-def sweep(shapes=None, Ms=(1, 2), seed: int = 0, iters: int = 60) -> list[dict]:
+def sweep(shapes=None, Ms=(1, 2), seed: int = 0, reps: int = 10) -> list[dict]:
     rng = np.random.default_rng(seed)
     shapes = shapes or [(12288, 4096), (4096, 12288), (4096, 4096), (248320, 4096)]
     rows = []
@@ -64,20 +59,22 @@ def sweep(shapes=None, Ms=(1, 2), seed: int = 0, iters: int = 60) -> list[dict]:
                 pv = [DeviceArray((P,), np.float32) for _ in range(M)]
                 pi = [DeviceArray((P,), np.uint32) for _ in range(M)]
                 if M == 1:
-                    fn = lambda lin: lin.encode_bf16_argmax_partial(x[0], pv[0], pi[0])
+                    fn = lambda lin, s: lin.encode_bf16_argmax_partial(x[0], pv[0], pi[0], stream=s)
                 else:
-                    fn = lambda lin: lin.encode_bf16_argmax_partial2(x[0], x[1], pv[0], pi[0], pv[1], pi[1])
+                    fn = lambda lin, s: lin.encode_bf16_argmax_partial2(x[0], x[1], pv[0], pi[0], pv[1], pi[1],
+                                                                        stream=s)
                 out_bytes = M * P * 8
             else:
                 y = DeviceArray((M, N), np.uint16)
                 xx = DeviceArray.from_numpy(random_bf16(rng, (M, K)))
-                fn = lambda lin: lin.encode_bf16_fast(xx, y, token_count=M)
+                fn = lambda lin, s: lin.encode_bf16_fast(xx, y, token_count=M, stream=s)
                 out_bytes = M * N * 2
-            ms = time_launches(fn, ring, iters=iters)
+            ms = time_launches(fn, ring, reps=reps)
             algo = q4_bytes(N, K) + M * K * 2 + out_bytes
             gbs = algo / (ms * 1e-3) / 1e9
             rows.append({"kernel": "lm_head_argmax" if lm_head else "q4_gemv", "N": N, "K": K, "M": M,
-                         "us": ms * 1e3, "algo_bytes": algo, "GBps": gbs, "frac_peak": gbs / HBM_PEAK_GBS})
+                         "us": ms * 1e3, "algo_bytes": algo, "GBps": gbs, "frac_peak": gbs / HBM_PEAK_GBS,
+                         "ring": len(ring)})
             if lm_head:
                 o = DeviceArray((1,), np.uint32)
                 argmax_pairs(pv[0], pi[0], o, N // 8)
@@ -88,7 +85,7 @@ def sweep(shapes=None, Ms=(1, 2), seed: int = 0, iters: int = 60) -> list[dict]:
     return rows
 
 
-def silu_sweep(seed: int = 1, iters: int = 60) -> dict:
+def silu_sweep(seed: int = 1, reps: int = 10) -> dict:
     rng = np.random.default_rng(seed)
     N, K = 12288, 4096
     one_g, one_u = random_q4(rng, N, K), random_q4(rng, N, K)
@@ -96,7 +93,7 @@ def silu_sweep(seed: int = 1, iters: int = 60) -> dict:
     ring = [(Q4Linear.upload(one_g), Q4Linear.upload(one_u)) for _ in range(copies)]
     x = DeviceArray.from_numpy(random_bf16(rng, (1, K)))
     out = DeviceArray((1, N), np.uint16)
-    ms = time_launches(lambda gu: gate_up_silu(gu[0], gu[1], x, out), ring, iters=iters)
+    ms = time_launches(lambda gu, s: gate_up_silu(gu[0], gu[1], x, out, stream=s), ring, reps=reps)
     algo = 2 * q4_bytes(N, K) + K * 2 + N * 2
     gbs = algo / (ms * 1e-3) / 1e9
     return {"kernel": "q4_gemv_silu_gate", "N": N, "K": K, "M": 1, "us": ms * 1e3, "algo_bytes": algo,

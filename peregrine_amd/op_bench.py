@@ -13,9 +13,9 @@
   split-context attention with its gated merge (prg_attn_decode_bf16), alone
   and as 8 stacked layers with distinct caches, rotated the same way.
 
-Each case is captured once into a HIP graph on its own stream and replayed
-between two HIP events; times are per layer (or per stack) with no host
-launch overhead. Inputs are synthetic and seeded.
+Each case is captured once into a HIP graph on its own stream and replayed;
+times are the median over replays bracketed by HIP events, per layer (or per
+stack), with no host launch overhead. Inputs are synthetic and seeded.
 """
 from __future__ import annotations
 
@@ -31,8 +31,9 @@ HBM_PEAK_GBS = 8000.0
 ROTATE_BYTES = 512 * 1024 * 1024
 
 
-def _time_graph(stream: Stream, issue, reps: int) -> float:
-    """Milliseconds per replay of the graph of issue()."""
+def time_graph(stream: Stream, issue, reps: int) -> float:
+    """Milliseconds per replay of the graph of issue(): the median over
+    `reps` replays, each bracketed by its own pair of HIP events on `stream`."""
     issue()  # eager first pass: kernel selection outside the capture
     stream.synchronize()
     with Graph.capture(stream) as g:
@@ -40,15 +41,16 @@ def _time_graph(stream: Stream, issue, reps: int) -> float:
     for _ in range(2):
         g.launch()
     stream.synchronize()
-    a, b = Event(), Event()
-    a.record(C.c_void_p(stream.handle))
-    for _ in range(reps):
+    evs = [(Event(), Event()) for _ in range(reps)]
+    for a, b in evs:
+        a.record(C.c_void_p(stream.handle))
         g.launch()
-    b.record(C.c_void_p(stream.handle))
+        b.record(C.c_void_p(stream.handle))
     stream.synchronize()
-    ms = a.elapsed_ms(b) / reps
-    for x in (a, b):
-        x.close()
+    ms = float(np.median([a.elapsed_ms(b) for a, b in evs]))
+    for a, b in evs:
+        a.close()
+        b.close()
     g.close()
     return ms
 
@@ -89,7 +91,7 @@ def gdn_layers(layers: int = 24, seed: int = 3, reps: int = 20, fused_norm: bool
                 ops.gated_delta_decode(ly["S"], ly["c"], a, b, A_log, dt, ly["y"], stream=st.handle)
                 ops.rmsnorm_gated(ly["y"], nw, ly["z"], ly["o"], stream=st.handle)
 
-    ms = _time_graph(st, issue, reps) / sets
+    ms = time_graph(st, issue, reps) / sets
     st.close()
     for ly in L:
         for v in ly.values():
@@ -130,7 +132,7 @@ def attention(L: int, layers: int = 1, seed: int = 4, reps: int = 20) -> dict:
             ops.attn_decode_prepare(pq, qw, q, gate, kin, vin, kw, kc, vc, stride, pos, pos, stream=st.handle)
             ops.attn_decode(q, kc, vc, gate, out, part, stride, L, stream=st.handle)
 
-    ms = _time_graph(st, issue, reps) / sets
+    ms = time_graph(st, issue, reps) / sets
     st.close()
     for kc, vc in caches:
         kc.close()

@@ -227,3 +227,36 @@ def test_state_calls_need_a_model():
         c.entry_state_handle(m.index)
     with pytest.raises(PrgError):
         c.save("/tmp/never-written.bin", 1)
+
+
+def test_index_matches_brute_force_under_random_operations():
+    """The hash-and-length index against a brute-force scan of the live
+    entries: longest cached prefix, exact containment, creation-order
+    numbering across removals and evictions, and the budget invariant."""
+    rng = np.random.default_rng(0)
+    c = PrefixCache(None, 64, 4)
+    for step in range(400):
+        op = rng.integers(0, 10)
+        if op < 6:  # cache a prefix drawn from a small alphabet (shared prefixes, repeats)
+            n = int(rng.integers(1, 9))
+            toks = rng.integers(0, 3, size=n).tolist()
+            try:
+                _add(c, toks, bool(rng.integers(0, 8) == 0), int(rng.integers(0, 100)))
+            except Exception:
+                pass  # budget exhausted by pinned entries
+        elif op < 8 and c.entry_count():
+            c.remove(int(rng.integers(0, c.entry_count())))
+        live = [c.entry_tokens(i).tolist() for i in range(c.entry_count())]
+        assert len({tuple(t) for t in live}) == len(live), "one entry per exact prefix"
+        s = c.stats()
+        assert s["reserved_tokens"] <= 64
+        assert s["resident_tokens"] == sum(len(t) for t in live)
+        prompt = rng.integers(0, 3, size=int(rng.integers(0, 12))).tolist()
+        best = max((i for i, t in enumerate(live) if t == prompt[:len(t)]), key=lambda i: len(live[i]), default=None)
+        m = c.find(prompt)
+        if best is None:
+            assert m is None
+        else:
+            assert m is not None and (m.index, m.len) == (best, len(live[best])), step
+        for k in range(len(prompt) + 1):
+            assert c.contains(prompt, k) == (k == 0 or prompt[:k] in live)
