@@ -304,6 +304,23 @@ int prg_attn_decode_bf16(void *stream, const uint16_t *q, const uint16_t *key_ca
                          float scale);
 size_t prg_attn_decode_partials_bytes(uint32_t cache_stride_tokens);
 
+/* One decode step of a full-attention layer from the raw projections of the
+ * new token: packed_q [16, 512] (q | gate per head), k_input / v_input
+ * [4, 256]. Attends over the cached slots [0, cache_pos) plus the new token
+ * (its q and k RMSNormed with q_weight / k_weight, partial RoPE at rope_pos),
+ * writes out = bf16(softmax(scale q.K^T) V * sigmoid(gate)) [16, 256] and
+ * appends the new K / V at cache_pos. workspace: device memory of
+ * prg_attn_decode_step_workspace_bytes(stride). Two launches (split partials
+ * over the cache with q prepared in-kernel, then the merge that adds the new
+ * token and appends it). Replaces prepare + partials + merge of
+ * FullAttentionBlock.decodeStepBf16 (block_attn.zig:321-358;
+ * attention.metal:327-421, attention_decode.metal:24-243). */
+int prg_attn_decode_step_bf16(void *stream, const uint16_t *packed_q, const uint16_t *q_weight,
+                              const uint16_t *k_input, const uint16_t *v_input, const uint16_t *k_weight,
+                              uint16_t *key_cache, uint16_t *value_cache, uint16_t *out, void *workspace,
+                              uint32_t cache_stride_tokens, uint32_t cache_pos, uint32_t rope_pos, float scale);
+size_t prg_attn_decode_step_workspace_bytes(uint32_t cache_stride_tokens);
+
 /* prg_attn_decode_bf16 without the partials argument, for callers that cannot
  * allocate (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc). No counterpart in the reference. It allocates nothing:

@@ -51,6 +51,28 @@ __device__ inline float row16_sum(float v) {
   v = dpp_add<0x140>(v);  // row_mirror
   return v;
 }
+template <int CTRL>
+__device__ inline float dpp_max(float v) {
+  return fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF,
+                                                                          false)));
+}
+// Max / sum over all 64 lanes (every lane gets the result): DPP within each
+// 16-lane row, then the 4 row values by readlane.
+__device__ inline float wave_max_dpp(float v) {
+  v = dpp_max<0x141>(dpp_max<0x140>(dpp_max<0x4E>(dpp_max<0xB1>(v))));
+  const int x = __builtin_bit_cast(int, v);
+  return fmaxf(fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(x, 0)),
+                     __builtin_bit_cast(float, __builtin_amdgcn_readlane(x, 16))),
+               fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(x, 32)),
+                     __builtin_bit_cast(float, __builtin_amdgcn_readlane(x, 48))));
+}
+__device__ inline float wave_sum_dpp(float v) {
+  const int x = __builtin_bit_cast(int, row16_sum(v));
+  return (__builtin_bit_cast(float, __builtin_amdgcn_readlane(x, 0)) +
+          __builtin_bit_cast(float, __builtin_amdgcn_readlane(x, 16))) +
+         (__builtin_bit_cast(float, __builtin_amdgcn_readlane(x, 32)) +
+          __builtin_bit_cast(float, __builtin_amdgcn_readlane(x, 48)));
+}
 // Sum over each aligned group of 8 lanes.
 __device__ inline float row8_sum(float v) {
   v = dpp_add<0xB1>(v);
@@ -129,37 +151,118 @@ __device__ inline AttnDecodeArgs attn_row_args(const AttnDecodeArgs& a0, uint32_
     a.out += r * (kAttnQHeads * kAttnHeadDim);
     a.partials += static_cast<size_t>(r) * kAttnQHeads * a.nsplit * kAttnPartialStride;
     a.step += r;
+    if (a.packed_q) a.packed_q += r * (2 * kAttnQHeads * kAttnHeadDim);
   }
   return a;
 }
 
+// Tokens the partials cover: all seq_len cached tokens, or, in the
+// decode-step form, those before the first new token.
+__device__ inline uint32_t attn_cached_tokens(const AttnDecodeArgs& a0) {
+  const uint32_t L = a0.step ? a0.step->seq_len : a0.seq_len_host;
+  return min(a0.packed_q ? L - 1 : L, a0.stride);
+}
+
+// Sum over the 256 threads of a block for 4 values at once (one per head);
+// every thread gets the 4 totals. red: LDS [4 waves][4]. Lanes of a 16-lane
+// row are combined with DPP, the 4 rows with readlane.
+__device__ inline void block_sum4(float (&v)[4], float* red) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int x = __builtin_bit_cast(int, row16_sum(v[g]));
+    const float s = (__builtin_bit_cast(float, __builtin_amdgcn_readlane(x, 0)) +
+                     __builtin_bit_cast(float, __builtin_amdgcn_readlane(x, 16))) +
+                    (__builtin_bit_cast(float, __builtin_amdgcn_readlane(x, 32)) +
+                     __builtin_bit_cast(float, __builtin_amdgcn_readlane(x, 48)));
+    if (lane == 0) red[w * 4 + g] = s;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int g = 0; g < 4; ++g) v[g] = (red[g] + red[4 + g]) + (red[8 + g] + red[12 + g]);
+}
+
+// Normalise + rotate the NH heads x[h] (dim = threadIdx.x of 256) with RMSNorm
+// weight w and partial NeoX RoPE at pos (dims [0, 64), pairs i, i + 32; normed
+// values rounded to bf16 before the rotation, attention.metal:391-392), as the
+// prepare kernel does per dim. The bf16 results go to out[h][256] in LDS.
+template <int NH>
+__device__ inline void norm_rope_heads(const float (&x)[4], float wt, uint32_t pos, float* red, float* xch,
+                                       uint16_t* out) {
+  const uint32_t col = threadIdx.x;
+  float ss[4];
+#pragma unroll
+  for (int h = 0; h < 4; ++h) ss[h] = h < NH ? x[h] * x[h] : 0.0f;
+  block_sum4(ss, red);
+  constexpr uint32_t half = kAttnRotary / 2;
+  float c = 1.0f, sn = 0.0f;
+  if (col < kAttnRotary) {
+    const uint32_t i = col & (half - 1);
+    const float inv_freq = powf(kAttnTheta, -(2.0f * static_cast<float>(i)) / static_cast<float>(kAttnRotary));
+    const float angle = static_cast<float>(pos) * inv_freq;
+    c = cosf(angle);
+    sn = sinf(angle);
+  }
+  float n[4];
+#pragma unroll
+  for (int h = 0; h < NH; ++h) {
+    const float inv_rms = rsqrtf(ss[h] / static_cast<float>(kAttnHeadDim) + kAttnEps);
+    n[h] = x[h] * inv_rms * wt;
+    if (col < kAttnRotary) {
+      n[h] = round_bf(n[h]);
+      xch[h * kAttnRotary + col] = n[h];
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int h = 0; h < NH; ++h) {
+    float o = n[h];
+    if (col < half)
+      o = n[h] * c - xch[h * kAttnRotary + col + half] * sn;
+    else if (col < kAttnRotary)
+      o = n[h] * c + xch[h * kAttnRotary + col - half] * sn;
+    out[h * kAttnHeadDim + col] = f2bf(o);
+  }
+}
+
 __global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnDecodeArgs a0) {
-  extern __shared__ float sc[];  // [4][split_tokens] scores, then probabilities
+  extern __shared__ float sc[];  // [4][split_tokens + 2] scores, then probabilities
   __shared__ float mh[kAttnGroup], lh[kAttnGroup];
-  const AttnDecodeArgs a = attn_row_args(a0, blockIdx.z);
+  // decode-step form: prepared q of the group's 4 heads, new tokens' k and v
+  __shared__ uint16_t qf[kAttnGroup * kAttnHeadDim];
+  __shared__ uint16_t kf[2 * kAttnHeadDim], vf[2 * kAttnHeadDim];
+  __shared__ float red[16], xch[kAttnGroup * kAttnRotary];
+  const uint32_t row = blockIdx.z;
+  const AttnDecodeArgs a = attn_row_args(a0, row);
 
   const uint32_t kvh = blockIdx.y;
   const uint32_t split = blockIdx.x;
-  const uint32_t L = min(a.step ? a.step->seq_len : a.seq_len_host, a.stride);
+  const uint32_t L = attn_cached_tokens(a0);
   uint32_t chunk = (L + a.nsplit - 1) / a.nsplit;
   chunk = (chunk + kAttnChunkAlign - 1) & ~(kAttnChunkAlign - 1);
-  const uint32_t t0 = split * chunk;
+  const uint32_t t0 = min(split * chunk, L);
   const uint32_t t1 = min(t0 + chunk, L);
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   float* part = a.partials + (static_cast<size_t>(kvh) * kAttnGroup * a.nsplit + split) * kAttnPartialStride;
   const size_t head_stride = static_cast<size_t>(a.nsplit) * kAttnPartialStride;
+  // In the decode-step form the new tokens of rows 0..row are extra tokens of
+  // the split that holds the last cached token (split 0 on an empty cache).
+  const bool fresh = a.packed_q != nullptr;
+  const uint32_t last = L == 0 ? 0u : (L - 1) / chunk;
+  const uint32_t nx = (fresh && split == last) ? row + 1 : 0u;
 
-  if (t0 >= t1) {  // empty range: neutral partial
+  if (t0 >= t1 && nx == 0) {  // empty range: neutral partial
     for (uint32_t i = threadIdx.x; i < kAttnGroup * kAttnPartialStride; i += kAttnThreads) {
       const uint32_t g = i / kAttnPartialStride, k = i % kAttnPartialStride;
       part[g * head_stride + k] = (k == 0) ? -INFINITY : 0.0f;
     }
     return;
   }
-  const uint32_t T = t1 - t0;
-  const uint32_t ld = a.split_tokens;
+  const uint32_t T = t1 - t0;  // cached tokens of this split
+  const uint32_t TX = T + nx;  // plus the new tokens
+  const uint32_t ld = a.split_tokens + 2;
   // A range of <= 64 tokens (every split of a cache up to 4096 tokens) issues
-  // all of its q, K and V loads before any arithmetic: one memory round trip.
+  // all of its K and V loads before any arithmetic: one memory round trip.
   const bool one_tile = T <= 64;
   const int jd = lane & 15, r = lane >> 4;
   const int rr = lane >> 3, ts = lane & 7;
@@ -184,15 +287,58 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnD
     }
   }
 
-  // ---- phase 1: scores. lane -> (token row r = lane/16, dims 16*jd .. +16)
+  // ---- decode-step form: q of the group's 4 heads (one dim per thread, as
+  // the prepare kernel computes it) and, in the split that takes them, the
+  // new tokens' k (normalised + rotated) and v, appended to the cache by the
+  // block of their own row.
   uint32_t qd[kAttnGroup][8];
+  if (fresh) {
+    const uint32_t col = threadIdx.x;
+    float xq[4];
 #pragma unroll
-  for (int g = 0; g < static_cast<int>(kAttnGroup); ++g) {
-    const uint4* qp = reinterpret_cast<const uint4*>(a.q + (static_cast<size_t>(kvh) * kAttnGroup + g) * kAttnHeadDim + 16 * jd);
-    const uint4 q0 = qp[0], q1 = qp[1];
-    qd[g][0] = q0.x; qd[g][1] = q0.y; qd[g][2] = q0.z; qd[g][3] = q0.w;
-    qd[g][4] = q1.x; qd[g][5] = q1.y; qd[g][6] = q1.z; qd[g][7] = q1.w;
+    for (int g = 0; g < static_cast<int>(kAttnGroup); ++g)
+      xq[g] = bf2f(a.packed_q[(static_cast<size_t>(kvh) * kAttnGroup + g) * 2 * kAttnHeadDim + col]);
+    const float wq = bf2f(a.q_norm[col]);
+    float xk[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    uint16_t vb[2] = {0, 0};
+    for (uint32_t j = 0; j < nx; ++j) {
+      xk[j] = bf2f(a0.k_in[(static_cast<size_t>(j) * kAttnKvHeads + kvh) * kAttnHeadDim + col]);
+      vb[j] = a0.v_in[(static_cast<size_t>(j) * kAttnKvHeads + kvh) * kAttnHeadDim + col];
+    }
+    const float wk = nx ? bf2f(a0.k_norm[col]) : 0.0f;
+    norm_rope_heads<kAttnGroup>(xq, wq, a.step ? a.step->rope_pos : a.rope_pos_host, red, xch, qf);
+    for (uint32_t j = 0; j < nx; ++j) {
+      __syncthreads();  // red / xch reuse
+      const float xj[4] = {xk[j], 0.0f, 0.0f, 0.0f};
+      const uint32_t pos = a0.step ? a0.step[j].rope_pos : a0.rope_pos_host + j;
+      norm_rope_heads<1>(xj, wk, pos, red, xch, kf + j * kAttnHeadDim);
+      vf[j * kAttnHeadDim + col] = vb[j];
+      const uint32_t cpos = a0.step ? a0.step[j].cache_pos : a0.cache_pos_host + j;
+      if (j == row && cpos < a.stride) {
+        a.key_cache_w[(static_cast<size_t>(kvh) * a.stride + cpos) * kAttnHeadDim + col] = kf[j * kAttnHeadDim + col];
+        a.value_cache_w[(static_cast<size_t>(kvh) * kAttnHeadDim + col) * a.stride + cpos] = vb[j];
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < static_cast<int>(kAttnGroup); ++g) {
+      const uint4* qp = reinterpret_cast<const uint4*>(qf + g * kAttnHeadDim + 16 * jd);
+      const uint4 q0 = qp[0], q1 = qp[1];
+      qd[g][0] = q0.x; qd[g][1] = q0.y; qd[g][2] = q0.z; qd[g][3] = q0.w;
+      qd[g][4] = q1.x; qd[g][5] = q1.y; qd[g][6] = q1.z; qd[g][7] = q1.w;
+    }
+  } else {
+#pragma unroll
+    for (int g = 0; g < static_cast<int>(kAttnGroup); ++g) {
+      const uint4* qp =
+          reinterpret_cast<const uint4*>(a.q + (static_cast<size_t>(kvh) * kAttnGroup + g) * kAttnHeadDim + 16 * jd);
+      const uint4 q0 = qp[0], q1 = qp[1];
+      qd[g][0] = q0.x; qd[g][1] = q0.y; qd[g][2] = q0.z; qd[g][3] = q0.w;
+      qd[g][4] = q1.x; qd[g][5] = q1.y; qd[g][6] = q1.z; qd[g][7] = q1.w;
+    }
   }
+
+  // ---- phase 1: scores. lane -> (token row r = lane/16, dims 16*jd .. +16)
   auto score = [&](uint32_t tt, uint4 k0, uint4 k1, bool valid) {
     const uint32_t kd[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
     float s[kAttnGroup];
@@ -235,6 +381,11 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnD
       score(tt, kp[0], kp[1], true);
     }
   }
+  // the new tokens: 16-lane row j of wave 0 scores token T + j
+  if (nx > 0 && w == 0 && static_cast<uint32_t>(r) < nx) {
+    const uint4* kp = reinterpret_cast<const uint4*>(kf + r * kAttnHeadDim + 16 * jd);
+    score(T + r, kp[0], kp[1], true);
+  }
   // The first two 64-token V tiles do not depend on the softmax: their loads
   // are issued here, so they stream in while phase 2 runs.
   const bool vpre = !one_tile && T >= 128;
@@ -254,18 +405,16 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnD
   {
     const int g = w;
     float m = -INFINITY;
-    for (uint32_t t = lane; t < T; t += 64) m = fmaxf(m, sc[g * ld + t]);
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    for (uint32_t t = lane; t < TX; t += 64) m = fmaxf(m, sc[g * ld + t]);
+    m = wave_max_dpp(m);
     float l = 0.0f;
-    for (uint32_t t = lane; t < T; t += 64) {
+    for (uint32_t t = lane; t < TX; t += 64) {
       const float s = sc[g * ld + t];
       const float p = (s == -INFINITY) ? 0.0f : expf(s - m);
       sc[g * ld + t] = p;
       l += p;
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o, 64);
+    l = wave_sum_dpp(l);
     if (lane == 0) {
       mh[g] = m;
       lh[g] = l;
@@ -346,6 +495,16 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnD
         for (int i = 0; i < 8; ++i) acc[p][g] += pv[g][i] * v8[i];
     }
   }
+  if (nx > 0 && ts == 0) {  // the new tokens' values, once per dim
+    for (uint32_t j = 0; j < nx; ++j) {
+#pragma unroll
+      for (int p = 0; p < 8; ++p) {
+        const float vv = bf2f(vf[j * kAttnHeadDim + 64 * w + 8 * p + rr]);
+#pragma unroll
+        for (int g = 0; g < static_cast<int>(kAttnGroup); ++g) acc[p][g] += sc[g * ld + T + j] * vv;
+      }
+    }
+  }
 #pragma unroll
   for (int p = 0; p < 8; ++p)
 #pragma unroll
@@ -364,48 +523,51 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnD
   }
 }
 
-// ------------------------------------------------------------------- reduce --
-// One block per q head, one thread per dim. The split statistics (m, denom)
-// are merged in parallel first (weights in LDS), then each thread sums its
-// dim over the splits with independent loads.
+// -------------------------------------------------------------------- merge --
+// Block (head h, quarter qt, row r) of 64 threads; thread t owns output dim
+// d = 64 qt + t. The split statistics (m, denom) are merged first (weights
+// in LDS), then each thread sums its dim over the splits with independent
+// loads, and applies the sigmoid gate (from packed q in the decode-step form).
 constexpr uint32_t kMaxSplits = 1024;
+constexpr int kMergeThreads = 64;
 
-__global__ __launch_bounds__(kAttnThreads) void attn_reduce_kernel(const AttnDecodeArgs a0) {
+
+__global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(const AttnDecodeArgs a0) {
   __shared__ float wsh[kMaxSplits];
-  __shared__ float red[kAttnThreads / kWave];
-  const AttnDecodeArgs a = attn_row_args(a0, blockIdx.y);
-  const uint32_t h = blockIdx.x;  // q head
-  const uint32_t t = threadIdx.x;
+  const uint32_t row = blockIdx.z;
+  const AttnDecodeArgs a = attn_row_args(a0, row);
+  const uint32_t h = blockIdx.x, qt = blockIdx.y, t = threadIdx.x;
+  const uint32_t d = 64 * qt + t;
+  const bool fresh = a0.packed_q != nullptr;
   const float* base = a.partials + static_cast<size_t>(h) * a.nsplit * kAttnPartialStride;
-  // Only splits that hold tokens carry weight (the others are neutral), and
-  // for a short cache their accumulators are loaded up front, together with
-  // the statistics: one memory round trip.
-  const uint32_t L = min(a.step ? a.step->seq_len : a.seq_len_host, a.stride);
-  uint32_t chunk = (L + a.nsplit - 1) / a.nsplit;
-  chunk = (chunk + kAttnChunkAlign - 1) & ~(kAttnChunkAlign - 1);
-  const uint32_t nact = min(a.nsplit, (L + chunk - 1) / chunk);
-  const uint32_t d = t;
+  const uint32_t L = attn_cached_tokens(a0);
+  // splits holding tokens (on an empty cache, split 0 holds the new tokens)
+  uint32_t nact = fresh ? 1u : 0u;
+  if (L > 0) {
+    uint32_t chunk = (L + a.nsplit - 1) / a.nsplit;
+    chunk = (chunk + kAttnChunkAlign - 1) & ~(kAttnChunkAlign - 1);
+    nact = min(a.nsplit, (L + chunk - 1) / chunk);
+  }
+  // accumulators of a short cache are loaded up front with the statistics
   constexpr uint32_t kPre = 64;
   float pre[kPre];
 #pragma unroll
   for (uint32_t c = 0; c < kPre; ++c) pre[c] = c < nact ? base[c * kAttnPartialStride + 2 + d] : 0.0f;
+  const uint16_t gbits = fresh ? a.packed_q[static_cast<size_t>(h) * 2 * kAttnHeadDim + kAttnHeadDim + d]
+                               : a.gate[static_cast<size_t>(h) * kAttnHeadDim + d];
   float m_local = -INFINITY;
-  for (uint32_t c = t; c < nact; c += kAttnThreads) m_local = fmaxf(m_local, base[c * kAttnPartialStride]);
-  m_local = wave_max(m_local);
-  if ((t & 63) == 0) red[t >> 6] = m_local;
-  __syncthreads();
-  float m_all = red[0];
-#pragma unroll
-  for (int i = 1; i < kAttnThreads / kWave; ++i) m_all = fmaxf(m_all, red[i]);
-  __syncthreads();
+  for (uint32_t c = t; c < nact; c += kMergeThreads) m_local = fmaxf(m_local, base[c * kAttnPartialStride]);
+
+  const float m_all = wave_max_dpp(m_local);
   float den_local = 0.0f;
-  for (uint32_t c = t; c < nact; c += kAttnThreads) {
+  for (uint32_t c = t; c < nact; c += kMergeThreads) {
     const float mc = base[c * kAttnPartialStride];
     const float wgt = (mc == -INFINITY) ? 0.0f : expf(mc - m_all);
     wsh[c] = wgt;
     den_local += base[c * kAttnPartialStride + 1] * wgt;
   }
-  const float den = block_sum<kAttnThreads>(den_local, red);  // also orders the wsh writes
+  const float den = wave_sum_dpp(den_local);
+  __syncthreads();  // wsh
   float acc = 0.0f;
 #pragma unroll
   for (uint32_t c = 0; c < kPre; ++c)
@@ -413,7 +575,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_reduce_kernel(const AttnDec
 #pragma unroll 8
   for (uint32_t c = kPre; c < nact; ++c) acc += base[c * kAttnPartialStride + 2 + d] * wsh[c];
   const size_t i = static_cast<size_t>(h) * kAttnHeadDim + d;
-  const float sig = 1.0f / (1.0f + expf(-bf2f(a.gate[i])));
+  const float sig = 1.0f / (1.0f + expf(-bf2f(gbits)));
   a.out[i] = f2bf((acc / den) * sig);
 }
 
@@ -432,10 +594,22 @@ static uint32_t attn_max_split_tokens() {
   return v;
 }
 
+// Fewest splits per kv head; PEREGRINE_ATTN_MIN_SPLITS (a power of two,
+// 16..256) overrides it for tuning.
+static uint32_t attn_min_splits() {
+  static const uint32_t v = [] {
+    const char* e = getenv("PEREGRINE_ATTN_MIN_SPLITS");
+    const long t = e ? atol(e) : 0;
+    return (t >= 16 && t <= 256 && (t & (t - 1)) == 0) ? static_cast<uint32_t>(t) : 64u;
+  }();
+  return v;
+}
+
 uint32_t attn_num_splits(uint32_t capacity) {
-  // >= 64 splits per kv head (256 blocks) and <= attn_max_split_tokens() per split.
+  // >= attn_min_splits() splits per kv head (256 blocks by default) and
+  // <= attn_max_split_tokens() per split.
   const uint32_t cap = attn_max_split_tokens();
-  uint32_t n = 64;
+  uint32_t n = attn_min_splits();
   while ((capacity + n - 1) / n > cap && n < kMaxSplits) n *= 2;
   return n;
 }
@@ -456,11 +630,14 @@ int launch_attn_prepare(hipStream_t s, const AttnPrepareArgs& a) {
 int launch_attn_decode(hipStream_t s, const AttnDecodeArgs& a) {
   if (a.rows < 1 || a.rows > 2 || (a.rows == 2 && a.step == nullptr))
     return set_error(PRG_ERR_INVALID_ARG, "attn_decode: rows %u (two rows need device step scalars)", a.rows);
-  const size_t lds = static_cast<size_t>(kAttnGroup) * a.split_tokens * sizeof(float);
+  if (a.packed_q && !(a.q_norm && a.k_in && a.v_in && a.k_norm && a.key_cache_w && a.value_cache_w))
+    return set_error(PRG_ERR_INVALID_ARG, "attn_decode: the decode-step form needs every input");
+  const size_t lds = static_cast<size_t>(kAttnGroup) * (a.split_tokens + 2) * sizeof(float);
   hipLaunchKernelGGL(attn_partials_kernel, dim3(a.nsplit, kAttnKvHeads, a.rows), dim3(kAttnThreads), lds, s, a);
   PRG_CHECK_LAUNCH("attn_partials");
-  hipLaunchKernelGGL(attn_reduce_kernel, dim3(kAttnQHeads, a.rows), dim3(kAttnHeadDim), 0, s, a);
-  PRG_CHECK_LAUNCH("attn_reduce");
+  hipLaunchKernelGGL(attn_merge_kernel, dim3(kAttnQHeads, kAttnHeadDim / kMergeThreads, a.rows), dim3(kMergeThreads),
+                     0, s, a);
+  PRG_CHECK_LAUNCH("attn_merge");
   return PRG_OK;
 }
 
@@ -579,6 +756,41 @@ int prg_attn_decode_noalloc_bf16(void* stream, const uint16_t* q, const uint16_t
 size_t prg_attn_decode_partials_bytes(uint32_t cache_stride_tokens) {
   const uint32_t n = prg::attn_num_splits(cache_stride_tokens);
   return static_cast<size_t>(prg::kAttnQHeads) * n * prg::kAttnPartialStride * sizeof(float);
+}
+
+size_t prg_attn_decode_step_workspace_bytes(uint32_t cache_stride_tokens) {
+  return prg_attn_decode_partials_bytes(cache_stride_tokens);
+}
+
+int prg_attn_decode_step_bf16(void* stream, const uint16_t* packed_q, const uint16_t* q_weight,
+                              const uint16_t* k_input, const uint16_t* v_input, const uint16_t* k_weight,
+                              uint16_t* key_cache, uint16_t* value_cache, uint16_t* out, void* workspace,
+                              uint32_t cache_stride_tokens, uint32_t cache_pos, uint32_t rope_pos, float scale) {
+  const char* name = "prg_attn_decode_step_bf16";
+  PRG_CHECK_ARG(packed_q && q_weight && k_input && v_input && k_weight && key_cache && value_cache && out && workspace,
+                "%s: null pointer", name);
+  PRG_CHECK_ARG(cache_stride_tokens % 64 == 0, "%s: stride %u must be a multiple of 64", name, cache_stride_tokens);
+  if (cache_pos >= cache_stride_tokens)
+    return prg::set_error(PRG_ERR_SEQUENCE_TOO_LONG, "%s: cache_pos %u >= stride %u", name, cache_pos,
+                          cache_stride_tokens);
+  prg::AttnDecodeArgs a{};
+  a.partials = static_cast<float*>(workspace);
+  a.key_cache = a.key_cache_w = key_cache;
+  a.value_cache = a.value_cache_w = value_cache;
+  a.out = out;
+  a.stride = cache_stride_tokens;
+  a.nsplit = prg::attn_num_splits(cache_stride_tokens);
+  a.split_tokens = prg::attn_split_tokens(cache_stride_tokens, a.nsplit);
+  a.seq_len_host = cache_pos + 1;
+  a.cache_pos_host = cache_pos;
+  a.rope_pos_host = rope_pos;
+  a.scale = scale;
+  a.packed_q = packed_q;
+  a.q_norm = q_weight;
+  a.k_in = k_input;
+  a.v_in = v_input;
+  a.k_norm = k_weight;
+  return prg::launch_attn_decode(prg::as_stream(stream), a);
 }
 
 }  // extern "C"

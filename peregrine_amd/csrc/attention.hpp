@@ -65,6 +65,24 @@ struct AttnDecodeArgs {
   // Consecutive tokens handled by one launch (1 or 2; 2 needs step). Query r
   // uses q / gate / out + r*4096, partials + r*16*nsplit*258 and step[r].
   uint32_t rows = 1;
+  // Decode-step form (packed_q != nullptr): the inputs are the raw q | gate,
+  // k and v projections of the `rows` new tokens, not yet in the cache. The
+  // partials cover the cached tokens [0, step[0].seq_len - 1) and normalise +
+  // rotate q themselves; the split holding the last cached token (split 0 on
+  // an empty cache) also prepares the new tokens' k / v and attends to them
+  // as extra tokens (row r to rows 0..r), and the block of each row appends
+  // that row's K / V at step[r].cache_pos. The merge takes the gate from
+  // packed_q. Without packed_q, q and gate are prepared and the cache already
+  // holds all seq_len tokens.
+  const uint16_t* packed_q = nullptr;  // [rows][16][512]
+  const uint16_t* q_norm = nullptr;    // [256]
+  const uint16_t* k_in = nullptr;      // [rows][4][256]
+  const uint16_t* v_in = nullptr;      // [rows][4][256]
+  const uint16_t* k_norm = nullptr;    // [256]
+  uint16_t* key_cache_w = nullptr;     // writable views of the caches for the append
+  uint16_t* value_cache_w = nullptr;
+  uint32_t cache_pos_host = 0;         // row 0's slot and RoPE position when step == nullptr
+  uint32_t rope_pos_host = 0;
 };
 
 int launch_attn_decode(hipStream_t s, const AttnDecodeArgs& a);

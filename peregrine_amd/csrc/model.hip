@@ -364,10 +364,38 @@ int encode_linear_attention2(PrgModel* m, PrgModelState* st, const DecoderLayer&
   return run_gemv(s, o, kEpiResidual, kNormGated, "linear_attn.out_proj2");
 }
 
+// Decode-step attention over a layer's cache: split partials over the cached
+// tokens (q normalised and rotated in the kernel), then the gated merge that
+// adds the new token(s) and appends their K / V (prepare, partials and merge
+// of FullAttentionBlock.decodeStepBf16, block_attn.zig:321-358, in two launches).
+static AttnDecodeArgs attn_step_args(PrgModelState* st, const FullAttentionBlock& b, LayerState& ls, const uint16_t* qp,
+                              const uint16_t* k, const uint16_t* v, uint16_t* ctx, const StepScalars* step) {
+  AttnDecodeArgs da{};
+  da.q = st->qbuf;
+  da.key_cache = ls.cache_k;
+  da.value_cache = ls.cache_v;
+  da.gate = nullptr;
+  da.out = ctx;
+  da.partials = st->partials;
+  da.stride = st->stride;
+  da.nsplit = st->nsplit;
+  da.split_tokens = st->split_tokens;
+  da.step = step;
+  da.scale = kAttnScale;
+  da.packed_q = qp;
+  da.q_norm = b.q_norm;
+  da.k_in = k;
+  da.v_in = v;
+  da.k_norm = b.k_norm;
+  da.key_cache_w = ls.cache_k;
+  da.value_cache_w = ls.cache_v;
+  return da;
+}
+
 // Two consecutive tokens through one attention layer: q/k/v for both rows in
-// one M = 2 GEMV, one prepare + append launch and one split decode for both
-// rows (row 1 attends to row 0's appended K/V), and o_proj for both rows in
-// one M = 2 GEMV.
+// one M = 2 GEMV, one split decode over the cached tokens for both rows plus
+// one merge (row 1 also attends to row 0's new token), and o_proj for both
+// rows in one M = 2 GEMV.
 int encode_full_attention2(PrgModel* m, PrgModelState* st, const DecoderLayer& L, LayerState& ls,
                            const uint16_t* const* x, uint16_t* const* h, const StepScalars* step) {
   const FullAttentionBlock& b = L.full;
@@ -390,24 +418,9 @@ int encode_full_attention2(PrgModel* m, PrgModelState* st, const DecoderLayer& L
   add_seg(p, b.v_proj, vb[0]);
   p.seg[2].out[1] = vb[1];
   if (int rc = run_gemv(s, p, kEpiPlain, kNormRms, "self_attn.qkv_proj2")) return rc;
-  // Both rows' K/V are appended first; row 0 attends to seq_len = pos + 1, so
-  // row 1's slot is outside its range.
-  AttnPrepareArgs pa{qp[0], b.q_norm, kb[0], vb[0], b.k_norm, st->qbuf, st->gatebuf, ls.cache_k, ls.cache_v,
-                     st->stride, 0, 0, step};
-  pa.rows = 2;
-  if (int rc = launch_attn_prepare(s, pa)) return rc;
-  AttnDecodeArgs da{};
-  da.q = st->qbuf;
-  da.key_cache = ls.cache_k;
-  da.value_cache = ls.cache_v;
-  da.gate = st->gatebuf;
-  da.out = ctx[0];
-  da.partials = st->partials;
-  da.stride = st->stride;
-  da.nsplit = st->nsplit;
-  da.split_tokens = st->split_tokens;
-  da.step = step;
-  da.scale = kAttnScale;
+  // Both rows attend over the cached tokens [0, pos); the merge adds row 0's
+  // new token to both rows and row 1's to row 1 only, and appends both.
+  AttnDecodeArgs da = attn_step_args(st, b, ls, qp[0], kb[0], vb[0], ctx[0], step);
   da.rows = 2;
   if (int rc = launch_attn_decode(s, da)) return rc;
   GemvParams o = gemv_params(ctx[0], kCtx);
@@ -432,21 +445,7 @@ int encode_full_attention(PrgModel* m, PrgModelState* st, const DecoderLayer& L,
   add_seg(p, b.k_proj, st->kbuf);
   add_seg(p, b.v_proj, st->vbuf);
   if (int rc = run_gemv(s, p, kEpiPlain, kNormRms, "self_attn.qkv_proj")) return rc;
-  AttnPrepareArgs pa{st->qp, b.q_norm, st->kbuf, st->vbuf, b.k_norm, st->qbuf, st->gatebuf, ls.cache_k, ls.cache_v,
-                     st->stride, 0, 0, step};
-  if (int rc = launch_attn_prepare(s, pa)) return rc;
-  AttnDecodeArgs da{};
-  da.q = st->qbuf;
-  da.key_cache = ls.cache_k;
-  da.value_cache = ls.cache_v;
-  da.gate = st->gatebuf;
-  da.out = st->ctx;
-  da.partials = st->partials;
-  da.stride = st->stride;
-  da.nsplit = st->nsplit;
-  da.split_tokens = st->split_tokens;
-  da.step = step;
-  da.scale = kAttnScale;
+  AttnDecodeArgs da = attn_step_args(st, b, ls, st->qp, st->kbuf, st->vbuf, st->ctx, step);
   if (int rc = launch_attn_decode(s, da)) return rc;
   GemvParams o = gemv_params(st->ctx, kAttnQHeads * kAttnHeadDim);
   add_seg(o, b.o_proj, h);

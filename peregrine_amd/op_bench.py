@@ -8,10 +8,11 @@
   distinct state is touched between two uses (MI355X's Infinity Cache is
   256 MiB).
 * Config 4: one full-attention GQA decode layer at context L (16 q heads,
-  4 KV heads, head_dim 256, RoPE theta 1e7 at position L - 1): the q/k
-  norm + RoPE + cache append (prg_attn_decode_prepare_bf16) and the
-  split-context attention with its gated merge (prg_attn_decode_bf16), alone
-  and as 8 stacked layers with distinct caches, rotated the same way.
+  4 KV heads, head_dim 256, RoPE theta 1e7 at position L - 1) as the model
+  runs it (prg_attn_decode_step_bf16: split partials over the cached tokens
+  with q normalised and rotated in the kernel, then the gated merge that adds
+  the new token and appends its K/V), alone and as 8 stacked layers with
+  distinct caches, rotated the same way.
 
 Each case is captured once into a HIP graph on its own stream and replayed;
 times are the median over replays bracketed by HIP events, per layer (or per
@@ -107,6 +108,9 @@ def gdn_layers(layers: int = 24, seed: int = 3, reps: int = 20, fused_norm: bool
 
 
 def attention(L: int, layers: int = 1, seed: int = 4, reps: int = 20) -> dict:
+    """One decode step of a full-attention layer as the model runs it
+    (prg_attn_decode_step_bf16: q/k norm + RoPE, split partials over the L - 1
+    cached tokens, merge with the new token and its K/V append) at context L."""
     rng = np.random.default_rng(seed + L + layers)
     stride = L
     kv_bytes = 4 * stride * 256 * 2
@@ -119,33 +123,30 @@ def attention(L: int, layers: int = 1, seed: int = 4, reps: int = 20) -> dict:
     vin = DeviceArray.from_numpy(random_bf16(rng, (1024,)))
     kc0 = random_bf16(rng, (4, stride, 256))
     vc0 = random_bf16(rng, (4, 256, stride))
-    part_bytes = ops.attn_partials_bytes(stride)
     caches = [(DeviceArray.from_numpy(kc0), DeviceArray.from_numpy(vc0)) for _ in range(sets * layers)]
-    q, gate = DeviceArray((16 * 256,), np.uint16), DeviceArray((16 * 256,), np.uint16)
     out = DeviceArray((16 * 256,), np.uint16)
-    part = DeviceArray((part_bytes // 4,), np.float32)
+    ws = DeviceArray((ops.attn_step_workspace_bytes(stride),), np.uint8)
     st = Stream()
     pos = L - 1
 
     def issue():
         for kc, vc in caches:
-            ops.attn_decode_prepare(pq, qw, q, gate, kin, vin, kw, kc, vc, stride, pos, pos, stream=st.handle)
-            ops.attn_decode(q, kc, vc, gate, out, part, stride, L, stream=st.handle)
+            ops.attn_decode_step(pq, qw, kin, vin, kw, kc, vc, out, ws, stride, pos, pos, stream=st.handle)
 
     ms = time_graph(st, issue, reps) / sets
     st.close()
     for kc, vc in caches:
         kc.close()
         vc.close()
-    for x in (pq, qw, kw, kin, vin, q, gate, out, part):
+    for x in (pq, qw, kw, kin, vin, out, ws):
         x.close()
     synchronize()
     total = layers * per_layer_algo
     gbs = total / (ms * 1e-3) / 1e9
-    return {"config": 4, "case": f"gqa decode attention L={L} x{layers} layer(s) (prepare + partials + merge)",
+    return {"config": 4, "case": f"gqa decode attention L={L} x{layers} layer(s) (decode step: partials + merge)",
             "L": L, "layers": layers, "us": round(ms * 1e3, 2), "us_per_layer": round(ms * 1e3 / layers, 3),
             "algo_bytes": int(total), "GBps": round(gbs, 1), "frac_peak": round(gbs / HBM_PEAK_GBS, 4),
-            "launches_per_layer": 3, "rotated_sets": sets}
+            "launches_per_layer": 2, "rotated_sets": sets}
 
 
 def configs_3_4() -> list[dict]:

@@ -157,6 +157,19 @@ def attn_decode(q, key_cache, value_cache, gate, out, partials, stride: int, seq
          ptr(partials), stride, seq_len, scale)
 
 
+def attn_step_workspace_bytes(stride: int) -> int:
+    from ._lib import lib
+
+    return int(lib.prg_attn_decode_step_workspace_bytes(stride))
+
+
+# block_attn.zig:321-358 (prepare + partials + merge of one decode step)
+def attn_decode_step(packed_q, q_w, k_in, v_in, k_w, key_cache, value_cache, out, workspace, stride: int,
+                     cache_pos: int, rope_pos: int, scale: float = 1.0 / 16.0, stream=None) -> None:
+    call("prg_attn_decode_step_bf16", _s(stream), ptr(packed_q), ptr(q_w), ptr(k_in), ptr(v_in), ptr(k_w),
+         ptr(key_cache), ptr(value_cache), ptr(out), ptr(workspace), stride, cache_pos, rope_pos, scale)
+
+
 def attn_decode_noalloc(q, key_cache, value_cache, gate, out, stride: int, seq_len: int,
                         scale: float = 1.0 / 16.0, stream=None) -> None:
     call("prg_attn_decode_noalloc_bf16", _s(stream), ptr(q), ptr(key_cache), ptr(value_cache), ptr(gate),

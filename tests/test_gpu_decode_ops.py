@@ -205,3 +205,32 @@ def test_attn_decode_bad_len_is_error(gpu):
     z = _e((16 * 256,))
     with pytest.raises(PrgError):
         ops.attn_decode(z, z, z, z, z, z, 64, 65)
+
+
+@pytest.mark.parametrize("L,stride", [(0, 64), (1, 64), (100, 128), (1023, 2048), (4095, 4096), (30000, 65536)])
+def test_attn_decode_step(gpu, orc, L, stride):
+    """prg_attn_decode_step_bf16 (q/k norm + RoPE, attention over the L cached
+    slots plus the new token, K/V append at slot L) against the oracle's
+    prepare (attention.metal:327-421) then flash decode over L + 1 tokens."""
+    from peregrine_amd import ops
+
+    rng = np.random.default_rng(100 + L)
+    pq = random_bf16(rng, (16 * 512,))
+    qw, kw = random_bf16(rng, (256,), std=0.1, mean=1.0), random_bf16(rng, (256,), std=0.1, mean=1.0)
+    kin, vin = random_bf16(rng, (4 * 256,)), random_bf16(rng, (4 * 256,))
+    kc = random_bf16(rng, (4, stride, 256))
+    vc = random_bf16(rng, (4, 256, stride))
+    kc[:, L:] = 0x7FC0  # slots from L on are not attended before the append, even as NaN
+    vc[:, :, L:] = 0x7FC0
+    dkc, dvc = _d(kc), _d(vc)
+    out = _e((16 * 256,))
+    ws = _e((ops.attn_step_workspace_bytes(stride),), np.uint8)
+    ops.attn_decode_step(_d(pq), _d(qw), _d(kin), _d(vin), _d(kw), dkc, dvc, out, ws, stride, L, L)
+    rq, rg, rkc, rvc = orc.attn_prepare(pq, qw, kin, vin, kw, kc, vc, stride, L, L)
+    ref = orc.attn_decode(rq, rkc, rvc, rg, stride, L + 1)
+    assert_bf16_close(out.numpy(), ref, min_exact=0.8, what=f"attn step L={L}")
+    gk, gv = dkc.numpy(), dvc.numpy()
+    np.testing.assert_array_equal(gv[:, :, L], rvc[:, :, L])  # V column copied
+    assert_bf16_close(gk[:, L], rkc[:, L], min_exact=0.97, what="appended k")
+    np.testing.assert_array_equal(gk[:, :L], kc[:, :L])  # cached slots untouched
+    np.testing.assert_array_equal(gv[:, :, :L], vc[:, :, :L])
