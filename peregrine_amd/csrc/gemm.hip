@@ -38,8 +38,11 @@ __device__ inline uint32_t pack_bf16(float lo, float hi) {
 // order. s*q is exact in f32 (8-bit by 4-bit significands), so the fma rounds
 // once, exactly like the reference's separate multiply and add.
 __device__ inline uint4 dequant_word(uint32_t w, float s, float b) {
-  const uint32_t lo = w & 0x0F0F0F0Fu;         // columns 0, 2, 4, 6 in bytes 0..3
-  const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;  // columns 1, 3, 5, 7
+  uint32_t lo = w & 0x0F0F0F0Fu;         // columns 0, 2, 4, 6 in bytes 0..3
+  uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;  // columns 1, 3, 5, 7
+  // Hide the masks from the optimiser so each byte converts with one
+  // v_cvt_f32_ubyteN instead of a bit-field extract plus a convert.
+  asm("" : "+v"(lo), "+v"(hi));
   uint4 r;
   r.x = pack_bf16(fmaf(s, static_cast<float>(lo & 0xffu), b), fmaf(s, static_cast<float>(hi & 0xffu), b));
   r.y = pack_bf16(fmaf(s, static_cast<float>((lo >> 8) & 0xffu), b), fmaf(s, static_cast<float>((hi >> 8) & 0xffu), b));
@@ -242,6 +245,251 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const GemmArgs g) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Q4 weights: 256-row x 128-B-row tiles, 8 waves (4 along M x 2 along N, 64x64
+// each). Every weight element is dequantised once per 256 activation rows.
+//
+// Pipeline per 64-k step s (one barrier per step), three LDS stages in a ring:
+//   - stage s is consumed: fragments of its second 32-k half are read while the
+//     matrix cores run the first half, then the first half of stage s+1 (written
+//     during step s-1 and published by the previous barrier) while they run the
+//     second;
+//   - stage s+2 is written from registers holding the global data of step s+2
+//     (issued two steps earlier), and the global loads of step s+4 are issued.
+// LDS rows are 128 B with 16-byte chunk c of row r stored at chunk c ^ (r & 7):
+// the coalesced staging writes (8 lanes = one row) and the MFMA fragment reads
+// (lanes = 16 rows x 4 chunks) both run at the full LDS rate on gfx950.
+constexpr int kQ4BM = 256, kQ4Threads = 512, kQ4Stages = 3;
+constexpr uint32_t kQ4ABytes = kQ4BM * 128, kQ4BBytes = 128 * 128, kQ4Stage = kQ4ABytes + kQ4BBytes;
+constexpr uint32_t kBufferWord3 = 0x00020000;  // raw buffer descriptor, 32-bit data format
+
+__device__ inline __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, kBufferWord3);
+}
+
+template <int EPI>
+__global__ __launch_bounds__(kQ4Threads) void gemm_q4_kernel(const GemmArgs g) {
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[kQ4Stages * kQ4Stage];
+  constexpr bool kPair = (EPI == kGemmSiluPair);
+  constexpr uint32_t kTileN = kPair ? 64 : 128;  // output columns per block
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+
+  // Block -> tile: block b runs on XCD b % 8; each XCD walks a contiguous range
+  // of tiles, ordered tm-fastest within groups of 4 tile rows, so the blocks
+  // resident on one XCD share A rows and weight columns in its L2.
+  const uint32_t tiles_m = (g.M + kQ4BM - 1) / kQ4BM;
+  uint32_t tm, tn;
+  {
+    const uint32_t T = gridDim.x, b = blockIdx.x, x = b % 8, q = T / 8, r = T % 8;
+    const uint32_t L = x * q + (x < r ? x : r) + b / 8;
+    const uint32_t tiles_n = T / tiles_m;
+    const uint32_t width = 4 * tiles_n, first = (L / width) * 4;
+    const uint32_t gs = tiles_m - first < 4u ? tiles_m - first : 4u;
+    tm = first + (L % width) % gs;
+    tn = (L % width) / gs;
+  }
+  uint32_t seg = 0;
+  if constexpr (!kPair) {
+#pragma unroll
+    for (int i = 1; i < kGemmMaxSegs; ++i)
+      if (i < static_cast<int>(g.nq) && tn >= g.q[i].tile0) seg = i;
+  }
+  const uint32_t m0 = tm * kQ4BM;
+  const uint32_t n0 = (tn - g.q[seg].tile0) * kTileN;
+  const uint32_t N = g.q[seg].n;
+  const uint32_t K = g.K, steps = K / kBK;
+
+  // A: thread t stages rows (t >> 3) + 64 i, chunk t & 7; rows >= M read as zero.
+  const __amdgpu_buffer_rsrc_t a_rsrc = buffer_rsrc(g.a, static_cast<uint32_t>(static_cast<uint64_t>(g.M) * g.lda * 2));
+  const uint32_t ar = tid >> 3, ac = tid & 7;
+  const uint32_t a_voff = static_cast<uint32_t>(((m0 + ar) * g.lda + ac * 8) * 2);
+  const uint32_t a_row64 = static_cast<uint32_t>(64 * g.lda * 2);
+  const uint32_t a_lds = ar * 128 + ((ac ^ (ar & 7)) << 4);
+  // B: thread t dequantises word t & 7 (columns 8 (t&7) .. +8 of the step) of
+  // tile rows (t >> 3) + 64 j. Pair: j = 0 gate, j = 1 up (same output columns).
+  const uint32_t br = tid >> 3, bw = tid & 7;
+  __amdgpu_buffer_rsrc_t w_rsrc[2];
+  uint32_t w_off[2];
+  const uint16_t *ps[2], *pb[2];
+  uint32_t b_lds[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const GemmQ4& Q = g.q[kPair ? j : seg];
+    const uint32_t row = kPair ? n0 + br : n0 + br + 64 * j;
+    const uint32_t nn = row < N ? row : N - 1;  // rows past N are computed, never stored
+    w_rsrc[j] = buffer_rsrc(Q.w, static_cast<uint32_t>(static_cast<uint64_t>(N) * K / 2));
+    w_off[j] = nn * (K / 2) + bw * 4;
+    ps[j] = Q.s + static_cast<uint64_t>(nn) * (K / 64);
+    pb[j] = Q.b + static_cast<uint64_t>(nn) * (K / 64);
+    const uint32_t lrow = br + 64 * j;
+    b_lds[j] = kQ4ABytes + lrow * 128 + ((bw ^ (lrow & 7)) << 4);
+  }
+
+  u32x4 ra[2][4];
+  uint32_t rw[2][2];
+  uint16_t rs[2][2], rb[2][2];
+  auto gload = [&](int set, uint32_t ks) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ra[set][i] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, a_voff, ks * 128 + i * a_row64, 0);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      rw[set][j] = __builtin_amdgcn_raw_buffer_load_b32(w_rsrc[j], w_off[j], ks * 32, 0);
+      rs[set][j] = ps[j][ks];
+      rb[set][j] = pb[j][ks];
+    }
+  };
+  auto store_a = [&](int set, uint32_t stage) {
+    uint8_t* base = lds + stage * kQ4Stage + a_lds;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(base + i * 8192) = ra[set][i];
+  };
+  auto store_b = [&](int set, uint32_t stage) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint4 d = dequant_word(rw[set][j], bf2f(rs[set][j]), bf2f(rb[set][j]));
+      *reinterpret_cast<uint4*>(lds + stage * kQ4Stage + b_lds[j]) = d;
+    }
+  };
+
+  // MFMA fragments: lane holds row (lane & 15) of a 16-row block, chunk
+  // (lane >> 4) + 4 kk of the 64-k step.
+  const uint32_t fsw = (lane >> 4) ^ (lane & 7);
+  const uint32_t fa0 = (wm * 64 + (lane & 15)) * 128 + (fsw << 4);
+  const uint32_t fa1 = (wm * 64 + (lane & 15)) * 128 + ((fsw ^ 4) << 4);
+  uint32_t fb0[4], fb1[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t brow = kPair ? ((j < 2) ? wn * 32 + 16 * j : 64 + wn * 32 + 16 * (j - 2)) : wn * 64 + 16 * j;
+    fb0[j] = kQ4ABytes + (brow + (lane & 15)) * 128 + (fsw << 4);
+    fb1[j] = kQ4ABytes + (brow + (lane & 15)) * 128 + ((fsw ^ 4) << 4);
+  }
+  bf16x8 fa[2][4], fb[2][4];
+  auto fread = [&](int f, uint32_t stage, int kk) {
+    const uint8_t* base = lds + stage * kQ4Stage;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) fa[f][i] = *reinterpret_cast<const bf16x8*>(base + (kk ? fa1 : fa0) + i * 2048);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) fb[f][j] = *reinterpret_cast<const bf16x8*>(base + (kk ? fb1[j] : fb0[j]));
+  };
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto mfma = [&](int f) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[f][i], fb[f][j], acc[i][j], 0, 0, 0);
+  };
+  // Steps past the end reload the last one (kept in bounds, never consumed).
+  auto clampk = [&](uint32_t k) { return k < steps ? k : steps - 1; };
+
+  gload(0, 0);
+  gload(1, clampk(1));
+  store_a(0, 0);
+  store_b(0, 0);
+  gload(0, clampk(2));
+  store_a(1, 1);
+  store_b(1, 1);
+  gload(1, clampk(3));
+  __syncthreads();
+  fread(0, 0, 0);
+
+  uint32_t st0 = 0;  // stage of step s
+  auto step = [&](int set, uint32_t s) {
+    const uint32_t st1 = st0 == kQ4Stages - 1 ? 0 : st0 + 1;
+    const uint32_t st2 = st1 == kQ4Stages - 1 ? 0 : st1 + 1;
+    store_a(set, st2);
+    fread(1, st0, 1);
+    mfma(0);
+    store_b(set, st2);
+    gload(set, clampk(s + 4));
+    fread(0, st1, 0);
+    mfma(1);
+    // Spread the LDS traffic, the global loads and the dequantisation between
+    // the 32 matrix instructions of the step.
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+      __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+    }
+    __syncthreads();
+    st0 = st1;
+  };
+  uint32_t s = 0;
+  for (; s + 1 < steps; s += 2) {
+    step(0, s);
+    step(1, s + 1);
+  }
+  if (s < steps) step(0, s);
+
+  // Epilogue: lane holds rows 4 (lane / 16) + r, column lane % 16 of each block.
+  const int crow = 4 * (lane >> 4), ccol = lane & 15;
+  uint16_t* C = g.q[seg].c;
+  if constexpr (kPair) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const uint32_t m = m0 + wm * 64 + 16 * i + crow + r;
+        if (m >= g.M) continue;
+        uint16_t* out = C + static_cast<uint64_t>(m) * N;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const uint32_t n = n0 + wn * 32 + 16 * j + ccol;
+          if (n >= N) continue;
+          const float gate = round_bf(acc[i][j][r]), up = round_bf(acc[i][j + 2][r]);
+          out[n] = f2bf(silu(gate) * up);
+        }
+      }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const uint32_t m = m0 + wm * 64 + 16 * i + crow + r;
+        if (m >= g.M) continue;
+        uint16_t* out = C + static_cast<uint64_t>(m) * N;
+        const uint16_t* rin = (EPI == kGemmResidual) ? g.res + static_cast<uint64_t>(m) * N : nullptr;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t n = n0 + wn * 64 + 16 * j + ccol;
+          if (n >= N) continue;
+          const float v = acc[i][j][r];
+          if constexpr (EPI == kGemmStore) {
+            out[n] = f2bf(v);
+          } else {
+            out[n] = f2bf(round_bf(v) + bf2f(rin[n]));
+          }
+        }
+      }
+  }
+}
+
+template <int EPI>
+int launch_q4_t(hipStream_t s, const GemmArgs& g, const char* name) {
+  const uint32_t tiles_n = (EPI == kGemmSiluPair) ? (g.q[0].n + 63) / 64
+                                                  : g.q[g.nq - 1].tile0 + (g.q[g.nq - 1].n + 127) / 128;
+  const uint32_t tiles = ((g.M + kQ4BM - 1) / kQ4BM) * tiles_n;
+  hipLaunchKernelGGL((gemm_q4_kernel<EPI>), dim3(tiles), dim3(kQ4Threads), 0, s, g);
+  PRG_CHECK_LAUNCH(name);
+  return PRG_OK;
+}
+
 template <bool Q4, int EPI>
 int launch_t(hipStream_t s, const GemmArgs& g, uint32_t batch, const char* name) {
   constexpr uint32_t kTileN = (EPI == kGemmSiluPair) ? kBN / 2 : kBN;
@@ -290,11 +538,17 @@ int launch_gemm_q4(hipStream_t s, GemmArgs g, int epi, const char* name) {
   }
   if (int rc = check_common(g, epi, name)) return rc;
   PRG_CHECK_ARG(g.K % 64 == 0, "%s: in_dim %u must be a multiple of 64", name, g.K);
+  // 32-bit buffer offsets: the A rows of the last tile and every weight matrix
+  // must lie within 4 GiB of their base.
+  PRG_CHECK_ARG(static_cast<uint64_t>(g.M + kQ4BM) * g.lda * 2 < (1ull << 32), "%s: A too large (M=%u lda=%llu)", name,
+                g.M, static_cast<unsigned long long>(g.lda));
+  for (uint32_t i = 0; i < g.nq; ++i)
+    PRG_CHECK_ARG(static_cast<uint64_t>(g.q[i].n) * g.K / 2 < (1ull << 32), "%s: Q4 segment %u too large", name, i);
+  PRG_CHECK_ARG(g.a_group == 0 && g.a_z == 0, "%s: Q4 GEMM takes plain [M, K] activations", name);
   switch (epi) {
-    case kGemmStore: return launch_t<true, kGemmStore>(s, g, 1, name);
-    case kGemmResidual: return launch_t<true, kGemmResidual>(s, g, 1, name);
-    case kGemmSiluPair: return launch_t<true, kGemmSiluPair>(s, g, 1, name);
-    default: return launch_t<true, kGemmSigmoidGate>(s, g, 1, name);
+    case kGemmStore: return launch_q4_t<kGemmStore>(s, g, name);
+    case kGemmResidual: return launch_q4_t<kGemmResidual>(s, g, name);
+    default: return launch_q4_t<kGemmSiluPair>(s, g, name);
   }
 }
 
