@@ -231,7 +231,9 @@ __global__ __launch_bounds__(kQkNormThreads) void gdn_prefill_prepare_kernel(
 // The per-token inputs (q, k of the k-head, gates, v of the block's rows) are
 // staged through LDS in chunks of kGdnChunk tokens, double-buffered: the
 // next chunk's global loads are in flight while the current chunk runs, so the
-// sequential loop only waits on LDS.
+// sequential loop only waits on LDS. Outputs collect in LDS and leave once per
+// chunk. (One wave per SIMD: the loop is instruction-issue bound, so a layout
+// with more lanes per row and more waves per SIMD only adds reduction work.)
 constexpr int kGdnPRowsPerBlock = 16;
 constexpr int kGdnChunk = 32;
 
@@ -248,6 +250,7 @@ __global__ __launch_bounds__(256) void gdn_prefill_kernel(float* __restrict__ st
   __shared__ float4 sk[2][kGdnChunk][kGdnDk / 4];
   __shared__ float sg[2][kGdnChunk], sb[2][kGdnChunk], skq[2][kGdnChunk];
   __shared__ float sv[2][kGdnChunk][kGdnPRowsPerBlock];
+  __shared__ uint16_t sy[2][kGdnChunk][kGdnPRowsPerBlock];
   constexpr uint32_t blocks_per_head = kGdnDv / kGdnPRowsPerBlock;
   const uint32_t tid = threadIdx.x;
   const uint32_t hv = blockIdx.x / blocks_per_head;
@@ -307,7 +310,44 @@ __global__ __launch_bounds__(256) void gdn_prefill_kernel(float* __restrict__ st
     }
   };
 
-  uint16_t* yb = y + hv * kGdnDv + row0 + rb;
+  // Per-token operands, read from LDS one token ahead into alternating sets.
+  struct Tok {
+    float4 qa, qc, ka, kc;
+    float decay, beta, kq, v;
+  };
+  auto fetch = [&](Tok& o, int b, uint32_t tt) {
+    o.qa = sq[b][tt][2 * j];
+    o.qc = sq[b][tt][2 * j + 1];
+    o.ka = sk[b][tt][2 * j];
+    o.kc = sk[b][tt][2 * j + 1];
+    o.decay = sg[b][tt];
+    o.beta = sb[b][tt];
+    o.kq = skq[b][tt];
+    o.v = sv[b][tt][rb];
+  };
+  // Outputs of a chunk collect in LDS (lane 0 of each row) and leave in one
+  // coalesced pass after the chunk's barrier.
+  auto token = [&](const Tok& o, int b, uint32_t tt) {
+    const float q[8] = {o.qa.x, o.qa.y, o.qa.z, o.qa.w, o.qc.x, o.qc.y, o.qc.z, o.qc.w};
+    const float k[8] = {o.ka.x, o.ka.y, o.ka.z, o.ka.w, o.kc.x, o.kc.y, o.kc.z, o.kc.w};
+    float d[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) d[i] = S[i] * o.decay;
+    // two independent partial sums per dot product shorten the chain
+    const float kv = row16_sum((d[0] * k[0] + d[1] * k[1] + d[2] * k[2] + d[3] * k[3]) +
+                               (d[4] * k[4] + d[5] * k[5] + d[6] * k[6] + d[7] * k[7]));
+    const float ob = row16_sum((d[0] * q[0] + d[1] * q[1] + d[2] * q[2] + d[3] * q[3]) +
+                               (d[4] * q[4] + d[5] * q[5] + d[6] * q[6] + d[7] * q[7]));
+    const float delta = (o.v - kv) * o.beta;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) S[i] = d[i] + k[i] * delta;
+    float kqd = o.kq;
+    if constexpr (!PRE_KQ)
+      kqd = row16_sum((k[0] * q[0] + k[1] * q[1] + k[2] * q[2] + k[3] * q[3]) +
+                      (k[4] * q[4] + k[5] * q[5] + k[6] * q[6] + k[7] * q[7]));
+    if (j == 0) sy[b][tt][rb] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(ob + delta * kqd));
+  };
+
   load(0);
   store(0);
   __syncthreads();
@@ -316,37 +356,26 @@ __global__ __launch_bounds__(256) void gdn_prefill_kernel(float* __restrict__ st
     const bool more = c0 + kGdnChunk < T;
     if (more) load(c0 + kGdnChunk);
     const uint32_t n = min(static_cast<uint32_t>(kGdnChunk), T - c0);
-    // Operands of token tt are read from LDS one step ahead.
-    float4 qa = sq[buf][0][2 * j], qc = sq[buf][0][2 * j + 1];
-    float4 ka = sk[buf][0][2 * j], kc = sk[buf][0][2 * j + 1];
-    float decay = sg[buf][0], bet = sb[buf][0], kq = skq[buf][0], v = sv[buf][0][rb];
-    for (uint32_t tt = 0; tt < n; ++tt) {
-      const float q[8] = {qa.x, qa.y, qa.z, qa.w, qc.x, qc.y, qc.z, qc.w};
-      const float k[8] = {ka.x, ka.y, ka.z, ka.w, kc.x, kc.y, kc.z, kc.w};
-      const float dec = decay, bt = bet, kqt = kq, vt = v;
-      const uint32_t nx = tt + 1 < n ? tt + 1 : tt;
-      qa = sq[buf][nx][2 * j]; qc = sq[buf][nx][2 * j + 1];
-      ka = sk[buf][nx][2 * j]; kc = sk[buf][nx][2 * j + 1];
-      decay = sg[buf][nx]; bet = sb[buf][nx]; kq = skq[buf][nx]; v = sv[buf][nx][rb];
-      float d[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) d[i] = S[i] * dec;
-      // two independent partial sums per dot product shorten the chain
-      const float kv = row16_sum((d[0] * k[0] + d[1] * k[1] + d[2] * k[2] + d[3] * k[3]) +
-                                 (d[4] * k[4] + d[5] * k[5] + d[6] * k[6] + d[7] * k[7]));
-      const float ob = row16_sum((d[0] * q[0] + d[1] * q[1] + d[2] * q[2] + d[3] * q[3]) +
-                                 (d[4] * q[4] + d[5] * q[5] + d[6] * q[6] + d[7] * q[7]));
-      const float delta = (vt - kv) * bt;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) S[i] = d[i] + k[i] * delta;
-      float kqd = kqt;
-      if constexpr (!PRE_KQ)
-        kqd = row16_sum((k[0] * q[0] + k[1] * q[1] + k[2] * q[2] + k[3] * q[3]) +
-                        (k[4] * q[4] + k[5] * q[5] + k[6] * q[6] + k[7] * q[7]));
-      if (j == 0) yb[static_cast<size_t>(c0 + tt) * kGdnValDim] = f2bf(ob + delta * kqd);
+    Tok ta, tb;
+    fetch(ta, buf, 0);
+    uint32_t tt = 0;
+    for (; tt + 1 < n; tt += 2) {
+      fetch(tb, buf, tt + 1);
+      token(ta, buf, tt);
+      fetch(ta, buf, tt + 2 < n ? tt + 2 : tt + 1);
+      token(tb, buf, tt + 1);
     }
+    if (tt < n) token(ta, buf, tt);
     if (more) store(buf ^ 1);
     __syncthreads();
+    // 16 rows x n tokens of this chunk: two rows per thread
+    {
+      const uint32_t t_out = tid >> 3, r2 = 2 * (tid & 7);
+      if (t_out < n) {
+        const uint32_t pair = static_cast<uint32_t>(sy[buf][t_out][r2]) | (static_cast<uint32_t>(sy[buf][t_out][r2 + 1]) << 16);
+        *reinterpret_cast<uint32_t*>(y + static_cast<size_t>(c0 + t_out) * kGdnValDim + hv * kGdnDv + row0 + r2) = pair;
+      }
+    }
   }
   srow[0] = make_float4(S[0], S[1], S[2], S[3]);
   srow[1] = make_float4(S[4], S[5], S[6], S[7]);
