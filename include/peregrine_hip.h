@@ -310,9 +310,10 @@ size_t prg_attn_decode_partials_bytes(uint32_t cache_stride_tokens);
  * (its q and k RMSNormed with q_weight / k_weight, partial RoPE at rope_pos),
  * writes out = bf16(softmax(scale q.K^T) V * sigmoid(gate)) [16, 256] and
  * appends the new K / V at cache_pos. workspace: device memory of
- * prg_attn_decode_step_workspace_bytes(stride). Two launches (split partials
- * over the cache with q prepared in-kernel, then the merge that adds the new
- * token and appends it). Replaces prepare + partials + merge of
+ * prg_attn_decode_step_workspace_bytes(stride). Two launches: split partials
+ * over the cache with q prepared in every block, the split holding the last
+ * cached slot also taking the new token and appending its K / V; then the
+ * gated merge. Replaces prepare + partials + merge of
  * FullAttentionBlock.decodeStepBf16 (block_attn.zig:321-358;
  * attention.metal:327-421, attention_decode.metal:24-243). */
 int prg_attn_decode_step_bf16(void *stream, const uint16_t *packed_q, const uint16_t *q_weight,
