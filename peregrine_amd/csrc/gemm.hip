@@ -246,8 +246,9 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const GemmArgs g) {
 }
 
 // ---------------------------------------------------------------------------
-// Q4 weights: 256-row x 128-B-row tiles, 8 waves (4 along M x 2 along N, 64x64
-// each). Every weight element is dequantised once per 256 activation rows.
+// Q4 weights: BM-row x 128-weight-row tiles (BM = 256 or 192), 8 waves (4 along
+// M x 2 along N, (BM/4) x 64 each). Every weight element is dequantised once
+// per BM activation rows.
 //
 // Pipeline per 64-k step s (one barrier per step), three LDS stages in a ring:
 //   - stage s is consumed: fragments of its second 32-k half are read while the
@@ -259,16 +260,19 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const GemmArgs g) {
 // LDS rows are 128 B with 16-byte chunk c of row r stored at chunk c ^ (r & 7):
 // the coalesced staging writes (8 lanes = one row) and the MFMA fragment reads
 // (lanes = 16 rows x 4 chunks) both run at the full LDS rate on gfx950.
-constexpr int kQ4BM = 256, kQ4Threads = 512, kQ4Stages = 3;
-constexpr uint32_t kQ4ABytes = kQ4BM * 128, kQ4BBytes = 128 * 128, kQ4Stage = kQ4ABytes + kQ4BBytes;
+constexpr int kQ4Threads = 512, kQ4Stages = 3;
+constexpr uint32_t kQ4BBytes = 128 * 128;
 constexpr uint32_t kBufferWord3 = 0x00020000;  // raw buffer descriptor, 32-bit data format
 
 __device__ inline __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, kBufferWord3);
 }
 
-template <int EPI>
+template <int EPI, int BM>
 __global__ __launch_bounds__(kQ4Threads) void gemm_q4_kernel(const GemmArgs g) {
+  static_assert(BM == 256 || BM == 192, "row tile");
+  constexpr int WTM = BM / 4, IM = WTM / 16;  // wave tile rows, 16-row MFMA blocks per wave
+  constexpr uint32_t kQ4ABytes = BM * 128, kQ4Stage = kQ4ABytes + kQ4BBytes;
   __shared__ __attribute__((aligned(1024))) uint8_t lds[kQ4Stages * kQ4Stage];
   constexpr bool kPair = (EPI == kGemmSiluPair);
   constexpr uint32_t kTileN = kPair ? 64 : 128;  // output columns per block
@@ -280,7 +284,7 @@ __global__ __launch_bounds__(kQ4Threads) void gemm_q4_kernel(const GemmArgs g) {
   // Block -> tile: block b runs on XCD b % 8; each XCD walks a contiguous range
   // of tiles, ordered tm-fastest within groups of 4 tile rows, so the blocks
   // resident on one XCD share A rows and weight columns in its L2.
-  const uint32_t tiles_m = (g.M + kQ4BM - 1) / kQ4BM;
+  const uint32_t tiles_m = (g.M + BM - 1) / BM;
   uint32_t tm, tn;
   {
     const uint32_t T = gridDim.x, b = blockIdx.x, x = b % 8, q = T / 8, r = T % 8;
@@ -297,12 +301,13 @@ __global__ __launch_bounds__(kQ4Threads) void gemm_q4_kernel(const GemmArgs g) {
     for (int i = 1; i < kGemmMaxSegs; ++i)
       if (i < static_cast<int>(g.nq) && tn >= g.q[i].tile0) seg = i;
   }
-  const uint32_t m0 = tm * kQ4BM;
+  const uint32_t m0 = tm * BM;
   const uint32_t n0 = (tn - g.q[seg].tile0) * kTileN;
   const uint32_t N = g.q[seg].n;
   const uint32_t K = g.K, steps = K / kBK;
 
-  // A: thread t stages rows (t >> 3) + 64 i, chunk t & 7; rows >= M read as zero.
+  // A: thread t stages rows (t >> 3) + 64 i (i < BM / 64), chunk t & 7; rows >= M
+  // read as zero.
   const __amdgpu_buffer_rsrc_t a_rsrc = buffer_rsrc(g.a, static_cast<uint32_t>(static_cast<uint64_t>(g.M) * g.lda * 2));
   const uint32_t ar = tid >> 3, ac = tid & 7;
   const uint32_t a_voff = static_cast<uint32_t>(((m0 + ar) * g.lda + ac * 8) * 2);
@@ -328,12 +333,12 @@ __global__ __launch_bounds__(kQ4Threads) void gemm_q4_kernel(const GemmArgs g) {
     b_lds[j] = kQ4ABytes + lrow * 128 + ((bw ^ (lrow & 7)) << 4);
   }
 
-  u32x4 ra[2][4];
+  u32x4 ra[2][BM / 64];
   uint32_t rw[2][2];
   uint16_t rs[2][2], rb[2][2];
   auto gload = [&](int set, uint32_t ks) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) ra[set][i] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, a_voff, ks * 128 + i * a_row64, 0);
+    for (int i = 0; i < BM / 64; ++i) ra[set][i] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, a_voff, ks * 128 + i * a_row64, 0);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       rw[set][j] = __builtin_amdgcn_raw_buffer_load_b32(w_rsrc[j], w_off[j], ks * 32, 0);
@@ -344,7 +349,7 @@ __global__ __launch_bounds__(kQ4Threads) void gemm_q4_kernel(const GemmArgs g) {
   auto store_a = [&](int set, uint32_t stage) {
     uint8_t* base = lds + stage * kQ4Stage + a_lds;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(base + i * 8192) = ra[set][i];
+    for (int i = 0; i < BM / 64; ++i) *reinterpret_cast<u32x4*>(base + i * 8192) = ra[set][i];
   };
   auto store_b = [&](int set, uint32_t stage) {
 #pragma unroll
@@ -357,8 +362,8 @@ __global__ __launch_bounds__(kQ4Threads) void gemm_q4_kernel(const GemmArgs g) {
   // MFMA fragments: lane holds row (lane & 15) of a 16-row block, chunk
   // (lane >> 4) + 4 kk of the 64-k step.
   const uint32_t fsw = (lane >> 4) ^ (lane & 7);
-  const uint32_t fa0 = (wm * 64 + (lane & 15)) * 128 + (fsw << 4);
-  const uint32_t fa1 = (wm * 64 + (lane & 15)) * 128 + ((fsw ^ 4) << 4);
+  const uint32_t fa0 = (wm * WTM + (lane & 15)) * 128 + (fsw << 4);
+  const uint32_t fa1 = (wm * WTM + (lane & 15)) * 128 + ((fsw ^ 4) << 4);
   uint32_t fb0[4], fb1[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -366,22 +371,22 @@ __global__ __launch_bounds__(kQ4Threads) void gemm_q4_kernel(const GemmArgs g) {
     fb0[j] = kQ4ABytes + (brow + (lane & 15)) * 128 + (fsw << 4);
     fb1[j] = kQ4ABytes + (brow + (lane & 15)) * 128 + ((fsw ^ 4) << 4);
   }
-  bf16x8 fa[2][4], fb[2][4];
+  bf16x8 fa[2][IM], fb[2][4];
   auto fread = [&](int f, uint32_t stage, int kk) {
     const uint8_t* base = lds + stage * kQ4Stage;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) fa[f][i] = *reinterpret_cast<const bf16x8*>(base + (kk ? fa1 : fa0) + i * 2048);
+    for (int i = 0; i < IM; ++i) fa[f][i] = *reinterpret_cast<const bf16x8*>(base + (kk ? fa1 : fa0) + i * 2048);
 #pragma unroll
     for (int j = 0; j < 4; ++j) fb[f][j] = *reinterpret_cast<const bf16x8*>(base + (kk ? fb1[j] : fb0[j]));
   };
-  f32x4 acc[4][4];
+  f32x4 acc[IM][4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < IM; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   auto mfma = [&](int f) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < IM; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[f][i], fb[f][j], acc[i][j], 0, 0, 0);
   };
@@ -411,16 +416,16 @@ __global__ __launch_bounds__(kQ4Threads) void gemm_q4_kernel(const GemmArgs g) {
     fread(0, st1, 0);
     mfma(1);
     // Spread the LDS traffic, the global loads and the dequantisation between
-    // the 32 matrix instructions of the step.
+    // the matrix instructions of the step.
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
+    for (int i = 0; i < IM * 4; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
       __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
       __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
     }
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
+    for (int i = 0; i < IM * 4; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
@@ -442,10 +447,10 @@ __global__ __launch_bounds__(kQ4Threads) void gemm_q4_kernel(const GemmArgs g) {
   uint16_t* C = g.q[seg].c;
   if constexpr (kPair) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < IM; ++i)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const uint32_t m = m0 + wm * 64 + 16 * i + crow + r;
+        const uint32_t m = m0 + wm * WTM + 16 * i + crow + r;
         if (m >= g.M) continue;
         uint16_t* out = C + static_cast<uint64_t>(m) * N;
 #pragma unroll
@@ -458,10 +463,10 @@ __global__ __launch_bounds__(kQ4Threads) void gemm_q4_kernel(const GemmArgs g) {
       }
   } else {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < IM; ++i)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const uint32_t m = m0 + wm * 64 + 16 * i + crow + r;
+        const uint32_t m = m0 + wm * WTM + 16 * i + crow + r;
         if (m >= g.M) continue;
         uint16_t* out = C + static_cast<uint64_t>(m) * N;
         const uint16_t* rin = (EPI == kGemmResidual) ? g.res + static_cast<uint64_t>(m) * N : nullptr;
@@ -480,14 +485,39 @@ __global__ __launch_bounds__(kQ4Threads) void gemm_q4_kernel(const GemmArgs g) {
   }
 }
 
+// Row tile per launch: one block per CU (the LDS ring holds one), so a launch
+// takes about (rounds of 256 blocks) x BM. 192-row tiles win where they save a
+// mostly empty last tile or round (a 1600-row prompt: 7 x 256 rows -> 9 x 192);
+// 2048-row chunks and the N = 4096 projections keep 256.
+inline uint32_t gemm_device_cus() {
+  static const uint32_t cus = []() -> uint32_t {
+    int dev = 0;
+    hipDeviceProp_t prop;
+    if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&prop, dev) != hipSuccess) return 256u;
+    return static_cast<uint32_t>(prop.multiProcessorCount);
+  }();
+  return cus;
+}
+
+template <int EPI, int BM>
+int launch_q4_bm(hipStream_t s, const GemmArgs& g, uint32_t tiles_n, const char* name) {
+  const uint32_t tiles = ((g.M + BM - 1) / BM) * tiles_n;
+  hipLaunchKernelGGL((gemm_q4_kernel<EPI, BM>), dim3(tiles), dim3(kQ4Threads), 0, s, g);
+  PRG_CHECK_LAUNCH(name);
+  return PRG_OK;
+}
+
 template <int EPI>
 int launch_q4_t(hipStream_t s, const GemmArgs& g, const char* name) {
   const uint32_t tiles_n = (EPI == kGemmSiluPair) ? (g.q[0].n + 63) / 64
                                                   : g.q[g.nq - 1].tile0 + (g.q[g.nq - 1].n + 127) / 128;
-  const uint32_t tiles = ((g.M + kQ4BM - 1) / kQ4BM) * tiles_n;
-  hipLaunchKernelGGL((gemm_q4_kernel<EPI>), dim3(tiles), dim3(kQ4Threads), 0, s, g);
-  PRG_CHECK_LAUNCH(name);
-  return PRG_OK;
+  const uint32_t cus = gemm_device_cus();
+  auto cost = [&](uint32_t bm) -> uint64_t {
+    const uint32_t blocks = ((g.M + bm - 1) / bm) * tiles_n;
+    return static_cast<uint64_t>((blocks + cus - 1) / cus) * bm;
+  };
+  if (cost(192) < cost(256)) return launch_q4_bm<EPI, 192>(s, g, tiles_n, name);
+  return launch_q4_bm<EPI, 256>(s, g, tiles_n, name);
 }
 
 template <bool Q4, int EPI>
@@ -540,7 +570,7 @@ int launch_gemm_q4(hipStream_t s, GemmArgs g, int epi, const char* name) {
   PRG_CHECK_ARG(g.K % 64 == 0, "%s: in_dim %u must be a multiple of 64", name, g.K);
   // 32-bit buffer offsets: the A rows of the last tile and every weight matrix
   // must lie within 4 GiB of their base.
-  PRG_CHECK_ARG(static_cast<uint64_t>(g.M + kQ4BM) * g.lda * 2 < (1ull << 32), "%s: A too large (M=%u lda=%llu)", name,
+  PRG_CHECK_ARG(static_cast<uint64_t>(g.M + 256) * g.lda * 2 < (1ull << 32), "%s: A too large (M=%u lda=%llu)", name,
                 g.M, static_cast<unsigned long long>(g.lda));
   for (uint32_t i = 0; i < g.nq; ++i)
     PRG_CHECK_ARG(static_cast<uint64_t>(g.q[i].n) * g.K / 2 < (1ull << 32), "%s: Q4 segment %u too large", name, i);
