@@ -248,7 +248,7 @@ __global__ __launch_bounds__(256) void gdn_prefill_kernel(float* __restrict__ st
                                                           uint32_t has_state) {
   __shared__ float4 sq[2][kGdnChunk][kGdnDk / 4];
   __shared__ float4 sk[2][kGdnChunk][kGdnDk / 4];
-  __shared__ float sg[2][kGdnChunk], sb[2][kGdnChunk], skq[2][kGdnChunk];
+  __shared__ float4 sgk[2][kGdnChunk];  // decay, beta, k.q of each token (one LDS read)
   __shared__ float sv[2][kGdnChunk][kGdnPRowsPerBlock];
   __shared__ uint16_t sy[2][kGdnChunk][kGdnPRowsPerBlock];
   constexpr uint32_t blocks_per_head = kGdnDv / kGdnPRowsPerBlock;
@@ -303,11 +303,7 @@ __global__ __launch_bounds__(256) void gdn_prefill_kernel(float* __restrict__ st
       const uint32_t idx = tid + 256 * i;
       sv[buf][idx / 16][idx % 16] = rv[i];
     }
-    if (tid < kGdnChunk) {
-      sg[buf][tid] = rg;
-      sb[buf][tid] = rbt;
-      skq[buf][tid] = rkq;
-    }
+    if (tid < kGdnChunk) sgk[buf][tid] = make_float4(rg, rbt, rkq, 0.f);
   };
 
   // Per-token operands, read from LDS one token ahead into alternating sets.
@@ -320,9 +316,10 @@ __global__ __launch_bounds__(256) void gdn_prefill_kernel(float* __restrict__ st
     o.qc = sq[b][tt][2 * j + 1];
     o.ka = sk[b][tt][2 * j];
     o.kc = sk[b][tt][2 * j + 1];
-    o.decay = sg[b][tt];
-    o.beta = sb[b][tt];
-    o.kq = skq[b][tt];
+    const float4 gk = sgk[b][tt];
+    o.decay = gk.x;
+    o.beta = gk.y;
+    o.kq = gk.z;
     o.v = sv[b][tt][rb];
   };
   // Outputs of a chunk collect in LDS (lane 0 of each row) and leave in one
@@ -358,14 +355,25 @@ __global__ __launch_bounds__(256) void gdn_prefill_kernel(float* __restrict__ st
     const uint32_t n = min(static_cast<uint32_t>(kGdnChunk), T - c0);
     Tok ta, tb;
     fetch(ta, buf, 0);
-    uint32_t tt = 0;
-    for (; tt + 1 < n; tt += 2) {
-      fetch(tb, buf, tt + 1);
-      token(ta, buf, tt);
-      fetch(ta, buf, tt + 2 < n ? tt + 2 : tt + 1);
-      token(tb, buf, tt + 1);
+    if (n == kGdnChunk) {
+      // full chunk: unrolled, every LDS operand at a constant offset
+#pragma unroll
+      for (uint32_t tt = 0; tt < kGdnChunk; tt += 2) {
+        fetch(tb, buf, tt + 1);
+        token(ta, buf, tt);
+        if (tt + 2 < kGdnChunk) fetch(ta, buf, tt + 2);
+        token(tb, buf, tt + 1);
+      }
+    } else {
+      uint32_t tt = 0;
+      for (; tt + 1 < n; tt += 2) {
+        fetch(tb, buf, tt + 1);
+        token(ta, buf, tt);
+        fetch(ta, buf, tt + 2 < n ? tt + 2 : tt + 1);
+        token(tb, buf, tt + 1);
+      }
+      if (tt < n) token(ta, buf, tt);
     }
-    if (tt < n) token(ta, buf, tt);
     if (more) store(buf ^ 1);
     __syncthreads();
     // 16 rows x n tokens of this chunk: two rows per thread
