@@ -322,8 +322,8 @@ __global__ __launch_bounds__(256) void gdn_prefill_kernel(float* __restrict__ st
     o.kq = gk.z;
     o.v = sv[b][tt][rb];
   };
-  // Outputs of a chunk collect in LDS (lane 0 of each row) and leave in one
-  // coalesced pass after the chunk's barrier.
+  // Outputs of a chunk collect in LDS and leave in one coalesced pass after
+  // the chunk's barrier.
   auto token = [&](const Tok& o, int b, uint32_t tt) {
     const float q[8] = {o.qa.x, o.qa.y, o.qa.z, o.qa.w, o.qc.x, o.qc.y, o.qc.z, o.qc.w};
     const float k[8] = {o.ka.x, o.ka.y, o.ka.z, o.ka.w, o.kc.x, o.kc.y, o.kc.z, o.kc.w};
@@ -342,7 +342,9 @@ __global__ __launch_bounds__(256) void gdn_prefill_kernel(float* __restrict__ st
     if constexpr (!PRE_KQ)
       kqd = row16_sum((k[0] * q[0] + k[1] * q[1] + k[2] * q[2] + k[3] * q[3]) +
                       (k[4] * q[4] + k[5] * q[5] + k[6] * q[6] + k[7] * q[7]));
-    if (j == 0) sy[b][tt][rb] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(ob + delta * kqd));
+    // every lane of the row holds the same y; all of them store it (same
+    // address, same bits), which keeps the loop free of exec-mask branches
+    sy[b][tt][rb] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(ob + delta * kqd));
   };
 
   load(0);
