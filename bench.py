@@ -113,6 +113,23 @@ def dominant_kernel_roofline(iters: int = 100) -> dict:
     stream.synchronize()
     read_us = a.elapsed_ms(b) * 1e3 / launches
     rgraph.close()
+    # Cross-check: a device-to-device hipMemcpyAsync of the same bytes from the
+    # same ring (reads them once and writes them once), timed the same way.
+    dst = DeviceArray((nbytes,), np.uint8)
+    with Graph.capture(stream) as cgraph:
+        for buf in bufs:
+            call("prg_hip_memcpy", C.c_void_p(dst.ptr), C.c_void_p(buf.ptr), C.c_size_t(nbytes), 2,
+                 C.c_void_p(stream.handle), 0)
+    cgraph.launch()
+    stream.synchronize()
+    a.record(C.c_void_p(stream.handle))
+    for _ in range(reps):
+        cgraph.launch()
+    b.record(C.c_void_p(stream.handle))
+    stream.synchronize()
+    copy_us = a.elapsed_ms(b) * 1e3 / launches
+    cgraph.close()
+    dst.close()
     for buf in bufs:
         buf.close()
     stream.close()
@@ -124,6 +141,7 @@ def dominant_kernel_roofline(iters: int = 100) -> dict:
             "avg_us": round(avg_us, 3), "timing": "HIP events around graph replays (no host launch overhead)",
             "read_floor_us": round(read_us, 3), "read_floor_GBps": round(nbytes / (read_us * 1e-6) / 1e9, 1),
             "frac_of_read_floor": round(read_us / avg_us, 4),
+            "memcpy_d2d_us": round(copy_us, 3), "memcpy_d2d_GBps_rw": round(2 * nbytes / (copy_us * 1e-6) / 1e9, 1),
             "algo_bytes_per_launch": int(algo), "launches": launches, "ring_copies": copies}
 
 
