@@ -357,6 +357,25 @@ int prg_model_generate_speculative(PrgModel *model, PrgModelState *state, const 
                                    uint32_t prompt_len, uint32_t n_new, uint32_t *tokens_out,
                                    uint32_t *accepted, uint32_t *attempted, float *decode_ms);
 
+/* The same loop continuing from a prefix-cache hit: the state already holds
+ * prompt[0, prefix_len) (prg_prefix_cache_restore), and prefix_hidden (device
+ * bf16 [prefix_len, hidden], e.g. prg_prefix_cache_entry_hidden) holds the
+ * final-normed hidden rows of those positions. The drafter is seeded from
+ * them (row t with prompt[t + 1]), prompt[prefix_len, prompt_len) is
+ * prefilled (seeding the drafter from the new rows), and the draft / verify
+ * loop runs as above; the tokens equal the greedy continuation of the whole
+ * prompt. hidden_out (device bf16 [prompt_len, hidden], may be NULL) receives
+ * the prompt's hidden rows (the prefix rows copied, the rest computed), ready
+ * for prg_prefix_cache_store. prefix_len = 0 (prefix_hidden unused) is
+ * prg_model_generate_speculative with the hidden rows captured. Replaces
+ * decodeSpeculativeFromPrefixCache with prefix_len > 0
+ * (src/server/decode_loop.zig:163-293) and seedMtpDrafter
+ * (src/server.zig:1240-1330). */
+int prg_model_generate_speculative_from(PrgModel *model, PrgModelState *state, const uint32_t *prompt,
+                                        uint32_t prompt_len, uint32_t prefix_len, const uint16_t *prefix_hidden,
+                                        uint16_t *hidden_out, uint32_t n_new, uint32_t *tokens_out,
+                                        uint32_t *accepted, uint32_t *attempted, float *decode_ms);
+
 #ifdef __cplusplus
 }
 #endif

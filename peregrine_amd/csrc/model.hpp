@@ -245,8 +245,10 @@ int prefill_layer(PrgModel* m, PrgModelState* st, const DecoderLayer& L, LayerSt
                   uint16_t* out, uint32_t T, uint32_t start);
 // Ingest st->prompt[from, len) on top of positions [0, from); with_mtp also
 // seeds the drafter's KV cache and leaves the last prompt row's normalised
-// hidden in st->cur_hidden.
-int run_prefill(PrgModel* m, PrgModelState* st, uint32_t from, uint32_t len, bool with_mtp);
+// hidden in st->cur_hidden. hidden_out (with_mtp only, may be null) receives
+// the final-normed hidden row of every ingested position p at row p.
+int run_prefill(PrgModel* m, PrgModelState* st, uint32_t from, uint32_t len, bool with_mtp,
+                uint16_t* hidden_out = nullptr);
 
 // ------------------------------------------------------ state transfers ---
 // ModelState.copyFullAttentionRangeFrom / copyLinearStateFrom

@@ -174,7 +174,7 @@ int prefill_layer(PrgModel* m, PrgModelState* st, const DecoderLayer& L, LayerSt
 // final-normed hidden rows also seed its KV cache (server.zig:1286-1325: the
 // drafter consumes hidden[t] with token[t+1]) and the last row is kept in
 // st->cur_hidden for the speculative loop.
-int run_prefill(PrgModel* m, PrgModelState* st, uint32_t from, uint32_t len, bool with_mtp) {
+int run_prefill(PrgModel* m, PrgModelState* st, uint32_t from, uint32_t len, bool with_mtp, uint16_t* hidden_out) {
   if (int rc = ensure_prefill_ws(st)) return rc;
   const PrgModelConfig& c = m->cfg;
   hipStream_t s = st->stream;
@@ -195,6 +195,9 @@ int run_prefill(PrgModel* m, PrgModelState* st, uint32_t from, uint32_t len, boo
     if (!with_mtp) continue;
     // normalised hidden rows of this chunk (model.zig:1049-1058)
     if (int rc = launch_rmsnorm(s, x, m->final_norm, w.resid, c.hidden, T, c.rms_eps)) return rc;
+    if (hidden_out)
+      PRG_HIP(hipMemcpyAsync(hidden_out + static_cast<size_t>(start) * c.hidden, w.resid,
+                             sizeof(uint16_t) * T * c.hidden, hipMemcpyDeviceToDevice, s));
     if (start + T < len) {
       // every row has its successor token; the drafter reuses h0/h1 (x is done)
       if (int rc = mtp_prefill_rows(m, st, st->prompt + start + 1, w.resid, T, start)) return rc;

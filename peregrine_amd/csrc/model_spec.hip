@@ -364,19 +364,33 @@ int prg_model_mtp_prefill(PrgModel* model, PrgModelState* st, const uint32_t* to
   return PRG_OK;
 }
 
-int prg_model_generate_speculative(PrgModel* model, PrgModelState* st, const uint32_t* prompt, uint32_t prompt_len,
-                                   uint32_t n_new, uint32_t* tokens_out, uint32_t* accepted, uint32_t* attempted,
-                                   float* decode_ms) {
+}  // extern "C"
+
+namespace {
+
+// Shared body of the two speculative entry points. prefix_len == 0: reset and
+// prefill the whole prompt. prefix_len > 0: the state already holds
+// prompt[0, prefix_len); the drafter is seeded from prefix_hidden for those
+// positions (seedMtpDrafter, server.zig:1240-1330), then the rest of the
+// prompt is prefilled as usual.
+int generate_speculative(PrgModel* model, PrgModelState* st, const uint32_t* prompt, uint32_t prompt_len,
+                         uint32_t prefix_len, const uint16_t* prefix_hidden, uint16_t* hidden_out, uint32_t n_new,
+                         uint32_t* tokens_out, uint32_t* accepted, uint32_t* attempted, float* decode_ms) {
   PRG_CHECK_ARG(model && st && prompt && tokens_out && st->model == model,
                 "prg_model_generate_speculative: bad argument");
   PRG_CHECK_ARG(model->mtp.present, "prg_model_generate_speculative: the model has no MTP drafter");
   PRG_CHECK_ARG(prompt_len >= 1 && n_new >= 1, "prg_model_generate_speculative: empty prompt or n_new == 0");
+  PRG_CHECK_ARG(prefix_len < prompt_len, "prg_model_generate_speculative: prefix_len %u must be below prompt_len %u",
+                prefix_len, prompt_len);
+  PRG_CHECK_ARG(prefix_len == 0 || prefix_hidden != nullptr,
+                "prg_model_generate_speculative: a cached prefix needs its hidden rows");
   if (static_cast<uint64_t>(prompt_len) + n_new + 2 > st->max_seq)
     return set_error(PRG_ERR_SEQUENCE_TOO_LONG, "prompt %u + %u new tokens (+2 verify slots) exceed max_seq %u",
                      prompt_len, n_new, st->max_seq);
   if (int rc = check_tokens(model, prompt, prompt_len)) return rc;
   if (int rc = ensure_spec_ws(st)) return rc;
-  if (int rc = prg_model_state_reset(st)) return rc;
+  if (prefix_len == 0)
+    if (int rc = prg_model_state_reset(st)) return rc;
   // prompt: target prefill + drafter seeding; next token -> predictions[len-1]
   DecodeCtl ctl{};
   ctl.s = StepScalars{prompt[prompt_len - 1], prompt_len - 1, prompt_len - 1, prompt_len};
@@ -385,7 +399,21 @@ int prg_model_generate_speculative(PrgModel* model, PrgModelState* st, const uin
   ctl.capacity = st->max_seq;
   PRG_HIP(hipMemcpyAsync(st->prompt, prompt, sizeof(uint32_t) * prompt_len, hipMemcpyHostToDevice, st->stream));
   PRG_HIP(hipMemcpyAsync(st->ctl, &ctl, sizeof(ctl), hipMemcpyHostToDevice, st->stream));
-  if (int rc = run_prefill(model, st, 0, prompt_len, true)) return rc;
+  if (prefix_len > 0) {
+    // drafter rows t < prefix_len pair hidden[t] with prompt[t + 1]; they go
+    // first, since the suffix rows attend to them
+    if (int rc = ensure_prefill_ws(st)) return rc;
+    const size_t H = model->cfg.hidden;
+    for (uint32_t t = 0; t < prefix_len;) {
+      const uint32_t T = prefill_chunk_tokens(st, t, prefix_len - t);
+      if (int rc = mtp_prefill_rows(model, st, st->prompt + t + 1, prefix_hidden + t * H, T, t)) return rc;
+      t += T;
+    }
+    if (hidden_out)
+      PRG_HIP(hipMemcpyAsync(hidden_out, prefix_hidden, sizeof(uint16_t) * prefix_len * H, hipMemcpyDeviceToDevice,
+                             st->stream));
+  }
+  if (int rc = run_prefill(model, st, prefix_len, prompt_len, true, hidden_out)) return rc;
   uint32_t first = 0;
   PRG_HIP(hipMemcpyAsync(&first, st->predictions + (prompt_len - 1), sizeof(uint32_t), hipMemcpyDeviceToHost,
                          st->stream));
@@ -422,6 +450,25 @@ int prg_model_generate_speculative(PrgModel* model, PrgModelState* st, const uin
   if (accepted) *accepted = c.accepted;
   if (attempted) *attempted = c.attempted;
   return PRG_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int prg_model_generate_speculative(PrgModel* model, PrgModelState* st, const uint32_t* prompt, uint32_t prompt_len,
+                                   uint32_t n_new, uint32_t* tokens_out, uint32_t* accepted, uint32_t* attempted,
+                                   float* decode_ms) {
+  return generate_speculative(model, st, prompt, prompt_len, 0, nullptr, nullptr, n_new, tokens_out, accepted,
+                              attempted, decode_ms);
+}
+
+int prg_model_generate_speculative_from(PrgModel* model, PrgModelState* st, const uint32_t* prompt,
+                                        uint32_t prompt_len, uint32_t prefix_len, const uint16_t* prefix_hidden,
+                                        uint16_t* hidden_out, uint32_t n_new, uint32_t* tokens_out,
+                                        uint32_t* accepted, uint32_t* attempted, float* decode_ms) {
+  return generate_speculative(model, st, prompt, prompt_len, prefix_len, prefix_hidden, hidden_out, n_new,
+                              tokens_out, accepted, attempted, decode_ms);
 }
 
 }  // extern "C"

@@ -191,6 +191,24 @@ class ModelState:
              len(prompt), n_new, out.ctypes.data_as(C.c_void_p), C.byref(acc), C.byref(att), C.byref(ms))
         return out, int(acc.value), int(att.value), float(ms.value)
 
+    # decode_loop.zig:163-293 with prefix_len > 0, seedMtpDrafter (server.zig:1240-1330)
+    def generate_speculative_from(self, prompt, prefix_len: int, prefix_hidden, n_new: int,
+                                  hidden_out=None) -> tuple[np.ndarray, int, int, float]:
+        """Speculative generation on top of a state holding prompt[:prefix_len]
+        (e.g. restored from a prefix cache entry); prefix_hidden: device bf16
+        [prefix_len, hidden] rows of that prefix (None when prefix_len == 0);
+        hidden_out: optional device bf16 [len(prompt), hidden] for the prompt's
+        hidden rows."""
+        from .device import ptr
+
+        prompt = np.ascontiguousarray(prompt, np.uint32)
+        out = np.empty(n_new, np.uint32)
+        acc, att, ms = C.c_uint32(0), C.c_uint32(0), C.c_float(0.0)
+        call("prg_model_generate_speculative_from", self.model.handle, self.handle,
+             prompt.ctypes.data_as(C.c_void_p), len(prompt), prefix_len, ptr(prefix_hidden), ptr(hidden_out), n_new,
+             out.ctypes.data_as(C.c_void_p), C.byref(acc), C.byref(att), C.byref(ms))
+        return out, int(acc.value), int(att.value), float(ms.value)
+
     # model.zig:1627-1659
     def forward_two_tokens(self, t0: int, t1: int, cache_pos: int, hidden_out=None) -> tuple[int, int]:
         v, b = C.c_uint32(0), C.c_uint32(0)

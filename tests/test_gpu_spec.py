@@ -177,6 +177,90 @@ def test_speculative_equals_greedy_copy_drafter(gpu):
     m.close()
 
 
+def test_speculative_continues_from_a_prefix_cache_hit(gpu):
+    """decodeSpeculativeFromPrefixCache with prefix_len > 0
+    (decode_loop.zig:163-293, seedMtpDrafter server.zig:1240-1330): a first
+    request runs from scratch and captures its prompt's hidden rows; that
+    prompt is stored in the prefix cache with them; a second request whose
+    prompt extends it restores the entry, seeds the drafter from the cached
+    rows and prefills only the rest. Its tokens equal greedy decoding of the
+    whole second prompt, its accepted / attempted counts equal a from-scratch
+    speculative run (same drafter cache), and its captured hidden rows equal
+    the from-scratch capture bit for bit. The copy drafter makes accepts
+    happen, so the accept path runs on the restored state."""
+    from peregrine_amd.device import DeviceArray
+    from peregrine_amd.model import DeviceModel, ModelConfig, ModelState
+    from peregrine_amd.prefix import PrefixCache
+
+    H = SMALL["hidden"]
+    m = DeviceModel(ModelConfig(**SMALL), seed=13)
+    _make_copy_drafter(m, H)
+    e0 = np.zeros(H, np.uint16)
+    e0[0] = int(f32_to_bf16(np.float32(1.0)))
+    _write(m, "language_model.model.norm.weight", e0)
+    rng = np.random.default_rng(21)
+    base = rng.integers(0, SMALL["vocab"], size=20).astype(np.uint32)
+    prompt = np.concatenate([base, rng.integers(0, SMALL["vocab"], size=9).astype(np.uint32)])
+    n = 32
+
+    # request 1: from scratch, capturing the prompt's hidden rows
+    st = ModelState(m, max_seq=128)
+    hid1 = DeviceArray.zeros((len(base), H), np.uint16)
+    toks1, _, _, _ = st.generate_speculative_from(base, 0, None, n, hidden_out=hid1)
+    np.testing.assert_array_equal(toks1, _greedy(m, base, n))
+    # the prompt's state right after its prefill goes into the cache with the rows
+    pre = ModelState(m, max_seq=128)
+    first = pre.prefill(base)
+    assert first == toks1[0]
+    cache = PrefixCache(m, 4096, 64)
+    cache.enable_hidden()
+    cache.store(base, work=pre, work_hidden=hid1.ptr, next_token=first)
+
+    # request 2: prefix hit, continue speculatively
+    match = cache.find(prompt)
+    assert match is not None and match.len == len(base)
+    rows, valid = cache.entry_hidden(match)
+    assert valid and rows
+    w = ModelState(m, max_seq=128)
+    cache.restore(match, w)
+    hid2 = DeviceArray.zeros((len(prompt), H), np.uint16)
+    toks2, acc2, att2, _ = w.generate_speculative_from(prompt, len(base), rows, n, hidden_out=hid2)
+    ref = _greedy(m, prompt, n)
+    np.testing.assert_array_equal(toks2, ref)
+
+    s = ModelState(m, max_seq=128)
+    hid3 = DeviceArray.zeros((len(prompt), H), np.uint16)
+    toks3, acc3, att3, _ = s.generate_speculative_from(prompt, 0, None, n, hidden_out=hid3)
+    np.testing.assert_array_equal(toks3, ref)
+    print(f"prefix hit: accepted {acc2}/{att2}; from scratch {acc3}/{att3}")
+    assert (acc2, att2) == (acc3, att3)
+    assert acc2 >= 1, "the copy drafter never matched a repeat"
+    np.testing.assert_array_equal(hid2.numpy(), hid3.numpy())
+    np.testing.assert_array_equal(hid3.numpy()[: len(base)], hid1.numpy())
+    for x in (st, pre, w, s, hid1, hid2, hid3):
+        x.close()
+    cache.close()
+    m.close()
+
+
+def test_speculative_from_prefix_errors(model):
+    from peregrine_amd._lib import PrgError
+    from peregrine_amd.device import DeviceArray
+    from peregrine_amd.model import ModelState
+
+    st = ModelState(model, max_seq=64)
+    p = np.arange(10, dtype=np.uint32)
+    with pytest.raises(PrgError) as e:
+        st.generate_speculative_from(p, 4, None, 4)  # a cached prefix needs its rows
+    assert e.value.code == 1
+    h = DeviceArray.zeros((10, SMALL["hidden"]), np.uint16)
+    with pytest.raises(PrgError) as e:
+        st.generate_speculative_from(p, 10, h, 4)  # nothing left to prefill
+    assert e.value.code == 1
+    h.close()
+    st.close()
+
+
 def test_speculative_errors(model):
     from peregrine_amd._lib import PrgError
     from peregrine_amd.model import DeviceModel, ModelConfig, ModelState
