@@ -54,6 +54,17 @@ int prg_model_create_random(const PrgModelConfig *cfg, uint64_t seed, PrgModel *
 void prg_model_destroy(PrgModel *model);
 /* Total bytes of device weights. */
 size_t prg_model_weight_bytes(const PrgModel *model);
+/* Prepared dense weights for the prompt path: every Q4 matrix the prefill
+ * GEMMs read (projections and MLP of every layer and of the drafter) is
+ * dequantised once into a bf16 [out, in] copy (4x its Q4 bytes: ~14 GB for
+ * the 9B shape), and the prefill GEMMs then stage those values instead of
+ * dequantising each tile; prefill results are identical bit for bit, decode
+ * keeps reading the Q4 weights. Call again after changing weights through
+ * prg_model_tensor. Replaces the prepared dense RHS buffers
+ * (src/model/block_attn.zig:143-215, linear_q4.denseRhsBf16ByteLen). */
+int prg_model_prepare_dense(PrgModel *model);
+/* Bytes of the prepared dense copies (0 before prg_model_prepare_dense). */
+size_t prg_model_dense_bytes(const PrgModel *model);
 /* Device pointer and byte size of a named tensor, e.g.
  * "language_model.model.layers.3.self_attn.q_proj.weight" (names as the
  * reference's checkpoint, decoder_layer.zig:376-412). */

@@ -268,7 +268,10 @@ __device__ inline __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t 
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, kBufferWord3);
 }
 
-template <int EPI, int BM>
+// DENSE: every segment has its prepared bf16 copy (GemmQ4::dense, the values
+// dequant_word produces), staged as is: the same LDS tile, hence the same
+// results bit for bit, without the per-tile dequantisation.
+template <int EPI, int BM, bool DENSE>
 __global__ __launch_bounds__(kQ4Threads) void gemm_q4_kernel(const GemmArgs g) {
   static_assert(BM == 256 || BM == 192, "row tile");
   constexpr int WTM = BM / 4, IM = WTM / 16;  // wave tile rows, 16-row MFMA blocks per wave
@@ -325,8 +328,14 @@ __global__ __launch_bounds__(kQ4Threads) void gemm_q4_kernel(const GemmArgs g) {
     const GemmQ4& Q = g.q[kPair ? j : seg];
     const uint32_t row = kPair ? n0 + br : n0 + br + 64 * j;
     const uint32_t nn = row < N ? row : N - 1;  // rows past N are computed, never stored
-    w_rsrc[j] = buffer_rsrc(Q.w, static_cast<uint32_t>(static_cast<uint64_t>(N) * K / 2));
-    w_off[j] = nn * (K / 2) + bw * 4;
+    if constexpr (DENSE) {
+      // 16 bytes = the 8 prepared values of word bw of the step
+      w_rsrc[j] = buffer_rsrc(Q.dense, static_cast<uint32_t>(static_cast<uint64_t>(N) * K * 2));
+      w_off[j] = nn * (K * 2) + bw * 16;
+    } else {
+      w_rsrc[j] = buffer_rsrc(Q.w, static_cast<uint32_t>(static_cast<uint64_t>(N) * K / 2));
+      w_off[j] = nn * (K / 2) + bw * 4;
+    }
     ps[j] = Q.s + static_cast<uint64_t>(nn) * (K / 64);
     pb[j] = Q.b + static_cast<uint64_t>(nn) * (K / 64);
     const uint32_t lrow = br + 64 * j;
@@ -336,14 +345,19 @@ __global__ __launch_bounds__(kQ4Threads) void gemm_q4_kernel(const GemmArgs g) {
   u32x4 ra[2][BM / 64];
   uint32_t rw[2][2];
   uint16_t rs[2][2], rb[2][2];
+  u32x4 rd[DENSE ? 2 : 1][2];
   auto gload = [&](int set, uint32_t ks) {
 #pragma unroll
     for (int i = 0; i < BM / 64; ++i) ra[set][i] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, a_voff, ks * 128 + i * a_row64, 0);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      rw[set][j] = __builtin_amdgcn_raw_buffer_load_b32(w_rsrc[j], w_off[j], ks * 32, 0);
-      rs[set][j] = ps[j][ks];
-      rb[set][j] = pb[j][ks];
+      if constexpr (DENSE) {
+        rd[set][j] = __builtin_amdgcn_raw_buffer_load_b128(w_rsrc[j], w_off[j], ks * 128, 0);
+      } else {
+        rw[set][j] = __builtin_amdgcn_raw_buffer_load_b32(w_rsrc[j], w_off[j], ks * 32, 0);
+        rs[set][j] = ps[j][ks];
+        rb[set][j] = pb[j][ks];
+      }
     }
   };
   auto store_a = [&](int set, uint32_t stage) {
@@ -354,8 +368,12 @@ __global__ __launch_bounds__(kQ4Threads) void gemm_q4_kernel(const GemmArgs g) {
   auto store_b = [&](int set, uint32_t stage) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const uint4 d = dequant_word(rw[set][j], bf2f(rs[set][j]), bf2f(rb[set][j]));
-      *reinterpret_cast<uint4*>(lds + stage * kQ4Stage + b_lds[j]) = d;
+      if constexpr (DENSE) {
+        *reinterpret_cast<u32x4*>(lds + stage * kQ4Stage + b_lds[j]) = rd[set][j];
+      } else {
+        const uint4 d = dequant_word(rw[set][j], bf2f(rs[set][j]), bf2f(rb[set][j]));
+        *reinterpret_cast<uint4*>(lds + stage * kQ4Stage + b_lds[j]) = d;
+      }
     }
   };
 
@@ -502,7 +520,12 @@ inline uint32_t gemm_device_cus() {
 template <int EPI, int BM>
 int launch_q4_bm(hipStream_t s, const GemmArgs& g, uint32_t tiles_n, const char* name) {
   const uint32_t tiles = ((g.M + BM - 1) / BM) * tiles_n;
-  hipLaunchKernelGGL((gemm_q4_kernel<EPI, BM>), dim3(tiles), dim3(kQ4Threads), 0, s, g);
+  bool dense = true;
+  for (uint32_t i = 0; i < g.nq; ++i) dense = dense && g.q[i].dense != nullptr;
+  if (dense)
+    hipLaunchKernelGGL((gemm_q4_kernel<EPI, BM, true>), dim3(tiles), dim3(kQ4Threads), 0, s, g);
+  else
+    hipLaunchKernelGGL((gemm_q4_kernel<EPI, BM, false>), dim3(tiles), dim3(kQ4Threads), 0, s, g);
   PRG_CHECK_LAUNCH(name);
   return PRG_OK;
 }
@@ -547,7 +570,38 @@ int check_common(const GemmArgs& g, int epi, const char* name) {
 
 }  // namespace
 
+namespace {
+
+// Prepared bf16 copy of a Q4 matrix: dense[n][k] = bf16(s*q + b), the values
+// the Q4 GEMM stages (dequant_word). One thread per 8-value word.
+__global__ __launch_bounds__(256) void dequant_dense_kernel(const uint32_t* __restrict__ w,
+                                                            const uint16_t* __restrict__ sc,
+                                                            const uint16_t* __restrict__ bi, uint4* __restrict__ out,
+                                                            uint64_t words, uint32_t K) {
+  const uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= words) return;
+  const uint64_t grp = i / 8;  // 8 words of a row per 64-value group; K % 64 == 0
+  (void)K;
+  out[i] = dequant_word(__builtin_nontemporal_load(w + i), bf2f(sc[grp]), bf2f(bi[grp]));
+}
+
+}  // namespace
+
 namespace prg {
+
+int launch_dequant_dense(hipStream_t s, const uint32_t* w, const uint16_t* sc, const uint16_t* bi, uint16_t* out,
+                         uint32_t n, uint32_t K, const char* name) {
+  PRG_CHECK_ARG(w && sc && bi && out, "%s: null pointer", name);
+  PRG_CHECK_ARG(n > 0 && K > 0 && K % 64 == 0, "%s: shape %u x %u (K must be a multiple of 64)", name, n, K);
+  PRG_CHECK_ARG(reinterpret_cast<uintptr_t>(out) % 16 == 0, "%s: output must be 16-byte aligned", name);
+  const uint64_t words = static_cast<uint64_t>(n) * K / 8;
+  const uint64_t blocks = (words + 255) / 256;
+  PRG_CHECK_ARG(blocks < (1ull << 31), "%s: matrix too large", name);
+  hipLaunchKernelGGL(dequant_dense_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, s, w, sc, bi,
+                     reinterpret_cast<uint4*>(out), words, K);
+  PRG_CHECK_LAUNCH(name);
+  return PRG_OK;
+}
 
 int launch_gemm_q4(hipStream_t s, GemmArgs g, int epi, const char* name) {
   PRG_CHECK_ARG(g.nq >= 1 && g.nq <= kGemmMaxSegs, "%s: %u weight segments", name, g.nq);
@@ -572,8 +626,12 @@ int launch_gemm_q4(hipStream_t s, GemmArgs g, int epi, const char* name) {
   // must lie within 4 GiB of their base.
   PRG_CHECK_ARG(static_cast<uint64_t>(g.M + 256) * g.lda * 2 < (1ull << 32), "%s: A too large (M=%u lda=%llu)", name,
                 g.M, static_cast<unsigned long long>(g.lda));
-  for (uint32_t i = 0; i < g.nq; ++i)
+  for (uint32_t i = 0; i < g.nq; ++i) {
     PRG_CHECK_ARG(static_cast<uint64_t>(g.q[i].n) * g.K / 2 < (1ull << 32), "%s: Q4 segment %u too large", name, i);
+    PRG_CHECK_ARG(!g.q[i].dense || (static_cast<uint64_t>(g.q[i].n) * g.K * 2 < (1ull << 32) &&
+                                    reinterpret_cast<uintptr_t>(g.q[i].dense) % 16 == 0),
+                  "%s: prepared bf16 copy of segment %u too large or misaligned", name, i);
+  }
   PRG_CHECK_ARG(g.a_group == 0 && g.a_z == 0, "%s: Q4 GEMM takes plain [M, K] activations", name);
   switch (epi) {
     case kGemmStore: return launch_q4_t<kGemmStore>(s, g, name);

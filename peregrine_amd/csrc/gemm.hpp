@@ -42,6 +42,10 @@ struct GemmQ4 {
   uint16_t* c = nullptr;        // bf16 [M, n]
   uint32_t n = 0;
   uint32_t tile0 = 0;           // first output tile of the segment (set by the launcher)
+  // Optional prepared copy bf16 [n, K] = dequantised w (launch_dequant_dense).
+  // When every segment has one, the kernel stages it instead of
+  // dequantising per tile; the results are the same bit for bit.
+  const uint16_t* dense = nullptr;
 };
 
 struct GemmArgs {
@@ -69,6 +73,10 @@ struct GemmArgs {
 // Q4 weights in g.q[0..nq). K % 64 == 0; A rows 16-byte aligned (lda % 8 == 0).
 // The residual epilogue reads g.res [M, q[0].n].
 int launch_gemm_q4(hipStream_t s, GemmArgs g, int epi, const char* name);
+// Prepared bf16 copy out [n, K] of Q4 weights (w, sc, bi): the values the Q4
+// GEMM dequantises per tile.
+int launch_dequant_dense(hipStream_t s, const uint32_t* w, const uint16_t* sc, const uint16_t* bi, uint16_t* out,
+                         uint32_t n, uint32_t K, const char* name);
 // bf16 B, `batch` independent problems along grid.z (offsets a_z, b_z, c_z).
 int launch_gemm_bf16(hipStream_t s, const GemmArgs& g, int epi, uint32_t batch, const char* name);
 

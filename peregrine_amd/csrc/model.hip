@@ -598,8 +598,51 @@ int prg_model_create_random(const PrgModelConfig* cfg, uint64_t seed, PrgModel**
 void prg_model_destroy(PrgModel* model) {
   if (!model) return;
   (void)hipFree(model->arena);
+  (void)hipFree(model->dense_arena);
   delete model;
 }
+
+// The reference's prepared dense RHS for the prompt path
+// (block_attn.zig:143-215, linear_q4.denseRhsBf16ByteLen): every Q4 matrix
+// the prompt GEMMs read, dequantised once into bf16 [out, in].
+int prg_model_prepare_dense(PrgModel* model) {
+  PRG_CHECK_ARG(model, "prg_model_prepare_dense: null model");
+  std::vector<Q4Linear*> lins;
+  auto add_layer = [&](DecoderLayer& L) {
+    if (L.linear) {
+      for (Q4Linear* q : {&L.lin.in_qkv, &L.lin.in_z, &L.lin.in_a, &L.lin.in_b, &L.lin.out_proj}) lins.push_back(q);
+    } else {
+      for (Q4Linear* q : {&L.full.q_proj, &L.full.k_proj, &L.full.v_proj, &L.full.o_proj}) lins.push_back(q);
+    }
+    for (Q4Linear* q : {&L.mlp.gate_proj, &L.mlp.up_proj, &L.mlp.down_proj}) lins.push_back(q);
+  };
+  for (DecoderLayer& L : model->layers) add_layer(L);
+  if (model->mtp.present) {
+    lins.push_back(&model->mtp.fc);
+    add_layer(model->mtp.layer);
+  }
+  size_t total = 0;
+  for (const Q4Linear* q : lins) total += align_up(static_cast<size_t>(q->out_dim) * q->in_dim * 2, kAlign);
+  if (!model->dense_arena) {
+    void* p = nullptr;
+    if (hipMalloc(&p, total) != hipSuccess)
+      return set_error(PRG_ERR_OOM, "prg_model_prepare_dense: %zu bytes", total);
+    model->dense_arena = static_cast<uint8_t*>(p);
+    model->dense_bytes = total;
+  }
+  size_t off = 0;
+  for (Q4Linear* q : lins) {
+    q->dense = reinterpret_cast<uint16_t*>(model->dense_arena + off);
+    if (int rc = launch_dequant_dense(nullptr, q->weight, q->scales, q->biases, q->dense, q->out_dim, q->in_dim,
+                                      "prg_model_prepare_dense"))
+      return rc;
+    off += align_up(static_cast<size_t>(q->out_dim) * q->in_dim * 2, kAlign);
+  }
+  PRG_HIP(hipDeviceSynchronize());
+  return PRG_OK;
+}
+
+size_t prg_model_dense_bytes(const PrgModel* model) { return model ? model->dense_bytes : 0; }
 
 size_t prg_model_weight_bytes(const PrgModel* model) { return model ? model->arena_bytes : 0; }
 

@@ -36,6 +36,9 @@ struct Q4Linear {
   uint16_t* scales = nullptr;
   uint16_t* biases = nullptr;
   uint32_t out_dim = 0, in_dim = 0;
+  // Prepared bf16 [out_dim, in_dim] copy for the prompt GEMMs (inside
+  // PrgModel::dense_arena; null until prg_model_prepare_dense).
+  uint16_t* dense = nullptr;
 };
 
 struct LinearAttentionBlock {
@@ -154,6 +157,9 @@ struct PrgModel {
   uint16_t* final_norm = nullptr;
   prg::Q4Linear lm_head;
   prg::MtpWeights mtp;
+  // Prepared bf16 copies of the prompt GEMMs' weights (prg_model_prepare_dense).
+  uint8_t* dense_arena = nullptr;
+  size_t dense_bytes = 0;
 };
 
 struct PrgModelState {

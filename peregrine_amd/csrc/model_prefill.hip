@@ -91,10 +91,10 @@ int qmm(hipStream_t s, const uint16_t* x, const Q4Linear& l, uint16_t* out, uint
   GemmArgs g;
   g.a = x;
   g.lda = l.in_dim;
-  g.q[0] = GemmQ4{l.weight, l.scales, l.biases, out, l.out_dim, 0};
+  g.q[0] = GemmQ4{l.weight, l.scales, l.biases, out, l.out_dim, 0, l.dense};
   g.nq = 1;
   if (up) {
-    g.q[1] = GemmQ4{up->weight, up->scales, up->biases, nullptr, up->out_dim, 0};
+    g.q[1] = GemmQ4{up->weight, up->scales, up->biases, nullptr, up->out_dim, 0, up->dense};
     g.nq = 2;
   }
   g.res = res;
@@ -112,7 +112,7 @@ int qmm_multi(hipStream_t s, const uint16_t* x, uint32_t K, uint32_t T, std::ini
   g.lda = K;
   for (const auto& sg : segs) {
     const Q4Linear& l = *sg.first;
-    g.q[g.nq++] = GemmQ4{l.weight, l.scales, l.biases, sg.second, l.out_dim, 0};
+    g.q[g.nq++] = GemmQ4{l.weight, l.scales, l.biases, sg.second, l.out_dim, 0, l.dense};
   }
   g.M = T;
   g.K = K;

@@ -99,6 +99,13 @@ class DeviceModel:
     def weight_bytes(self) -> int:
         return int(lib.prg_model_weight_bytes(self.handle))
 
+    # block_attn.zig:143-215 prepared dense RHS
+    def prepare_dense(self) -> int:
+        """Dequantise every prompt-GEMM weight once into a bf16 copy (the
+        prefill then stages it as is); returns its size in bytes."""
+        call("prg_model_prepare_dense", self.handle)
+        return int(lib.prg_model_dense_bytes(self.handle))
+
     def tensor_ptr(self, name: str) -> tuple[int, int]:
         return _tensor("prg_model_tensor", self.handle, name, None)
 

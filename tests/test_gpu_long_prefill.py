@@ -88,3 +88,40 @@ def test_long_context_stride_and_score_block_shrink(m9b, monkeypatch):
     assert ModelState(m9b, max_seq=15000).stride == 15104  # below 16000: aligned to 256
     prompt = np.random.default_rng(2).integers(0, 248320, size=9000).astype(np.uint32)
     _compare(m9b, prompt, 16000, [None, 512], monkeypatch)
+
+
+def test_prepared_dense_prefill_is_identical(m9b, monkeypatch):
+    """The prepared dense route (prg_model_prepare_dense; the reference's
+    prepared dense RHS, block_attn.zig:143-215) stages bf16 copies of the
+    weights that hold exactly the values the Q4 GEMM dequantises per tile, so
+    a 1600-token prefill leaves the same next token, GDN states and KV caches
+    bit for bit, and the same decoded tokens. Runs last in this module: the
+    shared model keeps its dense copies afterwards."""
+    import time
+
+    from peregrine_amd.device import synchronize
+
+    prompt = np.random.default_rng(5).integers(0, 248320, size=1600).astype(np.uint32)
+    a = _state(m9b, 2048, None, monkeypatch)
+    b = _state(m9b, 2048, None, monkeypatch)
+    a.prefill(prompt)  # warm
+    synchronize()
+    t0 = time.perf_counter()
+    fa = a.prefill(prompt)
+    synchronize()
+    t1 = time.perf_counter()
+    nbytes = m9b.prepare_dense()
+    assert nbytes > 13 * 10**9  # every prompt GEMM weight as bf16 (13.8 GB at the 9B shape)
+    b.prefill(prompt)
+    synchronize()
+    t2 = time.perf_counter()
+    fb = b.prefill(prompt)
+    synchronize()
+    t3 = time.perf_counter()
+    print(f"[dense] 1600-token prefill {1e3 * (t1 - t0):.1f} ms Q4 -> {1e3 * (t3 - t2):.1f} ms dense "
+          f"({nbytes / 2**30:.1f} GiB prepared)", flush=True)
+    assert fa == fb
+    _same_states(a, b, m9b, len(prompt))
+    np.testing.assert_array_equal(a.decode(4)[0], b.decode(4)[0])
+    a.close()
+    b.close()
