@@ -44,10 +44,12 @@ __host__ __device__ inline float bf2f(uint16_t b) {
 }
 
 __host__ __device__ inline uint16_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+  const uint32_t u = __float_as_uint(f);
+  // both results, then a select: a NaN branch would split the caller's code
+  // into basic blocks (and its memory waits with them)
+  const uint32_t nan = (u >> 16) | 0x40u;
+  const uint32_t rne = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  return static_cast<uint16_t>((u & 0x7fffffffu) > 0x7f800000u ? nan : rne);
 }
 
 // Round an f32 to the nearest bf16 value and return it as f32.

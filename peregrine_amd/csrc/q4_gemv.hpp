@@ -151,8 +151,8 @@ __device__ inline void unpack_q4_word(uint32_t word, uint32_t (&t)[4]) {
 template <int NMAT, int ROWS, int ITERS>
 struct GemvBuf {
   u32x4 w[NMAT][ROWS][ITERS];
-  uint32_t sc[NMAT][ROWS][ITERS];  // bf16 scale bits (zero-extended)
-  uint32_t bi[NMAT][ROWS][ITERS];  // bf16 bias bits (zero-extended)
+  uint16_t sc[NMAT][ROWS][ITERS];  // bf16 scale bits, widened where they are used
+  uint16_t bi[NMAT][ROWS][ITERS];  // bf16 bias bits
 };
 
 // Where group g of the launch lives: segment index and first row.
@@ -190,8 +190,8 @@ __device__ inline void gemv_load(const GemvParams& p, uint32_t g, int lane, bool
           b.bi[mat][r][it] = sg.b[mat][meta + it * (kGemvKStep / 64)];
         } else {
           b.w[mat][r][it] = u32x4{0u, 0u, 0u, 0u};
-          b.sc[mat][r][it] = 0u;
-          b.bi[mat][r][it] = 0u;
+          b.sc[mat][r][it] = 0;
+          b.bi[mat][r][it] = 0;
         }
       }
     }
@@ -257,8 +257,8 @@ __device__ inline void gemv_dot_step(const GemvBuf<NMAT, ROWS, ITERS>& b, int it
           for (int c = 0; c < 4; ++c) aq[m][c & 1] = dot2_bf16(t[c], x.xp[m][4 * j + c], aq[m][c & 1]);
         }
       }
-      const float sc = bf_lo(b.sc[mat][r][it]);
-      const float bi = bf_lo(b.bi[mat][r][it]);
+      const float sc = bf_lo(static_cast<uint32_t>(b.sc[mat][r][it]));
+      const float bi = bf_lo(static_cast<uint32_t>(b.bi[mat][r][it]));
 #pragma unroll
       for (int m = 0; m < M; ++m) {
         const float qx = aq[m][0] + aq[m][1];  // sum(q * x)
@@ -465,7 +465,7 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(const GemvParams 
   constexpr int NMAT = (EPI == kEpiSiluGate) ? 2 : 1;
   constexpr bool XREG = ITERS * M <= 4;  // <= 64 VGPRs of activation pairs
   extern __shared__ uint32_t xs[];  // [M][K/2] permuted bf16 pairs
-  __shared__ float red[kGemvWaves];
+  __shared__ float red[M * kGemvWaves];  // per activation row: the waves' sums of squares
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform
@@ -475,7 +475,11 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(const GemvParams 
   const uint32_t n8 = p.K / 8;
 
   // 1) activations (+ norm weights, + gates): one uint4 (8 values) per thread
-  // per K-step.
+  // per K-step. Without a K tail (K == ITERS * 2048) every thread's units
+  // exist, and these loads and the first group's (below) are issued on
+  // straight-line code: behind a branch the compiler's wait before the
+  // staging would also cover the first group's weights, so the staging (and
+  // the norm's reductions) would start only when those arrive.
   constexpr int XU = (ITERS * (kGemvKStep / 8) + kGemvThreads - 1) / kGemvThreads;  // uint4 units per thread
   uint4 xv[M][XU];
   uint4 nw[NORM != kNormNone ? XU : 1];
@@ -483,19 +487,33 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(const GemvParams 
 #pragma unroll
   for (int it = 0; it < XU; ++it) {
     const uint32_t gi = it * kGemvThreads + threadIdx.x;
+    const bool in_k = !TAIL || gi < n8;
 #pragma unroll
-    for (int m = 0; m < M; ++m)
-      xv[m][it] = gi < n8 ? reinterpret_cast<const uint4*>(p.x[m])[gi] : make_uint4(0, 0, 0, 0);
-    if constexpr (NORM == kNormRms)
-      nw[it] = gi < n8 ? reinterpret_cast<const uint4*>(p.norm_w)[gi] : make_uint4(0, 0, 0, 0);
+    for (int m = 0; m < M; ++m) {
+      if constexpr (TAIL)
+        xv[m][it] = in_k ? reinterpret_cast<const uint4*>(p.x[m])[gi] : make_uint4(0, 0, 0, 0);
+      else
+        xv[m][it] = reinterpret_cast<const uint4*>(p.x[m])[gi];
+    }
+    if constexpr (NORM == kNormRms) {
+      if constexpr (TAIL)
+        nw[it] = in_k ? reinterpret_cast<const uint4*>(p.norm_w)[gi] : make_uint4(0, 0, 0, 0);
+      else
+        nw[it] = reinterpret_cast<const uint4*>(p.norm_w)[gi];
+    }
     if constexpr (NORM == kNormGated) {
       // 8 values of head gi / 16: weight entries 8 (gi % 16) .. +8 of the [128] vector.
       nw[it] = reinterpret_cast<const uint4*>(p.norm_w)[gi % (kGdnDv / 8)];
 #pragma unroll
       for (int m = 0; m < M; ++m) {
-        zv[m][it][0] = zv[m][it][1] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (gi < n8) {
-          const float4* zp = reinterpret_cast<const float4*>(p.gz[m]) + 2 * gi;
+        const float4* zp = reinterpret_cast<const float4*>(p.gz[m]) + 2 * gi;
+        if constexpr (TAIL) {
+          zv[m][it][0] = zv[m][it][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+          if (in_k) {
+            zv[m][it][0] = zp[0];
+            zv[m][it][1] = zp[1];
+          }
+        } else {
           zv[m][it][0] = zp[0];
           zv[m][it][1] = zp[1];
         }
@@ -503,12 +521,14 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(const GemvParams 
     }
   }
 
-  // 2) the first group's weights. The wave handles n groups (wave-uniform).
+  // 2) the first group's weights. The wave handles n groups (wave-uniform);
+  // a wave with none (the grid's last block only) loads the last group and
+  // leaves it unused, so the load needs no branch.
   constexpr bool kRounds = (ROWS == 1 && EPI != kEpiArgmax);
   GemvBuf<NMAT, ROWS, ITERS> b0, b1;
   uint32_t g = blockIdx.x * kGemvWaves + wid;
   uint32_t n = g < G ? (G - 1 - g) / W + 1 : 0;
-  if (n > 0) gemv_load<NMAT, ROWS, ITERS, TAIL>(p, g, lane, tail_active, b0);
+  gemv_load<NMAT, ROWS, ITERS, TAIL>(p, g < G ? g : G - 1, lane, tail_active, b0);
 
   // 3) stage x into LDS (normalised with NORM), then into registers.
 #pragma unroll
@@ -526,7 +546,13 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(const GemvParams 
           ss = __fmaf_rn(b, b, ss);
         }
       }
-      const float total = block_sum<kGemvThreads>(ss, red);
+      // one barrier: DPP row sums + readlane per wave, then the four wave
+      // sums from LDS (each activation row has its own slots)
+      ss = wave_sum_uniform(ss);
+      if (lane == 0) red[m * kGemvWaves + wid] = ss;
+      __syncthreads();
+      const float total = (red[m * kGemvWaves + 0] + red[m * kGemvWaves + 1]) +
+                          (red[m * kGemvWaves + 2] + red[m * kGemvWaves + 3]);
       scale = 1.0f / sqrtf(__fadd_rn(total / static_cast<float>(p.K), p.eps));
     }
     uint4* dst = reinterpret_cast<uint4*>(xs + m * (p.K / 2));
@@ -544,8 +570,9 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(const GemvParams 
           ss = __fmaf_rn(b, b, ss);
         }
         const float hscale = rsqrtf(__fadd_rn(__fmul_rn(row16_sum(ss), 1.0f / kGdnDv), p.eps));
-        if (gi < n8) dst[gi] = permute_pairs(gated_rms_apply(xv[m][it], nw[it], zv[m][it][0], zv[m][it][1], hscale));
-      } else if (gi < n8) {
+        if (!TAIL || gi < n8)
+          dst[gi] = permute_pairs(gated_rms_apply(xv[m][it], nw[it], zv[m][it][0], zv[m][it][1], hscale));
+      } else if (!TAIL || gi < n8) {
         if constexpr (NORM == kNormRms)
           dst[gi] = permute_pairs(rms_apply(xv[m][it], nw[it], scale));
         else
@@ -553,7 +580,11 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(const GemvParams 
       }
     }
   }
+  // Keep the first group's scale / bias register copies below the barrier:
+  // moved above it they would make every wave wait for that group's loads.
+  __builtin_amdgcn_sched_barrier(0);
   __syncthreads();
+  __builtin_amdgcn_sched_barrier(0);
 
   XStep<M> xr[XREG ? ITERS : 1];
   if constexpr (XREG) {
