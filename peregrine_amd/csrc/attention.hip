@@ -225,6 +225,12 @@ __device__ inline void norm_rope_heads(const float (&x)[4], float wt, uint32_t p
   }
 }
 
+// FRESH: the decode-step form (packed_q set). Every load that does not depend
+// on the step scalars (q, the norm weights, the new tokens' k / v) is issued
+// first, then the K / V tile of the split, all on straight-line code: behind
+// a branch the compiler's wait at the join would also cover the loads issued
+// before it, so q would be prepared only once the K / V tile had arrived.
+template <bool FRESH>
 __global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnDecodeArgs a0) {
   extern __shared__ float sc[];  // [4][split_tokens + 2] scores, then probabilities
   __shared__ float mh[kAttnGroup], lh[kAttnGroup];
@@ -237,6 +243,24 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnD
 
   const uint32_t kvh = blockIdx.y;
   const uint32_t split = blockIdx.x;
+  const uint32_t col = threadIdx.x;
+  // q of the group's 4 heads (one dim per thread), its norm weight, and the
+  // new tokens' raw k / v (row 1 repeats row 0 when the launch has one row)
+  float xq[kAttnGroup], xk[2] = {0.0f, 0.0f}, wq = 0.0f, wk = 0.0f;
+  uint16_t vb[2] = {0, 0};
+  if constexpr (FRESH) {
+#pragma unroll
+    for (int g = 0; g < static_cast<int>(kAttnGroup); ++g)
+      xq[g] = bf2f(a.packed_q[(static_cast<size_t>(kvh) * kAttnGroup + g) * 2 * kAttnHeadDim + col]);
+    wq = bf2f(a.q_norm[col]);
+    wk = bf2f(a0.k_norm[col]);
+#pragma unroll
+    for (uint32_t j = 0; j < 2; ++j) {
+      const uint32_t jr = min(j, a0.rows - 1);
+      xk[j] = bf2f(a0.k_in[(static_cast<size_t>(jr) * kAttnKvHeads + kvh) * kAttnHeadDim + col]);
+      vb[j] = a0.v_in[(static_cast<size_t>(jr) * kAttnKvHeads + kvh) * kAttnHeadDim + col];
+    }
+  }
   const uint32_t L = attn_cached_tokens(a0);
   uint32_t chunk = (L + a.nsplit - 1) / a.nsplit;
   chunk = (chunk + kAttnChunkAlign - 1) & ~(kAttnChunkAlign - 1);
@@ -247,7 +271,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnD
   const size_t head_stride = static_cast<size_t>(a.nsplit) * kAttnPartialStride;
   // In the decode-step form the new tokens of rows 0..row are extra tokens of
   // the split that holds the last cached token (split 0 on an empty cache).
-  const bool fresh = a.packed_q != nullptr;
+  constexpr bool fresh = FRESH;
   const uint32_t last = L == 0 ? 0u : (L - 1) / chunk;
   const uint32_t nx = (fresh && split == last) ? row + 1 : 0u;
 
@@ -268,23 +292,23 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnD
   const int rr = lane >> 3, ts = lane & 7;
   const uint16_t* kbase = a.key_cache + static_cast<size_t>(kvh) * a.stride * kAttnHeadDim + 16 * jd;
   const uint16_t* vbase = a.value_cache + (static_cast<size_t>(kvh) * kAttnHeadDim + 64 * w + rr) * a.stride;
+  // The first 64-token K / V tile of the range (the whole range when T <= 64)
+  // is loaded unconditionally: rows and tokens past T read clamped in-bounds
+  // cache slots (which may hold anything) and are never used. Longer ranges
+  // take it as their first tile.
   uint4 kt[4][2], vt[8];
-  if (one_tile) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t tt = 4 * w + r + 16 * i;
-      kt[i][0] = kt[i][1] = make_uint4(0, 0, 0, 0);
-      if (tt < T) {
-        const uint4* kp = reinterpret_cast<const uint4*>(kbase + static_cast<size_t>(t0 + tt) * kAttnHeadDim);
-        kt[i][0] = kp[0];
-        kt[i][1] = kp[1];
-      }
-    }
-    if (static_cast<uint32_t>(8 * ts) < T) {
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t tt = min(t0 + 4 * w + r + 16 * i, a.stride - 1);
+    const uint4* kp = reinterpret_cast<const uint4*>(kbase + static_cast<size_t>(tt) * kAttnHeadDim);
+    kt[i][0] = kp[0];
+    kt[i][1] = kp[1];
+  }
+  {
+    const uint32_t tv = min(t0 + 8 * ts, a.stride - 8);
 #pragma unroll
-      for (int p = 0; p < 8; ++p)
-        vt[p] = *reinterpret_cast<const uint4*>(vbase + static_cast<size_t>(8 * p) * a.stride + t0 + 8 * ts);
-    }
+    for (int p = 0; p < 8; ++p)
+      vt[p] = *reinterpret_cast<const uint4*>(vbase + static_cast<size_t>(8 * p) * a.stride + tv);
   }
 
   // ---- decode-step form: q of the group's 4 heads (one dim per thread, as
@@ -292,31 +316,30 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnD
   // new tokens' k (normalised + rotated) and v, appended to the cache by the
   // block of their own row.
   uint32_t qd[kAttnGroup][8];
-  if (fresh) {
-    const uint32_t col = threadIdx.x;
-    float xq[4];
+  if constexpr (FRESH) {
+    // positions of the new tokens (row 1 repeats row 0 when there is one row)
+    uint32_t npos[2], ncpos[2];
 #pragma unroll
-    for (int g = 0; g < static_cast<int>(kAttnGroup); ++g)
-      xq[g] = bf2f(a.packed_q[(static_cast<size_t>(kvh) * kAttnGroup + g) * 2 * kAttnHeadDim + col]);
-    const float wq = bf2f(a.q_norm[col]);
-    float xk[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    uint16_t vb[2] = {0, 0};
-    for (uint32_t j = 0; j < nx; ++j) {
-      xk[j] = bf2f(a0.k_in[(static_cast<size_t>(j) * kAttnKvHeads + kvh) * kAttnHeadDim + col]);
-      vb[j] = a0.v_in[(static_cast<size_t>(j) * kAttnKvHeads + kvh) * kAttnHeadDim + col];
+    for (uint32_t j = 0; j < 2; ++j) {
+      const uint32_t jr = min(j, a0.rows - 1);
+      npos[j] = a0.step ? a0.step[jr].rope_pos : a0.rope_pos_host + j;
+      ncpos[j] = a0.step ? a0.step[jr].cache_pos : a0.cache_pos_host + j;
     }
-    const float wk = nx ? bf2f(a0.k_norm[col]) : 0.0f;
     norm_rope_heads<kAttnGroup>(xq, wq, a.step ? a.step->rope_pos : a.rope_pos_host, red, xch, qf);
-    for (uint32_t j = 0; j < nx; ++j) {
-      __syncthreads();  // red / xch reuse
-      const float xj[4] = {xk[j], 0.0f, 0.0f, 0.0f};
-      const uint32_t pos = a0.step ? a0.step[j].rope_pos : a0.rope_pos_host + j;
-      norm_rope_heads<1>(xj, wk, pos, red, xch, kf + j * kAttnHeadDim);
-      vf[j * kAttnHeadDim + col] = vb[j];
-      const uint32_t cpos = a0.step ? a0.step[j].cache_pos : a0.cache_pos_host + j;
-      if (j == row && cpos < a.stride) {
-        a.key_cache_w[(static_cast<size_t>(kvh) * a.stride + cpos) * kAttnHeadDim + col] = kf[j * kAttnHeadDim + col];
-        a.value_cache_w[(static_cast<size_t>(kvh) * kAttnHeadDim + col) * a.stride + cpos] = vb[j];
+    // unrolled with uniform guards (no loop back-edge), so the compiler's
+    // waits here cover the new tokens' k / v loads, not the K / V tile
+#pragma unroll
+    for (uint32_t j = 0; j < 2; ++j) {
+      if (j < nx) {
+        __syncthreads();  // red / xch reuse
+        const float xj[4] = {xk[j], 0.0f, 0.0f, 0.0f};
+        norm_rope_heads<1>(xj, wk, npos[j], red, xch, kf + j * kAttnHeadDim);
+        vf[j * kAttnHeadDim + col] = vb[j];
+        if (j == row && ncpos[j] < a.stride) {
+          a.key_cache_w[(static_cast<size_t>(kvh) * a.stride + ncpos[j]) * kAttnHeadDim + col] =
+              kf[j * kAttnHeadDim + col];
+          a.value_cache_w[(static_cast<size_t>(kvh) * kAttnHeadDim + col) * a.stride + ncpos[j]] = vb[j];
+        }
       }
     }
     __syncthreads();
@@ -362,9 +385,12 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnD
       if (4 * w + 16 * i < T) score(tt, kt[i][0], kt[i][1], tt < T);
     }
   } else {
+    // The first 64 tokens (all valid: T > 64) from the preloaded tile.
+#pragma unroll
+    for (int i = 0; i < 4; ++i) score(4 * w + r + 16 * i, kt[i][0], kt[i][1], true);
     // Four tokens per lane per pass: all eight K loads are issued before the
     // first dot product, so a wave keeps 8 KiB of K in flight.
-    uint32_t tt = 4 * w + r;
+    uint32_t tt = 4 * w + r + 64;
     for (; tt + 48 < T; tt += 64) {
       uint4 k4[4][2];
 #pragma unroll
@@ -390,15 +416,16 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnD
   // are issued here, so they stream in while phase 2 runs.
   const bool vpre = !one_tile && T >= 128;
   uint4 v2[2][8];
-  auto load_v2 = [&](uint32_t tb) {
+  auto load_v2 = [&](uint32_t tb, bool first) {  // first: tile 0 is the preloaded one
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
       for (int p = 0; p < 8; ++p)
-        v2[h][p] = *reinterpret_cast<const uint4*>(vbase + static_cast<size_t>(8 * p) * a.stride + t0 + tb +
-                                                   64 * h + 8 * ts);
+        v2[h][p] = (first && h == 0) ? vt[p]
+                                     : *reinterpret_cast<const uint4*>(vbase + static_cast<size_t>(8 * p) * a.stride +
+                                                                       t0 + tb + 64 * h + 8 * ts);
   };
-  if (vpre) load_v2(0);
+  if (vpre) load_v2(0, true);
   __syncthreads();
 
   // ---- phase 2: softmax statistics, wave g owns head g.
@@ -433,7 +460,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnD
     // Two full 64-token tiles per pass: all sixteen V loads are issued before
     // the first FMA, so a wave keeps 16 KiB of V in flight.
     for (; tb0 + 128 <= T; tb0 += 128) {
-      if (tb0 > 0) load_v2(tb0);  // the first pair was loaded before phase 2
+      if (tb0 > 0) load_v2(tb0, false);  // the first pair was loaded before phase 2
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const uint32_t tl = tb0 + 64 * h + 8 * ts;
@@ -469,7 +496,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnD
 #pragma unroll
       for (int i = 0; i < 8; ++i) pv[g][i] = (static_cast<uint32_t>(i) < nvalid) ? sc[g * ld + tl + i] : 0.0f;
     uint4 vv[8];
-    if (one_tile) {
+    if (tb == 0) {  // the preloaded first tile
 #pragma unroll
       for (int p = 0; p < 8; ++p) vv[p] = vt[p];
     } else {
@@ -540,40 +567,58 @@ __global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(const AttnDec
   const uint32_t d = 64 * qt + t;
   const bool fresh = a0.packed_q != nullptr;
   const float* base = a.partials + static_cast<size_t>(h) * a.nsplit * kAttnPartialStride;
-  const uint32_t L = attn_cached_tokens(a0);
-  // splits holding tokens (on an empty cache, split 0 holds the new tokens)
-  uint32_t nact = fresh ? 1u : 0u;
-  if (L > 0) {
-    uint32_t chunk = (L + a.nsplit - 1) / a.nsplit;
-    chunk = (chunk + kAttnChunkAlign - 1) & ~(kAttnChunkAlign - 1);
-    nact = min(a.nsplit, (L + chunk - 1) / chunk);
-  }
-  // accumulators of a short cache are loaded up front with the statistics
+  const uint16_t* gsrc = fresh ? a.packed_q + static_cast<size_t>(h) * 2 * kAttnHeadDim + kAttnHeadDim
+                               : a.gate + static_cast<size_t>(h) * kAttnHeadDim;
+  const uint16_t gbits = gsrc[d];
   constexpr uint32_t kPre = 64;
-  float pre[kPre];
+  float acc = 0.0f, den;
+  if (a.nsplit <= kPre) {
+    // Every split, read up front: a split without tokens holds the neutral
+    // partial (m = -inf, denominator and accumulators 0), which adds exact
+    // zeros, so no sequence length (a dependent load) is needed first.
+    float pre[kPre];
 #pragma unroll
-  for (uint32_t c = 0; c < kPre; ++c) pre[c] = c < nact ? base[c * kAttnPartialStride + 2 + d] : 0.0f;
-  const uint16_t gbits = fresh ? a.packed_q[static_cast<size_t>(h) * 2 * kAttnHeadDim + kAttnHeadDim + d]
-                               : a.gate[static_cast<size_t>(h) * kAttnHeadDim + d];
-  float m_local = -INFINITY;
-  for (uint32_t c = t; c < nact; c += kMergeThreads) m_local = fmaxf(m_local, base[c * kAttnPartialStride]);
-
-  const float m_all = wave_max_dpp(m_local);
-  float den_local = 0.0f;
-  for (uint32_t c = t; c < nact; c += kMergeThreads) {
-    const float mc = base[c * kAttnPartialStride];
+    for (uint32_t c = 0; c < kPre; ++c) pre[c] = c < a.nsplit ? base[c * kAttnPartialStride + 2 + d] : 0.0f;
+    const float mc = t < a.nsplit ? base[t * kAttnPartialStride] : -INFINITY;
+    const float lc = t < a.nsplit ? base[t * kAttnPartialStride + 1] : 0.0f;
+    const float m_all = wave_max_dpp(mc);
     const float wgt = (mc == -INFINITY) ? 0.0f : expf(mc - m_all);
-    wsh[c] = wgt;
-    den_local += base[c * kAttnPartialStride + 1] * wgt;
-  }
-  const float den = wave_sum_dpp(den_local);
-  __syncthreads();  // wsh
-  float acc = 0.0f;
+    wsh[t] = wgt;
+    den = wave_sum_dpp(lc * wgt);
+    __syncthreads();  // wsh
 #pragma unroll
-  for (uint32_t c = 0; c < kPre; ++c)
-    if (c < nact) acc += pre[c] * wsh[c];
+    for (uint32_t c = 0; c < kPre; ++c)
+      if (c < a.nsplit) acc += pre[c] * wsh[c];
+  } else {
+    // splits holding tokens (on an empty cache, split 0 holds the new tokens)
+    const uint32_t L = attn_cached_tokens(a0);
+    uint32_t nact = fresh ? 1u : 0u;
+    if (L > 0) {
+      uint32_t chunk = (L + a.nsplit - 1) / a.nsplit;
+      chunk = (chunk + kAttnChunkAlign - 1) & ~(kAttnChunkAlign - 1);
+      nact = min(a.nsplit, (L + chunk - 1) / chunk);
+    }
+    float pre[kPre];
+#pragma unroll
+    for (uint32_t c = 0; c < kPre; ++c) pre[c] = c < nact ? base[c * kAttnPartialStride + 2 + d] : 0.0f;
+    float m_local = -INFINITY;
+    for (uint32_t c = t; c < nact; c += kMergeThreads) m_local = fmaxf(m_local, base[c * kAttnPartialStride]);
+    const float m_all = wave_max_dpp(m_local);
+    float den_local = 0.0f;
+    for (uint32_t c = t; c < nact; c += kMergeThreads) {
+      const float mc = base[c * kAttnPartialStride];
+      const float wgt = (mc == -INFINITY) ? 0.0f : expf(mc - m_all);
+      wsh[c] = wgt;
+      den_local += base[c * kAttnPartialStride + 1] * wgt;
+    }
+    den = wave_sum_dpp(den_local);
+    __syncthreads();  // wsh
+#pragma unroll
+    for (uint32_t c = 0; c < kPre; ++c)
+      if (c < nact) acc += pre[c] * wsh[c];
 #pragma unroll 8
-  for (uint32_t c = kPre; c < nact; ++c) acc += base[c * kAttnPartialStride + 2 + d] * wsh[c];
+    for (uint32_t c = kPre; c < nact; ++c) acc += base[c * kAttnPartialStride + 2 + d] * wsh[c];
+  }
   const size_t i = static_cast<size_t>(h) * kAttnHeadDim + d;
   const float sig = 1.0f / (1.0f + expf(-bf2f(gbits)));
   a.out[i] = f2bf((acc / den) * sig);
@@ -633,7 +678,12 @@ int launch_attn_decode(hipStream_t s, const AttnDecodeArgs& a) {
   if (a.packed_q && !(a.q_norm && a.k_in && a.v_in && a.k_norm && a.key_cache_w && a.value_cache_w))
     return set_error(PRG_ERR_INVALID_ARG, "attn_decode: the decode-step form needs every input");
   const size_t lds = static_cast<size_t>(kAttnGroup) * (a.split_tokens + 2) * sizeof(float);
-  hipLaunchKernelGGL(attn_partials_kernel, dim3(a.nsplit, kAttnKvHeads, a.rows), dim3(kAttnThreads), lds, s, a);
+  if (a.packed_q)
+    hipLaunchKernelGGL(attn_partials_kernel<true>, dim3(a.nsplit, kAttnKvHeads, a.rows), dim3(kAttnThreads), lds, s,
+                       a);
+  else
+    hipLaunchKernelGGL(attn_partials_kernel<false>, dim3(a.nsplit, kAttnKvHeads, a.rows), dim3(kAttnThreads), lds, s,
+                       a);
   PRG_CHECK_LAUNCH("attn_partials");
   hipLaunchKernelGGL(attn_merge_kernel, dim3(kAttnQHeads, kAttnHeadDim / kMergeThreads, a.rows), dim3(kMergeThreads),
                      0, s, a);

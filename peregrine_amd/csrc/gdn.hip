@@ -37,15 +37,43 @@ __device__ inline float hsum32(float v) { return group_sum<32>(v); }
 // multiply-add is an explicit __fmaf_rn / __fmul_rn / __fadd_rn, so both
 // kernels round identically (the two-token verify must equal two single
 // steps bit for bit).
+//
+// A token's inputs are loaded together, before any arithmetic and on
+// straight-line code, so the block pays one memory round trip for them (in
+// parallel with its state rows) instead of one per dependent step.
+template <int RPH>
+struct GdnIn {
+  uint16_t a, b, dt;  // per-head gate inputs (bf16 bits)
+  float alog;
+  uint2 q, k;         // this lane's 4 dk of the head's q and k
+  uint16_t v[RPH];    // the half-wave's rows of v
+};
+template <int RPH>
+__device__ inline GdnIn<RPH> gdn_load(const uint16_t* conv_out, const uint16_t* a, const uint16_t* bgate,
+                                      const float* A_log, const uint16_t* dt_bias, uint32_t hv, uint32_t hk,
+                                      int j, uint32_t row0) {
+  GdnIn<RPH> in;
+  in.a = a[hv];
+  in.b = bgate[hv];
+  in.dt = dt_bias[hv];
+  in.alog = A_log[hv];
+  in.q = *reinterpret_cast<const uint2*>(conv_out + hk * kGdnDk + 4 * j);
+  in.k = *reinterpret_cast<const uint2*>(conv_out + kGdnKeyDim + hk * kGdnDk + 4 * j);
+  const uint16_t* vsrc = conv_out + 2 * kGdnKeyDim + hv * kGdnDv + row0;
+#pragma unroll
+  for (int r = 0; r < RPH; ++r) in.v[r] = vsrc[r];
+  return in;
+}
+
 struct GdnGates {
   float decay, beta;
 };
 // gating_many_bf16 math (shaders/gated_norm.metal:247-268).
-__device__ inline GdnGates gdn_gates(const uint16_t* a, const uint16_t* bgate, const float* A_log,
-                                     const uint16_t* dt_bias, uint32_t hv) {
-  const float gx = __fadd_rn(bf2f(a[hv]), bf2f(dt_bias[hv]));
+template <int RPH>
+__device__ inline GdnGates gdn_gates(const GdnIn<RPH>& in) {
+  const float gx = __fadd_rn(bf2f(in.a), bf2f(in.dt));
   const float softplus = __fadd_rn(fmaxf(gx, 0.0f), logf(__fadd_rn(1.0f, expf(-fabsf(gx)))));
-  return GdnGates{expf(-__fmul_rn(expf(A_log[hv]), softplus)), 1.0f / __fadd_rn(1.0f, expf(-bf2f(bgate[hv])))};
+  return GdnGates{expf(-__fmul_rn(expf(in.alog), softplus)), 1.0f / __fadd_rn(1.0f, expf(-bf2f(in.b)))};
 }
 
 // q/k L2 norms (qk_l2norm_prefill_bf16 math, shaders/gated_norm.metal:191-245)
@@ -53,9 +81,7 @@ __device__ inline GdnGates gdn_gates(const uint16_t* a, const uint16_t* bgate, c
 struct GdnQK {
   float qn[4], kn[4], kq;
 };
-__device__ inline GdnQK gdn_qk(const uint16_t* conv_out, uint32_t hk, int j) {
-  const uint2 qv = *reinterpret_cast<const uint2*>(conv_out + hk * kGdnDk + 4 * j);
-  const uint2 kv = *reinterpret_cast<const uint2*>(conv_out + kGdnKeyDim + hk * kGdnDk + 4 * j);
+__device__ inline GdnQK gdn_qk(uint2 qv, uint2 kv) {
   const float q[4] = {bf_lo(qv.x), bf_hi(qv.x), bf_lo(qv.y), bf_hi(qv.y)};
   const float k[4] = {bf_lo(kv.x), bf_hi(kv.x), bf_lo(kv.y), bf_hi(kv.y)};
   float qss = 0.f, kss = 0.f;
@@ -76,6 +102,12 @@ __device__ inline GdnQK gdn_qk(const uint16_t* conv_out, uint32_t hk, int j) {
   }
   r.kq = hsum32(kq);
   return r;
+}
+
+// S & keep bit for bit: keep = 0 gives +0.0 (a fresh sequence), ~0 leaves S.
+__device__ inline float4 gdn_mask(float4 S, uint32_t keep) {
+  return make_float4(__uint_as_float(__float_as_uint(S.x) & keep), __uint_as_float(__float_as_uint(S.y) & keep),
+                     __uint_as_float(__float_as_uint(S.z) & keep), __uint_as_float(__float_as_uint(S.w) & keep));
 }
 
 // One state row (this lane's 4 of its 128 dk): d = S*decay; kv = d.k;
@@ -128,18 +160,18 @@ __global__ __launch_bounds__(NT) void gdn_decode_kernel(
   float4* sout = reinterpret_cast<float4*>((IN_PLACE ? state : state_out) + row_off) + j;
 #pragma unroll
   for (int r = 0; r < RPH; ++r) S[r] = srow[r * (kGdnDk / 4)];
+  const GdnIn<RPH> in = gdn_load<RPH>(conv_out, a, bgate, A_log, dt_bias, hv, hk, j, row0);
+  // A fresh sequence ignores the stored state (it may hold anything): a mask,
+  // not a branch, so no wait for the state rows is forced here.
   const bool has_state = step ? (step->rope_pos != 0) : (has_state_host != 0);
-  if (!has_state) {  // a fresh sequence: the stored state is ignored (may hold anything)
-#pragma unroll
-    for (int r = 0; r < RPH; ++r) S[r] = make_float4(0.f, 0.f, 0.f, 0.f);
-  }
+  const uint32_t keep = has_state ? 0xffffffffu : 0u;
 
-  const GdnGates gates = gdn_gates(a, bgate, A_log, dt_bias, hv);
-  const GdnQK qk = gdn_qk(conv_out, hk, j);
-  const uint16_t* vsrc = conv_out + 2 * kGdnKeyDim + hv * kGdnDv + row0;
+  const GdnGates gates = gdn_gates(in);
+  const GdnQK qk = gdn_qk(in.q, in.k);
 #pragma unroll
   for (int r = 0; r < RPH; ++r) {
-    const uint16_t yb = gdn_row(S[r], qk, gates, bf2f(vsrc[r]));
+    S[r] = gdn_mask(S[r], keep);
+    const uint16_t yb = gdn_row(S[r], qk, gates, bf2f(in.v[r]));
     sout[r * (kGdnDk / 4)] = S[r];
     if (j == 0) {
       if constexpr (FUSE_NORM)
@@ -185,20 +217,22 @@ __global__ __launch_bounds__(NT) void gdn_decode2_kernel(
   float4 S[RPH];
 #pragma unroll
   for (int r = 0; r < RPH; ++r) S[r] = reinterpret_cast<const float4*>(state + row_off)[j + r * (kGdnDk / 4)];
+  GdnIn<RPH> in[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+    in[t] = gdn_load<RPH>(conv_out + t * kGdnConvDim, a + t * kGdnHv, bgate + t * kGdnHv, A_log, dt_bias, hv, hk, j,
+                          row0);
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
-    if (step[t].rope_pos == 0) {  // a fresh sequence: the incoming state is ignored
-#pragma unroll
-      for (int r = 0; r < RPH; ++r) S[r] = make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-    const uint16_t* co = conv_out + t * kGdnConvDim;
-    const GdnGates gates = gdn_gates(a + t * kGdnHv, bgate + t * kGdnHv, A_log, dt_bias, hv);
-    const GdnQK qk = gdn_qk(co, hk, j);
-    const uint16_t* vsrc = co + 2 * kGdnKeyDim + hv * kGdnDv + row0;
+    // a fresh sequence: the incoming state is ignored (mask, no branch)
+    const uint32_t keep = step[t].rope_pos != 0 ? 0xffffffffu : 0u;
+    const GdnGates gates = gdn_gates(in[t]);
+    const GdnQK qk = gdn_qk(in[t].q, in[t].k);
     float4* dst = reinterpret_cast<float4*>((t == 0 ? snap : state_out) + row_off) + j;
 #pragma unroll
     for (int r = 0; r < RPH; ++r) {
-      const uint16_t yb = gdn_row(S[r], qk, gates, bf2f(vsrc[r]));
+      S[r] = gdn_mask(S[r], keep);
+      const uint16_t yb = gdn_row(S[r], qk, gates, bf2f(in[t].v[r]));
       dst[r * (kGdnDk / 4)] = S[r];
       if (j == 0) y_out[t * kGdnValDim + hv * kGdnDv + row0 + r] = yb;
     }
