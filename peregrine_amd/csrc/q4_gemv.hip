@@ -152,14 +152,20 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_pairs_kernel(
   __shared__ uint32_t sp[kArgmaxThreads / 64];
   float bv = -INFINITY;
   uint32_t bp = 0xffffffffu;
-  constexpr int kU = 8;  // independent loads in flight per thread
+  // 32 independent loads per thread (clamped in bounds, masked after the
+  // load, no branches): the lm_head's 31040 partials take one memory round
+  // trip instead of one per batch.
+  constexpr int kU = 32;
   for (uint32_t base = threadIdx.x; base < n; base += kArgmaxThreads * kU) {
     float v[kU];
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
       const uint32_t p = base + u * kArgmaxThreads;
-      v[u] = p < n ? values[p] : -INFINITY;
+      v[u] = values[min(p, n - 1)];
     }
+#pragma unroll
+    for (int u = 0; u < kU; ++u)
+      if (base + u * kArgmaxThreads >= n) v[u] = -INFINITY;
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
       const uint32_t p = base + u * kArgmaxThreads;
