@@ -126,6 +126,32 @@ __device__ inline float row16_sum(float v) {
   return v;
 }
 
+// Sum of a float over all 64 lanes; the result is wave-uniform. Lanes of a
+// 16-lane row are combined with DPP (quad_perm, half-mirror, mirror), after
+// which all 16 hold the same bits; the 4 row sums are read with readlane.
+__device__ inline float wave_sum_uniform(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
+  const int iv = __builtin_bit_cast(int, v);
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 0));
+  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 32));
+  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 48));
+  return (r0 + r1) + (r2 + r3);
+}
+
+// Sum over a 256-thread block in a fixed order: wave_sum_uniform per wave,
+// then (w0 + w1) + (w2 + w3) from LDS. One barrier; red (4 floats) may be
+// written again only after another barrier. Every thread gets the total.
+__device__ inline float block_sum256_dpp(float v, float* red) {
+  v = wave_sum_uniform(v);
+  if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = v;
+  __syncthreads();
+  return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
 __device__ inline float silu(float g) { return g / (1.0f + expf(-g)); }
 __device__ inline float sigmoid(float g) { return 1.0f / (1.0f + expf(-g)); }
 

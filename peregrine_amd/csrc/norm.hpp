@@ -20,12 +20,13 @@ __device__ inline float rms_scale(const uint4* src, uint32_t n8, uint32_t hidden
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float a = bf_lo(d[i]), b = bf_hi(d[i]);
-      ss += a * a;
-      ss += b * b;
+      ss = __fmaf_rn(a, a, ss);
+      ss = __fmaf_rn(b, b, ss);
     }
   }
-  const float total = block_sum<kNormThreads>(ss, red);
-  return 1.0f / sqrtf(total / static_cast<float>(hidden) + eps);
+  static_assert(kNormThreads == 256, "block_sum256_dpp reduces a 256-thread block");
+  const float total = block_sum256_dpp(ss, red);
+  return 1.0f / sqrtf(__fadd_rn(total / static_cast<float>(hidden), eps));
 }
 
 // bf16(x * scale * w) for 8 values (reference order: (x * scale) * w).

@@ -101,22 +101,6 @@ __device__ inline float dot2_bf16(uint32_t a, uint32_t b, float c) {
                                          __builtin_bit_cast(bf16x2_t, b), c, false);
 }
 
-// Sum of a float over all 64 lanes; the result is wave-uniform. Lanes of a
-// 16-lane row are combined with DPP (quad_perm, half-mirror, mirror), after
-// which all 16 hold the same bits; the 4 row sums are read with readlane.
-__device__ inline float wave_sum_uniform(float v) {
-  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
-  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
-  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
-  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
-  const int iv = __builtin_bit_cast(int, v);
-  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 0));
-  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 16));
-  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 32));
-  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(iv, 48));
-  return (r0 + r1) + (r2 + r3);
-}
-
 // 8 bf16 (as a uint4 of pairs (x0,x1),(x2,x3),(x4,x5),(x6,x7)) -> the dot2
 // order of the nibble unpack below: (x0,x2),(x4,x6),(x1,x3),(x5,x7).
 __device__ inline uint4 permute_pairs(uint4 v) {
@@ -546,13 +530,9 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(const GemvParams 
           ss = __fmaf_rn(b, b, ss);
         }
       }
-      // one barrier: DPP row sums + readlane per wave, then the four wave
-      // sums from LDS (each activation row has its own slots)
-      ss = wave_sum_uniform(ss);
-      if (lane == 0) red[m * kGemvWaves + wid] = ss;
-      __syncthreads();
-      const float total = (red[m * kGemvWaves + 0] + red[m * kGemvWaves + 1]) +
-                          (red[m * kGemvWaves + 2] + red[m * kGemvWaves + 3]);
+      // one barrier per activation row (each has its own slots); the same
+      // reduction as the standalone RMSNorm, so both give identical bits
+      const float total = block_sum256_dpp(ss, red + m * kGemvWaves);
       scale = 1.0f / sqrtf(__fadd_rn(total / static_cast<float>(p.K), p.eps));
     }
     uint4* dst = reinterpret_cast<uint4*>(xs + m * (p.K / 2));

@@ -131,6 +131,38 @@ def test_silu_gate_parity(gpu, orc, N, K, M):
     assert_bf16_close(got, orc.q4_gemv_silu_gate(x, g, u), min_exact=0.9, what=f"silu {N}x{K}")
 
 
+@pytest.mark.parametrize("N,K", [(12288, 4096), (4096, 12288), (256, 6144)])
+def test_fused_norm_equals_standalone_norm(gpu, N, K):
+    """The GEMV's fused RMSNorm prologue and the standalone RMSNorm reduce in
+    the same order, so rmsnorm-then-GEMV equals the fused launch bit for bit
+    (plain and SiLU-pair epilogues). The model relies on it: decode fuses the
+    final norm into the lm_head, the two-token verify normalises first."""
+    from peregrine_amd._lib import call
+    from peregrine_amd.device import DeviceArray, ptr
+    from peregrine_amd.ops import gate_up_silu, rmsnorm
+
+    rng = np.random.default_rng(N + K)
+    wt, up = random_q4(rng, N, K), random_q4(rng, N, K)
+    x = random_bf16(rng, (1, K), std=3.0)
+    nw = random_bf16(rng, (K,), std=0.3, mean=1.0)
+    lin, lup = _lin(wt), _lin(up)
+    xd, nwd = _dev(x), _dev(nw)
+    normed = DeviceArray((1, K), np.uint16)
+    rmsnorm(xd, nwd, normed, K, 1, 1e-6)
+    ref = DeviceArray((1, N), np.uint16)
+    lin.encode_bf16_fast(normed, ref)
+    fused = DeviceArray((1, N), np.uint16)
+    call("prg_q4_gemv_norm_bf16", None, ptr(xd), ptr(nwd), 1e-6, *lin._wsb(), ptr(fused), N, K)
+    np.testing.assert_array_equal(fused.numpy(), ref.numpy())
+
+    ref2 = DeviceArray((1, N), np.uint16)
+    gate_up_silu(lin, lup, normed, ref2)
+    fused2 = DeviceArray((1, N), np.uint16)
+    call("prg_q4_gemv_silu_gate_norm_bf16", None, ptr(xd), ptr(nwd), 1e-6, *lin._wsb(), *lup._wsb(), ptr(fused2),
+         N, K)
+    np.testing.assert_array_equal(fused2.numpy(), ref2.numpy())
+
+
 def test_argmax_pairs_exact(gpu, orc):
     """Same partials in, same index out — ties, NaN, -inf, lengths."""
     from peregrine_amd.device import DeviceArray
