@@ -100,11 +100,10 @@ int encode_mtp_step(PrgModel* m, PrgModelState* st, const uint32_t* token_dev, c
   const PrgModelConfig& c = m->cfg;
   hipStream_t s = st->stream;
   const uint32_t H = c.hidden;
-  // encodePreFcRows: norm(embed(token)) ‖ norm(hidden) -> fc
-  if (int rc = launch_embedding(s, m->embed.weight, m->embed.scales, m->embed.biases, st->mtp_x, token_dev, 0, 1, H))
+  // encodePreFcRows: norm(embed(token)) ‖ norm(hidden) -> fc (one launch)
+  if (int rc = launch_embed_norm_pair(s, m->embed.weight, m->embed.scales, m->embed.biases, token_dev,
+                                     t.pre_fc_norm_embedding, hidden, t.pre_fc_norm_hidden, st->fc_in, H, c.rms_eps))
     return rc;
-  if (int rc = launch_rmsnorm(s, st->mtp_x, t.pre_fc_norm_embedding, st->fc_in, H, 1, c.rms_eps)) return rc;
-  if (int rc = launch_rmsnorm(s, hidden, t.pre_fc_norm_hidden, st->fc_in + H, H, 1, c.rms_eps)) return rc;
   GemvParams f = gemv_params(st->fc_in, 2 * H);
   add_seg(f, t.fc, st->mtp_h);
   if (int rc = run_gemv(s, f, kEpiPlain, kNormNone, "mtp.fc")) return rc;
@@ -138,9 +137,10 @@ int encode_verify(PrgModel* m, PrgModelState* st) {
   uint16_t* xa[2] = {st->h2a, st->h2a + H};
   uint16_t* xb[2] = {st->h2b, st->h2b + H};
   uint16_t* inter[2] = {st->inter2, st->inter2 + c.intermediate};
-  if (int rc = launch_embedding(s, m->embed.weight, m->embed.scales, m->embed.biases, xa[0], &sc->v0.token, 0, 1, H))
-    return rc;
-  if (int rc = launch_embedding(s, m->embed.weight, m->embed.scales, m->embed.biases, xa[1], &sc->v1.token, 0, 1, H))
+  // both rows' tokens in one launch (v0 and v1 are consecutive StepScalars; xa[1] = xa[0] + H)
+  static_assert(sizeof(StepScalars) % sizeof(uint32_t) == 0, "token stride");
+  if (int rc = launch_embedding(s, m->embed.weight, m->embed.scales, m->embed.biases, xa[0], &sc->v0.token, 0, 2, H,
+                                sizeof(StepScalars) / sizeof(uint32_t)))
     return rc;
   for (size_t i = 0; i < m->layers.size(); ++i) {
     const DecoderLayer& L = m->layers[i];
@@ -168,6 +168,8 @@ int encode_verify(PrgModel* m, PrgModelState* st) {
   p.seg[0].pidx[0] = st->pidx;
   p.seg[0].pval[1] = st->pval2;
   p.seg[0].pidx[1] = st->pidx2;
+  // (the norm stays a launch of its own: fused into this M = 2 prologue it
+  // measured 138 us against 126 + 4)
   if (int rc = launch_q4_gemv(s, p, 2, 8, kEpiArgmax, kNormNone, "lm_head.argmax2")) return rc;
   if (int rc = launch_argmax_pairs(s, st->pval, st->pidx, c.vocab / 8, &sc->verify)) return rc;
   return launch_argmax_pairs(s, st->pval2, st->pidx2, c.vocab / 8, &sc->bonus);

@@ -50,14 +50,9 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(
   for (uint32_t g = threadIdx.x; g < n8; g += kNormThreads) dst[g] = rms_apply(src[g], ws[g], scale);
 }
 
-__global__ void embedding_kernel(const uint32_t* __restrict__ w, const uint16_t* __restrict__ s,
-                                 const uint16_t* __restrict__ b, uint16_t* __restrict__ out,
-                                 const uint32_t* __restrict__ tokens, uint32_t token_host,
-                                 uint32_t hidden) {
-  // one thread per packed word (8 outputs); blockIdx.y = row of `tokens`
-  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= hidden / 8) return;
-  const uint32_t token = tokens ? tokens[blockIdx.y] : token_host;
+// The 8 bf16 of packed word i of row `token` of the Q4 table.
+__device__ inline uint4 embed_unit(const uint32_t* __restrict__ w, const uint16_t* __restrict__ s,
+                                   const uint16_t* __restrict__ b, uint32_t token, uint32_t i, uint32_t hidden) {
   const size_t words = hidden / 8, groups = hidden / 64;
   const uint32_t word = w[static_cast<size_t>(token) * words + i];
   const size_t meta = static_cast<size_t>(token) * groups + i / 8;
@@ -70,7 +65,59 @@ __global__ void embedding_kernel(const uint32_t* __restrict__ w, const uint16_t*
     const float hi = __fadd_rn(sc * static_cast<float>((word >> (8 * j + 4)) & 0xF), bi);
     o[j] = f2bf(lo) | (static_cast<uint32_t>(f2bf(hi)) << 16);
   }
-  reinterpret_cast<uint4*>(out + static_cast<size_t>(blockIdx.y) * hidden)[i] = make_uint4(o[0], o[1], o[2], o[3]);
+  return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+__global__ void embedding_kernel(const uint32_t* __restrict__ w, const uint16_t* __restrict__ s,
+                                 const uint16_t* __restrict__ b, uint16_t* __restrict__ out,
+                                 const uint32_t* __restrict__ tokens, uint32_t token_stride, uint32_t token_host,
+                                 uint32_t hidden) {
+  // one thread per packed word (8 outputs); blockIdx.y = row r, token tokens[r * token_stride]
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= hidden / 8) return;
+  const uint32_t token = tokens ? tokens[blockIdx.y * token_stride] : token_host;
+  reinterpret_cast<uint4*>(out + static_cast<size_t>(blockIdx.y) * hidden)[i] = embed_unit(w, s, b, token, i, hidden);
+}
+
+// Two RMSNorms in one launch, block 0: out[0, H) = rmsnorm(embedding(token),
+// w0); block 1: out[H, 2H) = rmsnorm(x1, w1). Same per-thread order and block
+// reduction as rmsnorm_kernel (rms_scale), so the bits equal the three
+// separate launches. The drafter's pre-fc rows (mtp.zig:200-212).
+constexpr int kPairUnits = 4;  // hidden <= 8 * 256 * kPairUnits
+__global__ __launch_bounds__(kNormThreads) void embed_norm_pair_kernel(
+    const uint32_t* __restrict__ ew, const uint16_t* __restrict__ es, const uint16_t* __restrict__ eb,
+    const uint32_t* __restrict__ token, const uint16_t* __restrict__ w0, const uint16_t* __restrict__ x1,
+    const uint16_t* __restrict__ w1, uint16_t* __restrict__ out, uint32_t hidden, float eps) {
+  __shared__ float red[kNormThreads / kWave];
+  const uint32_t n8 = hidden / 8;
+  const bool emb = blockIdx.x == 0;
+  const uint32_t tok = emb ? *token : 0u;
+  uint4 v[kPairUnits];
+  float ss = 0.0f;
+#pragma unroll
+  for (int u = 0; u < kPairUnits; ++u) {
+    const uint32_t g = threadIdx.x + u * kNormThreads;
+    v[u] = make_uint4(0, 0, 0, 0);
+    if (g < n8) {
+      v[u] = emb ? embed_unit(ew, es, eb, tok, g, hidden) : reinterpret_cast<const uint4*>(x1)[g];
+      const uint32_t d[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float a = bf_lo(d[i]), b = bf_hi(d[i]);
+        ss = __fmaf_rn(a, a, ss);
+        ss = __fmaf_rn(b, b, ss);
+      }
+    }
+  }
+  const float total = block_sum256_dpp(ss, red);
+  const float scale = 1.0f / sqrtf(__fadd_rn(total / static_cast<float>(hidden), eps));
+  const uint4* ws = reinterpret_cast<const uint4*>(emb ? w0 : w1);
+  uint4* dst = reinterpret_cast<uint4*>(out + (emb ? 0 : hidden));
+#pragma unroll
+  for (int u = 0; u < kPairUnits; ++u) {
+    const uint32_t g = threadIdx.x + u * kNormThreads;
+    if (g < n8) dst[g] = rms_apply(v[u], ws[g], scale);
+  }
 }
 
 }  // namespace
@@ -87,11 +134,22 @@ int launch_rmsnorm(hipStream_t s, const uint16_t* x, const uint16_t* w, uint16_t
 
 int launch_embedding(hipStream_t s, const uint32_t* w, const uint16_t* sc, const uint16_t* bi,
                      uint16_t* out, const uint32_t* tokens_dev, uint32_t token_host,
-                     uint32_t rows, uint32_t hidden) {
+                     uint32_t rows, uint32_t hidden, uint32_t token_stride) {
   const uint32_t words = hidden / 8;
   hipLaunchKernelGGL(embedding_kernel, dim3((words + 255) / 256, rows), dim3(256), 0, s, w, sc, bi, out,
-                     tokens_dev, token_host, hidden);
+                     tokens_dev, token_stride, token_host, hidden);
   PRG_CHECK_LAUNCH("embedding");
+  return PRG_OK;
+}
+
+int launch_embed_norm_pair(hipStream_t s, const uint32_t* ew, const uint16_t* es, const uint16_t* eb,
+                           const uint32_t* token_dev, const uint16_t* w0, const uint16_t* x1, const uint16_t* w1,
+                           uint16_t* out, uint32_t hidden, float eps) {
+  if (hidden % 64 != 0 || hidden > 8u * kNormThreads * kPairUnits)
+    return set_error(PRG_ERR_INVALID_ARG, "embed_norm_pair: hidden %u unsupported", hidden);
+  hipLaunchKernelGGL(embed_norm_pair_kernel, dim3(2), dim3(kNormThreads), 0, s, ew, es, eb, token_dev, w0, x1, w1,
+                     out, hidden, eps);
+  PRG_CHECK_LAUNCH("embed_norm_pair");
   return PRG_OK;
 }
 

@@ -61,8 +61,14 @@ __device__ inline uint4 gated_rms_apply(uint4 v, uint4 w, float4 z0, float4 z1, 
 
 int launch_rmsnorm(hipStream_t s, const uint16_t* x, const uint16_t* w, uint16_t* out,
                    uint32_t hidden, uint32_t rows, float eps);
+// Row r embeds tokens_dev[r * token_stride] (or token_host without tokens_dev).
 int launch_embedding(hipStream_t s, const uint32_t* w, const uint16_t* sc, const uint16_t* bi,
                      uint16_t* out, const uint32_t* tokens_dev, uint32_t token_host, uint32_t rows,
-                     uint32_t hidden);
+                     uint32_t hidden, uint32_t token_stride = 1);
+// out[0, H) = rmsnorm(embedding(*token_dev), w0), out[H, 2H) = rmsnorm(x1, w1) in
+// one launch, bit-identical to the separate launches.
+int launch_embed_norm_pair(hipStream_t s, const uint32_t* ew, const uint16_t* es, const uint16_t* eb,
+                           const uint32_t* token_dev, const uint16_t* w0, const uint16_t* x1, const uint16_t* w1,
+                           uint16_t* out, uint32_t hidden, float eps);
 
 }  // namespace prg
