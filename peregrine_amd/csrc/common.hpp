@@ -152,6 +152,33 @@ __device__ inline float block_sum256_dpp(float v, float* red) {
   return (red[0] + red[1]) + (red[2] + red[3]);
 }
 
+// v_permlane32_swap / v_permlane16_swap of two floats: returns {new a, new b}.
+// Both results are copied out of the builtin's pair into scalars before use.
+__device__ inline void swap32(float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b),
+                                                  false, false);
+  const uint32_t x = r[0], y = r[1];
+  a = __builtin_bit_cast(float, x);
+  b = __builtin_bit_cast(float, y);
+}
+__device__ inline void swap16(float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b),
+                                                  false, false);
+  const uint32_t x = r[0], y = r[1];
+  a = __builtin_bit_cast(float, x);
+  b = __builtin_bit_cast(float, y);
+}
+
+// Sum over each 32-lane half of the wave with DPP and one v_permlane16_swap
+// (no LDS round trips); every lane of a half receives the same bits:
+// (even row total) + (odd row total).
+__device__ inline float half_sum32(float v) {
+  v = row16_sum(v);
+  float a = v, b = v;
+  swap16(a, b);  // each lane now holds its own row's total and its partner row's
+  return a + b;
+}
+
 __device__ inline float silu(float g) { return g / (1.0f + expf(-g)); }
 __device__ inline float sigmoid(float g) { return 1.0f / (1.0f + expf(-g)); }
 

@@ -31,7 +31,7 @@ using namespace prg;
 constexpr int kGdnFusedThreads = 512;  // fused gated norm: 16 half-waves x 8 rows = one head
 constexpr int kGdnSplitThreads = 256;  // unfused: 8 half-waves x 2 rows = 16 rows per block
 
-__device__ inline float hsum32(float v) { return group_sum<32>(v); }
+__device__ inline float hsum32(float v) { return half_sum32(v); }
 
 // The per-token math, shared by the one- and two-token kernels. Every
 // multiply-add is an explicit __fmaf_rn / __fmul_rn / __fadd_rn, so both

@@ -329,23 +329,6 @@ __device__ inline void gemv_store_row(const GemvRowDst& d, const float (&tot)[NM
 // which a DPP row sum finishes. 10 ops per value instead of a full 64-lane
 // reduction per group; the combination order of every value is the same for
 // any E, so M = 1 and M = 2 launches give identical bits per row.
-// v_permlane32_swap / v_permlane16_swap of two floats: returns {new a, new b}.
-// Both results are copied out of the builtin's pair into scalars before use.
-__device__ inline void swap32(float& a, float& b) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b),
-                                                  false, false);
-  const uint32_t x = r[0], y = r[1];
-  a = __builtin_bit_cast(float, x);
-  b = __builtin_bit_cast(float, y);
-}
-__device__ inline void swap16(float& a, float& b) {
-  const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b),
-                                                  false, false);
-  const uint32_t x = r[0], y = r[1];
-  a = __builtin_bit_cast(float, x);
-  b = __builtin_bit_cast(float, y);
-}
-
 template <int E>
 __device__ inline void reduce4_rows(float (&v)[4][E]) {
 #pragma unroll
