@@ -38,6 +38,23 @@ def log(*a) -> None:
     print(*a, file=sys.stderr, flush=True)
 
 
+def token_gemv_bytes(cfg) -> int:
+    """Algorithmic bytes of one decode token's GEMVs (Q4 weights + scales +
+    biases): per GDN layer in_proj (qkv 8192 | z 4096 | a 32 | b 32 rows) and
+    out_proj 4096 x 4096, per attention layer q|gate 8192 + k 1024 + v 1024 rows
+    and o_proj 4096 x 4096, per layer gate/up 2 x 12288 and down 4096 x 12288,
+    and the lm_head."""
+    from peregrine_amd.gemv_bench import q4_bytes
+
+    H, F = cfg.hidden, cfg.intermediate
+    n_attn = cfg.num_layers // cfg.full_attention_interval
+    n_gdn = cfg.num_layers - n_attn
+    gdn = q4_bytes(8192 + 4096 + 32 + 32, H) + q4_bytes(4096, 4096)
+    attn = q4_bytes(8192 + 1024 + 1024, H) + q4_bytes(H, 4096)
+    mlp = 2 * q4_bytes(F, H) + q4_bytes(H, F)
+    return n_gdn * gdn + n_attn * attn + cfg.num_layers * mlp + q4_bytes(cfg.vocab, H)
+
+
 def dominant_kernel_roofline(iters: int = 100) -> dict:
     """Fused post_attention_layernorm + gate/up SiLU GEMV at the MLP shape
     (2 x 12288x4096 Q4): ~40% of the bytes a decode step streams. One launch per
@@ -453,6 +470,17 @@ def main() -> int:
     tok_s = a.steps / (ms * 1e-3)
     log(f"[bench] decode {a.steps} steps {ms:.1f} ms -> {tok_s:.1f} tok/s; last tokens {toks[-4:].tolist()}")
 
+    # The token loop's GEMVs alone, graph-replayed with the model's weights
+    # (the decode state is not used again: the CPU baseline starts from `snap`).
+    gemv_us = st.time_token_gemvs(32)
+    gemv_bytes = token_gemv_bytes(QWEN35_9B)
+    token_loop = {"gemv_us_per_token": round(gemv_us, 2), "gemv_bytes_per_token": gemv_bytes,
+                  "gemv_launches_per_token": 4 * QWEN35_9B.num_layers + 1,
+                  "GBps": round(gemv_bytes / (gemv_us * 1e-6) / 1e9, 1),
+                  "frac_peak": round(gemv_bytes / (gemv_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                  "share_of_step": round(gemv_us / (ms / a.steps * 1e3), 4)}
+    log(f"[bench] token-loop GEMVs {token_loop}")
+
     roof = dominant_kernel_roofline()
     log(f"[bench] dominant kernel {roof['avg_us']} us, {roof['achieved']} GB/s ({roof['frac'] * 100:.1f}% of peak); "
         f"a streaming read of the same bytes takes {roof['read_floor_us']} us ({roof['read_floor_GBps']} GB/s)")
@@ -500,6 +528,7 @@ def main() -> int:
                    "weight_bytes": weight_bytes, "parallelism": "single GPU",
                    "execution": "eager launches" if a.eager else "one HIP graph replay per token"},
         "roofline": roof,
+        "token_loop": token_loop,
         "cpu_baseline": cpu,
         "prefill": prefill,
         "mtp": mtp,

@@ -303,6 +303,16 @@ int prg_model_prefill(PrgModel *model, PrgModelState *state, const uint32_t *pro
 int prg_model_decode(PrgModel *model, PrgModelState *state, uint32_t n_steps, uint32_t *tokens_out,
                      float *gpu_ms);
 
+/* Measurement entry point, no counterpart in the reference: one decode token's
+ * GEMV launches only (the model's weights, fused norms and epilogues; no
+ * embedding, GDN recurrence, attention or argmax) captured as a graph and
+ * replayed `replays` times; *us_per_token receives the average GPU time of one
+ * replay. For the token-loop GEMV bandwidth of the benchmark. The state's
+ * activations and conv states are undefined afterwards until the next
+ * prg_model_prefill. */
+int prg_model_time_token_gemvs(PrgModel *model, PrgModelState *state, uint32_t replays,
+                               float *us_per_token);
+
 /* Greedy generation from an empty state, the whole loop device-resident (one
  * captured HIP graph per token, no host sync between tokens). Step n consumes
  * the token at position n.

@@ -298,9 +298,10 @@ int encode_linear_attention(PrgModel* m, PrgModelState* st, const DecoderLayer& 
   if (int rc = run_gemv(s, p, kEpiPlain, kNormRms, "linear_attn.in_proj")) return rc;
   // Recurrence -> raw y (bf16); the gated RMSNorm runs in the out_proj
   // GEMV's prologue (per 128-wide head, gate z from in_proj).
-  if (int rc = launch_gdn_decode(s, io.recur_in, st->conv_out, st->abuf, st->bbuf, b.a_log, b.dt_bias, st->gated,
-                                 step, 0, nullptr, nullptr, 0.0f, io.recur_out))
-    return rc;
+  if (!st->gemv_only)
+    if (int rc = launch_gdn_decode(s, io.recur_in, st->conv_out, st->abuf, st->bbuf, b.a_log, b.dt_bias, st->gated,
+                                   step, 0, nullptr, nullptr, 0.0f, io.recur_out))
+      return rc;
   GemvParams o = gemv_params(st->gated, kGdnValDim);
   o.norm_w = b.norm_weight;
   o.eps = c.rms_eps;
@@ -446,7 +447,8 @@ int encode_full_attention(PrgModel* m, PrgModelState* st, const DecoderLayer& L,
   add_seg(p, b.v_proj, st->vbuf);
   if (int rc = run_gemv(s, p, kEpiPlain, kNormRms, "self_attn.qkv_proj")) return rc;
   AttnDecodeArgs da = attn_step_args(st, b, ls, st->qp, st->kbuf, st->vbuf, st->ctx, step);
-  if (int rc = launch_attn_decode(s, da)) return rc;
+  if (!st->gemv_only)
+    if (int rc = launch_attn_decode(s, da)) return rc;
   GemvParams o = gemv_params(st->ctx, kAttnQHeads * kAttnHeadDim);
   add_seg(o, b.o_proj, h);
   o.seg[0].res[0] = x;
@@ -487,9 +489,10 @@ namespace {
 int encode_token(PrgModel* m, PrgModelState* st, bool with_head) {
   hipStream_t s = st->stream;
   const StepScalars* step = &st->ctl->s;
-  if (int rc = launch_embedding(s, m->embed.weight, m->embed.scales, m->embed.biases, st->hA, &st->ctl->s.token, 0,
-                                1, m->cfg.hidden))
-    return rc;
+  if (!st->gemv_only)
+    if (int rc = launch_embedding(s, m->embed.weight, m->embed.scales, m->embed.biases, st->hA, &st->ctl->s.token,
+                                  0, 1, m->cfg.hidden))
+      return rc;
   for (size_t i = 0; i < m->layers.size(); ++i) {
     const DecoderLayer& L = m->layers[i];
     LayerState& ls = st->layers[i];
@@ -510,6 +513,7 @@ int encode_token(PrgModel* m, PrgModelState* st, bool with_head) {
   p.seg[0].pval[0] = st->pval;
   p.seg[0].pidx[0] = st->pidx;
   if (int rc = launch_q4_gemv(s, p, 1, 8, kEpiArgmax, kNormRms, "lm_head.argmax")) return rc;
+  if (st->gemv_only) return PRG_OK;
   return launch_argmax_advance(s, st->pval, st->pidx, m->cfg.vocab / 8, st->ctl, st->prompt, st->predictions);
 }
 
@@ -859,6 +863,33 @@ int prg_model_decode(PrgModel* model, PrgModelState* st, uint32_t n_steps, uint3
                          st->stream));
   PRG_HIP(hipStreamSynchronize(st->stream));
   if (gpu_ms) PRG_HIP(hipEventElapsedTime(gpu_ms, st->ev0, st->ev1));
+  return PRG_OK;
+}
+
+// Measurement only: one decode token's GEMV launches (all 129 of them, with
+// the model's weights, fused norms and epilogues) captured as a graph and
+// replayed `replays` times between two events; the other kernels are left
+// out. The GEMVs write the state's activations and conv states, which stay
+// undefined until the next prefill from position 0.
+int prg_model_time_token_gemvs(PrgModel* model, PrgModelState* st, uint32_t replays, float* us_per_token) {
+  PRG_CHECK_ARG(model && st && us_per_token && st->model == model, "prg_model_time_token_gemvs: bad argument");
+  PRG_CHECK_ARG(replays >= 1, "prg_model_time_token_gemvs: replays == 0");
+  hipGraphExec_t ge = nullptr;
+  st->gemv_only = true;
+  const int rc = capture(model, st, true, &ge);
+  st->gemv_only = false;
+  if (rc) return rc;
+  hipError_t e = hipSuccess;
+  for (int i = 0; i < 2 && e == hipSuccess; ++i) e = hipGraphLaunch(ge, st->stream);
+  if (e == hipSuccess) e = hipEventRecord(st->ev0, st->stream);
+  for (uint32_t i = 0; i < replays && e == hipSuccess; ++i) e = hipGraphLaunch(ge, st->stream);
+  if (e == hipSuccess) e = hipEventRecord(st->ev1, st->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(st->stream);
+  float ms = 0.0f;
+  if (e == hipSuccess) e = hipEventElapsedTime(&ms, st->ev0, st->ev1);
+  (void)hipGraphExecDestroy(ge);  // cleanup: its own error does not change the result
+  if (e != hipSuccess) return set_error(PRG_ERR_HIP, "prg_model_time_token_gemvs: %s", hipGetErrorString(e));
+  *us_per_token = ms * 1000.0f / static_cast<float>(replays);
   return PRG_OK;
 }
 

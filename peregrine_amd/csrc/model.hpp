@@ -195,6 +195,7 @@ struct PrgModelState {
   // replaying the captured graph (same kernels and arguments; for tools such as
   // kernel tracers that do not follow graph launches).
   bool eager = false;
+  bool gemv_only = false;  // measurement capture: only the token's GEMV launches
   prg::PrefillWs pf;
   // speculative decode (allocated on first use; the drafter state only when
   // the model has MTP weights)

@@ -178,6 +178,13 @@ class ModelState:
              C.byref(ms))
         return toks, float(ms.value)
 
+    def time_token_gemvs(self, replays: int = 32) -> float:
+        """Average GPU us of one decode token's GEMV launches alone (graph
+        replay; measurement only: the state needs a new prefill afterwards)."""
+        us = C.c_float(0.0)
+        call("prg_model_time_token_gemvs", self.model.handle, self.handle, replays, C.byref(us))
+        return float(us.value)
+
     # decode_loop.zig:96-160 (empty prefix)
     def generate(self, prompt, n_new: int, teacher_force: bool = False) -> tuple[np.ndarray, float]:
         prompt = np.ascontiguousarray(prompt, np.uint32)

@@ -103,6 +103,26 @@ def test_step_api_matches_graph_loop(small):
     np.testing.assert_array_equal(np.array(steps, np.uint32), preds)
 
 
+def test_time_token_gemvs_then_prefill(small):
+    """The measurement entry point replays the token's GEMVs alone and returns a
+    positive time; a prefill afterwards gives the same tokens as before it."""
+    from peregrine_amd.model import ModelState
+
+    m, _, _ = small
+    rng = np.random.default_rng(5)
+    prompt = rng.integers(0, SMALL["vocab"], size=20).astype(np.uint32)
+    st = ModelState(m, max_seq=64)
+    try:
+        first = st.prefill(prompt)
+        toks, _ = st.decode(6)
+        us = st.time_token_gemvs(8)
+        assert 0.0 < us < 1e5, us
+        assert st.prefill(prompt) == first
+        np.testing.assert_array_equal(st.decode(6)[0], toks)
+    finally:
+        st.close()
+
+
 def test_step_api_errors(small):
     from peregrine_amd._lib import PrgError
 
