@@ -512,9 +512,10 @@ int encode_token(PrgModel* m, PrgModelState* st, bool with_head) {
   add_seg(p, m->lm_head, nullptr);
   p.seg[0].pval[0] = st->pval;
   p.seg[0].pidx[0] = st->pidx;
+  p.argmax_waves = st->argmax_waves;
   if (int rc = launch_q4_gemv(s, p, 1, 8, kEpiArgmax, kNormRms, "lm_head.argmax")) return rc;
   if (st->gemv_only) return PRG_OK;
-  return launch_argmax_advance(s, st->pval, st->pidx, m->cfg.vocab / 8, st->ctl, st->prompt, st->predictions);
+  return launch_argmax_waves_advance(s, st->pval, st->pidx, st->argmax_waves, st->ctl, st->prompt, st->predictions);
 }
 
 int capture(PrgModel* m, PrgModelState* st, bool with_head, hipGraphExec_t* out) {
@@ -747,8 +748,9 @@ int prg_model_state_create(PrgModel* model, uint32_t max_seq, PrgModelState** ou
   items.push_back({"ws.partials", 2 * sizeof(float) * kAttnQHeads * st->nsplit * kAttnPartialStride,
                    reinterpret_cast<void**>(&st->partials)});
   items.push_back({"ws.inter", bf * c.intermediate, reinterpret_cast<void**>(&st->inter)});
-  items.push_back({"ws.pval", sizeof(float) * (c.vocab / 8), reinterpret_cast<void**>(&st->pval)});
-  items.push_back({"ws.pidx", sizeof(uint32_t) * (c.vocab / 8), reinterpret_cast<void**>(&st->pidx)});
+  items.push_back({"ws.pval", sizeof(float) * kArgmaxMaxWaves, reinterpret_cast<void**>(&st->pval)});
+  items.push_back({"ws.pidx", sizeof(uint32_t) * kArgmaxMaxWaves, reinterpret_cast<void**>(&st->pidx)});
+  items.push_back({"ws.argmax_waves", sizeof(uint32_t), reinterpret_cast<void**>(&st->argmax_waves)});
   items.push_back({"ws.ctl", sizeof(DecodeCtl), reinterpret_cast<void**>(&st->ctl)});
   items.push_back({"ws.prompt", sizeof(uint32_t) * st->stride, reinterpret_cast<void**>(&st->prompt)});
   items.push_back({"ws.predictions", sizeof(uint32_t) * st->stride, reinterpret_cast<void**>(&st->predictions)});

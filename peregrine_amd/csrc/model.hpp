@@ -180,8 +180,9 @@ struct PrgModelState {
   uint16_t *qp = nullptr, *kbuf = nullptr, *vbuf = nullptr, *qbuf = nullptr, *gatebuf = nullptr, *ctx = nullptr;
   float* partials = nullptr;
   uint16_t* inter = nullptr;
-  float* pval = nullptr;
+  float* pval = nullptr;      // lm_head argmax: per-wave entries (kArgmaxMaxWaves)
   uint32_t* pidx = nullptr;
+  uint32_t* argmax_waves = nullptr;  // entry count written by the lm_head GEMV
   prg::DecodeCtl* ctl = nullptr;
   uint32_t* prompt = nullptr;
   uint32_t* predictions = nullptr;

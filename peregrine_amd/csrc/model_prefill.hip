@@ -214,8 +214,10 @@ int run_prefill(PrgModel* m, PrgModelState* st, uint32_t from, uint32_t len, boo
   add_seg(p, m->lm_head, nullptr);
   p.seg[0].pval[0] = st->pval;
   p.seg[0].pidx[0] = st->pidx;
+  p.argmax_waves = st->argmax_waves;
   if (int rc = launch_q4_gemv(s, p, 1, 8, kEpiArgmax, kNormRms, "lm_head.argmax")) return rc;
-  if (int rc = launch_argmax_advance(s, st->pval, st->pidx, c.vocab / 8, st->ctl, st->prompt, st->predictions))
+  if (int rc = launch_argmax_waves_advance(s, st->pval, st->pidx, st->argmax_waves, st->ctl, st->prompt,
+                                           st->predictions))
     return rc;
   if (tail_rows > 0)  // after the tail: the drafter overwrites the rows `last` points into
     return mtp_prefill_rows(m, st, st->prompt + tail_start + 1, w.resid, tail_rows, tail_start);

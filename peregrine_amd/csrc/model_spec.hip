@@ -121,8 +121,12 @@ int encode_mtp_step(PrgModel* m, PrgModelState* st, const uint32_t* token_dev, c
   add_seg(p, m->lm_head, nullptr);
   p.seg[0].pval[0] = st->pval;
   p.seg[0].pidx[0] = st->pidx;
+  p.argmax_waves = st->argmax_waves;
   if (int rc = launch_q4_gemv(s, p, 1, 8, kEpiArgmax, kNormRms, "mtp.lm_head.argmax")) return rc;
-  return launch_argmax_pairs(s, st->pval, st->pidx, c.vocab / 8, out_token);
+  const float* vals[1] = {st->pval};
+  const uint32_t* rows[1] = {st->pidx};
+  uint32_t* outs[1] = {out_token};
+  return launch_argmax_waves(s, 1, vals, rows, st->argmax_waves, outs);
 }
 
 // Two tokens through the target (tokens and positions in spec->v0 / v1):
@@ -168,11 +172,14 @@ int encode_verify(PrgModel* m, PrgModelState* st) {
   p.seg[0].pidx[0] = st->pidx;
   p.seg[0].pval[1] = st->pval2;
   p.seg[0].pidx[1] = st->pidx2;
+  p.argmax_waves = st->argmax_waves;
   // (the norm stays a launch of its own: fused into this M = 2 prologue it
   // measured 138 us against 126 + 4)
   if (int rc = launch_q4_gemv(s, p, 2, 8, kEpiArgmax, kNormNone, "lm_head.argmax2")) return rc;
-  if (int rc = launch_argmax_pairs(s, st->pval, st->pidx, c.vocab / 8, &sc->verify)) return rc;
-  return launch_argmax_pairs(s, st->pval2, st->pidx2, c.vocab / 8, &sc->bonus);
+  const float* vals[2] = {st->pval, st->pval2};
+  const uint32_t* rows[2] = {st->pidx, st->pidx2};
+  uint32_t* outs[2] = {&sc->verify, &sc->bonus};
+  return launch_argmax_waves(s, 2, vals, rows, st->argmax_waves, outs);
 }
 
 // One speculative step (decode_loop.zig:173-284).
@@ -246,8 +253,8 @@ int ensure_spec_ws(PrgModelState* st) {
       {reinterpret_cast<void**>(&st->fc_in), bf * 2 * H},
       {reinterpret_cast<void**>(&st->mtp_x), bf * H},
       {reinterpret_cast<void**>(&st->mtp_h), bf * H},
-      {reinterpret_cast<void**>(&st->pval2), sizeof(float) * (c.vocab / 8)},
-      {reinterpret_cast<void**>(&st->pidx2), sizeof(uint32_t) * (c.vocab / 8)},
+      {reinterpret_cast<void**>(&st->pval2), sizeof(float) * kArgmaxMaxWaves},
+      {reinterpret_cast<void**>(&st->pidx2), sizeof(uint32_t) * kArgmaxMaxWaves},
       {reinterpret_cast<void**>(&st->spec_out), sizeof(uint32_t) * (S + 4)},
       {reinterpret_cast<void**>(&st->drafts), sizeof(uint32_t) * (S + 4)},
       {reinterpret_cast<void**>(&st->spec), sizeof(SpecCtl)},

@@ -54,6 +54,8 @@ int launch_q4_gemv(hipStream_t stream, GemvParams& p, int M, int rows, int epi, 
   p.tail_lanes = rem == 0 ? 64u : rem / 32u;
   if (M < 1 || M > 2) return set_error(PRG_ERR_INVALID_ARG, "%s: M=%d", name, M);
   if (p.nseg < 1 || p.nseg > kGemvMaxSegs) return set_error(PRG_ERR_INVALID_ARG, "%s: nseg", name);
+  if (p.argmax_waves != nullptr && (epi != kEpiArgmax || p.nseg != 1))
+    return set_error(PRG_ERR_INVALID_ARG, "%s: per-wave argmax needs the argmax epilogue and one segment", name);
   uint32_t groups = 0;
   for (uint32_t i = 0; i < p.nseg; ++i) {
     GemvSeg& sg = p.seg[i];
@@ -93,8 +95,6 @@ int launch_q4_gemv(hipStream_t stream, GemvParams& p, int M, int rows, int epi, 
 
 // ================================================================ kernels ====
 namespace prg {
-int launch_argmax_advance(hipStream_t s, const float* values, const uint32_t* indices, uint32_t n,
-                          DecodeCtl* ctl, const uint32_t* prompt, uint32_t* predictions);
 int launch_advance_forced(hipStream_t s, DecodeCtl* ctl, const uint32_t* prompt);
 }  // namespace prg
 
@@ -108,21 +108,10 @@ namespace {
 // = 0 mod 4, and so on: among equal maxima the winner minimises
 // (bitreverse8(p mod 256), p div 256). NaN never compares greater, and if
 // nothing beats -inf the answer is index 0. This kernel evaluates that order
-// directly with 1024 threads and a total order on (value, key).
+// directly with 1024 threads and a total order on (value, key)
+// (prg::argmax_better).
 constexpr int kArgmaxThreads = 1024;
-
-__device__ inline uint32_t argmax_tie_key(uint32_t p) {
-  return ((__builtin_bitreverse32(p & 255u) >> 24) << 24) | (p >> 8);
-}
-
-__device__ inline bool argmax_better(float v, uint32_t p, float bv, uint32_t bp) {
-  // true when (v, p) beats (bv, bp). NaN never beats; -inf never beats.
-  if (!(v > -INFINITY)) return false;
-  if (!(bv > -INFINITY)) return true;
-  if (v > bv) return true;
-  if (v < bv) return false;
-  return argmax_tie_key(p) < argmax_tie_key(bp);
-}
+using prg::argmax_better;
 
 // Advance the token loop by one step (see DecodeCtl). `pred` is ignored when
 // the step has no argmax (prompt ingestion).
@@ -143,11 +132,9 @@ __device__ inline void advance_ctl(prg::DecodeCtl* ctl, const uint32_t* prompt, 
   ctl->n = n1;
 }
 
-template <bool ADVANCE>
 __global__ __launch_bounds__(kArgmaxThreads) void argmax_pairs_kernel(
-    const float* __restrict__ values, const uint32_t* __restrict__ indices,
-    uint32_t* __restrict__ out, uint32_t n, prg::DecodeCtl* ctl, const uint32_t* prompt,
-    uint32_t* predictions) {
+    const float* __restrict__ values, const uint32_t* __restrict__ indices, uint32_t* __restrict__ out,
+    uint32_t n) {
   __shared__ float sv[kArgmaxThreads / 64];
   __shared__ uint32_t sp[kArgmaxThreads / 64];
   float bv = -INFINITY;
@@ -196,7 +183,74 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_pairs_kernel(
         bv = sv[i];
         bp = sp[i];
       }
-    const uint32_t winner = (bp == 0xffffffffu) ? 0u : indices[bp];
+    out[0] = (bp == 0xffffffffu) ? 0u : indices[bp];
+  }
+}
+
+// Final argmax over the per-wave entries of a GEMV launched with
+// GemvParams::argmax_waves: entry e holds a wave's best (value, row) under the
+// same order (its partial position is row / 8), so the winner equals the one
+// argmax_pairs_kernel picks from the full partial list. The entries and the
+// count are loaded together (every index < kArgmaxMaxWaves is in bounds) and
+// entries at or past the count are masked afterwards: one memory round trip.
+// Block b reduces activation row b's entries (values[b], rows[b] -> out[b]).
+struct ArgmaxWavesArgs {
+  const float* values[2];
+  const uint32_t* rows[2];
+  uint32_t* out[2];
+};
+template <bool ADVANCE>
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_waves_kernel(
+    ArgmaxWavesArgs a, const uint32_t* __restrict__ count, prg::DecodeCtl* ctl, const uint32_t* prompt,
+    uint32_t* predictions) {
+  const float* __restrict__ values = a.values[blockIdx.x];
+  const uint32_t* __restrict__ rows = a.rows[blockIdx.x];
+  uint32_t* out = a.out[blockIdx.x];
+  __shared__ float sv[kArgmaxThreads / 64];
+  __shared__ uint32_t sr[kArgmaxThreads / 64];
+  constexpr int kU = prg::kArgmaxMaxWaves / kArgmaxThreads;
+  static_assert(kU * kArgmaxThreads == prg::kArgmaxMaxWaves, "entries per thread");
+  const uint32_t n = *count;
+  float v[kU];
+  uint32_t r[kU];
+#pragma unroll
+  for (int u = 0; u < kU; ++u) {
+    v[u] = values[threadIdx.x + u * kArgmaxThreads];
+    r[u] = rows[threadIdx.x + u * kArgmaxThreads];
+  }
+  float bv = -INFINITY;
+  uint32_t br = 0xffffffffu;
+#pragma unroll
+  for (int u = 0; u < kU; ++u) {
+    const bool live = threadIdx.x + u * kArgmaxThreads < n;
+    const float vu = live ? v[u] : -INFINITY;
+    if (argmax_better(vu, r[u] >> 3, bv, br >> 3)) {
+      bv = vu;
+      br = r[u];
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(bv, o, 64);
+    const uint32_t orow = __shfl_xor(br, o, 64);
+    if (argmax_better(ov, orow >> 3, bv, br >> 3)) {
+      bv = ov;
+      br = orow;
+    }
+  }
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  if (lane == 0) {
+    sv[wid] = bv;
+    sr[wid] = br;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int i = 1; i < kArgmaxThreads / 64; ++i)
+      if (argmax_better(sv[i], sr[i] >> 3, bv, br >> 3)) {
+        bv = sv[i];
+        br = sr[i];
+      }
+    const uint32_t winner = (br == 0xffffffffu) ? 0u : br;
     if (out) out[0] = winner;
     if constexpr (ADVANCE) advance_ctl(ctl, prompt, predictions, true, winner);
   }
@@ -255,17 +309,26 @@ prg::GemvParams one_seg(const uint32_t* w, const uint16_t* s, const uint16_t* b,
 using prg::launch_q4_gemv;
 
 namespace prg {
-int launch_argmax_advance(hipStream_t s, const float* values, const uint32_t* indices, uint32_t n,
-                          DecodeCtl* ctl, const uint32_t* prompt, uint32_t* predictions) {
-  hipLaunchKernelGGL(argmax_pairs_kernel<true>, dim3(1), dim3(kArgmaxThreads), 0, s, values, indices,
-                     nullptr, n, ctl, prompt, predictions);
-  PRG_CHECK_LAUNCH("argmax_advance");
+int launch_argmax_waves_advance(hipStream_t s, const float* values, const uint32_t* rows, const uint32_t* count,
+                                DecodeCtl* ctl, const uint32_t* prompt, uint32_t* predictions) {
+  ArgmaxWavesArgs a{{values, values}, {rows, rows}, {nullptr, nullptr}};
+  hipLaunchKernelGGL(argmax_waves_kernel<true>, dim3(1), dim3(kArgmaxThreads), 0, s, a, count, ctl, prompt,
+                     predictions);
+  PRG_CHECK_LAUNCH("argmax_waves_advance");
   return PRG_OK;
 }
-int launch_argmax_pairs(hipStream_t s, const float* values, const uint32_t* indices, uint32_t n, uint32_t* out) {
-  hipLaunchKernelGGL(argmax_pairs_kernel<false>, dim3(1), dim3(kArgmaxThreads), 0, s, values, indices, out, n,
-                     nullptr, nullptr, nullptr);
-  PRG_CHECK_LAUNCH("argmax_pairs");
+int launch_argmax_waves(hipStream_t s, int M, const float* const* values, const uint32_t* const* rows,
+                        const uint32_t* count, uint32_t* const* out) {
+  if (M < 1 || M > 2) return set_error(PRG_ERR_INVALID_ARG, "argmax_waves: M=%d", M);
+  ArgmaxWavesArgs a{};
+  for (int m = 0; m < M; ++m) {
+    a.values[m] = values[m];
+    a.rows[m] = rows[m];
+    a.out[m] = out[m];
+  }
+  hipLaunchKernelGGL(argmax_waves_kernel<false>, dim3(M), dim3(kArgmaxThreads), 0, s, a, count, nullptr, nullptr,
+                     nullptr);
+  PRG_CHECK_LAUNCH("argmax_waves");
   return PRG_OK;
 }
 int launch_advance_forced(hipStream_t s, DecodeCtl* ctl, const uint32_t* prompt) {
@@ -451,8 +514,8 @@ int prg_argmax_pairs_f32_u32(void* stream, const float* values, const uint32_t* 
   const char* name = "prg_argmax_pairs_f32_u32";
   PRG_CHECK_ARG(values && indices && out_index, "%s: null pointer", name);
   PRG_CHECK_ARG(pair_count > 0, "%s: pair_count == 0", name);
-  hipLaunchKernelGGL(argmax_pairs_kernel<false>, dim3(1), dim3(kArgmaxThreads), 0, prg::as_stream(stream),
-                     values, indices, out_index, pair_count, nullptr, nullptr, nullptr);
+  hipLaunchKernelGGL(argmax_pairs_kernel, dim3(1), dim3(kArgmaxThreads), 0, prg::as_stream(stream), values,
+                     indices, out_index, pair_count);
   PRG_CHECK_LAUNCH(name);
   return PRG_OK;
 }

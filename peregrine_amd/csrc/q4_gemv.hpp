@@ -92,7 +92,30 @@ struct GemvParams {
   uint32_t nseg;
   uint32_t tail_lanes;        // active lanes in the last K step (64 if full)
   uint32_t total_groups;      // groups of ROWS rows over all segments (set by the launcher)
+  // kEpiArgmax: if set, each wave writes one entry (its best partial under the
+  // final argmax's order) to pval / pidx[wave] instead of one per 8 rows, and
+  // the launch's wave count goes here (the grid is capped at kArgmaxMaxWaves).
+  uint32_t* argmax_waves;
 };
+
+constexpr uint32_t kArgmaxMaxWaves = 4096;
+
+// The final argmax's order on partials (value, partial position p): among
+// equal maxima the winner minimises (bitreverse8(p mod 256), p div 256), the
+// effective order of the reference's 256-thread scan and halving tree
+// (shaders/argmax.metal:6-43); NaN and -inf never win. A strict total order,
+// so any reduction tree picks the same winner.
+__device__ inline uint32_t argmax_tie_key(uint32_t p) {
+  return ((__builtin_bitreverse32(p & 255u) >> 24) << 24) | (p >> 8);
+}
+__device__ inline bool argmax_better(float v, uint32_t p, float bv, uint32_t bp) {
+  // true when (v, p) beats (bv, bp)
+  if (!(v > -INFINITY)) return false;
+  if (!(bv > -INFINITY)) return true;
+  if (v > bv) return true;
+  if (v < bv) return false;
+  return argmax_tie_key(p) < argmax_tie_key(bp);
+}
 
 // ------------------------------------------------------------ device ---------
 __device__ inline float dot2_bf16(uint32_t a, uint32_t b, float c) {
@@ -346,9 +369,11 @@ __device__ inline void reduce4_rows(float (&v)[4][E]) {
 }
 
 // Reduce one group's accumulators across the wave and write its outputs.
+// (wbv, wbi): the wave's running best partial and its row when the argmax
+// epilogue writes per wave (p.argmax_waves).
 template <int M, int NMAT, int ROWS, int EPI>
 __device__ inline void gemv_epilogue(const GemvParams& p, const GemvLoc& loc, int lane,
-                                     float (&acc)[NMAT][ROWS][M]) {
+                                     float (&acc)[NMAT][ROWS][M], float (&wbv)[M], uint32_t (&wbi)[M]) {
   float tot[NMAT][ROWS][M];
 #pragma unroll
   for (int mat = 0; mat < NMAT; ++mat)
@@ -374,8 +399,16 @@ __device__ inline void gemv_epilogue(const GemvParams& p, const GemvLoc& loc, in
           best_i = row0 + r;
         }
       }
-      sg.pval[m][row0 / 8] = best;
-      sg.pidx[m][row0 / 8] = best_i;
+      if (p.argmax_waves != nullptr) {
+        // the group's partial position is best_i / 8 (= row0 / 8)
+        if (argmax_better(best, best_i >> 3, wbv[m], wbi[m] >> 3)) {
+          wbv[m] = best;
+          wbi[m] = best_i;
+        }
+      } else {
+        sg.pval[m][row0 / 8] = best;
+        sg.pidx[m][row0 / 8] = best_i;
+      }
     }
   } else {
 #pragma unroll
@@ -656,10 +689,17 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(const GemvParams 
       default: break;
     }
   } else {
+    float wbv[M];
+    uint32_t wbi[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      wbv[m] = -INFINITY;
+      wbi[m] = 0xffffffffu;  // no partial yet (never compared: -inf never wins)
+    }
     auto process = [&](const GemvBuf<NMAT, ROWS, ITERS>& b, uint32_t grp) {
       float acc[NMAT][ROWS][M];
       accumulate(b, acc);
-      gemv_epilogue<M, NMAT, ROWS, EPI>(p, gemv_locate<ROWS>(p, grp), lane, acc);
+      gemv_epilogue<M, NMAT, ROWS, EPI>(p, gemv_locate<ROWS>(p, grp), lane, acc, wbv, wbi);
     };
     while (n > 2) {
       gemv_load<NMAT, ROWS, ITERS, TAIL>(p, g + W, lane, tail_active, b1);
@@ -675,6 +715,17 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(const GemvParams 
       process(b1, g + W);
     } else if (n == 1) {
       process(b0, g);
+    }
+    if constexpr (EPI == kEpiArgmax) {
+      if (p.argmax_waves != nullptr && lane == 0) {
+        const uint32_t wave = blockIdx.x * kGemvWaves + wid;
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+          p.seg[0].pval[m][wave] = wbv[m];
+          p.seg[0].pidx[m][wave] = wbi[m];
+        }
+        if (wave == 0) *p.argmax_waves = gridDim.x * kGemvWaves;
+      }
     }
   }
 }
@@ -693,11 +744,14 @@ int launch_q4_gemv(hipStream_t stream, GemvParams& p, int M, int rows_per_wave, 
 // Rows per wave picked for a launch of `total_rows` rows at in_dim K.
 int gemv_rows_per_wave(uint32_t total_rows, uint32_t K, int epi, int M);
 
-// Final argmax over partials + advance of the device token loop.
-int launch_argmax_advance(hipStream_t s, const float* values, const uint32_t* indices, uint32_t n,
-                          DecodeCtl* ctl, const uint32_t* prompt, uint32_t* predictions);
-// Final argmax over partials into out[0] (no control-block update).
-int launch_argmax_pairs(hipStream_t s, const float* values, const uint32_t* indices, uint32_t n, uint32_t* out);
+// Final argmax over the per-wave entries of an argmax GEMV launched with
+// GemvParams::argmax_waves = count (values / rows hold kArgmaxMaxWaves
+// entries), with and without the control-block update.
+int launch_argmax_waves_advance(hipStream_t s, const float* values, const uint32_t* rows, const uint32_t* count,
+                                DecodeCtl* ctl, const uint32_t* prompt, uint32_t* predictions);
+// M (1 or 2) activation rows in one launch: row m's entries -> out[m][0].
+int launch_argmax_waves(hipStream_t s, int M, const float* const* values, const uint32_t* const* rows,
+                        const uint32_t* count, uint32_t* const* out);
 // Advance with the next token forced from prompt (no lm_head this step).
 int launch_advance_forced(hipStream_t s, DecodeCtl* ctl, const uint32_t* prompt);
 

@@ -73,7 +73,10 @@ int launch_one_t(hipStream_t s, const GemvParams& p, size_t lds) {
   // K = 12288.
   const uint32_t want = (p.total_groups + kGemvWaves - 1) / kGemvWaves;
   const uint32_t cap = std::min<uint32_t>(resident, static_cast<uint32_t>(device_cus() * gemv_blocks_per_cu()));
-  const uint32_t blocks = std::max<uint32_t>(1, std::min<uint32_t>(want, cap));
+  uint32_t blocks = std::max<uint32_t>(1, std::min<uint32_t>(want, cap));
+  // per-wave argmax entries must fit the final kernel's kArgmaxMaxWaves
+  if (EPI == kEpiArgmax && p.argmax_waves != nullptr)
+    blocks = std::min<uint32_t>(blocks, kArgmaxMaxWaves / kGemvWaves);
   hipLaunchKernelGGL((q4_gemv_kernel<M, ROWS, ITERS, EPI, NORM, TAIL>), dim3(blocks), dim3(kGemvThreads), lds, s, p);
   return 0;
 }

@@ -436,3 +436,63 @@ def test_qwen35_9b_shape_speculative(gpu):
     assert same >= 2
     st.close()
     m.close()
+
+
+def test_lm_head_planted_ties_every_argmax_path(gpu, orc):
+    """Equal logits planted in the lm_head: two rows inside one 8-row partial,
+    partials that one wave of the lm_head GEMV visits in turn (positions 3072
+    apart) and partials of different waves. Prefill, the graph-replayed decode
+    step, the step API, both rows of the two-token verify and the drafter
+    must all pick the winner of the reference's partial + pairs order.
+
+    With every scale 0, row r's logit is bias_r * sum(x) for whatever x the
+    model feeds the lm_head: rows planted with +b tie at +v, rows with -b tie
+    at -v, all others are 0. Which set wins depends on the sign of v, so each
+    path runs under both sign assignments and must return the two sets'
+    winners, one each. The winners come from the oracle's partial + pairs
+    argmax over the same pattern (x = ones) and are also fixed by hand:
+    partial 256 (tie key 1) beats 1, 128, 3328, 4352 and its first row 2050
+    beats 2053; partial 512 (key 2) beats 5, 384, 7680 and row 4101 beats 4103.
+    """
+    from peregrine_amd.device import DeviceArray
+    from peregrine_amd.model import DeviceModel, ModelConfig, ModelState
+    from peregrine_amd.synth import Q4Weight
+
+    V, H = 65536, 1024
+    m = DeviceModel(ModelConfig(num_layers=4, hidden=H, intermediate=2048, vocab=V, mtp_layers=1), seed=12)
+    st = ModelState(m, max_seq=16)
+    hid = DeviceArray((2, H), np.uint16)
+    set_a = [8 * 1 + 3, 2050, 2053, 8 * 128 + 7, 8 * 3328 + 1, 8 * 4352 + 4]
+    set_b = [8 * 5 + 2, 8 * 384, 4101, 4103, 8 * 7680 + 5]
+    pos, neg = f32_to_bf16(np.float32(0.5))[()], f32_to_bf16(np.float32(-0.5))[()]
+    zeros_w = np.zeros((V, H // 8), np.uint32)
+    zeros_s = np.zeros((V, H // 64), np.uint16)
+    _write(m, "language_model.lm_head.weight", zeros_w)
+    _write(m, "language_model.lm_head.scales", zeros_s)
+    ones = np.full((1, H), f32_to_bf16(np.float32(1.0))[()], np.uint16)
+    runs = []
+    try:
+        for sa, sb in ((pos, neg), (neg, pos)):
+            bias = np.zeros((V, H // 64), np.uint16)
+            bias[set_a] = sa
+            bias[set_b] = sb
+            _write(m, "language_model.lm_head.biases", bias)
+            pv, pi = orc.q4_argmax_partial(ones, Q4Weight(zeros_w, zeros_s, bias))
+            expect = orc.argmax_pairs(pv[0], pi[0])
+            st.reset()
+            first = st.prefill(np.array([7, 9, 3], np.uint32))
+            nxt = int(st.decode(1)[0][0])
+            st.reset()
+            step = st.forward_next_token(7, 0)
+            st.reset()
+            verify, bonus = st.forward_two_tokens(7, 9, 0, hidden_out=hid)
+            draft = st.mtp_draft(9, hid, 0)
+            runs.append((expect, [first, nxt, step, verify, bonus, draft]))
+    finally:
+        hid.close()
+        st.close()
+        m.close()
+    (ea, ga), (eb, gb) = runs
+    assert (ea, eb) == (2050, 4101)
+    for what, x, y in zip(["prefill", "decode", "step", "verify", "bonus", "draft"], ga, gb):
+        assert {x, y} == {ea, eb}, (what, ga, gb)
