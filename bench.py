@@ -472,14 +472,18 @@ def main() -> int:
 
     # The token loop's GEMVs alone, graph-replayed with the model's weights
     # (the decode state is not used again: the CPU baseline starts from `snap`).
-    gemv_us = st.time_token_gemvs(32)
-    gemv_bytes = token_gemv_bytes(QWEN35_9B)
-    token_loop = {"gemv_us_per_token": round(gemv_us, 2), "gemv_bytes_per_token": gemv_bytes,
-                  "gemv_launches_per_token": 4 * QWEN35_9B.num_layers + 1,
-                  "GBps": round(gemv_bytes / (gemv_us * 1e-6) / 1e9, 1),
-                  "frac_peak": round(gemv_bytes / (gemv_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-                  "share_of_step": round(gemv_us / (ms / a.steps * 1e3), 4)}
-    log(f"[bench] token-loop GEMVs {token_loop}")
+    # Not under --eager: that mode is for kernel tracers, and rocprofv3's
+    # kernel trace has crashed in this capture (host SIGSEGV inside the tool).
+    token_loop = None
+    if not a.eager:
+        gemv_us = st.time_token_gemvs(32)
+        gemv_bytes = token_gemv_bytes(QWEN35_9B)
+        token_loop = {"gemv_us_per_token": round(gemv_us, 2), "gemv_bytes_per_token": gemv_bytes,
+                      "gemv_launches_per_token": 4 * QWEN35_9B.num_layers + 1,
+                      "GBps": round(gemv_bytes / (gemv_us * 1e-6) / 1e9, 1),
+                      "frac_peak": round(gemv_bytes / (gemv_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                      "share_of_step": round(gemv_us / (ms / a.steps * 1e3), 4)}
+        log(f"[bench] token-loop GEMVs {token_loop}")
 
     roof = dominant_kernel_roofline()
     log(f"[bench] dominant kernel {roof['avg_us']} us, {roof['achieved']} GB/s ({roof['frac'] * 100:.1f}% of peak); "
