@@ -23,6 +23,7 @@
 //   * Fused gated norm: one 512-thread block per head (16 half-waves x 8 rows)
 //     holds all 128 outputs of its head and normalises them in place.
 #include "gdn.hpp"
+#include "q4_gemv.hpp"
 
 namespace {
 
@@ -48,13 +49,16 @@ struct GdnIn {
   uint2 q, k;         // this lane's 4 dk of the head's q and k
   uint16_t v[RPH];    // the half-wave's rows of v
 };
-template <int RPH>
+// GATES: a / b come from gdn_gate_proj instead of memory.
+template <int RPH, bool GATES = false>
 __device__ inline GdnIn<RPH> gdn_load(const uint16_t* conv_out, const uint16_t* a, const uint16_t* bgate,
                                       const float* A_log, const uint16_t* dt_bias, uint32_t hv, uint32_t hk,
                                       int j, uint32_t row0) {
   GdnIn<RPH> in;
-  in.a = a[hv];
-  in.b = bgate[hv];
+  if constexpr (!GATES) {
+    in.a = a[hv];
+    in.b = bgate[hv];
+  }
   in.dt = dt_bias[hv];
   in.alog = A_log[hv];
   in.q = *reinterpret_cast<const uint2*>(conv_out + hk * kGdnDk + 4 * j);
@@ -63,6 +67,94 @@ __device__ inline GdnIn<RPH> gdn_load(const uint16_t* conv_out, const uint16_t* 
 #pragma unroll
   for (int r = 0; r < RPH; ++r) in.v[r] = vsrc[r];
   return in;
+}
+
+// ---- gate projections in the kernel (GdnGateProj), over a 256-thread
+// block: thread t takes a quarter (16 values) of quantisation group t / 4
+// of head hv's a and b rows (threads past K / 64 groups load the last group
+// and add 0), with the Q4 GEMV's arithmetic: the nibbles unpacked as bf16
+// 128 + q, dot2 against the activation pairs in the image's order. The four
+// quarters are summed with quad DPP (all four lanes then hold the same bits),
+// each group adds s * sum(q x) + b * sum(x), the wave sums go through LDS
+// and the block total is (w0 + w1) + (w2 + w3), rounded to bf16 as the GEMV's
+// output. One barrier; every block of the head gets the same bits.
+constexpr int kGateThreads = 256;
+struct GdnGateW {
+  uint2 wa, wb;  // 16 nibbles of each row
+  uint16_t sa, ba, sb, bb;
+};
+struct GdnGateX {
+  uint4 x[2];  // 16 activation values (image order)
+};
+__device__ inline uint32_t gdn_gate_group(const GdnGateProj& g, int tid) {
+  return min(static_cast<uint32_t>(tid) / 4u, g.K / 64 - 1);
+}
+__device__ inline GdnGateW gdn_gate_load_w(const GdnGateProj& g, uint32_t hv, int tid) {
+  const uint32_t gl = gdn_gate_group(g, tid);
+  const size_t meta = static_cast<size_t>(hv) * (g.K / 64) + gl;
+  const size_t word = static_cast<size_t>(hv) * (g.K / 8) + 8 * gl + 2 * (tid & 3);
+  GdnGateW w;
+  w.wa = *reinterpret_cast<const uint2*>(g.wa + word);
+  w.wb = *reinterpret_cast<const uint2*>(g.wb + word);
+  w.sa = g.sa[meta];
+  w.ba = g.ba[meta];
+  w.sb = g.sb[meta];
+  w.bb = g.bb[meta];
+  return w;
+}
+__device__ inline GdnGateX gdn_gate_load_x(const GdnGateProj& g, uint32_t row, int tid) {
+  const uint4* xp = reinterpret_cast<const uint4*>(g.x_image + static_cast<size_t>(row) * (g.K / 2)) +
+                    8 * gdn_gate_group(g, tid) + 2 * (tid & 3);
+  GdnGateX x;
+  x.x[0] = xp[0];
+  x.x[1] = xp[1];
+  return x;
+}
+__device__ inline float quad_sum(float v) {
+  v += dpp_f<0xB1>(v);
+  v += dpp_f<0x4E>(v);
+  return v;
+}
+__device__ inline float gdn_gate_qx(uint2 w, const GdnGateX& x, float xsum_part) {
+  float aq[2] = {-128.0f * xsum_part, 0.0f};  // removes the 128 offset of the unpacked nibbles
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    uint32_t t[4];
+    unpack_q4_word(j == 0 ? w.x : w.y, t);
+    const uint32_t xd[4] = {x.x[j].x, x.x[j].y, x.x[j].z, x.x[j].w};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) aq[c & 1] = dot2_bf16(t[c], xd[c], aq[c & 1]);
+  }
+  return aq[0] + aq[1];
+}
+// The wave's share of row r's a and b, into red[r][0..1][wave]; the totals
+// are read by gdn_gate_total after a barrier.
+__device__ inline void gdn_gate_partial(const GdnGateProj& g, const GdnGateW& w, const GdnGateX& x, int tid,
+                                        float (*red)[kGateThreads / kWave]) {
+  constexpr uint32_t kOnes = 0x3F803F80u;  // bf16 pair (1, 1)
+  float s[2] = {0.0f, 0.0f};
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const uint32_t xd[4] = {x.x[j].x, x.x[j].y, x.x[j].z, x.x[j].w};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) s[c & 1] = dot2_bf16(kOnes, xd[c], s[c & 1]);
+  }
+  const float xs_part = s[0] + s[1];
+  const float xs = quad_sum(xs_part);
+  const float qa = quad_sum(gdn_gate_qx(w.wa, x, xs_part));
+  const float qb = quad_sum(gdn_gate_qx(w.wb, x, xs_part));
+  const bool lead = (tid & 3) == 0 && static_cast<uint32_t>(tid) / 4u < g.K / 64;
+  const float va = lead ? __fmaf_rn(bf_lo(w.ba), xs, __fmul_rn(bf_lo(w.sa), qa)) : 0.0f;
+  const float vb = lead ? __fmaf_rn(bf_lo(w.bb), xs, __fmul_rn(bf_lo(w.sb), qb)) : 0.0f;
+  const float ta = wave_sum_uniform(va), tb = wave_sum_uniform(vb);
+  if ((tid & (kWave - 1)) == 0) {
+    red[0][tid / kWave] = ta;
+    red[1][tid / kWave] = tb;
+  }
+}
+__device__ inline void gdn_gate_total(const float (*red)[kGateThreads / kWave], uint16_t& a, uint16_t& b) {
+  a = f2bf((red[0][0] + red[0][1]) + (red[0][2] + red[0][3]));
+  b = f2bf((red[1][0] + red[1][1]) + (red[1][2] + red[1][3]));
 }
 
 struct GdnGates {
@@ -131,14 +223,16 @@ __device__ inline uint16_t gdn_row(float4& S, const GdnQK& qk, const GdnGates& g
 
 // IN_PLACE: state_out is state (each thread reads its rows before writing
 // them); otherwise the two buffers are distinct. NT threads, RPH rows per
-// half-wave; FUSE_NORM needs the whole head in one block.
-template <bool IN_PLACE, int NT, int RPH, bool FUSE_NORM>
+// half-wave; FUSE_NORM needs the whole head in one block. GATES: a / b are
+// computed from `gp` (GdnGateProj) instead of read.
+template <bool IN_PLACE, int NT, int RPH, bool FUSE_NORM, bool GATES>
 __global__ __launch_bounds__(NT) void gdn_decode_kernel(
     float* __restrict__ state, const uint16_t* __restrict__ conv_out, const uint16_t* __restrict__ a,
     const uint16_t* __restrict__ bgate, const float* __restrict__ A_log,
     const uint16_t* __restrict__ dt_bias, uint16_t* __restrict__ y_out,
     const StepScalars* __restrict__ step, uint32_t has_state_host,
-    const uint16_t* __restrict__ norm_w, const uint16_t* __restrict__ z, float eps, float* __restrict__ state_out) {
+    const uint16_t* __restrict__ norm_w, const uint16_t* __restrict__ z, float eps, float* __restrict__ state_out,
+    const GdnGateProj gp) {
   constexpr int kRowsPerBlock = (NT / 32) * RPH;
   constexpr int kBlocksPerHead = kGdnDv / kRowsPerBlock;
   static_assert(!FUSE_NORM || kBlocksPerHead == 1, "the fused norm needs a whole head per block");
@@ -160,12 +254,25 @@ __global__ __launch_bounds__(NT) void gdn_decode_kernel(
   float4* sout = reinterpret_cast<float4*>((IN_PLACE ? state : state_out) + row_off) + j;
 #pragma unroll
   for (int r = 0; r < RPH; ++r) S[r] = srow[r * (kGdnDk / 4)];
-  const GdnIn<RPH> in = gdn_load<RPH>(conv_out, a, bgate, A_log, dt_bias, hv, hk, j, row0);
+  GdnIn<RPH> in = gdn_load<RPH, GATES>(conv_out, a, bgate, A_log, dt_bias, hv, hk, j, row0);
+  GdnGateW gw;
+  GdnGateX gx;
+  __shared__ float gred[GATES ? 2 : 1][kGateThreads / kWave];
+  if constexpr (GATES) {
+    static_assert(!GATES || NT == kGateThreads, "gate projections need 256-thread blocks");
+    gw = gdn_gate_load_w(gp, hv, tid);
+    gx = gdn_gate_load_x(gp, 0, tid);
+  }
   // A fresh sequence ignores the stored state (it may hold anything): a mask,
   // not a branch, so no wait for the state rows is forced here.
   const bool has_state = step ? (step->rope_pos != 0) : (has_state_host != 0);
   const uint32_t keep = has_state ? 0xffffffffu : 0u;
 
+  if constexpr (GATES) {
+    gdn_gate_partial(gp, gw, gx, tid, gred);
+    __syncthreads();
+    gdn_gate_total(gred, in.a, in.b);
+  }
   const GdnGates gates = gdn_gates(in);
   const GdnQK qk = gdn_qk(in.q, in.k);
 #pragma unroll
@@ -200,11 +307,12 @@ __global__ __launch_bounds__(NT) void gdn_decode_kernel(
 // it in registers and writes `state_out` (may equal state). Inputs per token
 // r: conv_out + r*8192, a / b + r*32, y_out + r*4096, step[r]. The per-token
 // math is the single-token kernel's (gdn_gates, gdn_qk, gdn_row).
-template <int NT, int RPH>
+template <int NT, int RPH, bool GATES>
 __global__ __launch_bounds__(NT) void gdn_decode2_kernel(
     const float* state, float* __restrict__ snap, float* state_out, const uint16_t* __restrict__ conv_out,
     const uint16_t* __restrict__ a, const uint16_t* __restrict__ bgate, const float* __restrict__ A_log,
-    const uint16_t* __restrict__ dt_bias, uint16_t* __restrict__ y_out, const StepScalars* __restrict__ step) {
+    const uint16_t* __restrict__ dt_bias, uint16_t* __restrict__ y_out, const StepScalars* __restrict__ step,
+    const GdnGateProj gp) {
   constexpr int kRowsPerBlock = (NT / 32) * RPH;
   constexpr int kBlocksPerHead = kGdnDv / kRowsPerBlock;
   const uint32_t hv = blockIdx.x / kBlocksPerHead;
@@ -220,8 +328,22 @@ __global__ __launch_bounds__(NT) void gdn_decode2_kernel(
   GdnIn<RPH> in[2];
 #pragma unroll
   for (int t = 0; t < 2; ++t)
-    in[t] = gdn_load<RPH>(conv_out + t * kGdnConvDim, a + t * kGdnHv, bgate + t * kGdnHv, A_log, dt_bias, hv, hk, j,
-                          row0);
+    in[t] = gdn_load<RPH, GATES>(conv_out + t * kGdnConvDim, a + t * kGdnHv, bgate + t * kGdnHv, A_log, dt_bias, hv,
+                                 hk, j, row0);
+  GdnGateW gw;
+  GdnGateX gx[2];
+  __shared__ float gred[GATES ? 2 : 1][2][kGateThreads / kWave];
+  if constexpr (GATES) {
+    static_assert(!GATES || NT == kGateThreads, "gate projections need 256-thread blocks");
+    gw = gdn_gate_load_w(gp, hv, tid);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) gx[t] = gdn_gate_load_x(gp, t, tid);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) gdn_gate_partial(gp, gw, gx[t], tid, gred[t]);
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < 2; ++t) gdn_gate_total(gred[t], in[t].a, in[t].b);
+  }
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     // a fresh sequence: the incoming state is ignored (mask, no branch)
@@ -267,33 +389,59 @@ __global__ void rmsnorm_gated_kernel(const uint16_t* __restrict__ x, const uint1
 
 namespace prg {
 
+// Checks a GdnGateProj for the in-kernel gate projections.
+static int check_gates(const GdnGateProj* g, const char* name) {
+  if (!(g->x_image && g->wa && g->sa && g->ba && g->wb && g->sb && g->bb))
+    return set_error(PRG_ERR_INVALID_ARG, "%s: gate projections need the activation image and both matrices", name);
+  if (g->K == 0 || g->K % 64 != 0 || g->K > kGdnGateProjMaxK)
+    return set_error(PRG_ERR_INVALID_ARG, "%s: gate projections need K a multiple of 64 and <= %u (K = %u)", name,
+                     kGdnGateProjMaxK, g->K);
+  return PRG_OK;
+}
+
 int launch_gdn_decode(hipStream_t s, float* state, const uint16_t* conv_out, const uint16_t* a,
                       const uint16_t* b, const float* A_log, const uint16_t* dt_bias,
                       uint16_t* y_out, const StepScalars* step_dev, uint32_t has_state_host,
-                      const uint16_t* norm_w, const uint16_t* z, float eps, float* state_out) {
+                      const uint16_t* norm_w, const uint16_t* z, float eps, float* state_out,
+                      const GdnGateProj* gates) {
   const bool in_place = !(state_out && state_out != state);
+  const GdnGateProj gp = gates ? *gates : GdnGateProj{};
   if (norm_w) {
+    if (gates) return set_error(PRG_ERR_INVALID_ARG, "gated_delta_decode: gate projections need the unfused form");
     constexpr int kRph = 8;
     const dim3 grid(kGdnHv);
     if (in_place)
-      hipLaunchKernelGGL((gdn_decode_kernel<true, kGdnFusedThreads, kRph, true>), grid, dim3(kGdnFusedThreads), 0, s,
-                         state, conv_out, a, b, A_log, dt_bias, y_out, step_dev, has_state_host, norm_w, z, eps,
-                         nullptr);
+      hipLaunchKernelGGL((gdn_decode_kernel<true, kGdnFusedThreads, kRph, true, false>), grid, dim3(kGdnFusedThreads),
+                         0, s, state, conv_out, a, b, A_log, dt_bias, y_out, step_dev, has_state_host, norm_w, z, eps,
+                         nullptr, gp);
     else
-      hipLaunchKernelGGL((gdn_decode_kernel<false, kGdnFusedThreads, kRph, true>), grid, dim3(kGdnFusedThreads), 0,
-                         s, state, conv_out, a, b, A_log, dt_bias, y_out, step_dev, has_state_host, norm_w, z, eps,
-                         state_out);
+      hipLaunchKernelGGL((gdn_decode_kernel<false, kGdnFusedThreads, kRph, true, false>), grid,
+                         dim3(kGdnFusedThreads), 0, s, state, conv_out, a, b, A_log, dt_bias, y_out, step_dev,
+                         has_state_host, norm_w, z, eps, state_out, gp);
   } else {
     constexpr int kRph = 2;
     const dim3 grid(kGdnHv * (kGdnDv / ((kGdnSplitThreads / 32) * kRph)));
-    if (in_place)
-      hipLaunchKernelGGL((gdn_decode_kernel<true, kGdnSplitThreads, kRph, false>), grid, dim3(kGdnSplitThreads), 0,
-                         s, state, conv_out, a, b, A_log, dt_bias, y_out, step_dev, has_state_host, nullptr, nullptr,
-                         0.0f, nullptr);
-    else
-      hipLaunchKernelGGL((gdn_decode_kernel<false, kGdnSplitThreads, kRph, false>), grid, dim3(kGdnSplitThreads), 0,
-                         s, state, conv_out, a, b, A_log, dt_bias, y_out, step_dev, has_state_host, nullptr, nullptr,
-                         0.0f, state_out);
+    float* out = in_place ? nullptr : state_out;
+    if (gates) {
+      if (int rc = check_gates(gates, "gated_delta_decode")) return rc;
+      if (in_place)
+        hipLaunchKernelGGL((gdn_decode_kernel<true, kGdnSplitThreads, kRph, false, true>), grid,
+                           dim3(kGdnSplitThreads), 0, s, state, conv_out, a, b, A_log, dt_bias, y_out, step_dev,
+                           has_state_host, nullptr, nullptr, 0.0f, out, gp);
+      else
+        hipLaunchKernelGGL((gdn_decode_kernel<false, kGdnSplitThreads, kRph, false, true>), grid,
+                           dim3(kGdnSplitThreads), 0, s, state, conv_out, a, b, A_log, dt_bias, y_out, step_dev,
+                           has_state_host, nullptr, nullptr, 0.0f, out, gp);
+    } else {
+      if (in_place)
+        hipLaunchKernelGGL((gdn_decode_kernel<true, kGdnSplitThreads, kRph, false, false>), grid,
+                           dim3(kGdnSplitThreads), 0, s, state, conv_out, a, b, A_log, dt_bias, y_out, step_dev,
+                           has_state_host, nullptr, nullptr, 0.0f, out, gp);
+      else
+        hipLaunchKernelGGL((gdn_decode_kernel<false, kGdnSplitThreads, kRph, false, false>), grid,
+                           dim3(kGdnSplitThreads), 0, s, state, conv_out, a, b, A_log, dt_bias, y_out, step_dev,
+                           has_state_host, nullptr, nullptr, 0.0f, out, gp);
+    }
   }
   PRG_CHECK_LAUNCH("gated_delta_decode");
   return PRG_OK;
@@ -301,13 +449,19 @@ int launch_gdn_decode(hipStream_t s, float* state, const uint16_t* conv_out, con
 
 int launch_gdn_decode2(hipStream_t s, const float* state, float* snap, float* state_out, const uint16_t* conv_out,
                        const uint16_t* a, const uint16_t* b, const float* A_log, const uint16_t* dt_bias,
-                       uint16_t* y_out, const StepScalars* step_dev) {
+                       uint16_t* y_out, const StepScalars* step_dev, const GdnGateProj* gates) {
   if (!state || !snap || !state_out || !step_dev || snap == state || snap == state_out)
     return set_error(PRG_ERR_INVALID_ARG, "gated_delta_decode2: needs state, a distinct snapshot and step scalars");
   constexpr int kRph = 2;
   const dim3 grid(kGdnHv * (kGdnDv / ((kGdnSplitThreads / 32) * kRph)));
-  hipLaunchKernelGGL((gdn_decode2_kernel<kGdnSplitThreads, kRph>), grid, dim3(kGdnSplitThreads), 0, s, state, snap,
-                     state_out, conv_out, a, b, A_log, dt_bias, y_out, step_dev);
+  if (gates) {
+    if (int rc = check_gates(gates, "gated_delta_decode2")) return rc;
+    hipLaunchKernelGGL((gdn_decode2_kernel<kGdnSplitThreads, kRph, true>), grid, dim3(kGdnSplitThreads), 0, s, state,
+                       snap, state_out, conv_out, a, b, A_log, dt_bias, y_out, step_dev, *gates);
+  } else {
+    hipLaunchKernelGGL((gdn_decode2_kernel<kGdnSplitThreads, kRph, false>), grid, dim3(kGdnSplitThreads), 0, s, state,
+                       snap, state_out, conv_out, a, b, A_log, dt_bias, y_out, step_dev, GdnGateProj{});
+  }
   PRG_CHECK_LAUNCH("gated_delta_decode2");
   return PRG_OK;
 }

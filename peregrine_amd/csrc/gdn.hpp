@@ -63,22 +63,44 @@ __device__ inline void conv1d_silu_step2(const float* state, float* snap, float*
   o1 = f2bf(a1 / (1.0f + expf(-a1)));
 }
 
+// The GDN gate projections a = in_proj_a(x) and b = in_proj_b(x) (bf16, [Hv]
+// each) computed by the recurrence kernel itself instead of by the in_proj
+// GEMV: from the GEMV's normalised activation image (GemvParams::x_image)
+// and the two Q4 matrices [Hv, K], a quarter of a quantisation group per
+// thread of a 256-thread block, so K <= kGdnGateProjMaxK. Taking the 64 rows
+// out of the in_proj launch leaves it 12288 rows, four per wave of its grid.
+struct GdnGateProj {
+  const uint32_t* x_image;  // activation rows back to back, K / 2 dwords each
+  const uint32_t* wa;
+  const uint16_t* sa;
+  const uint16_t* ba;
+  const uint32_t* wb;
+  const uint16_t* sb;
+  const uint16_t* bb;
+  uint32_t K;
+};
+constexpr uint32_t kGdnGateProjMaxK = 4096;
+
 // One block per v-head. With norm_w != nullptr the gated RMSNorm is fused and
 // y_out receives the normalised output. The state counts as present when
 // step_dev->rope_pos != 0 (decoder_layer.zig:564), or per has_state_host when
 // step_dev is null. The updated state is written to state_out (nullptr: in
-// place).
+// place). With `gates` (unfused form only; a / b then unused) the gate
+// projections are computed in the kernel.
 int launch_gdn_decode(hipStream_t s, float* state, const uint16_t* conv_out, const uint16_t* a,
                       const uint16_t* b, const float* A_log, const uint16_t* dt_bias,
                       uint16_t* y_out, const StepScalars* step_dev, uint32_t has_state_host,
-                      const uint16_t* norm_w, const uint16_t* z, float eps, float* state_out = nullptr);
+                      const uint16_t* norm_w, const uint16_t* z, float eps, float* state_out = nullptr,
+                      const GdnGateProj* gates = nullptr);
 
 // Two consecutive tokens (the two-token verify): token 0 reads `state` and
 // writes `snap`, token 1 continues and writes `state_out` (may equal state).
 // conv_out, a, b and y_out hold the two tokens' rows back to back
 // (8192 / 32 / 32 / 4096 values apart); step_dev[0..1] are their steps.
+// With `gates` (a / b then unused) the gate projections are computed in the
+// kernel from the two rows of gates->x_image.
 int launch_gdn_decode2(hipStream_t s, const float* state, float* snap, float* state_out, const uint16_t* conv_out,
                        const uint16_t* a, const uint16_t* b, const float* A_log, const uint16_t* dt_bias,
-                       uint16_t* y_out, const StepScalars* step_dev);
+                       uint16_t* y_out, const StepScalars* step_dev, const GdnGateProj* gates = nullptr);
 
 }  // namespace prg

@@ -278,6 +278,16 @@ int run_gemv(hipStream_t s, GemvParams& p, int epi, int norm, const char* name) 
 }
 
 // GDN layer: norm+in_proj(+conv) -> recurrence -> gated norm+out_proj + residual.
+// The GDN gate projections (in_proj_a / in_proj_b, 32 rows each) run inside
+// the recurrence kernel when the hidden size allows it (one quantisation
+// group per lane): the in_proj GEMV then has 8192 + 4096 rows, four per wave
+// of its grid, instead of a fifth round for 64 rows.
+static bool gates_in_gdn(const PrgModelConfig& c) { return c.hidden <= kGdnGateProjMaxK && c.hidden % 64 == 0; }
+static GdnGateProj gate_proj(PrgModelState* st, const LinearAttentionBlock& b, uint32_t hidden) {
+  return GdnGateProj{st->ximg,          b.in_a.weight, b.in_a.scales, b.in_a.biases,
+                     b.in_b.weight,     b.in_b.scales, b.in_b.biases, hidden};
+}
+
 int encode_linear_attention(PrgModel* m, PrgModelState* st, const DecoderLayer& L, const GdnIO& io,
                             const uint16_t* x, uint16_t* h, const StepScalars* step) {
   const LinearAttentionBlock& b = L.lin;
@@ -293,14 +303,19 @@ int encode_linear_attention(PrgModel* m, PrgModelState* st, const DecoderLayer& 
   p.seg[0].conv_dim = kGdnConvDim;
   add_seg(p, b.in_z, nullptr);
   p.seg[1].silu_out[0] = st->zsilu;
-  add_seg(p, b.in_a, st->abuf);
-  add_seg(p, b.in_b, st->bbuf);
+  const GdnGateProj gp = gate_proj(st, b, c.hidden);
+  if (gates_in_gdn(c)) {
+    p.x_image[0] = st->ximg;
+  } else {
+    add_seg(p, b.in_a, st->abuf);
+    add_seg(p, b.in_b, st->bbuf);
+  }
   if (int rc = run_gemv(s, p, kEpiPlain, kNormRms, "linear_attn.in_proj")) return rc;
   // Recurrence -> raw y (bf16); the gated RMSNorm runs in the out_proj
   // GEMV's prologue (per 128-wide head, gate z from in_proj).
   if (!st->gemv_only)
     if (int rc = launch_gdn_decode(s, io.recur_in, st->conv_out, st->abuf, st->bbuf, b.a_log, b.dt_bias, st->gated,
-                                   step, 0, nullptr, nullptr, 0.0f, io.recur_out))
+                                   step, 0, nullptr, nullptr, 0.0f, io.recur_out, gates_in_gdn(c) ? &gp : nullptr))
       return rc;
   GemvParams o = gemv_params(st->gated, kGdnValDim);
   o.norm_w = b.norm_weight;
@@ -342,15 +357,21 @@ int encode_linear_attention2(PrgModel* m, PrgModelState* st, const DecoderLayer&
   add_seg(p, b.in_z, nullptr);
   p.seg[1].silu_out[0] = zsilu[0];
   p.seg[1].silu_out[1] = zsilu[1];
-  add_seg(p, b.in_a, abuf[0]);
-  p.seg[2].out[1] = abuf[1];
-  add_seg(p, b.in_b, bbuf[0]);
-  p.seg[3].out[1] = bbuf[1];
+  const GdnGateProj gp = gate_proj(st, b, c.hidden);
+  if (gates_in_gdn(c)) {
+    p.x_image[0] = st->ximg;
+    p.x_image[1] = st->ximg + c.hidden / 2;
+  } else {
+    add_seg(p, b.in_a, abuf[0]);
+    p.seg[2].out[1] = abuf[1];
+    add_seg(p, b.in_b, bbuf[0]);
+    p.seg[3].out[1] = bbuf[1];
+  }
   if (int rc = run_gemv(s, p, kEpiPlain, kNormRms, "linear_attn.in_proj2")) return rc;
   // both recurrence steps in one launch: row 0's state to io.recur_out (the
   // snapshot), row 1's back to io.recur_in
   if (int rc = launch_gdn_decode2(s, io.recur_in, io.recur_out, io.recur_in, conv_out[0], abuf[0], bbuf[0], b.a_log,
-                                  b.dt_bias, gated[0], step))
+                                  b.dt_bias, gated[0], step, gates_in_gdn(c) ? &gp : nullptr))
     return rc;
   GemvParams o = gemv_params(gated[0], kGdnValDim);
   o.x[1] = gated[1];
@@ -737,6 +758,7 @@ int prg_model_state_create(PrgModel* model, uint32_t max_seq, PrgModelState** ou
   items.push_back({"ws.conv_out", 2 * bf * kGdnConvDim, reinterpret_cast<void**>(&st->conv_out)});
   items.push_back({"ws.z_silu", 2 * sizeof(float) * kGdnValDim, reinterpret_cast<void**>(&st->zsilu)});
   items.push_back({"ws.a", 2 * bf * kGdnHv, reinterpret_cast<void**>(&st->abuf)});
+  items.push_back({"ws.ximg", 2 * bf * c.hidden, reinterpret_cast<void**>(&st->ximg)});
   items.push_back({"ws.b", 2 * bf * kGdnHv, reinterpret_cast<void**>(&st->bbuf)});
   items.push_back({"ws.gated", 2 * bf * kGdnValDim, reinterpret_cast<void**>(&st->gated)});
   items.push_back({"ws.qp", 2 * bf * 2 * kAttnQHeads * kAttnHeadDim, reinterpret_cast<void**>(&st->qp)});

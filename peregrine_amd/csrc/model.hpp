@@ -176,6 +176,7 @@ struct PrgModelState {
   // decode workspace
   uint16_t *hA = nullptr, *hB = nullptr;
   uint16_t *conv_out = nullptr, *abuf = nullptr, *bbuf = nullptr, *gated = nullptr;
+  uint32_t* ximg = nullptr;  // [2][hidden / 2]: the GDN in_proj's normalised rows for the gate projections
   float* zsilu = nullptr;  // silu(z) of the GDN gate, f32 (feeds the gated norm)
   uint16_t *qp = nullptr, *kbuf = nullptr, *vbuf = nullptr, *qbuf = nullptr, *gatebuf = nullptr, *ctx = nullptr;
   float* partials = nullptr;

@@ -96,6 +96,10 @@ struct GemvParams {
   // final argmax's order) to pval / pidx[wave] instead of one per 8 rows, and
   // the launch's wave count goes here (the grid is capped at kArgmaxMaxWaves).
   uint32_t* argmax_waves;
+  // If set, block 0 also writes activation row m as staged (normalised with
+  // NORM, bf16 pairs in the dot order of unpack_q4_word: K / 2 dwords) to
+  // x_image[m], for a consumer that needs the same normalised row.
+  uint32_t* x_image[2];
 };
 
 constexpr uint32_t kArgmaxMaxWaves = 4096;
@@ -569,10 +573,15 @@ __global__ __launch_bounds__(kGemvThreads) void q4_gemv_kernel(const GemvParams 
         if (!TAIL || gi < n8)
           dst[gi] = permute_pairs(gated_rms_apply(xv[m][it], nw[it], zv[m][it][0], zv[m][it][1], hscale));
       } else if (!TAIL || gi < n8) {
+        uint4 v;
         if constexpr (NORM == kNormRms)
-          dst[gi] = permute_pairs(rms_apply(xv[m][it], nw[it], scale));
+          v = permute_pairs(rms_apply(xv[m][it], nw[it], scale));
         else
-          dst[gi] = permute_pairs(xv[m][it]);
+          v = permute_pairs(xv[m][it]);
+        dst[gi] = v;
+        // block 0 only (its waves may wait for this store together with the
+        // first group's weights; the other blocks take no store)
+        if (p.x_image[m] != nullptr && blockIdx.x == 0) reinterpret_cast<uint4*>(p.x_image[m])[gi] = v;
       }
     }
   }
