@@ -39,17 +39,19 @@ def log(*a) -> None:
 
 
 def token_gemv_bytes(cfg) -> int:
-    """Algorithmic bytes of one decode token's GEMVs (Q4 weights + scales +
-    biases): per GDN layer in_proj (qkv 8192 | z 4096 | a 32 | b 32 rows) and
-    out_proj 4096 x 4096, per attention layer q|gate 8192 + k 1024 + v 1024 rows
-    and o_proj 4096 x 4096, per layer gate/up 2 x 12288 and down 4096 x 12288,
-    and the lm_head."""
+    """Algorithmic bytes of one decode token's GEMV launches (Q4 weights +
+    scales + biases): per GDN layer in_proj (qkv 8192 | z 4096 rows; the a / b
+    gate rows, 32 each, are read by the recurrence kernel when hidden <= 4096)
+    and out_proj 4096 x 4096, per attention layer q|gate 8192 + k 1024 + v 1024
+    rows and o_proj 4096 x 4096, per layer gate/up 2 x 12288 and down
+    4096 x 12288, and the lm_head."""
     from peregrine_amd.gemv_bench import q4_bytes
 
     H, F = cfg.hidden, cfg.intermediate
     n_attn = cfg.num_layers // cfg.full_attention_interval
     n_gdn = cfg.num_layers - n_attn
-    gdn = q4_bytes(8192 + 4096 + 32 + 32, H) + q4_bytes(4096, 4096)
+    gate_rows = 0 if H <= 4096 else 64
+    gdn = q4_bytes(8192 + 4096 + gate_rows, H) + q4_bytes(4096, 4096)
     attn = q4_bytes(8192 + 1024 + 1024, H) + q4_bytes(H, 4096)
     mlp = 2 * q4_bytes(F, H) + q4_bytes(H, F)
     return n_gdn * gdn + n_attn * attn + cfg.num_layers * mlp + q4_bytes(cfg.vocab, H)
