@@ -239,12 +239,15 @@ __global__ __launch_bounds__(NT) void gdn_decode_kernel(
   __shared__ float ysh[kGdnDv];
   __shared__ float red[NT / kWave];
 
-  const uint32_t hv = blockIdx.x / kBlocksPerHead;
+  // Block b takes head b mod 32 and row slice b / 32: the workgroup
+  // dispatcher deals blocks to the 8 XCDs round-robin, so every slice of a
+  // head runs on the same XCD and its gate weights are fetched into one L2.
+  const uint32_t hv = blockIdx.x % kGdnHv;
   const uint32_t hk = hv / (kGdnHv / kGdnHk);
   const int tid = threadIdx.x;
   const int hw = tid >> 5;   // half-wave
   const int j = tid & 31;    // lane in half-wave
-  const uint32_t row0 = (blockIdx.x % kBlocksPerHead) * kRowsPerBlock + hw * RPH;  // first dv row
+  const uint32_t row0 = (blockIdx.x / kGdnHv) * kRowsPerBlock + hw * RPH;  // first dv row
   // State rows for this half-wave, issued first and unconditionally: the
   // step scalars decide only afterwards whether they are used, so the state
   // loads do not wait for the step block's load.
@@ -314,13 +317,16 @@ __global__ __launch_bounds__(NT) void gdn_decode2_kernel(
     const uint16_t* __restrict__ dt_bias, uint16_t* __restrict__ y_out, const StepScalars* __restrict__ step,
     const GdnGateProj gp) {
   constexpr int kRowsPerBlock = (NT / 32) * RPH;
-  constexpr int kBlocksPerHead = kGdnDv / kRowsPerBlock;
-  const uint32_t hv = blockIdx.x / kBlocksPerHead;
+  static_assert(kGdnDv % kRowsPerBlock == 0, "whole row slices per head");
+  // Block b takes head b mod 32 and row slice b / 32: the workgroup
+  // dispatcher deals blocks to the 8 XCDs round-robin, so every slice of a
+  // head runs on the same XCD and its gate weights are fetched into one L2.
+  const uint32_t hv = blockIdx.x % kGdnHv;
   const uint32_t hk = hv / (kGdnHv / kGdnHk);
   const int tid = threadIdx.x;
   const int hw = tid >> 5;
   const int j = tid & 31;
-  const uint32_t row0 = (blockIdx.x % kBlocksPerHead) * kRowsPerBlock + hw * RPH;
+  const uint32_t row0 = (blockIdx.x / kGdnHv) * kRowsPerBlock + hw * RPH;
   const size_t row_off = (static_cast<size_t>(hv) * kGdnDv + row0) * kGdnDk;
   float4 S[RPH];
 #pragma unroll
