@@ -172,66 +172,47 @@ __device__ inline uint32_t attn_cached_tokens(const AttnDecodeArgs& a0) {
   return min(a0.packed_q ? L - 1 : L, a0.stride);
 }
 
-// Sum over the 256 threads of a block for 4 values at once (one per head);
-// every thread gets the 4 totals. red: LDS [4 waves][4]. Lanes of a 16-lane
-// row are combined with DPP, the 4 rows with readlane.
-__device__ inline void block_sum4(float (&v)[4], float* red) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+// RMSNorm with weight wt and partial NeoX RoPE at pos (dims [0, 64), pairs
+// i, i + 32; normed values rounded to bf16 before the rotation,
+// attention.metal:391-392) of one 256-wide head held by one wave: lane l
+// holds dims l + 64k (k = 0..3) and gets their bf16 results in o[k]. The sum
+// of squares has a fixed order: per 64-dim group the row16 DPP sums of its
+// four 16-lane rows as (r0 + r1) + (r2 + r3), then the groups as
+// (g0 + g1) + (g2 + g3); every row of a two-token launch runs this same code,
+// so the verify rows equal single-token steps. No barrier: the rotary partner
+// of dim d < 64 is dim d ^ 32, i.e. lane l ^ 32.
+__device__ inline void norm_rope_wave(const float (&x)[4], const float (&wt)[4], uint32_t pos, int lane,
+                                      uint16_t (&o)[4]) {
+  float S[4];
 #pragma unroll
-  for (int g = 0; g < 4; ++g) {
-    const int x = __builtin_bit_cast(int, row16_sum(v[g]));
-    const float s = (__builtin_bit_cast(float, __builtin_amdgcn_readlane(x, 0)) +
-                     __builtin_bit_cast(float, __builtin_amdgcn_readlane(x, 16))) +
-                    (__builtin_bit_cast(float, __builtin_amdgcn_readlane(x, 32)) +
-                     __builtin_bit_cast(float, __builtin_amdgcn_readlane(x, 48)));
-    if (lane == 0) red[w * 4 + g] = s;
+  for (int k = 0; k < 4; ++k) {
+    const int v = __builtin_bit_cast(int, row16_sum(x[k] * x[k]));
+    S[k] = (__builtin_bit_cast(float, __builtin_amdgcn_readlane(v, 0)) +
+            __builtin_bit_cast(float, __builtin_amdgcn_readlane(v, 16))) +
+           (__builtin_bit_cast(float, __builtin_amdgcn_readlane(v, 32)) +
+            __builtin_bit_cast(float, __builtin_amdgcn_readlane(v, 48)));
   }
-  __syncthreads();
-#pragma unroll
-  for (int g = 0; g < 4; ++g) v[g] = (red[g] + red[4 + g]) + (red[8 + g] + red[12 + g]);
-}
-
-// Normalise + rotate the NH heads x[h] (dim = threadIdx.x of 256) with RMSNorm
-// weight w and partial NeoX RoPE at pos (dims [0, 64), pairs i, i + 32; normed
-// values rounded to bf16 before the rotation, attention.metal:391-392), as the
-// prepare kernel does per dim. The bf16 results go to out[h][256] in LDS.
-template <int NH>
-__device__ inline void norm_rope_heads(const float (&x)[4], float wt, uint32_t pos, float* red, float* xch,
-                                       uint16_t* out) {
-  const uint32_t col = threadIdx.x;
-  float ss[4];
-#pragma unroll
-  for (int h = 0; h < 4; ++h) ss[h] = h < NH ? x[h] * x[h] : 0.0f;
-  block_sum4(ss, red);
+  const float ss = (S[0] + S[1]) + (S[2] + S[3]);
   constexpr uint32_t half = kAttnRotary / 2;
-  float c = 1.0f, sn = 0.0f;
-  if (col < kAttnRotary) {
-    const uint32_t i = col & (half - 1);
-    const float inv_freq = powf(kAttnTheta, -(2.0f * static_cast<float>(i)) / static_cast<float>(kAttnRotary));
-    const float angle = static_cast<float>(pos) * inv_freq;
-    c = cosf(angle);
-    sn = sinf(angle);
-  }
+  const uint32_t i = static_cast<uint32_t>(lane) & (half - 1);
+  const float inv_freq = powf(kAttnTheta, -(2.0f * static_cast<float>(i)) / static_cast<float>(kAttnRotary));
+  const float angle = static_cast<float>(pos) * inv_freq;
+  const float c = cosf(angle);
+  const float sn = sinf(angle);
+  const float inv_rms = rsqrtf(ss / static_cast<float>(kAttnHeadDim) + kAttnEps);
   float n[4];
 #pragma unroll
-  for (int h = 0; h < NH; ++h) {
-    const float inv_rms = rsqrtf(ss[h] / static_cast<float>(kAttnHeadDim) + kAttnEps);
-    n[h] = x[h] * inv_rms * wt;
-    if (col < kAttnRotary) {
-      n[h] = round_bf(n[h]);
-      xch[h * kAttnRotary + col] = n[h];
-    }
-  }
-  __syncthreads();
+  for (int k = 0; k < 4; ++k) n[k] = x[k] * inv_rms * wt[k];
+  n[0] = round_bf(n[0]);  // dims [0, 64) rotate
+  const float other = __shfl_xor(n[0], static_cast<int>(half), kWave);
+  float r;
+  if (static_cast<uint32_t>(lane) < half)
+    r = n[0] * c - other * sn;
+  else
+    r = n[0] * c + other * sn;
+  o[0] = f2bf(r);
 #pragma unroll
-  for (int h = 0; h < NH; ++h) {
-    float o = n[h];
-    if (col < half)
-      o = n[h] * c - xch[h * kAttnRotary + col + half] * sn;
-    else if (col < kAttnRotary)
-      o = n[h] * c + xch[h * kAttnRotary + col - half] * sn;
-    out[h * kAttnHeadDim + col] = f2bf(o);
-  }
+  for (int k = 1; k < 4; ++k) o[k] = f2bf(n[k]);
 }
 
 // FRESH: the decode-step form (packed_q set). Every load that does not depend
@@ -246,27 +227,33 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnD
   // decode-step form: prepared q of the group's 4 heads, new tokens' k and v
   __shared__ uint16_t qf[kAttnGroup * kAttnHeadDim];
   __shared__ uint16_t kf[2 * kAttnHeadDim], vf[2 * kAttnHeadDim];
-  __shared__ float red[16], xch[kAttnGroup * kAttnRotary];
   const uint32_t row = blockIdx.z;
   const AttnDecodeArgs a = attn_row_args(a0, row);
 
   const uint32_t kvh = blockIdx.y;
   const uint32_t split = blockIdx.x;
   const uint32_t col = threadIdx.x;
-  // q of the group's 4 heads (one dim per thread), its norm weight, and the
-  // new tokens' raw k / v (row 1 repeats row 0 when the launch has one row)
-  float xq[kAttnGroup], xk[2] = {0.0f, 0.0f}, wq = 0.0f, wk = 0.0f;
+  // Wave w prepares q head w of the group and, in the split that takes the
+  // new tokens, new token w's k (lane l: dims l + 64k, with their norm
+  // weights); thread col keeps the new tokens' v at dim col. Row 1 repeats
+  // row 0 when the launch has one row.
+  const int wv = threadIdx.x >> 6, ln = threadIdx.x & 63;
+  float xq[4] = {}, wq[4] = {}, xk[4] = {}, wk[4] = {};
   uint16_t vb[2] = {0, 0};
   if constexpr (FRESH) {
+    const uint16_t* qsrc = a.packed_q + (static_cast<size_t>(kvh) * kAttnGroup + wv) * 2 * kAttnHeadDim;
+    const uint32_t kr = min(static_cast<uint32_t>(wv), a0.rows - 1);
+    const uint16_t* ksrc = a0.k_in + (static_cast<size_t>(kr) * kAttnKvHeads + kvh) * kAttnHeadDim;
 #pragma unroll
-    for (int g = 0; g < static_cast<int>(kAttnGroup); ++g)
-      xq[g] = bf2f(a.packed_q[(static_cast<size_t>(kvh) * kAttnGroup + g) * 2 * kAttnHeadDim + col]);
-    wq = bf2f(a.q_norm[col]);
-    wk = bf2f(a0.k_norm[col]);
+    for (int k = 0; k < 4; ++k) {
+      xq[k] = bf2f(qsrc[ln + 64 * k]);
+      wq[k] = bf2f(a.q_norm[ln + 64 * k]);
+      xk[k] = bf2f(ksrc[ln + 64 * k]);
+      wk[k] = bf2f(a0.k_norm[ln + 64 * k]);
+    }
 #pragma unroll
     for (uint32_t j = 0; j < 2; ++j) {
       const uint32_t jr = min(j, a0.rows - 1);
-      xk[j] = bf2f(a0.k_in[(static_cast<size_t>(jr) * kAttnKvHeads + kvh) * kAttnHeadDim + col]);
       vb[j] = a0.v_in[(static_cast<size_t>(jr) * kAttnKvHeads + kvh) * kAttnHeadDim + col];
     }
   }
@@ -333,21 +320,33 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnD
       npos[j] = a0.step ? a0.step[jr].rope_pos : a0.rope_pos_host + j;
       ncpos[j] = a0.step ? a0.step[jr].cache_pos : a0.cache_pos_host + j;
     }
-    norm_rope_heads<kAttnGroup>(xq, wq, a.step ? a.step->rope_pos : a.rope_pos_host, red, xch, qf);
-    // unrolled with uniform guards (no loop back-edge), so the compiler's
-    // waits here cover the new tokens' k / v loads, not the K / V tile
+    {
+      uint16_t o[4];
+      norm_rope_wave(xq, wq, a.step ? a.step->rope_pos : a.rope_pos_host, ln, o);
 #pragma unroll
-    for (uint32_t j = 0; j < 2; ++j) {
-      if (j < nx) {
-        __syncthreads();  // red / xch reuse
-        const float xj[4] = {xk[j], 0.0f, 0.0f, 0.0f};
-        norm_rope_heads<1>(xj, wk, npos[j], red, xch, kf + j * kAttnHeadDim);
-        vf[j * kAttnHeadDim + col] = vb[j];
-        if (j == row && ncpos[j] < a.stride) {
-          a.key_cache_w[(static_cast<size_t>(kvh) * a.stride + ncpos[j]) * kAttnHeadDim + col] =
-              kf[j * kAttnHeadDim + col];
-          a.value_cache_w[(static_cast<size_t>(kvh) * kAttnHeadDim + col) * a.stride + ncpos[j]] = vb[j];
-        }
+      for (int k = 0; k < 4; ++k) qf[wv * kAttnHeadDim + ln + 64 * k] = o[k];
+    }
+    // new token j = wv (wave-uniform guard; no loads behind it)
+    const uint32_t j = static_cast<uint32_t>(wv);
+    if (j < nx) {
+      const uint32_t pj = j == 0 ? npos[0] : npos[1];
+      const uint32_t cj = j == 0 ? ncpos[0] : ncpos[1];
+      uint16_t o[4];
+      norm_rope_wave(xk, wk, pj, ln, o);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) kf[j * kAttnHeadDim + ln + 64 * k] = o[k];
+      if (j == row && cj < a.stride) {
+        uint16_t* kdst = a.key_cache_w + (static_cast<size_t>(kvh) * a.stride + cj) * kAttnHeadDim;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) kdst[ln + 64 * k] = o[k];
+      }
+    }
+#pragma unroll
+    for (uint32_t jj = 0; jj < 2; ++jj) {
+      if (jj < nx) {
+        vf[jj * kAttnHeadDim + col] = vb[jj];
+        if (jj == row && ncpos[jj] < a.stride)
+          a.value_cache_w[(static_cast<size_t>(kvh) * kAttnHeadDim + col) * a.stride + ncpos[jj]] = vb[jj];
       }
     }
     __syncthreads();
