@@ -22,7 +22,7 @@
 //     whole chip; block b takes head b mod 32 (one XCD per head). The gated
 //     RMSNorm then runs in the out_proj GEMV prologue. In the model each
 //     block also computes the head's gate inputs a and b (the in_proj_a /
-//     in_proj_b rows of block_linear.zig:199-210) from the in_proj GEMV's
+//     in_proj_b rows of block_linear.zig:229-231) from the in_proj GEMV's
 //     normalised row, so that GEMV carries only the qkv and z rows.
 //   * Fused gated norm: one 512-thread block per head (16 half-waves x 8 rows)
 //     holds all 128 outputs of its head and normalises them in place.
