@@ -453,6 +453,10 @@ def test_lm_head_planted_ties_every_argmax_path(gpu, orc):
     argmax over the same pattern (x = ones) and are also fixed by hand:
     partial 256 (tie key 1) beats 1, 128, 3328, 4352 and its first row 2050
     beats 2053; partial 512 (key 2) beats 5, 384, 7680 and row 4101 beats 4103.
+    Two more partials (2000 and 3000) start with a NaN row followed by a row
+    at four times the planted magnitude, one per sign: the reference's
+    partial keeps its first strict maximum, so a NaN first row leaves the
+    whole partial NaN and it never wins, whichever sign config is active.
     """
     from peregrine_amd.device import DeviceArray
     from peregrine_amd.model import DeviceModel, ModelConfig, ModelState
@@ -465,6 +469,8 @@ def test_lm_head_planted_ties_every_argmax_path(gpu, orc):
     set_a = [8 * 1 + 3, 2050, 2053, 8 * 128 + 7, 8 * 3328 + 1, 8 * 4352 + 4]
     set_b = [8 * 5 + 2, 8 * 384, 4101, 4103, 8 * 7680 + 5]
     pos, neg = f32_to_bf16(np.float32(0.5))[()], f32_to_bf16(np.float32(-0.5))[()]
+    big_pos, big_neg = f32_to_bf16(np.float32(2.0))[()], f32_to_bf16(np.float32(-2.0))[()]
+    nan = np.uint16(0x7FC0)
     zeros_w = np.zeros((V, H // 8), np.uint32)
     zeros_s = np.zeros((V, H // 64), np.uint16)
     _write(m, "language_model.lm_head.weight", zeros_w)
@@ -476,6 +482,9 @@ def test_lm_head_planted_ties_every_argmax_path(gpu, orc):
             bias = np.zeros((V, H // 64), np.uint16)
             bias[set_a] = sa
             bias[set_b] = sb
+            bias[[8 * 2000, 8 * 3000]] = nan  # dead partials: NaN first rows
+            bias[8 * 2000 + 1] = big_pos
+            bias[8 * 3000 + 1] = big_neg
             _write(m, "language_model.lm_head.biases", bias)
             pv, pi = orc.q4_argmax_partial(ones, Q4Weight(zeros_w, zeros_s, bias))
             expect = orc.argmax_pairs(pv[0], pi[0])
