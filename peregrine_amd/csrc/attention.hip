@@ -257,18 +257,29 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnD
       vb[j] = a0.v_in[(static_cast<size_t>(jr) * kAttnKvHeads + kvh) * kAttnHeadDim + col];
     }
   }
-  const uint32_t L = attn_cached_tokens(a0);
+  // Row r partitions its own cached range [0, L_r), L_r = step[r].seq_len - 1,
+  // exactly as a one-token step at its position would, so both rows of a
+  // two-token launch equal single-token steps bit for bit (same splits, same
+  // per-lane summation order).
+  const uint32_t L = attn_cached_tokens(a);
   const uint32_t chunk = attn_chunk(L, a.nsplit);
   const uint32_t t0 = min(split * chunk, L);
   const uint32_t t1 = min(t0 + chunk, L);
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   float* part = a.partials + (static_cast<size_t>(kvh) * kAttnGroup * a.nsplit + split) * kAttnPartialStride;
   const size_t head_stride = static_cast<size_t>(a.nsplit) * kAttnPartialStride;
-  // In the decode-step form the new tokens of rows 0..row are extra tokens of
-  // the split that holds the last cached token (split 0 on an empty cache).
+  // In the decode-step form the row's own new token is an extra token of the
+  // split that holds its last cached token (split 0 on an empty cache). For
+  // row 1 of a two-token launch that last cached token is row 0's new token:
+  // its cache slot is being written by row 0's block in this same launch, so
+  // it is taken from the k / v this block prepares (kf / vf row 0) in place
+  // of the cache, at the same score index and lane slot (`virt`).
   constexpr bool fresh = FRESH;
   const uint32_t last = L == 0 ? 0u : (L - 1) / chunk;
-  const uint32_t nx = (fresh && split == last) ? row + 1 : 0u;
+  const bool in_last = fresh && split == last;
+  const uint32_t nx = in_last ? 1u : 0u;        // the row's own new token
+  const uint32_t nk = in_last ? row + 1 : 0u;   // new tokens whose k / v this block prepares
+  const uint32_t nvirt = in_last ? row : 0u;    // of them, cached tokens of this row
 
   if (t0 >= t1 && nx == 0) {  // empty range: neutral partial
     for (uint32_t i = threadIdx.x; i < kAttnGroup * kAttnPartialStride; i += kAttnThreads) {
@@ -278,7 +289,10 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnD
     return;
   }
   const uint32_t T = t1 - t0;  // cached tokens of this split
-  const uint32_t TX = T + nx;  // plus the new tokens
+  const uint32_t TX = T + nx;  // plus the new token
+  const uint32_t Tc = T - nvirt;  // of them, read from the cache
+  // split-local index of the cached token taken from vf row 0 (none: ~0u)
+  const uint32_t vslot = nvirt ? T - 1 : ~0u;
   const uint32_t ld = a.split_tokens + 2;
   // A range of <= 64 tokens (every split of a cache up to 4096 tokens) issues
   // all of its K and V loads before any arithmetic: one memory round trip.
@@ -328,7 +342,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnD
     }
     // new token j = wv (wave-uniform guard; no loads behind it)
     const uint32_t j = static_cast<uint32_t>(wv);
-    if (j < nx) {
+    if (j < nk) {
       const uint32_t pj = j == 0 ? npos[0] : npos[1];
       const uint32_t cj = j == 0 ? ncpos[0] : ncpos[1];
       uint16_t o[4];
@@ -343,7 +357,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnD
     }
 #pragma unroll
     for (uint32_t jj = 0; jj < 2; ++jj) {
-      if (jj < nx) {
+      if (jj < nk) {
         vf[jj * kAttnHeadDim + col] = vb[jj];
         if (jj == row && ncpos[jj] < a.stride)
           a.value_cache_w[(static_cast<size_t>(kvh) * kAttnHeadDim + col) * a.stride + ncpos[jj]] = vb[jj];
@@ -389,10 +403,11 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnD
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint32_t tt = 4 * w + r + 16 * i;
-      if (4 * w + 16 * i < T) score(tt, kt[i][0], kt[i][1], tt < T);
+      if (4 * w + 16 * i < T) score(tt, kt[i][0], kt[i][1], tt < Tc);
     }
   } else {
-    // The first 64 tokens (all valid: T > 64) from the preloaded tile.
+    // The first 64 tokens (all read from the cache: T > 64, so Tc >= 64)
+    // from the preloaded tile.
 #pragma unroll
     for (int i = 0; i < 4; ++i) score(4 * w + r + 16 * i, kt[i][0], kt[i][1], true);
     // Four tokens per lane per pass: all eight K loads are issued before the
@@ -407,21 +422,23 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnD
         k4[i][1] = kp[1];
       }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) score(tt + 16 * i, k4[i][0], k4[i][1], true);
+      for (int i = 0; i < 4; ++i) score(tt + 16 * i, k4[i][0], k4[i][1], tt + 16 * i < Tc);
     }
     for (; tt < T; tt += 16) {
       const uint4* kp = reinterpret_cast<const uint4*>(kbase + static_cast<size_t>(t0 + tt) * kAttnHeadDim);
-      score(tt, kp[0], kp[1], true);
+      score(tt, kp[0], kp[1], tt < Tc);
     }
   }
-  // the new tokens: 16-lane row j of wave 0 scores token T + j
-  if (nx > 0 && w == 0 && static_cast<uint32_t>(r) < nx) {
+  // The tokens prepared here (the cached virtual one, then the row's own new
+  // token): 16-lane row j of wave 0 scores kf row j at index Tc + j. The
+  // cache pass above stored nothing at those indices.
+  if (nk > 0 && w == 0 && static_cast<uint32_t>(r) < nk) {
     const uint4* kp = reinterpret_cast<const uint4*>(kf + r * kAttnHeadDim + 16 * jd);
-    score(T + r, kp[0], kp[1], true);
+    score(Tc + r, kp[0], kp[1], true);
   }
   // The first two 64-token V tiles do not depend on the softmax: their loads
   // are issued here, so they stream in while phase 2 runs.
-  const bool vpre = !one_tile && T >= 128;
+  const bool vpre = !one_tile && Tc >= 128;
   uint4 v2[2][8];
   auto load_v2 = [&](uint32_t tb, bool first) {  // first: tile 0 is the preloaded one
 #pragma unroll
@@ -433,6 +450,17 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnD
                                                                        t0 + tb + 64 * h + 8 * ts);
   };
   if (vpre) load_v2(0, true);
+  // The virtual cached token's value bits (vf row 0) replace what lane ts
+  // read from its cache slot, which row 0's block is writing in this launch:
+  // same lane, same element, so the summation order is a one-token step's.
+  // Branch-free bit merge on the packed words (mask m[c] selects the 16-bit
+  // half of word c that holds the virtual token; all zero in other lanes).
+  auto patch_virt = [&](uint32_t (&vd)[4], const uint32_t (&m)[4], int p) {
+    const uint32_t bits = vf[64 * w + 8 * p + rr];
+    const uint32_t dup = bits | (bits << 16);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) vd[c] = (vd[c] & ~m[c]) | (dup & m[c]);
+  };
   __syncthreads();
 
   // ---- phase 2: softmax statistics, wave g owns head g.
@@ -465,8 +493,10 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnD
   uint32_t tb0 = 0;
   if (!one_tile) {
     // Two full 64-token tiles per pass: all sixteen V loads are issued before
-    // the first FMA, so a wave keeps 16 KiB of V in flight.
-    for (; tb0 + 128 <= T; tb0 += 128) {
+    // the first FMA, so a wave keeps 16 KiB of V in flight. The tiles before
+    // the virtual token only: each acc[p][g] sums its tiles in the same order
+    // here and in the one-tile loop below, so where a pass ends changes no bits.
+    for (; tb0 + 128 <= Tc; tb0 += 128) {
       if (tb0 > 0) load_v2(tb0, false);  // the first pair was loaded before phase 2
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
@@ -497,6 +527,15 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnD
     const uint32_t tl = tb + 8 * ts;  // first of this lane's 8 tokens (block-local)
     if (tl >= T) continue;
     const uint32_t nvalid = min(8u, T - tl);
+    const bool vtile = (vslot - tb) < 64u;  // wave-uniform
+    uint32_t vmask[4];
+    {
+      const uint32_t e = vslot - tl;  // element of this lane's 8 tokens (>= 8: none)
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        vmask[c] = (e == static_cast<uint32_t>(2 * c) ? 0x0000FFFFu : 0u) |
+                   (e == static_cast<uint32_t>(2 * c + 1) ? 0xFFFF0000u : 0u);
+    }
     float pv[kAttnGroup][8];
 #pragma unroll
     for (int g = 0; g < static_cast<int>(kAttnGroup); ++g)
@@ -513,7 +552,8 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnD
     }
 #pragma unroll
     for (int p = 0; p < 8; ++p) {
-      const uint32_t vd[4] = {vv[p].x, vv[p].y, vv[p].z, vv[p].w};
+      uint32_t vd[4] = {vv[p].x, vv[p].y, vv[p].z, vv[p].w};
+      if (vtile) patch_virt(vd, vmask, p);
       float v8[8];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -529,14 +569,13 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnD
         for (int i = 0; i < 8; ++i) acc[p][g] += pv[g][i] * v8[i];
     }
   }
-  if (nx > 0 && ts == 0) {  // the new tokens' values, once per dim
-    for (uint32_t j = 0; j < nx; ++j) {
+  if (nx > 0 && ts == 0) {  // the row's own new token (vf row nk - 1, score index T), once per dim
+    const uint16_t* vown = vf + (nk - 1) * kAttnHeadDim + 64 * w + rr;
 #pragma unroll
-      for (int p = 0; p < 8; ++p) {
-        const float vv = bf2f(vf[j * kAttnHeadDim + 64 * w + 8 * p + rr]);
+    for (int p = 0; p < 8; ++p) {
+      const float vv = bf2f(vown[8 * p]);
 #pragma unroll
-        for (int g = 0; g < static_cast<int>(kAttnGroup); ++g) acc[p][g] += sc[g * ld + T + j] * vv;
-      }
+      for (int g = 0; g < static_cast<int>(kAttnGroup); ++g) acc[p][g] += sc[g * ld + T] * vv;
     }
   }
 #pragma unroll
@@ -598,7 +637,7 @@ __global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(const AttnDec
       if (c < a.nsplit) acc += pre[c] * wsh[c];
   } else {
     // splits holding tokens (on an empty cache, split 0 holds the new tokens)
-    const uint32_t L = attn_cached_tokens(a0);
+    const uint32_t L = attn_cached_tokens(a);  // this row's partition
     uint32_t nact = fresh ? 1u : 0u;
     if (L > 0) {
       const uint32_t chunk = attn_chunk(L, a.nsplit);

@@ -66,14 +66,16 @@ struct AttnDecodeArgs {
   // uses q / gate / out + r*4096, partials + r*16*nsplit*258 and step[r].
   uint32_t rows = 1;
   // Decode-step form (packed_q != nullptr): the inputs are the raw q | gate,
-  // k and v projections of the `rows` new tokens, not yet in the cache. The
-  // partials cover the cached tokens [0, step[0].seq_len - 1) and normalise +
-  // rotate q themselves; the split holding the last cached token (split 0 on
-  // an empty cache) also prepares the new tokens' k / v and attends to them
-  // as extra tokens (row r to rows 0..r), and the block of each row appends
-  // that row's K / V at step[r].cache_pos. The merge takes the gate from
-  // packed_q. Without packed_q, q and gate are prepared and the cache already
-  // holds all seq_len tokens.
+  // k and v projections of the `rows` new tokens, not yet in the cache. Row r
+  // covers its cached tokens [0, step[r].seq_len - 1), split exactly as a
+  // one-token step at its position splits them, and normalises + rotates q
+  // itself; the split holding row r's last cached token (split 0 on an empty
+  // cache) also prepares the new tokens' k / v, attends to row r's own new
+  // token as an extra token, and appends it at step[r].cache_pos. Row 1's last
+  // cached token is row 0's new token: its k / v come from that preparation,
+  // not from the cache slot row 0's block is writing. The merge takes the
+  // gate from packed_q. Without packed_q, q and gate are prepared and the
+  // cache already holds all seq_len tokens.
   const uint16_t* packed_q = nullptr;  // [rows][16][512]
   const uint16_t* q_norm = nullptr;    // [256]
   const uint16_t* k_in = nullptr;      // [rows][4][256]

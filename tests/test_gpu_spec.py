@@ -97,6 +97,50 @@ def test_two_token_verify_equals_two_single_steps(model):
     b.close()
 
 
+@pytest.mark.parametrize("pos", [0, 63, 64, 127, 7167])
+def test_two_token_verify_row1_is_a_single_step(gpu, pos):
+    """Row 1 of the verify attends to row 0's new token as the last cached
+    token, with the split partition of a one-token step at pos + 1. With two
+    attention layers (3 and 7), row 1's layer-3 attention output feeds the
+    GDN states of layers 4-6 and layer 7's K/V, so any difference in its
+    summation order shows up in those states. Positions: an empty cache
+    (pos 0), row 1's last cached token ending a 64-token split (63), opening
+    a new split (64), ending the second split (127), and, at 128-token
+    splits, ending a split whose single-token step runs the two-tile V pass
+    (7167)."""
+    from peregrine_amd.device import DeviceArray
+    from peregrine_amd.model import DeviceModel, ModelConfig, ModelState
+
+    cfg = ModelConfig(num_layers=8, hidden=1024, intermediate=2048, vocab=4096)
+    m = DeviceModel(cfg, seed=12)
+    try:
+        rng = np.random.default_rng(pos)
+        prompt = rng.integers(0, cfg.vocab, size=pos).astype(np.uint32)
+        a, b = ModelState(m, max_seq=pos + 8), ModelState(m, max_seq=pos + 8)
+        if pos:
+            a.prefill(prompt)
+            b.prefill(prompt)
+        t0, t1 = int(rng.integers(0, cfg.vocab)), int(rng.integers(0, cfg.vocab))
+        hid = DeviceArray((2, cfg.hidden), np.uint16)
+        v, bonus = a.forward_two_tokens(t0, t1, pos, hidden_out=hid)
+        n0 = b.forward_next_token(t0, pos)
+        n1 = b.forward_next_token(t1, pos + 1)
+        assert (v, bonus) == (n0, n1)
+        for i in range(cfg.num_layers):
+            names = ["recur", "conv"] if cfg.is_linear(i) else ["cache_k", "cache_v"]
+            for nm in names:
+                np.testing.assert_array_equal(a.read(f"layers.{i}.{nm}", np.uint16),
+                                              b.read(f"layers.{i}.{nm}", np.uint16), err_msg=f"pos {pos} layer {i} {nm}")
+        # the verify's hidden rows continue exactly: one more step from each
+        # state gives the same token
+        assert a.forward_next_token(n1, pos + 2) == b.forward_next_token(n1, pos + 2)
+        hid.close()
+        a.close()
+        b.close()
+    finally:
+        m.close()
+
+
 def test_mtp_drafter_matches_oracle(model):
     """Drafter prefill over 6 rows, then 3 draft steps, against the oracle's
     restatement of mtp.zig (same bf16 inputs: random normalised-scale hidden
