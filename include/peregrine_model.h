@@ -275,8 +275,8 @@ uint32_t prg_model_state_stride(const PrgModelState *state);
  * cache_pos: KV slot written; rope_pos: RoPE position (GDN state is used iff
  * rope_pos != 0); seq_len: tokens attended (must be cache_pos + 1: prefix
  * caches are not supported). Afterwards prg_model_decode continues at
- * cache_pos + 1 with *next_token as its input (positions then advance with
- * rope_pos == cache_pos). Errors: SEQUENCE_TOO_LONG, INVALID_TOKEN.
+ * cache_pos + 1 with *next_token as its input; its positions keep this
+ * call's offset rope_pos - cache_pos. Errors: SEQUENCE_TOO_LONG, INVALID_TOKEN.
  * Replaces DeviceModel.forwardNextTokenBf16WithPrefix (model.zig:1564-1578). */
 int prg_model_forward_next_token(PrgModel *model, PrgModelState *state, uint32_t token,
                                  uint32_t cache_pos, uint32_t rope_pos, uint32_t seq_len,
@@ -341,8 +341,8 @@ int prg_model_generate(PrgModel *model, PrgModelState *state, const uint32_t *pr
  * by both. verify_token = argmax after token0, bonus_token = argmax after
  * token1; hidden_out (device bf16 [2, hidden], may be NULL) receives the two
  * final-normed hidden rows. Afterwards prg_model_decode continues at
- * cache_pos + 2 with bonus_token as its input. Errors: SEQUENCE_TOO_LONG,
- * INVALID_TOKEN.
+ * cache_pos + 2 (RoPE position rope_pos + 2, keeping the offset) with
+ * bonus_token as its input. Errors: SEQUENCE_TOO_LONG, INVALID_TOKEN.
  * Replaces DeviceModel.forwardTwoTokenDecodeVerifierBf16WithPrefixProfiled
  * (model.zig:1627-1659; encodeStack2Bf16 :719-760, decodeStep2Bf16
  * decoder_layer.zig:485-516). */

@@ -36,6 +36,9 @@ struct DecodeCtl {
   uint32_t prompt_len;
   uint32_t capacity;  // KV cache slots; positions never advance past it
   uint32_t overflow;  // set when a step would have exceeded capacity
+  // rope_pos - cache_pos (mod 2^32) of the step the loop was entered with,
+  // kept for every later step: rope_pos = cache_pos + rope_off.
+  uint32_t rope_off;
 };
 
 // ---------------------------------------------------------------- bf16 -------

@@ -857,6 +857,7 @@ int prg_model_forward_next_token(PrgModel* model, PrgModelState* st, uint32_t to
   DecodeCtl ctl{};
   ctl.s = StepScalars{token, cache_pos, rope_pos, seq_len};
   ctl.n = cache_pos;
+  ctl.rope_off = rope_pos - cache_pos;  // later steps keep the caller's RoPE offset
   ctl.prompt_len = 0;
   ctl.capacity = st->max_seq;
   PRG_HIP(hipMemcpyAsync(st->ctl, &ctl, sizeof(ctl), hipMemcpyHostToDevice, st->stream));

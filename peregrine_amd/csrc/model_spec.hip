@@ -315,8 +315,9 @@ int prg_model_forward_two_tokens(PrgModel* model, PrgModelState* st, uint32_t to
   // cache_pos + 2 with the bonus token, as after two single steps.
   const uint32_t preds[2] = {c.verify, c.bonus};
   DecodeCtl ctl{};
-  ctl.s = StepScalars{c.bonus, cache_pos + 2, cache_pos + 2, cache_pos + 3};
+  ctl.s = StepScalars{c.bonus, cache_pos + 2, rope_pos + 2, cache_pos + 3};
   ctl.n = cache_pos + 2;
+  ctl.rope_off = rope_pos - cache_pos;
   ctl.capacity = st->max_seq;
   ctl.overflow = cache_pos + 2 >= st->max_seq;
   PRG_HIP(hipMemcpyAsync(st->predictions + cache_pos, preds, sizeof(preds), hipMemcpyHostToDevice, st->stream));

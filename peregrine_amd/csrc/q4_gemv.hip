@@ -127,7 +127,7 @@ __device__ inline void advance_ctl(prg::DecodeCtl* ctl, const uint32_t* prompt, 
   const uint32_t next = (n1 < ctl->prompt_len || !has_pred) ? prompt[n1] : pred;
   ctl->s.token = next;
   ctl->s.cache_pos = n1;
-  ctl->s.rope_pos = n1;
+  ctl->s.rope_pos = n1 + ctl->rope_off;
   ctl->s.seq_len = n1 + 1;
   ctl->n = n1;
 }

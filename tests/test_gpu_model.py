@@ -285,6 +285,35 @@ def test_decode_continues_after_forward_next_token(small):
     np.testing.assert_array_equal(np.concatenate([[first, second], rest]).astype(np.uint32), ref)
 
 
+def test_decode_keeps_the_rope_offset(small):
+    """forward_next_token at rope_pos = cache_pos + 5, then prg_model_decode:
+    every later step keeps the offset, i.e. the tokens and the rotated keys in
+    the attention cache equal stepping with rope_pos = cache_pos + 5 through
+    the step API. The same steps without the offset write different keys, so
+    a dropped offset cannot pass."""
+    m, st, om = small
+    rng = np.random.default_rng(8)
+    prompt = rng.integers(0, SMALL["vocab"], size=10).astype(np.uint32)
+    k_name = "layers.3.cache_k"
+
+    def stepped(off):
+        t = st.prefill(prompt)
+        toks = []
+        for i in range(6):
+            t = st.forward_next_token(t, 10 + i, rope_pos=10 + i + off)
+            toks.append(t)
+        return np.array(toks, np.uint32), st.read(k_name, np.uint16).copy()
+
+    ref, k_ref = stepped(5)
+    _, k_plain = stepped(0)
+    assert not np.array_equal(k_ref, k_plain)
+    first = st.prefill(prompt)
+    t0 = st.forward_next_token(first, 10, rope_pos=15)
+    rest, _ = st.decode(5)
+    np.testing.assert_array_equal(np.concatenate([[t0], rest]).astype(np.uint32), ref)
+    np.testing.assert_array_equal(st.read(k_name, np.uint16), k_ref)
+
+
 def test_decode_refuses_a_full_state(gpu):
     """A step at the last slot leaves nothing to decode: SequenceTooLong."""
     from peregrine_amd._lib import PrgError
