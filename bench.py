@@ -288,15 +288,19 @@ def cpu_configs(threads: int) -> list[dict]:
     return rows
 
 
-def cpu_baseline(model, snapshot: dict, tokens, start: int, info: dict, budget_s: float = 15.0) -> dict:
+def cpu_baseline(model, snapshot: dict, tokens, start: int, info: dict, budget_s: float = 20.0) -> dict:
     """The C oracle running the same 9B-shaped decode step on the host cores,
     row-parallel, at the GPU's context: its state is the GPU's state after
     the prompt (KV caches and GDN states copied from the device), and it is
     teacher-forced on the GPU's greedy tokens from position `start`, until
-    ~budget_s. Also reports how many of those steps predict the GPU's next
-    token."""
+    ~budget_s. Each step also computes the oracle's full bf16 logits, so the
+    agreement with the GPU's next token is classified by the oracle's top-2
+    margin: on a decisive step (margin above four bf16 ulps of the top logit)
+    the tokens must agree; below it a different winner is a tie-break by a
+    different fp32 summation order. Every disagreement is listed with both
+    tokens, the margin and the oracle's logit of the GPU's token."""
     from oracle import oracle
-    from oracle.model import OracleModel
+    from oracle.model import OracleModel, decisive_margin
 
     threads = info["threads"]
     o = oracle()
@@ -304,19 +308,22 @@ def cpu_baseline(model, snapshot: dict, tokens, start: int, info: dict, budget_s
     t0 = time.time()
     om = OracleModel(model, snapshot["max_seq"])
     load_s = time.time() - t0
-    assert om.stride == snapshot["stride"], (om.stride, snapshot["stride"])
-    for i, L in enumerate(om.layers):
-        if L["linear"]:
-            om.state[i]["conv"] = snapshot[f"layers.{i}.conv"].reshape(3, 8192).copy()
-            om.state[i]["recur"] = snapshot[f"layers.{i}.recur"].reshape(32, 128, 128).copy()
-        else:
-            om.state[i]["k"] = snapshot[f"layers.{i}.cache_k"].reshape(4, om.stride, 256).copy()
-            om.state[i]["v"] = snapshot[f"layers.{i}.cache_v"].reshape(4, 256, om.stride).copy()
-    n = same = 0
+    om.load_state(snapshot)
+    n = same = decisive = decisive_same = 0
+    mismatches = []
     t0 = time.time()
     while n + 1 < len(tokens):
-        pred, _ = om.step(int(tokens[n]), start + n)
-        same += int(pred == int(tokens[n + 1]))
+        pred, logits = om.step(int(tokens[n]), start + n, want_logits=True)
+        gpu = int(tokens[n + 1])
+        i1, i2, margin, guard = decisive_margin(logits)
+        dec = margin > guard
+        same += int(pred == gpu)
+        decisive += int(dec)
+        decisive_same += int(dec and pred == gpu)
+        if pred != gpu:
+            mismatches.append({"pos": start + n, "gpu": gpu, "oracle": int(pred), "runner_up": i2,
+                               "margin": float(margin), "guard": float(guard), "decisive": bool(dec),
+                               "oracle_logit_of_gpu_token": float(logits[gpu]), "oracle_top": float(logits[i1])})
         n += 1
         if time.time() - t0 > budget_s:
             break
@@ -325,8 +332,12 @@ def cpu_baseline(model, snapshot: dict, tokens, start: int, info: dict, budget_s
             "nproc": info["nproc"], "cpu_model": info["cpu_model"],
             "sample": f"{n} decode steps of the same 9B-shaped model at positions {start}..{start + n - 1}, "
                       f"on the GPU's state after the {start}-token prompt, teacher-forced on the GPU's tokens "
-                      f"(C oracle, {threads} threads; weight readback {load_s:.1f}s excluded)",
-            "predicts_gpu_token": f"{same}/{n}"}
+                      f"(C oracle, {threads} threads, each step with its full lm_head logits; weight readback "
+                      f"{load_s:.1f}s excluded)",
+            "predicts_gpu_token": f"{same}/{n}",
+            "decisive_agree": f"{decisive_same}/{decisive}",
+            "decisive_rule": "oracle top-1 minus top-2 logit > 4 bf16 ulps of the top logit",
+            "mismatches": mismatches}
 
 
 def snapshot_state(st) -> dict:

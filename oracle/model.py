@@ -28,6 +28,24 @@ from .binding import oracle
 ROOT = "language_model.model"
 
 
+def decisive_margin(logits) -> tuple[int, int, float, float]:
+    """(top-1 index, runner-up index, top-1 minus top-2 logit, guard) of one
+    step's bf16 logits. The guard is four bf16 ulps of the top logit: bf16
+    keeps 8 significant bits, and every projection output on both sides is
+    rounded to bf16, so one-ulp rounding flips from a different fp32
+    summation order propagate through the residual stream. A step is
+    decisive when the margin exceeds the guard; below it, a different winner
+    is a legitimate tie-break."""
+    lg = np.asarray(logits, np.float64)
+    i1 = int(np.argmax(lg))
+    rest = lg.copy()
+    rest[i1] = -np.inf
+    i2 = int(np.argmax(rest))
+    top1, top2 = float(lg[i1]), float(lg[i2])
+    ulp = 2.0 ** (np.floor(np.log2(max(abs(top1), 1e-30))) - 7)
+    return i1, i2, top1 - top2, 4.0 * ulp
+
+
 def _q4(model, base: str, out_dim: int, in_dim: int) -> Q4Weight:
     w = model.read(base + ".weight", np.uint32).reshape(out_dim, in_dim // 8)
     s = model.read(base + ".scales", np.uint16).reshape(out_dim, in_dim // 64)
@@ -108,6 +126,20 @@ class OracleModel:
                                    "v": np.zeros((4, 256, self.stride), np.uint16)})
         self.mtp_state = {"k": np.zeros((4, self.stride, 256), np.uint16),
                           "v": np.zeros((4, 256, self.stride), np.uint16)}
+
+    def load_state(self, snap: dict) -> None:
+        """Take over a device state: host copies of its GDN conv / recurrent
+        states and KV caches keyed "layers.<i>.conv|recur|cache_k|cache_v"
+        (f32 for the GDN states, bf16 bits for the caches), with the same
+        cache stride."""
+        assert snap["stride"] == self.stride, (snap["stride"], self.stride)
+        for i, L in enumerate(self.layers):
+            if L["linear"]:
+                self.state[i]["conv"] = np.asarray(snap[f"layers.{i}.conv"], np.float32).reshape(3, 8192).copy()
+                self.state[i]["recur"] = np.asarray(snap[f"layers.{i}.recur"], np.float32).reshape(32, 128, 128).copy()
+            else:
+                self.state[i]["k"] = np.asarray(snap[f"layers.{i}.cache_k"], np.uint16).reshape(4, self.stride, 256).copy()
+                self.state[i]["v"] = np.asarray(snap[f"layers.{i}.cache_v"], np.uint16).reshape(4, 256, self.stride).copy()
 
     def _layer(self, i: int, h: np.ndarray, pos: int) -> np.ndarray:
         return self._decode_layer(self.layers[i], self.state[i], h, pos)

@@ -225,3 +225,21 @@ def test_attn_decode_vs_float64(orc, L):
         v0 = F(vc[:, :, 0])
         np.testing.assert_allclose(got, np.repeat(v0, 4, axis=0) / (1 + np.exp(-F(gate).reshape(16, 256))),
                                    rtol=1e-2, atol=1e-3)
+
+
+def test_decisive_margin_rule():
+    """The greedy-parity guard: four bf16 ulps of the top logit (ulp of a
+    value in [2^e, 2^(e+1)) is 2^(e-7)). Top 8.0 (ulp 1/16, guard 0.25) beside
+    7.875 is a near-tie, beside 7.5 decisive; the runner-up is the second
+    largest even when it precedes the winner; negative tops use |top|."""
+    from oracle.model import decisive_margin
+
+    lg = np.zeros(10)
+    lg[3], lg[7] = 8.0, 7.875
+    assert decisive_margin(lg) == (3, 7, 0.125, 0.25)
+    lg[7] = 7.5
+    i1, i2, m, g = decisive_margin(lg)
+    assert (i1, i2, m, g) == (3, 7, 0.5, 0.25) and m > g
+    lg = np.full(6, -20.0)
+    lg[4], lg[1] = -3.0, -3.25  # |top| in [2, 4): ulp 1/64, guard 1/16
+    assert decisive_margin(lg) == (4, 1, 0.25, 0.0625)
