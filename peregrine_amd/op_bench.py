@@ -66,8 +66,9 @@ def gdn_layers(layers: int = 24, seed: int = 3, reps: int = 20, fused_norm: bool
     sets = max(1, -(-ROTATE_BYTES // (layers * per_layer)))
     # shared small inputs (read-only), per-layer states and weights
     a, b = DeviceArray.from_numpy(random_bf16(rng, (hv,))), DeviceArray.from_numpy(random_bf16(rng, (hv,)))
-    A_log = DeviceArray.from_numpy(rng.normal(0, 0.5, hv).astype(np.float32))
-    dt = DeviceArray.from_numpy(random_bf16(rng, (hv,), std=0.5))
+    # A_log = 0 and dt_bias = 0, so decay = exp(-softplus(a))
+    A_log = DeviceArray.from_numpy(np.zeros(hv, np.float32))
+    dt = DeviceArray.from_numpy(np.zeros(hv, np.uint16))
     nw = DeviceArray.from_numpy(random_bf16(rng, (d,), std=0.1, mean=1.0))
     S0 = rng.normal(0, 0.1, size=(hv, d, d)).astype(np.float32)
     cs0 = rng.normal(0, 1.0, size=(3, conv_dim)).astype(np.float32)

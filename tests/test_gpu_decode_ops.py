@@ -207,11 +207,15 @@ def test_attn_decode_bad_len_is_error(gpu):
         ops.attn_decode(z, z, z, z, z, z, 64, 65)
 
 
-@pytest.mark.parametrize("L,stride", [(0, 64), (1, 64), (100, 128), (1023, 2048), (4095, 4096), (30000, 65536)])
+@pytest.mark.parametrize("L,stride", [(0, 64), (1, 64), (100, 128), (1023, 2048), (4095, 4096), (30000, 65536),
+                                      (24575, 24576), (65535, 65536)])
 def test_attn_decode_step(gpu, orc, L, stride):
     """prg_attn_decode_step_bf16 (q/k norm + RoPE, attention over the L cached
     slots plus the new token, K/V append at slot L) against the oracle's
-    prepare (attention.metal:327-421) then flash decode over L + 1 tokens."""
+    prepare (attention.metal:327-421) then flash decode over L + 1 tokens.
+    The last two cases are BASELINE config 4's contexts (24576 and 65536
+    tokens attended) on the path the model runs, with the new token in the
+    cache's last slot."""
     from peregrine_amd import ops
 
     rng = np.random.default_rng(100 + L)
