@@ -413,6 +413,10 @@ def main() -> int:
                          "GQA decode attention at L = 4096 / 24576 / 65536), one JSON line")
     ap.add_argument("--roofline-only", action="store_true",
                     help="only the dominant-kernel loop and a 256 MiB copy-kernel reference (for PMC runs)")
+    ap.add_argument("--prefill-only", type=int, default=0, metavar="N",
+                    help="only N ingests of the 1600-token prompt into the 9B-shaped model with the prepared dense "
+                         "prompt weights (the first allocates the prompt workspace), one JSON line (for PMC runs "
+                         "on the prompt GEMMs)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(json.dumps({"error": "this build runs on exactly one GPU (no multi-GPU path); use --gpus 1"}))
@@ -449,6 +453,24 @@ def main() -> int:
         device.synchronize()
         roof = dominant_kernel_roofline(iters=20)
         print(json.dumps({"copy_bytes": nbytes, "roofline": roof}), flush=True)
+        return 0
+    if a.prefill_only:
+        model = DeviceModel(QWEN35_9B, seed=0)
+        model.prepare_dense()
+        st = ModelState(model, PROMPT_TOKENS + 64)
+        prompt = np.random.default_rng(0).integers(0, QWEN35_9B.vocab, size=PROMPT_TOKENS).astype(np.uint32)
+        runs = []
+        for i in range(a.prefill_only):
+            t0 = time.time()
+            first = st.prefill(prompt)
+            runs.append(round((time.time() - t0) * 1e3, 2))
+            log(f"[bench] ingest {i}: {runs[-1]} ms, first token {first}")
+        best = min(runs[1:] or runs)
+        print(json.dumps({"prefill_ms": runs, "tokens": PROMPT_TOKENS, "first_token": int(first),
+                          "tflops_best": round(prefill_flops(QWEN35_9B, PROMPT_TOKENS) / (best * 1e-3) / 1e12, 2)}),
+              flush=True)
+        st.close()
+        model.close()
         return 0
     t0 = time.time()
     model = DeviceModel(QWEN35_9B, seed=0)

@@ -56,17 +56,24 @@ def _run(cmd: list[str]) -> None:
         raise RuntimeError(f"command failed ({proc.returncode}): {' '.join(cmd)}\n{err}")
 
 
-def build_lib(jobs: int | None = None) -> Path:
+def build_lib(jobs: int | None = None, incremental: bool = False) -> Path:
+    """Compile every translation unit and link. incremental: recompile only
+    sources newer than their object (any header change recompiles all)."""
     hipcc = _hipcc()
     BUILD.mkdir(exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
     if not sources:
         raise RuntimeError(f"no HIP sources in {CSRC}")
     objs = [BUILD / (s.stem + ".o") for s in sources]
+    headers = max(p.stat().st_mtime for p in [*CSRC.glob("*.hpp"), *INCLUDE.glob("*.h")])
+
+    def stale(s: Path, o: Path) -> bool:
+        return not incremental or not o.exists() or o.stat().st_mtime < max(s.stat().st_mtime, headers)
+
     jobs = jobs or min(len(sources), os.cpu_count() or 4, 16)
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         futs = [ex.submit(_run, [hipcc, *HIPCC_FLAGS, "-c", str(s), "-o", str(o)])
-                for s, o in zip(sources, objs)]
+                for s, o in zip(sources, objs) if stale(s, o)]
         for f in futs:
             f.result()
     tmp = LIB.with_suffix(".so.tmp")
@@ -90,9 +97,10 @@ def main(argv: list[str] | None = None) -> int:
     ap.add_argument("--lib", action="store_true", help="HIP library only")
     ap.add_argument("--oracle", action="store_true", help="oracle only")
     ap.add_argument("-j", type=int, default=None)
+    ap.add_argument("--incremental", action="store_true", help="recompile only out-of-date objects")
     a = ap.parse_args(argv)
     if not a.oracle:
-        print("built", build_lib(a.j))
+        print("built", build_lib(a.j, a.incremental))
     if not a.lib:
         print("built", build_oracle())
     return 0
