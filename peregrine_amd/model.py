@@ -113,6 +113,15 @@ class DeviceModel:
         p, n = self.tensor_ptr(name)
         return _d2h(p, n, dtype)
 
+    def write(self, name: str, arr: np.ndarray) -> None:
+        """Overwrite a weight tensor with host data of exactly its byte size
+        (the prepared dense copy, if any, is not refreshed)."""
+        p, n = self.tensor_ptr(name)
+        arr = np.ascontiguousarray(arr)
+        if arr.nbytes != n:
+            raise ValueError(f"{name}: {arr.nbytes} bytes given, the tensor holds {n}")
+        call("prg_hip_memcpy", C.c_void_p(p), arr.ctypes.data_as(C.c_void_p), C.c_size_t(n), 0, None, 1)
+
     def close(self) -> None:
         if self.handle:
             lib.prg_model_destroy(self.handle)

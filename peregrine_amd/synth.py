@@ -88,3 +88,38 @@ def random_q4(rng: np.random.Generator, N: int, K: int, scale_lo: float = 0.001,
 
 def random_bf16(rng: np.random.Generator, shape, std: float = 1.0, mean: float = 0.0) -> np.ndarray:
     return f32_to_bf16(rng.normal(mean, std, size=shape).astype(np.float32))
+
+
+def copy_drafter_tensors(hidden: int, o_proj_meta: int, down_meta: int) -> dict:
+    """Tensors that turn a random 1-layer MTP drafter into a "copy" drafter
+    whose draft is the token it is given: fc = [0 | I] passes the target's
+    normalised hidden through (unit scales, zero biases), the drafter layer's
+    o_proj and down_proj have zero scales and biases (so its attention and
+    MLP add nothing), and the pre-fc hidden norm and final norm are ones, so
+    the shared lm_head sees the target's own hidden. o_proj_meta / down_meta:
+    element counts of those projections' scale (and bias) tensors.
+    Used to time and test the speculative loop's accept path."""
+    H = hidden
+    q = np.zeros((H, 2 * H), np.uint32)
+    q[np.arange(H), H + np.arange(H)] = 1
+    one = f32_to_bf16(np.float32(1.0))
+    return {
+        "mtp.fc.weight": pack_q4(q),
+        "mtp.fc.scales": np.full((H, 2 * H // 64), one, np.uint16),
+        "mtp.fc.biases": np.zeros((H, 2 * H // 64), np.uint16),
+        "mtp.layers.0.self_attn.o_proj.scales": np.zeros(o_proj_meta, np.uint16),
+        "mtp.layers.0.self_attn.o_proj.biases": np.zeros(o_proj_meta, np.uint16),
+        "mtp.layers.0.mlp.down_proj.scales": np.zeros(down_meta, np.uint16),
+        "mtp.layers.0.mlp.down_proj.biases": np.zeros(down_meta, np.uint16),
+        "mtp.pre_fc_norm_hidden.weight": np.full(H, one, np.uint16),
+        "mtp.norm.weight": np.full(H, one, np.uint16),
+    }
+
+
+def unit_norm_e0(hidden: int) -> np.ndarray:
+    """Final-norm weight e_0: the logits become lm_head[:, 0] * h_0 / rms(h),
+    so greedy decoding picks one of two tokens (by the sign of h_0) and
+    repeats often, which a copy drafter then predicts."""
+    w = np.zeros(hidden, np.uint16)
+    w[0] = f32_to_bf16(np.float32(1.0))
+    return w

@@ -12,8 +12,6 @@ is the current token (fc selects the target hidden, o_proj and down_proj are
 zero): it is accepted exactly where the greedy sequence repeats a token, which
 exercises the accept path and the state swap.
 """
-import ctypes as C
-
 import numpy as np
 import pytest
 
@@ -25,32 +23,18 @@ SMALL = dict(num_layers=4, hidden=1024, intermediate=2048, vocab=4096, mtp_layer
 
 
 def _write(m, name, arr):
-    from peregrine_amd._lib import call
-
-    p, n = m.tensor_ptr(name)
-    arr = np.ascontiguousarray(arr)
-    assert arr.nbytes == n, (name, arr.nbytes, n)
-    call("prg_hip_memcpy", C.c_void_p(p), arr.ctypes.data_as(C.c_void_p), C.c_size_t(n), 0, None, 1)
+    m.write(name, arr)
 
 
 def _make_copy_drafter(m, H):
     """fc = [0 | I] (draft input = the target hidden), attention and MLP
     outputs zero, unit norms: draft = argmax lm_head(h) = the current token."""
-    q = np.zeros((H, 2 * H), np.uint32)
-    q[np.arange(H), H + np.arange(H)] = 1
-    words = np.zeros((H, 2 * H // 8), np.uint32)
-    for j in range(8):
-        words |= q[:, j::8] << np.uint32(4 * j)
-    _write(m, "mtp.fc.weight", words)
-    one = f32_to_bf16(np.float32(1.0))
-    _write(m, "mtp.fc.scales", np.full((H, 2 * H // 64), one, np.uint16))
-    _write(m, "mtp.fc.biases", np.zeros((H, 2 * H // 64), np.uint16))
-    for t in ["mtp.layers.0.self_attn.o_proj", "mtp.layers.0.mlp.down_proj"]:
-        _, n = m.tensor_ptr(t + ".scales")
-        _write(m, t + ".scales", np.zeros(n // 2, np.uint16))
-        _write(m, t + ".biases", np.zeros(n // 2, np.uint16))
-    _write(m, "mtp.pre_fc_norm_hidden.weight", np.full(H, one, np.uint16))
-    _write(m, "mtp.norm.weight", np.full(H, one, np.uint16))
+    from peregrine_amd.synth import copy_drafter_tensors
+
+    o_meta = m.tensor_ptr("mtp.layers.0.self_attn.o_proj.scales")[1] // 2
+    d_meta = m.tensor_ptr("mtp.layers.0.mlp.down_proj.scales")[1] // 2
+    for name, arr in copy_drafter_tensors(H, o_meta, d_meta).items():
+        m.write(name, arr)
 
 
 @pytest.fixture(scope="module")
@@ -198,9 +182,9 @@ def test_speculative_equals_greedy_copy_drafter(gpu):
     _make_copy_drafter(m, SMALL["hidden"])
     # Final norm weight e_0: the logits become w[:, 0] * h_0 / rms, so greedy
     # output is one of two tokens (by the sign of h_0) and repeats often.
-    e0 = np.zeros(SMALL["hidden"], np.uint16)
-    e0[0] = int(f32_to_bf16(np.float32(1.0)))
-    _write(m, "language_model.model.norm.weight", e0)
+    from peregrine_amd.synth import unit_norm_e0
+
+    _write(m, "language_model.model.norm.weight", unit_norm_e0(SMALL["hidden"]))
     rng = np.random.default_rng(3)
     prompt = rng.integers(0, SMALL["vocab"], size=20).astype(np.uint32)
     n = 48
@@ -239,9 +223,9 @@ def test_speculative_continues_from_a_prefix_cache_hit(gpu):
     H = SMALL["hidden"]
     m = DeviceModel(ModelConfig(**SMALL), seed=13)
     _make_copy_drafter(m, H)
-    e0 = np.zeros(H, np.uint16)
-    e0[0] = int(f32_to_bf16(np.float32(1.0)))
-    _write(m, "language_model.model.norm.weight", e0)
+    from peregrine_amd.synth import unit_norm_e0
+
+    _write(m, "language_model.model.norm.weight", unit_norm_e0(H))
     rng = np.random.default_rng(21)
     base = rng.integers(0, SMALL["vocab"], size=20).astype(np.uint32)
     prompt = np.concatenate([base, rng.integers(0, SMALL["vocab"], size=9).astype(np.uint32)])
