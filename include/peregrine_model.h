@@ -273,14 +273,31 @@ uint32_t prg_model_state_stride(const PrgModelState *state);
 
 /* One token through the whole stack and the greedy argmax tail, synchronous.
  * cache_pos: KV slot written; rope_pos: RoPE position (GDN state is used iff
- * rope_pos != 0); seq_len: tokens attended (must be cache_pos + 1: prefix
- * caches are not supported). Afterwards prg_model_decode continues at
- * cache_pos + 1 with *next_token as its input; its positions keep this
- * call's offset rope_pos - cache_pos. Errors: SEQUENCE_TOO_LONG, INVALID_TOKEN.
- * Replaces DeviceModel.forwardNextTokenBf16WithPrefix (model.zig:1564-1578). */
+ * rope_pos != 0); seq_len: tokens attended (must be cache_pos + 1; for a
+ * cached prefix see prg_model_forward_next_token_prefixed). Afterwards
+ * prg_model_decode continues at cache_pos + 1 with *next_token as its input;
+ * its positions keep this call's offset rope_pos - cache_pos. Errors:
+ * SEQUENCE_TOO_LONG, INVALID_TOKEN.
+ * Replaces DeviceModel.forwardNextTokenBf16WithPrefix (model.zig:1564-1578)
+ * with prefix == null. */
 int prg_model_forward_next_token(PrgModel *model, PrgModelState *state, uint32_t token,
                                  uint32_t cache_pos, uint32_t rope_pos, uint32_t seq_len,
                                  uint32_t *next_token);
+
+/* The same step with the reference's prefix bookkeeping
+ * (decode_loop.zig:96-160): cache_pos = logical_pos - prefix_len is the
+ * slot after the prefix, rope_pos = logical_pos, seq_len = logical_pos + 1
+ * (must equal prefix_len + cache_pos + 1). The reference binds the prefix
+ * entry's K/V as a second attention source; here the state must already hold
+ * the prefix's tokens in its slots [0, prefix_len) (prg_prefix_cache_restore,
+ * then prg_model_prefill_from for the rest of the prompt), and the step writes
+ * slot prefix_len + cache_pos. Errors: SEQUENCE_TOO_LONG, INVALID_TOKEN,
+ * INVALID_ARG (seq_len mismatch).
+ * Replaces DeviceModel.forwardNextTokenBf16WithPrefix (model.zig:1564-1578)
+ * with prefix = {entry state, prefix_len}. */
+int prg_model_forward_next_token_prefixed(PrgModel *model, PrgModelState *state, uint32_t token,
+                                          uint32_t cache_pos, uint32_t rope_pos, uint32_t seq_len,
+                                          uint32_t prefix_len, uint32_t *next_token);
 
 /* Reset the state and ingest prompt[0..prompt_len) at positions 0.. layer-major
  * in chunks of up to 2048 tokens (MFMA QMMs, causal prefill attention, GDN

@@ -868,6 +868,20 @@ int prg_model_forward_next_token(PrgModel* model, PrgModelState* st, uint32_t to
   return PRG_OK;
 }
 
+int prg_model_forward_next_token_prefixed(PrgModel* model, PrgModelState* st, uint32_t token, uint32_t cache_pos,
+                                          uint32_t rope_pos, uint32_t seq_len, uint32_t prefix_len,
+                                          uint32_t* next_token) {
+  PRG_CHECK_ARG(model && st && next_token && st->model == model, "prg_model_forward_next_token_prefixed: bad argument");
+  const uint64_t slot = static_cast<uint64_t>(prefix_len) + cache_pos;
+  if (slot >= st->max_seq)
+    return set_error(PRG_ERR_SEQUENCE_TOO_LONG, "prefix_len %u + cache_pos %u >= max_seq %u", prefix_len, cache_pos,
+                     st->max_seq);
+  if (static_cast<uint64_t>(seq_len) != slot + 1)
+    return set_error(PRG_ERR_INVALID_ARG, "seq_len %u != prefix_len %u + cache_pos %u + 1", seq_len, prefix_len,
+                     cache_pos);
+  return prg_model_forward_next_token(model, st, token, static_cast<uint32_t>(slot), rope_pos, seq_len, next_token);
+}
+
 int prg_model_decode(PrgModel* model, PrgModelState* st, uint32_t n_steps, uint32_t* tokens_out, float* gpu_ms) {
   PRG_CHECK_ARG(model && st && tokens_out && st->model == model, "prg_model_decode: bad argument");
   PRG_CHECK_ARG(n_steps >= 1, "prg_model_decode: n_steps == 0");

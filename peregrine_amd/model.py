@@ -162,6 +162,18 @@ class ModelState:
              C.byref(out))
         return int(out.value)
 
+    # model.zig:1564-1578 with a prefix (decode_loop.zig:96-160 bookkeeping)
+    def forward_next_token_prefixed(self, token: int, cache_pos: int, prefix_len: int, rope_pos: int | None = None,
+                                    seq_len: int | None = None) -> int:
+        """cache_pos is relative to the prefix (logical_pos - prefix_len); the
+        state holds the prefix's tokens in its first prefix_len slots."""
+        rope_pos = prefix_len + cache_pos if rope_pos is None else rope_pos
+        seq_len = prefix_len + cache_pos + 1 if seq_len is None else seq_len
+        out = C.c_uint32(0)
+        call("prg_model_forward_next_token_prefixed", self.model.handle, self.handle, token, cache_pos, rope_pos,
+             seq_len, prefix_len, C.byref(out))
+        return int(out.value)
+
     def prefill(self, prompt) -> int:
         prompt = np.ascontiguousarray(prompt, np.uint32)
         out = C.c_uint32(0)

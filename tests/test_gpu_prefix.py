@@ -139,6 +139,41 @@ def test_cache_restore_then_continue(model, prompt, full_run):
     cache.close()
 
 
+def test_decode_with_prefix_bookkeeping(model, prompt, full_run):
+    """decodeFromPrefixCache (decode_loop.zig:96-160) on a prefix-cache hit:
+    restore the 24-token entry, prefill the rest of the prompt, then step with
+    the reference's bookkeeping (cache_pos = logical_pos - prefix_len,
+    rope_pos = logical_pos, seq_len = logical_pos + 1) through
+    prg_model_forward_next_token_prefixed: the same tokens as the one-pass
+    greedy run, and a seq_len that does not match is rejected."""
+    from peregrine_amd._lib import PrgError
+    from peregrine_amd.model import ModelState
+    from peregrine_amd.prefix import PrefixCache
+
+    nxt, toks, _ = full_run
+    cache = PrefixCache(model, 4096, 256)
+    w1 = ModelState(model, 128)
+    m = cache.store(prompt[:24], w1, next_token=w1.prefill(prompt[:24]))
+    w2 = ModelState(model, 128)
+    cache.restore(cache.find(prompt), w2)
+    prefix_len, prompt_len = m.len, len(prompt)
+    current = w2.prefill_from(prompt, prefix_len)
+    assert current == nxt
+    got = []
+    for n in range(1, 11):  # n tokens emitted so far
+        logical_pos = prompt_len + n - 1
+        current = w2.forward_next_token_prefixed(current, logical_pos - prefix_len, prefix_len, rope_pos=logical_pos,
+                                                 seq_len=logical_pos + 1)
+        got.append(current)
+    np.testing.assert_array_equal(np.array(got, np.uint32), toks)
+    with pytest.raises(PrgError) as e:
+        w2.forward_next_token_prefixed(current, 40, prefix_len, seq_len=40 + 1)
+    assert e.value.code == 1
+    for s in (w1, w2):
+        s.close()
+    cache.close()
+
+
 def test_store_with_reuse_extends_entry(model, prompt, full_run):
     from peregrine_amd.model import ModelState
     from peregrine_amd.prefix import PrefixCache
