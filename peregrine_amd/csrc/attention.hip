@@ -220,14 +220,16 @@ __device__ inline void norm_rope_wave(const float (&x)[4], const float (&wt)[4],
 // first, then the K / V tile of the split, all on straight-line code: behind
 // a branch the compiler's wait at the join would also cover the loads issued
 // before it, so q would be prepared only once the K / V tile had arrived.
-template <bool FRESH>
+// ROWS2: a two-token launch (the verify), whose row 1 takes row 0's new token
+// as its last cached token; one-row launches compile without that path.
+template <bool FRESH, bool ROWS2>
 __global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnDecodeArgs a0) {
   extern __shared__ float sc[];  // [4][split_tokens + 2] scores, then probabilities
   __shared__ float mh[kAttnGroup], lh[kAttnGroup];
   // decode-step form: prepared q of the group's 4 heads, new tokens' k and v
   __shared__ uint16_t qf[kAttnGroup * kAttnHeadDim];
   __shared__ uint16_t kf[2 * kAttnHeadDim], vf[2 * kAttnHeadDim];
-  const uint32_t row = blockIdx.z;
+  const uint32_t row = ROWS2 ? blockIdx.z : 0u;
   const AttnDecodeArgs a = attn_row_args(a0, row);
 
   const uint32_t kvh = blockIdx.y;
@@ -279,7 +281,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnD
   const bool in_last = fresh && split == last;
   const uint32_t nx = in_last ? 1u : 0u;        // the row's own new token
   const uint32_t nk = in_last ? row + 1 : 0u;   // new tokens whose k / v this block prepares
-  const uint32_t nvirt = in_last ? row : 0u;    // of them, cached tokens of this row
+  const uint32_t nvirt = (ROWS2 && in_last) ? row : 0u;  // of them, cached tokens of this row
 
   if (t0 >= t1 && nx == 0) {  // empty range: neutral partial
     for (uint32_t i = threadIdx.x; i < kAttnGroup * kAttnPartialStride; i += kAttnThreads) {
@@ -453,13 +455,18 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnD
   // The virtual cached token's value bits (vf row 0) replace what lane ts
   // read from its cache slot, which row 0's block is writing in this launch:
   // same lane, same element, so the summation order is a one-token step's.
-  // Branch-free bit merge on the packed words (mask m[c] selects the 16-bit
-  // half of word c that holds the virtual token; all zero in other lanes).
-  auto patch_virt = [&](uint32_t (&vd)[4], const uint32_t (&m)[4], int p) {
+  // Branch-free bit merge on the packed words: the mask selects the 16-bit
+  // half of word c that holds the virtual token (element e of the lane's 8
+  // tokens; e >= 8 in the other lanes, whose words stay as loaded).
+  auto patch_virt = [&](uint32_t (&vd)[4], uint32_t e, int p) {
     const uint32_t bits = vf[64 * w + 8 * p + rr];
     const uint32_t dup = bits | (bits << 16);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) vd[c] = (vd[c] & ~m[c]) | (dup & m[c]);
+    for (int c = 0; c < 4; ++c) {
+      const uint32_t m = (e == static_cast<uint32_t>(2 * c) ? 0x0000FFFFu : 0u) |
+                         (e == static_cast<uint32_t>(2 * c + 1) ? 0xFFFF0000u : 0u);
+      vd[c] = (vd[c] & ~m) | (dup & m);
+    }
   };
   __syncthreads();
 
@@ -527,15 +534,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnD
     const uint32_t tl = tb + 8 * ts;  // first of this lane's 8 tokens (block-local)
     if (tl >= T) continue;
     const uint32_t nvalid = min(8u, T - tl);
-    const bool vtile = (vslot - tb) < 64u;  // wave-uniform
-    uint32_t vmask[4];
-    {
-      const uint32_t e = vslot - tl;  // element of this lane's 8 tokens (>= 8: none)
-#pragma unroll
-      for (int c = 0; c < 4; ++c)
-        vmask[c] = (e == static_cast<uint32_t>(2 * c) ? 0x0000FFFFu : 0u) |
-                   (e == static_cast<uint32_t>(2 * c + 1) ? 0xFFFF0000u : 0u);
-    }
+    const bool vtile = ROWS2 && (vslot - tb) < 64u;  // wave-uniform
     float pv[kAttnGroup][8];
 #pragma unroll
     for (int g = 0; g < static_cast<int>(kAttnGroup); ++g)
@@ -553,7 +552,8 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partials_kernel(const AttnD
 #pragma unroll
     for (int p = 0; p < 8; ++p) {
       uint32_t vd[4] = {vv[p].x, vv[p].y, vv[p].z, vv[p].w};
-      if (vtile) patch_virt(vd, vmask, p);
+      if constexpr (ROWS2)
+        if (vtile) patch_virt(vd, vslot - tl, p);
       float v8[8];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -720,12 +720,10 @@ int launch_attn_decode(hipStream_t s, const AttnDecodeArgs& a) {
   if (a.packed_q && !(a.q_norm && a.k_in && a.v_in && a.k_norm && a.key_cache_w && a.value_cache_w))
     return set_error(PRG_ERR_INVALID_ARG, "attn_decode: the decode-step form needs every input");
   const size_t lds = static_cast<size_t>(kAttnGroup) * (a.split_tokens + 2) * sizeof(float);
-  if (a.packed_q)
-    hipLaunchKernelGGL(attn_partials_kernel<true>, dim3(a.nsplit, kAttnKvHeads, a.rows), dim3(kAttnThreads), lds, s,
-                       a);
-  else
-    hipLaunchKernelGGL(attn_partials_kernel<false>, dim3(a.nsplit, kAttnKvHeads, a.rows), dim3(kAttnThreads), lds, s,
-                       a);
+  void (*partials)(const AttnDecodeArgs) =
+      a.packed_q ? (a.rows == 2 ? attn_partials_kernel<true, true> : attn_partials_kernel<true, false>)
+                 : (a.rows == 2 ? attn_partials_kernel<false, true> : attn_partials_kernel<false, false>);
+  hipLaunchKernelGGL(partials, dim3(a.nsplit, kAttnKvHeads, a.rows), dim3(kAttnThreads), lds, s, a);
   PRG_CHECK_LAUNCH("attn_partials");
   hipLaunchKernelGGL(attn_merge_kernel, dim3(kAttnQHeads, kAttnHeadDim / kMergeThreads, a.rows), dim3(kMergeThreads),
                      0, s, a);
