@@ -206,6 +206,36 @@ int prg_q4_dequantize_bf16(void *stream, const uint32_t *w, const uint16_t *scal
                            const uint16_t *biases, uint16_t *out, uint32_t out_dim,
                            uint32_t in_dim);
 
+/* Decode layout: the same bytes as (w, scales, biases), permuted so that the
+ * matrix-core GEMV reads 1 KiB of contiguous memory per wave load. Rows in
+ * tiles of 16, K in windows of 256; tw holds, for tile t, window v, step s
+ * (0, 1) and lane l = j + 16 c, the 16 bytes of row 16 t + j at words
+ * 32 v + 16 s + 4 c .. +3 (unit 128 (t * in_dim / 256 + v) + 64 s + l); ts / tb
+ * entry 64 (t * in_dim / 256 + v) + l is group 4 v + c of row 16 t + j.
+ * Sizes equal the MLX arrays'. out_dim % 16 == 0, in_dim % 1024 == 0.
+ * No counterpart in the reference: its Metal kernels read the MLX layout. */
+int prg_q4_repack_t16(void *stream, const uint32_t *w, const uint16_t *scales,
+                      const uint16_t *biases, uint32_t *tw, uint16_t *ts, uint16_t *tb,
+                      uint32_t out_dim, uint32_t in_dim);
+
+/* prg_q4_gemv_bf16 on the decode layout, on the matrix cores (the kernel the
+ * model runs for its large decode GEMVs); in_dim 4096, 8192 or 12288.
+ * Replaces linear_q4_affine_group64_qmv_fast_bf16 (shaders/linear.metal:158-193). */
+int prg_q4_gemv_t16_bf16(void *stream, const uint16_t *x, const uint32_t *tw,
+                         const uint16_t *ts, const uint16_t *tb, uint16_t *y,
+                         uint32_t token_count, uint32_t out_dim, uint32_t in_dim);
+
+/* Greedy argmax of the bf16 logits of token_count (1 or 2) rows on the decode
+ * layout (in_dim 4096): out_index[t] under the order of prg_argmax_pairs_f32_u32
+ * over 8-row partials. workspace: prg_q4_gemv_t16_argmax_workspace_bytes().
+ * Replaces linear_vec_q4_affine_group64_qmv_fast_argmax_partial_bf16
+ * (shaders/linear.metal:195-255) + argmax_pairs_f32_u32 (shaders/argmax.metal:6-43). */
+int prg_q4_gemv_t16_argmax_bf16(void *stream, const uint16_t *x, const uint32_t *tw,
+                                const uint16_t *ts, const uint16_t *tb, uint32_t *out_index,
+                                uint32_t token_count, uint32_t out_dim, uint32_t in_dim,
+                                void *workspace);
+size_t prg_q4_gemv_t16_argmax_workspace_bytes(void);
+
 /* ======================================================================
  * Norms and embedding
  * ====================================================================== */

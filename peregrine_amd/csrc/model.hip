@@ -29,6 +29,7 @@
 #include <string.h>
 
 #include "model.hpp"
+#include "q4_gemv_t16.hpp"
 
 namespace prg {
 namespace {
@@ -259,6 +260,9 @@ void add_seg(GemvParams& p, const Q4Linear& l, uint16_t* out) {
   s.w[0] = l.weight;
   s.s[0] = l.scales;
   s.b[0] = l.biases;
+  s.tw[0] = l.t16_w;
+  s.ts[0] = l.t16_s;
+  s.tb[0] = l.t16_b;
   s.out[0] = out;
   s.rows = l.out_dim;
 }
@@ -271,10 +275,19 @@ uint32_t total_rows(const GemvParams& p) {
 }
 }  // namespace
 
+// Large launches whose segments all carry decode-layout copies run on the
+// matrix-core GEMV; the rest (and every launch of a model without copies) on
+// q4_gemv_kernel.
 int run_gemv(hipStream_t s, GemvParams& p, int epi, int norm, const char* name) {
   int M = p.x[1] ? 2 : 1;
+  if (t16_usable(p, M, epi, norm, true)) return launch_q4_gemv_t16(s, p, M, epi, norm, name);
   const int rows = gemv_rows_per_wave(total_rows(p), p.K, epi, M);
   return launch_q4_gemv(s, p, M, rows, epi, norm, name);
+}
+
+int run_argmax_gemv(hipStream_t s, GemvParams& p, int M, int norm, const char* name) {
+  if (t16_usable(p, M, kEpiArgmax, norm, true)) return launch_q4_gemv_t16(s, p, M, kEpiArgmax, norm, name);
+  return launch_q4_gemv(s, p, M, 8, kEpiArgmax, norm, name);
 }
 
 // GDN layer: norm+in_proj(+conv) -> recurrence -> gated norm+out_proj + residual.
@@ -488,6 +501,9 @@ int encode_mlp(PrgModel* m, PrgModelState* st, const DecoderLayer& L, int M, con
   p.seg[0].w[1] = L.mlp.up_proj.weight;
   p.seg[0].s[1] = L.mlp.up_proj.scales;
   p.seg[0].b[1] = L.mlp.up_proj.biases;
+  p.seg[0].tw[1] = L.mlp.up_proj.t16_w;
+  p.seg[0].ts[1] = L.mlp.up_proj.t16_s;
+  p.seg[0].tb[1] = L.mlp.up_proj.t16_b;
   if (M == 2) {
     p.x[1] = h[1];
     p.seg[0].out[1] = inter[1];
@@ -534,7 +550,7 @@ int encode_token(PrgModel* m, PrgModelState* st, bool with_head) {
   p.seg[0].pval[0] = st->pval;
   p.seg[0].pidx[0] = st->pidx;
   p.argmax_waves = st->argmax_waves;
-  if (int rc = launch_q4_gemv(s, p, 1, 8, kEpiArgmax, kNormRms, "lm_head.argmax")) return rc;
+  if (int rc = run_argmax_gemv(s, p, 1, kNormRms, "lm_head.argmax")) return rc;
   if (st->gemv_only) return PRG_OK;
   return launch_argmax_waves_advance(s, st->pval, st->pidx, st->argmax_waves, st->ctl, st->prompt, st->predictions);
 }
@@ -572,6 +588,63 @@ int run_step(PrgModelState* st, bool with_head) {
 }
 
 }  // namespace
+
+// Every GEMV weight that has a decode-layout shape: the layers' projections
+// and MLPs, the lm_head, and the MTP drafter's fc and layer.
+static std::vector<Q4Linear*> t16_linears(PrgModel* m) {
+  std::vector<Q4Linear*> lins;
+  auto add = [&](Q4Linear* q) {
+    if (q->weight && t16_shape_ok(q->out_dim, q->in_dim)) lins.push_back(q);
+  };
+  auto add_layer = [&](DecoderLayer& L) {
+    if (L.linear) {
+      for (Q4Linear* q : {&L.lin.in_qkv, &L.lin.in_z, &L.lin.in_a, &L.lin.in_b, &L.lin.out_proj}) add(q);
+    } else {
+      for (Q4Linear* q : {&L.full.q_proj, &L.full.k_proj, &L.full.v_proj, &L.full.o_proj}) add(q);
+    }
+    for (Q4Linear* q : {&L.mlp.gate_proj, &L.mlp.up_proj, &L.mlp.down_proj}) add(q);
+  };
+  for (DecoderLayer& L : m->layers) add_layer(L);
+  add(&m->lm_head);
+  if (m->mtp.present) {
+    add(&m->mtp.fc);
+    add_layer(m->mtp.layer);
+  }
+  return lins;
+}
+
+int prepare_t16(PrgModel* m) {
+  if (!m->t16_enabled) return PRG_OK;
+  const std::vector<Q4Linear*> lins = t16_linears(m);
+  auto wbytes = [](const Q4Linear* q) { return align_up(static_cast<size_t>(q->out_dim) * q->in_dim / 2, kAlign); };
+  auto mbytes = [](const Q4Linear* q) { return align_up(static_cast<size_t>(q->out_dim) * (q->in_dim / 64) * 2, kAlign); };
+  size_t total = 0;
+  for (const Q4Linear* q : lins) total += wbytes(q) + 2 * mbytes(q);
+  if (!m->t16_arena && total > 0) {
+    void* p = nullptr;
+    if (hipMalloc(&p, total) != hipSuccess) return set_error(PRG_ERR_OOM, "decode-layout weights: %zu bytes", total);
+    m->t16_arena = static_cast<uint8_t*>(p);
+    m->t16_bytes = total;
+  }
+  size_t off = 0;
+  for (Q4Linear* q : lins) {
+    q->t16_w = reinterpret_cast<uint32_t*>(m->t16_arena + off);
+    off += wbytes(q);
+    q->t16_s = reinterpret_cast<uint16_t*>(m->t16_arena + off);
+    off += mbytes(q);
+    q->t16_b = reinterpret_cast<uint16_t*>(m->t16_arena + off);
+    off += mbytes(q);
+    if (int rc = launch_t16_repack(nullptr, q->weight, q->scales, q->biases, q->t16_w, q->t16_s, q->t16_b,
+                                   q->out_dim, q->in_dim))
+      return rc;
+  }
+  PRG_HIP(hipDeviceSynchronize());
+  m->t16_dirty = false;
+  return PRG_OK;
+}
+
+int ensure_t16(PrgModel* m) { return m->t16_dirty ? prepare_t16(m) : PRG_OK; }
+
 }  // namespace prg
 
 using namespace prg;
@@ -595,6 +668,7 @@ int prg_model_create_random(const PrgModelConfig* cfg, uint64_t seed, PrgModel**
   if (int rc = validate_config(*cfg)) return rc;
   auto* m = new PrgModel();
   m->cfg = *cfg;
+  if (const char* e = getenv("PEREGRINE_T16")) m->t16_enabled = e[0] != '0';
   Builder sizing{m, seed};
   build_model(sizing);
   m->arena_bytes = sizing.offset;
@@ -617,6 +691,10 @@ int prg_model_create_random(const PrgModelConfig* cfg, uint64_t seed, PrgModel**
     delete m;
     return set_error(PRG_ERR_HIP, "model init: %s", hipGetErrorString(e));
   }
+  if (int rc = prepare_t16(m)) {
+    prg_model_destroy(m);
+    return rc;
+  }
   *out = m;
   return PRG_OK;
 }
@@ -625,8 +703,16 @@ void prg_model_destroy(PrgModel* model) {
   if (!model) return;
   (void)hipFree(model->arena);
   (void)hipFree(model->dense_arena);
+  (void)hipFree(model->t16_arena);
   delete model;
 }
+
+int prg_model_prepare_decode(PrgModel* model) {
+  PRG_CHECK_ARG(model, "prg_model_prepare_decode: null model");
+  return prepare_t16(model);
+}
+
+size_t prg_model_decode_layout_bytes(const PrgModel* model) { return model ? model->t16_bytes : 0; }
 
 // The reference's prepared dense RHS for the prompt path
 // (block_attn.zig:143-215, linear_q4.denseRhsBf16ByteLen): every Q4 matrix
@@ -710,6 +796,9 @@ int prg_model_tensor(const PrgModel* model, const char* name, void** ptr, size_t
   if (it == model->tensors.end()) return set_error(PRG_ERR_INVALID_ARG, "prg_model_tensor: no tensor '%s'", name);
   *ptr = it->second.ptr;
   *bytes = it->second.bytes;
+  // the caller may write the weights through ptr: rewrite the decode-layout
+  // copies before the next run
+  model->t16_dirty = model->t16_arena != nullptr;
   return PRG_OK;
 }
 
@@ -844,6 +933,7 @@ uint32_t prg_model_state_stride(const PrgModelState* st) { return st ? st->strid
 int prg_model_forward_next_token(PrgModel* model, PrgModelState* st, uint32_t token, uint32_t cache_pos,
                                  uint32_t rope_pos, uint32_t seq_len, uint32_t* next_token) {
   PRG_CHECK_ARG(model && st && next_token && st->model == model, "prg_model_forward_next_token: bad argument");
+  if (int rc = ensure_t16(model)) return rc;
   if (cache_pos >= st->max_seq)  // model.zig:805
     return set_error(PRG_ERR_SEQUENCE_TOO_LONG, "cache_pos %u >= max_seq %u", cache_pos, st->max_seq);
   if (token >= model->cfg.vocab)  // model.zig:806
@@ -872,6 +962,7 @@ int prg_model_forward_next_token_prefixed(PrgModel* model, PrgModelState* st, ui
                                           uint32_t rope_pos, uint32_t seq_len, uint32_t prefix_len,
                                           uint32_t* next_token) {
   PRG_CHECK_ARG(model && st && next_token && st->model == model, "prg_model_forward_next_token_prefixed: bad argument");
+  if (int rc = ensure_t16(model)) return rc;
   const uint64_t slot = static_cast<uint64_t>(prefix_len) + cache_pos;
   if (slot >= st->max_seq)
     return set_error(PRG_ERR_SEQUENCE_TOO_LONG, "prefix_len %u + cache_pos %u >= max_seq %u", prefix_len, cache_pos,
@@ -884,6 +975,7 @@ int prg_model_forward_next_token_prefixed(PrgModel* model, PrgModelState* st, ui
 
 int prg_model_decode(PrgModel* model, PrgModelState* st, uint32_t n_steps, uint32_t* tokens_out, float* gpu_ms) {
   PRG_CHECK_ARG(model && st && tokens_out && st->model == model, "prg_model_decode: bad argument");
+  if (int rc = ensure_t16(model)) return rc;
   PRG_CHECK_ARG(n_steps >= 1, "prg_model_decode: n_steps == 0");
   if (int rc = ensure_graphs(st)) return rc;
   DecodeCtl ctl{};
@@ -912,6 +1004,7 @@ int prg_model_decode(PrgModel* model, PrgModelState* st, uint32_t n_steps, uint3
 // undefined until the next prefill from position 0.
 int prg_model_time_token_gemvs(PrgModel* model, PrgModelState* st, uint32_t replays, float* us_per_token) {
   PRG_CHECK_ARG(model && st && us_per_token && st->model == model, "prg_model_time_token_gemvs: bad argument");
+  if (int rc = ensure_t16(model)) return rc;
   PRG_CHECK_ARG(replays >= 1, "prg_model_time_token_gemvs: replays == 0");
   hipGraphExec_t ge = nullptr;
   st->gemv_only = true;
@@ -935,6 +1028,7 @@ int prg_model_time_token_gemvs(PrgModel* model, PrgModelState* st, uint32_t repl
 int prg_model_generate(PrgModel* model, PrgModelState* st, const uint32_t* prompt, uint32_t prompt_len,
                        uint32_t n_new, int teacher_force, uint32_t* predictions, float* decode_ms) {
   PRG_CHECK_ARG(model && st && prompt && predictions && st->model == model, "prg_model_generate: bad argument");
+  if (int rc = ensure_t16(model)) return rc;
   PRG_CHECK_ARG(prompt_len >= 1, "prg_model_generate: empty prompt");
   if (teacher_force) PRG_CHECK_ARG(n_new == 0, "prg_model_generate: teacher forcing takes n_new == 0");
   else PRG_CHECK_ARG(n_new >= 1, "prg_model_generate: n_new == 0");

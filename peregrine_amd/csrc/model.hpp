@@ -39,6 +39,11 @@ struct Q4Linear {
   // Prepared bf16 [out_dim, in_dim] copy for the prompt GEMMs (inside
   // PrgModel::dense_arena; null until prg_model_prepare_dense).
   uint16_t* dense = nullptr;
+  // Decode-layout copy for the matrix-core GEMVs (q4_gemv_t16.hpp; inside
+  // PrgModel::t16_arena; null when the shape has none or copies are off).
+  uint32_t* t16_w = nullptr;
+  uint16_t* t16_s = nullptr;
+  uint16_t* t16_b = nullptr;
 };
 
 struct LinearAttentionBlock {
@@ -143,6 +148,10 @@ int validate_model_config(const PrgModelConfig& c);
 // filled, contents undefined. Returns a PRG_ERR_* code.
 int layout_model(PrgModel* m);
 uint32_t cache_stride_for(uint32_t max_seq);
+// Write the decode-layout copies (allocating them on first use); ensure_t16
+// does it only when a tensor pointer was handed out since the last write.
+int prepare_t16(PrgModel* m);
+int ensure_t16(PrgModel* m);
 
 }  // namespace prg
 
@@ -160,6 +169,14 @@ struct PrgModel {
   // Prepared bf16 copies of the prompt GEMMs' weights (prg_model_prepare_dense).
   uint8_t* dense_arena = nullptr;
   size_t dense_bytes = 0;
+  // Decode-layout copies of the GEMV weights, written at creation and again
+  // before the next run once a tensor pointer has been handed out
+  // (prg_model_tensor: the caller may write the Q4 weights through it).
+  // PEREGRINE_T16=0 at creation: no copies, every GEMV on q4_gemv_kernel.
+  uint8_t* t16_arena = nullptr;
+  size_t t16_bytes = 0;
+  bool t16_enabled = true;
+  mutable bool t16_dirty = false;
 };
 
 struct PrgModelState {
@@ -220,6 +237,9 @@ namespace prg {
 GemvParams gemv_params(const uint16_t* x, uint32_t K);
 void add_seg(GemvParams& p, const Q4Linear& l, uint16_t* out);
 int run_gemv(hipStream_t s, GemvParams& p, int epi, int norm, const char* name);
+// The lm_head argmax GEMV (one segment, per-block or per-wave entries in
+// pval / pidx and their count in p.argmax_waves) for M rows.
+int run_argmax_gemv(hipStream_t s, GemvParams& p, int M, int norm, const char* name);
 
 // Where a layer's GDN state is read and written for one token (in == out for
 // the ordinary in-place update).

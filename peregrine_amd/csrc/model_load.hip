@@ -13,6 +13,7 @@
 // one device arena laid out exactly as for a random model; each tensor is read
 // in chunks into two pinned staging buffers that alternate, so the pread of
 // chunk i+1 overlaps the DMA of chunk i.
+#include <stdlib.h>
 #include <string.h>
 
 #include <memory>
@@ -204,8 +205,10 @@ extern "C" int prg_model_load(const PrgModelConfig* cfg, const char* target_dir,
                 "prg_model_load: mtp_dir must be given exactly when cfg->mtp_layers is 1");
   auto* m = new PrgModel();
   m->cfg = *cfg;
+  if (const char* e = getenv("PEREGRINE_T16")) m->t16_enabled = e[0] != '0';
   int rc = layout_model(m);
   if (rc == PRG_OK) rc = upload_checkpoint(m, target_dir, mtp_dir);
+  if (rc == PRG_OK) rc = prepare_t16(m);
   if (rc != PRG_OK) {
     prg_model_destroy(m);
     return rc;

@@ -215,7 +215,7 @@ int run_prefill(PrgModel* m, PrgModelState* st, uint32_t from, uint32_t len, boo
   p.seg[0].pval[0] = st->pval;
   p.seg[0].pidx[0] = st->pidx;
   p.argmax_waves = st->argmax_waves;
-  if (int rc = launch_q4_gemv(s, p, 1, 8, kEpiArgmax, kNormRms, "lm_head.argmax")) return rc;
+  if (int rc = run_argmax_gemv(s, p, 1, kNormRms, "lm_head.argmax")) return rc;
   if (int rc = launch_argmax_waves_advance(s, st->pval, st->pidx, st->argmax_waves, st->ctl, st->prompt,
                                            st->predictions))
     return rc;
@@ -253,6 +253,7 @@ extern "C" {
 int prg_model_prefill(PrgModel* model, PrgModelState* st, const uint32_t* prompt, uint32_t prompt_len,
                       uint32_t* next_token) {
   PRG_CHECK_ARG(model && st && prompt && next_token && st->model == model, "prg_model_prefill: bad argument");
+  if (int rc = ensure_t16(model)) return rc;
   PRG_CHECK_ARG(prompt_len >= 1, "prg_model_prefill: empty prompt");
   if (prompt_len > st->max_seq)
     return set_error(PRG_ERR_SEQUENCE_TOO_LONG, "prompt of %u tokens exceeds max_seq %u", prompt_len, st->max_seq);

@@ -80,6 +80,7 @@ int prg_model_state_copy_prefix(PrgModelState* dst, const PrgModelState* src, ui
 int prg_model_prefill_from(PrgModel* model, PrgModelState* st, const uint32_t* prompt, uint32_t prompt_len,
                            uint32_t prefix_len, uint32_t* next_token) {
   PRG_CHECK_ARG(model && st && prompt && next_token && st->model == model, "prg_model_prefill_from: bad argument");
+  if (int rc = ensure_t16(model)) return rc;
   PRG_CHECK_ARG(prefix_len >= 1 && prefix_len < prompt_len,
                 "prg_model_prefill_from: prefix_len %u must be in [1, prompt_len %u)", prefix_len, prompt_len);
   if (prompt_len > st->max_seq)

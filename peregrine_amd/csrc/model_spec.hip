@@ -122,7 +122,7 @@ int encode_mtp_step(PrgModel* m, PrgModelState* st, const uint32_t* token_dev, c
   p.seg[0].pval[0] = st->pval;
   p.seg[0].pidx[0] = st->pidx;
   p.argmax_waves = st->argmax_waves;
-  if (int rc = launch_q4_gemv(s, p, 1, 8, kEpiArgmax, kNormRms, "mtp.lm_head.argmax")) return rc;
+  if (int rc = run_argmax_gemv(s, p, 1, kNormRms, "mtp.lm_head.argmax")) return rc;
   const float* vals[1] = {st->pval};
   const uint32_t* rows[1] = {st->pidx};
   uint32_t* outs[1] = {out_token};
@@ -175,7 +175,7 @@ int encode_verify(PrgModel* m, PrgModelState* st) {
   p.argmax_waves = st->argmax_waves;
   // (the norm stays a launch of its own: fused into this M = 2 prologue it
   // measured 138 us against 126 + 4)
-  if (int rc = launch_q4_gemv(s, p, 2, 8, kEpiArgmax, kNormNone, "lm_head.argmax2")) return rc;
+  if (int rc = run_argmax_gemv(s, p, 2, kNormNone, "lm_head.argmax2")) return rc;
   const float* vals[2] = {st->pval, st->pval2};
   const uint32_t* rows[2] = {st->pidx, st->pidx2};
   uint32_t* outs[2] = {&sc->verify, &sc->bonus};
@@ -291,6 +291,7 @@ int prg_model_forward_two_tokens(PrgModel* model, PrgModelState* st, uint32_t to
                                  uint32_t* verify_token, uint32_t* bonus_token, uint16_t* hidden_out) {
   PRG_CHECK_ARG(model && st && verify_token && bonus_token && st->model == model,
                 "prg_model_forward_two_tokens: bad argument");
+  if (int rc = ensure_t16(model)) return rc;
   if (static_cast<uint64_t>(cache_pos) + 2 > st->max_seq)  // model.zig:1645-1646
     return set_error(PRG_ERR_SEQUENCE_TOO_LONG, "cache_pos %u + 2 > max_seq %u", cache_pos, st->max_seq);
   const uint32_t toks[2] = {token0, token1};
@@ -329,6 +330,7 @@ int prg_model_forward_two_tokens(PrgModel* model, PrgModelState* st, uint32_t to
 int prg_model_mtp_draft(PrgModel* model, PrgModelState* st, uint32_t token, const uint16_t* hidden,
                         uint32_t cache_pos, uint32_t rope_pos, uint32_t seq_len, uint32_t* draft_token) {
   PRG_CHECK_ARG(model && st && hidden && draft_token && st->model == model, "prg_model_mtp_draft: bad argument");
+  if (int rc = ensure_t16(model)) return rc;
   PRG_CHECK_ARG(model->mtp.present, "prg_model_mtp_draft: the model has no MTP drafter");
   if (cache_pos >= st->max_seq)  // mtp.zig:202
     return set_error(PRG_ERR_SEQUENCE_TOO_LONG, "cache_pos %u >= max_seq %u", cache_pos, st->max_seq);
@@ -354,6 +356,7 @@ int prg_model_mtp_draft(PrgModel* model, PrgModelState* st, uint32_t token, cons
 int prg_model_mtp_prefill(PrgModel* model, PrgModelState* st, const uint32_t* tokens, uint32_t token_count,
                           const uint16_t* hidden_rows, uint32_t start_pos) {
   PRG_CHECK_ARG(model && st && tokens && hidden_rows && st->model == model, "prg_model_mtp_prefill: bad argument");
+  if (int rc = ensure_t16(model)) return rc;
   PRG_CHECK_ARG(model->mtp.present, "prg_model_mtp_prefill: the model has no MTP drafter");
   if (token_count == 0) return PRG_OK;  // mtp.zig:148
   if (static_cast<uint64_t>(start_pos) + token_count > st->max_seq)
@@ -388,6 +391,7 @@ int generate_speculative(PrgModel* model, PrgModelState* st, const uint32_t* pro
                          uint32_t* tokens_out, uint32_t* accepted, uint32_t* attempted, float* decode_ms) {
   PRG_CHECK_ARG(model && st && prompt && tokens_out && st->model == model,
                 "prg_model_generate_speculative: bad argument");
+  if (int rc = ensure_t16(model)) return rc;
   PRG_CHECK_ARG(model->mtp.present, "prg_model_generate_speculative: the model has no MTP drafter");
   PRG_CHECK_ARG(prompt_len >= 1 && n_new >= 1, "prg_model_generate_speculative: empty prompt or n_new == 0");
   PRG_CHECK_ARG(prefix_len < prompt_len, "prg_model_generate_speculative: prefix_len %u must be below prompt_len %u",

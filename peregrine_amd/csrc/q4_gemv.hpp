@@ -78,6 +78,10 @@ struct GemvSeg {
   // writes silu(bf16(dot)) in f32 to silu_out[m] instead of bf16 to out (the
   // GDN z gate).
   float* silu_out[2];
+  // Decode-layout copies of w / s / b (q4_gemv_t16.hpp); null when absent.
+  const uint32_t* tw[2];
+  const uint16_t* ts[2];
+  const uint16_t* tb[2];
   uint32_t rows;              // output rows of this segment
   uint32_t block_begin;       // first group index of this segment (set by the launcher)
 };
