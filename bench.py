@@ -28,10 +28,11 @@ sys.path.insert(0, str(ROOT))
 METRIC = "decode tok/s @batch1 (9B-shaped Q4) + Q4 GEMV achieved HBM GB/s vs peak"
 HBM_PEAK_GBS = 8000.0
 PROMPT_TOKENS = 1600
-# HBM bytes per launch of the dominant kernel, from two rocprofv3 --pmc passes
-# (FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000, the factors a plain 256 MiB copy
-# kernel reads on the same counters); profiles/gemv_silu_gate_hbm_traffic.md.
-DOMINANT_TRAFFIC_BYTES = 57_050_112
+# HBM bytes per launch of the dominant kernel (the decode-layout gate/up GEMV),
+# from two rocprofv3 --pmc passes (FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000, the
+# factors a plain 256 MiB copy kernel reads on the same counters);
+# profiles/gemv_silu_gate_hbm_traffic.md.
+DOMINANT_TRAFFIC_BYTES = 56_957_952
 
 
 def log(*a) -> None:
@@ -59,10 +60,13 @@ def token_gemv_bytes(cfg) -> int:
 
 def dominant_kernel_roofline(iters: int = 100) -> dict:
     """Fused post_attention_layernorm + gate/up SiLU GEMV at the MLP shape
-    (2 x 12288x4096 Q4): ~40% of the bytes a decode step streams. One launch per
-    ring copy (>= 512 MiB of distinct weights, so every launch reads HBM, not
-    the 256 MiB Infinity Cache) is captured into a HIP graph on its own stream;
-    the graph is replayed `iters / copies` times between two HIP events on that
+    (2 x 12288x4096 Q4): ~40% of the bytes a decode step streams. The kernel
+    timed is the one the model runs: the matrix-core GEMV over the decode
+    layout (prg_q4_gemv_t16_silu_gate_norm_bf16); the MLX-layout kernel
+    (prg_q4_gemv_silu_gate_norm_bf16) is timed beside it. One launch per ring
+    copy (>= 512 MiB of distinct weights, so every launch reads HBM, not the
+    256 MiB Infinity Cache) is captured into a HIP graph on its own stream; the
+    graph is replayed `iters / copies` times between two HIP events on that
     stream, as the decode loop replays its graph, so the average launch
     duration carries no host launch overhead."""
     import ctypes as C
@@ -78,35 +82,53 @@ def dominant_kernel_roofline(iters: int = 100) -> dict:
     g, u = random_q4(rng, N, K, zero_mean=True), random_q4(rng, N, K, zero_mean=True)
     copies = max(2, -(-ROTATE_BYTES // (2 * g.nbytes)))
     ring = [(Q4Linear.upload(g), Q4Linear.upload(u)) for _ in range(copies)]
+
+    def t16_copy(lin):
+        dst = [DeviceArray(a.shape, a.dtype) for a in (lin.weight, lin.scales, lin.biases)]
+        call("prg_q4_repack_t16", None, *lin._wsb(), *[C.c_void_p(d.ptr) for d in dst], N, K)
+        return dst
+
+    tring = [(t16_copy(gl), t16_copy(ul)) for gl, ul in ring]
     x = DeviceArray.from_numpy(random_bf16(rng, (K,), std=3.0))
     nw = DeviceArray.from_numpy(random_bf16(rng, (K,), std=0.1, mean=1.0))
     out = DeviceArray((N,), np.uint16)
     stream = Stream()
-
-    def launch(i: int) -> None:
-        gl, ul = ring[i % len(ring)]
-        call("prg_q4_gemv_silu_gate_norm_bf16", C.c_void_p(stream.handle), C.c_void_p(x.ptr), C.c_void_p(nw.ptr),
-             C.c_float(1e-6), *gl._wsb(), *ul._wsb(), C.c_void_p(out.ptr), N, K)
-
-    launch(0)  # eager first launch: kernel selection and occupancy queries happen outside the capture
-    stream.synchronize()
-    with Graph.capture(stream) as graph:
-        for i in range(copies):
-            launch(i)
+    sp = C.c_void_p(stream.handle)
     reps = max(1, iters // copies)
-    for _ in range(2):
-        graph.launch()
-    stream.synchronize()
-    a, b = Event(), Event()
-    a.record(C.c_void_p(stream.handle))
-    for _ in range(reps):
-        graph.launch()
-    b.record(C.c_void_p(stream.handle))
-    stream.synchronize()
     launches = reps * copies
-    avg_us = a.elapsed_ms(b) * 1e3 / launches
-    graph.close()
-    del ring
+    a, b = Event(), Event()
+
+    def time_ring(launch) -> float:
+        """Average launch duration (us) of launch(i) over the ring, graph-replayed."""
+        launch(0)  # eager first launch: kernel selection and occupancy queries happen outside the capture
+        stream.synchronize()
+        with Graph.capture(stream) as graph:
+            for i in range(copies):
+                launch(i)
+        for _ in range(2):
+            graph.launch()
+        stream.synchronize()
+        a.record(sp)
+        for _ in range(reps):
+            graph.launch()
+        b.record(sp)
+        stream.synchronize()
+        graph.close()
+        return a.elapsed_ms(b) * 1e3 / launches
+
+    def launch_t16(i: int) -> None:
+        gt, ut = tring[i % copies]
+        call("prg_q4_gemv_t16_silu_gate_norm_bf16", sp, C.c_void_p(x.ptr), C.c_void_p(nw.ptr), C.c_float(1e-6),
+             *[C.c_void_p(d.ptr) for d in gt], *[C.c_void_p(d.ptr) for d in ut], C.c_void_p(out.ptr), N, K)
+
+    def launch_mlx(i: int) -> None:
+        gl, ul = ring[i % copies]
+        call("prg_q4_gemv_silu_gate_norm_bf16", sp, C.c_void_p(x.ptr), C.c_void_p(nw.ptr), C.c_float(1e-6),
+             *gl._wsb(), *ul._wsb(), C.c_void_p(out.ptr), N, K)
+
+    avg_us = time_ring(launch_t16)
+    mlx_us = time_ring(launch_mlx)
+    del ring, tring
     algo = 2 * q4_bytes(N, K) + 2 * K * 2 + N * 2  # gate+up weights, x + norm weight, out
     gbs = algo / (avg_us * 1e-6) / 1e9
 
@@ -115,45 +137,20 @@ def dominant_kernel_roofline(iters: int = 100) -> dict:
     nbytes = (algo + 15) // 16 * 16
     bufs = [DeviceArray((nbytes,), np.uint8) for _ in range(copies)]
     sink = DeviceArray((1,), np.uint32)
-    for buf in bufs:
-        call("prg_hip_read_kernel", C.c_void_p(buf.ptr), C.c_size_t(nbytes), C.c_void_p(sink.ptr),
-             C.c_void_p(stream.handle))
-    stream.synchronize()
-    with Graph.capture(stream) as rgraph:
-        for buf in bufs:
-            call("prg_hip_read_kernel", C.c_void_p(buf.ptr), C.c_size_t(nbytes), C.c_void_p(sink.ptr),
-                 C.c_void_p(stream.handle))
-    rgraph.launch()
-    stream.synchronize()
-    a.record(C.c_void_p(stream.handle))
-    for _ in range(reps):
-        rgraph.launch()
-    b.record(C.c_void_p(stream.handle))
-    stream.synchronize()
-    read_us = a.elapsed_ms(b) * 1e3 / launches
-    rgraph.close()
+    read_us = time_ring(lambda i: call("prg_hip_read_kernel", C.c_void_p(bufs[i % copies].ptr), C.c_size_t(nbytes),
+                                       C.c_void_p(sink.ptr), sp))
     # Cross-check: a device-to-device hipMemcpyAsync of the same bytes from the
     # same ring (reads them once and writes them once), timed the same way.
     dst = DeviceArray((nbytes,), np.uint8)
-    with Graph.capture(stream) as cgraph:
-        for buf in bufs:
-            call("prg_hip_memcpy", C.c_void_p(dst.ptr), C.c_void_p(buf.ptr), C.c_size_t(nbytes), 2,
-                 C.c_void_p(stream.handle), 0)
-    cgraph.launch()
-    stream.synchronize()
-    a.record(C.c_void_p(stream.handle))
-    for _ in range(reps):
-        cgraph.launch()
-    b.record(C.c_void_p(stream.handle))
-    stream.synchronize()
-    copy_us = a.elapsed_ms(b) * 1e3 / launches
-    cgraph.close()
+    copy_us = time_ring(lambda i: call("prg_hip_memcpy", C.c_void_p(dst.ptr), C.c_void_p(bufs[i % copies].ptr),
+                                       C.c_size_t(nbytes), 2, sp, 0))
     dst.close()
     for buf in bufs:
         buf.close()
     stream.close()
     synchronize()
-    return {"kernel": "q4_gemv_kernel<M=1,ROWS=1,ITERS=2,EPI=silu_gate,NORM=rms> (mlp.gate_up, 2x12288x4096 Q4)",
+    return {"kernel": "q4_gemv_t16_kernel<M=1,NMAT=2,S=4,EPI=silu_gate,NORM=rms> (mlp.gate_up, 2x12288x4096 Q4, "
+                      "decode layout, matrix cores)",
             "bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": DOMINANT_TRAFFIC_BYTES,
             "traffic_unit": "bytes/launch (PMC, calibrated)",
@@ -161,6 +158,8 @@ def dominant_kernel_roofline(iters: int = 100) -> dict:
             "read_floor_us": round(read_us, 3), "read_floor_GBps": round(nbytes / (read_us * 1e-6) / 1e9, 1),
             "frac_of_read_floor": round(read_us / avg_us, 4),
             "memcpy_d2d_us": round(copy_us, 3), "memcpy_d2d_GBps_rw": round(2 * nbytes / (copy_us * 1e-6) / 1e9, 1),
+            "mlx_layout_kernel": {"kernel": "q4_gemv_kernel<M=1,ROWS=1,ITERS=2,EPI=silu_gate,NORM=rms>",
+                                  "avg_us": round(mlx_us, 3), "GBps": round(algo / (mlx_us * 1e-6) / 1e9, 1)},
             "algo_bytes_per_launch": int(algo), "launches": launches, "ring_copies": copies}
 
 

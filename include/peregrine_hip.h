@@ -225,6 +225,15 @@ int prg_q4_gemv_t16_bf16(void *stream, const uint16_t *x, const uint32_t *tw,
                          const uint16_t *ts, const uint16_t *tb, uint16_t *y,
                          uint32_t token_count, uint32_t out_dim, uint32_t in_dim);
 
+/* prg_q4_gemv_silu_gate_norm_bf16 on the decode layout (in_dim 4096): the
+ * model's post_attention_layernorm + gate/up SiLU launch
+ * (decoder_layer.zig:756-781 + block_mlp.zig:313-345). */
+int prg_q4_gemv_t16_silu_gate_norm_bf16(void *stream, const uint16_t *x, const uint16_t *norm_weight,
+                                        float eps, const uint32_t *gate_tw, const uint16_t *gate_ts,
+                                        const uint16_t *gate_tb, const uint32_t *up_tw,
+                                        const uint16_t *up_ts, const uint16_t *up_tb, uint16_t *out,
+                                        uint32_t out_dim, uint32_t in_dim);
+
 /* Greedy argmax of the bf16 logits of token_count (1 or 2) rows on the decode
  * layout (in_dim 4096): out_index[t] under the order of prg_argmax_pairs_f32_u32
  * over 8-row partials. workspace: prg_q4_gemv_t16_argmax_workspace_bytes().

@@ -486,6 +486,26 @@ int prg_q4_gemv_t16_bf16(void* stream, const uint16_t* x, const uint32_t* tw, co
   return PRG_OK;
 }
 
+int prg_q4_gemv_t16_silu_gate_norm_bf16(void* stream, const uint16_t* x, const uint16_t* norm_weight, float eps,
+                                        const uint32_t* gate_tw, const uint16_t* gate_ts, const uint16_t* gate_tb,
+                                        const uint32_t* up_tw, const uint16_t* up_ts, const uint16_t* up_tb,
+                                        uint16_t* out, uint32_t out_dim, uint32_t in_dim) {
+  const char* name = "prg_q4_gemv_t16_silu_gate_norm_bf16";
+  if (int rc = t16_check(name, x, gate_tw, gate_ts, gate_tb, out_dim, in_dim)) return rc;
+  PRG_CHECK_ARG(norm_weight && up_tw && up_ts && up_tb && out, "%s: null pointer", name);
+  prg::GemvParams p = t16_one_seg(gate_tw, gate_ts, gate_tb, out_dim, in_dim);
+  p.seg[0].tw[1] = up_tw;
+  p.seg[0].ts[1] = up_ts;
+  p.seg[0].tb[1] = up_tb;
+  p.seg[0].out[0] = out;
+  p.x[0] = x;
+  p.norm_w = norm_weight;
+  p.eps = eps;
+  if (!prg::t16_usable(p, 1, prg::kEpiSiluGate, prg::kNormRms, false))
+    return prg::set_error(PRG_ERR_INVALID_ARG, "%s: in_dim %u (4096)", name, in_dim);
+  return prg::launch_q4_gemv_t16(prg::as_stream(stream), p, 1, prg::kEpiSiluGate, prg::kNormRms, name);
+}
+
 size_t prg_q4_gemv_t16_argmax_workspace_bytes(void) { return kT16ArgmaxWs; }
 
 int prg_q4_gemv_t16_argmax_bf16(void* stream, const uint16_t* x, const uint32_t* tw, const uint16_t* ts,
