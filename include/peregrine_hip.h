@@ -249,6 +249,11 @@ size_t prg_q4_gemv_t16_argmax_workspace_bytes(void);
  * Norms and embedding
  * ====================================================================== */
 
+/* y[i] = bf16(x[i]): round to nearest even, NaN -> quiet NaN with the input's
+ * sign and top payload bits. The rounding every kernel applies where the
+ * reference's shaders write bfloat(f) (e.g. shaders/attention.metal:210). */
+int prg_f32_to_bf16(void *stream, const float *x, uint16_t *y, size_t n);
+
 /* out = bf16(x * rsqrt(mean(x^2) + eps) * w) per row of `hidden` values.
  * Replaces rmsnorm_bf16 (shaders/rmsnorm.metal:80-116,222-245), host
  * DecoderLayer.encodeRmsNormBf16 (src/model/decoder_layer.zig:419-437). */

@@ -46,17 +46,22 @@ __host__ __device__ inline float bf2f(uint16_t b) {
   return __uint_as_float(static_cast<uint32_t>(b) << 16);
 }
 
-__host__ __device__ inline uint16_t f2bf(float f) {
-  const uint32_t u = __float_as_uint(f);
-  // both results, then a select: a NaN branch would split the caller's code
-  // into basic blocks (and its memory waits with them)
-  const uint32_t nan = (u >> 16) | 0x40u;
-  const uint32_t rne = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
-  return static_cast<uint16_t>((u & 0x7fffffffu) > 0x7f800000u ? nan : rne);
+// f32 -> bf16 bits: round to nearest even, NaN -> the quiet NaN
+// (u >> 16) | 0x40 (the conversion the reference's shaders apply with
+// bfloat(f)). One v_cvt_pk_bf16_f32: gfx950's conversion gives exactly these
+// bits for every one of the 2^32 inputs (checked exhaustively on the MI355X
+// against the bit expression (u + 0x7fff + ((u >> 16) & 1)) >> 16 with the
+// NaN case; prg_f32_to_bf16's GPU test pins it against the oracle).
+typedef __bf16 bf16x2_cvt __attribute__((ext_vector_type(2)));
+typedef float f32x2_cvt __attribute__((ext_vector_type(2)));
+__device__ inline uint16_t f2bf(float f) { return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f)); }
+// Two values in one conversion: lo in bits 0..15, hi in bits 16..31.
+__device__ inline uint32_t f2bf2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_cvt{lo, hi}, bf16x2_cvt));
 }
 
 // Round an f32 to the nearest bf16 value and return it as f32.
-__host__ __device__ inline float round_bf(float f) { return bf2f(f2bf(f)); }
+__device__ inline float round_bf(float f) { return bf2f(f2bf(f)); }
 
 // Low / high bf16 of a packed pair, widened to f32.
 __device__ inline float bf_lo(uint32_t p) { return __uint_as_float(p << 16); }

@@ -11,6 +11,7 @@
 // step (one dwordx4), and the sum of squares uses the same per-thread order and
 // block reduction as the fused-norm GEMV prologue (q4_gemv.hpp), so the
 // standalone and fused norms produce identical bits.
+#include <algorithm>
 #include "norm.hpp"
 
 namespace {
@@ -155,7 +156,25 @@ int launch_embed_norm_pair(hipStream_t s, const uint32_t* ew, const uint16_t* es
 
 }  // namespace prg
 
+namespace {
+__global__ __launch_bounds__(256) void f32_to_bf16_kernel(const float* __restrict__ x, uint16_t* __restrict__ y,
+                                                          size_t n) {
+  for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n;
+       i += static_cast<size_t>(gridDim.x) * blockDim.x)
+    y[i] = prg::f2bf(x[i]);
+}
+}  // namespace
+
 extern "C" {
+
+int prg_f32_to_bf16(void* stream, const float* x, uint16_t* y, size_t n) {
+  PRG_CHECK_ARG(x && y, "prg_f32_to_bf16: null pointer");
+  if (n == 0) return PRG_OK;
+  const uint32_t blocks = static_cast<uint32_t>(std::min<size_t>((n + 255) / 256, 4096));
+  hipLaunchKernelGGL(f32_to_bf16_kernel, dim3(blocks), dim3(256), 0, prg::as_stream(stream), x, y, n);
+  PRG_CHECK_LAUNCH("prg_f32_to_bf16");
+  return PRG_OK;
+}
 
 int prg_rmsnorm_bf16(void* stream, const uint16_t* x, const uint16_t* weight, uint16_t* out,
                      uint32_t hidden, uint32_t rows, float eps) {

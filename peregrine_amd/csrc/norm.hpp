@@ -35,11 +35,7 @@ __device__ inline uint4 rms_apply(uint4 v, uint4 w, float scale) {
   const uint32_t e[4] = {w.x, w.y, w.z, w.w};
   uint32_t o[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t lo = f2bf(bf_lo(d[i]) * scale * bf_lo(e[i]));
-    const uint32_t hi = f2bf(bf_hi(d[i]) * scale * bf_hi(e[i]));
-    o[i] = lo | (hi << 16);
-  }
+  for (int i = 0; i < 4; ++i) o[i] = f2bf2(bf_lo(d[i]) * scale * bf_lo(e[i]), bf_hi(d[i]) * scale * bf_hi(e[i]));
   return make_uint4(o[0], o[1], o[2], o[3]);
 }
 
@@ -51,11 +47,8 @@ __device__ inline uint4 gated_rms_apply(uint4 v, uint4 w, float4 z0, float4 z1, 
   const float g[8] = {z0.x, z0.y, z0.z, z0.w, z1.x, z1.y, z1.z, z1.w};
   uint32_t o[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t lo = f2bf(bf_lo(d[i]) * scale * bf_lo(e[i]) * g[2 * i]);
-    const uint32_t hi = f2bf(bf_hi(d[i]) * scale * bf_hi(e[i]) * g[2 * i + 1]);
-    o[i] = lo | (hi << 16);
-  }
+  for (int i = 0; i < 4; ++i)
+    o[i] = f2bf2(bf_lo(d[i]) * scale * bf_lo(e[i]) * g[2 * i], bf_hi(d[i]) * scale * bf_hi(e[i]) * g[2 * i + 1]);
   return make_uint4(o[0], o[1], o[2], o[3]);
 }
 

@@ -181,10 +181,12 @@ __global__ __launch_bounds__(S * kWave) void q4_gemv_t16_kernel(const GemvParams
       sm = dot2_bf16(v.y, kOnes, sm);
       sm = dot2_bf16(v.z, kOnes, sm);
       sm = dot2_bf16(v.w, kOnes, sm);
-      // the 8 units of a group sit in 8 consecutive lanes
-      sm += __shfl_xor(sm, 1);
-      sm += __shfl_xor(sm, 2);
-      sm += __shfl_xor(sm, 4);
+      // the 8 units of a group sit in 8 consecutive lanes: DPP butterfly
+      // (quad_perm 1032, quad_perm 2301, half-row mirror); every lane of the
+      // 8 gets the same bits
+      sm += dpp_f<0xB1>(sm);
+      sm += dpp_f<0x4E>(sm);
+      sm += dpp_f<0x141>(sm);
       if ((gi & 7) == 0) xg[m * kGroups + gi / 8] = sm;
     }
   }
