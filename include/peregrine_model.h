@@ -67,14 +67,13 @@ int prg_model_prepare_dense(PrgModel *model);
 size_t prg_model_dense_bytes(const PrgModel *model);
 
 /* Decode-layout copies (prg_q4_repack_t16) of every GEMV weight whose shape
- * has one, read by the matrix-core GEMVs of the token loop (the large
- * launches: MLP, GDN in_proj, attention q/k/v, lm_head; the 4096 x 4096
- * projections keep the MLX-layout kernel). Written by model creation and
- * loading, and again before the next run once prg_model_tensor has handed
- * out a pointer; call this after writing weights through a pointer kept from
- * earlier. PEREGRINE_T16=0 at creation turns the copies (and the matrix-core
- * GEMVs) off. No counterpart in the reference: its Metal kernels read the
- * MLX layout. */
+ * has one (rows % 16 == 0, in_dim % 1024 == 0), read by the matrix-core
+ * GEMVs of the token loop, the two-token verify and the drafter. Written by
+ * model creation and loading, and again before the next run once
+ * prg_model_tensor has handed out a pointer; call this after writing weights
+ * through a pointer kept from earlier. PEREGRINE_T16=0 at creation turns the
+ * copies (and the matrix-core GEMVs) off. No counterpart in the reference:
+ * its Metal kernels read the MLX layout. */
 int prg_model_prepare_decode(PrgModel *model);
 /* Bytes of the decode-layout copies (0 when off). */
 size_t prg_model_decode_layout_bytes(const PrgModel *model);

@@ -275,18 +275,18 @@ uint32_t total_rows(const GemvParams& p) {
 }
 }  // namespace
 
-// Large launches whose segments all carry decode-layout copies run on the
+// Launches whose segments all carry decode-layout copies run on the
 // matrix-core GEMV; the rest (and every launch of a model without copies) on
 // q4_gemv_kernel.
 int run_gemv(hipStream_t s, GemvParams& p, int epi, int norm, const char* name) {
   int M = p.x[1] ? 2 : 1;
-  if (t16_usable(p, M, epi, norm, true)) return launch_q4_gemv_t16(s, p, M, epi, norm, name);
+  if (t16_usable(p, M, epi, norm)) return launch_q4_gemv_t16(s, p, M, epi, norm, name);
   const int rows = gemv_rows_per_wave(total_rows(p), p.K, epi, M);
   return launch_q4_gemv(s, p, M, rows, epi, norm, name);
 }
 
 int run_argmax_gemv(hipStream_t s, GemvParams& p, int M, int norm, const char* name) {
-  if (t16_usable(p, M, kEpiArgmax, norm, true)) return launch_q4_gemv_t16(s, p, M, kEpiArgmax, norm, name);
+  if (t16_usable(p, M, kEpiArgmax, norm)) return launch_q4_gemv_t16(s, p, M, kEpiArgmax, norm, name);
   return launch_q4_gemv(s, p, M, 8, kEpiArgmax, norm, name);
 }
 

@@ -1,5 +1,7 @@
 // Q4 GEMV on the matrix cores over the decode layout (see q4_gemv_t16.hpp):
 // the repack kernel, the GEMV kernel template and its launcher.
+#include <stdlib.h>
+
 #include <algorithm>
 #include <type_traits>
 
@@ -61,13 +63,13 @@ struct T16Win {
   uint16_t bi[NMAT];
 };
 
-// Window u (0..3) of wave w's K range of launch tile t.
-template <int NMAT, int S>
+// Window u (0..NW-1) of wave w's K range of launch tile t.
+template <int NMAT, int S, int NW>
 __device__ inline void t16_load(const GemvParams& p, uint32_t t, int w, int u, int lane, T16Win<NMAT>& b) {
-  constexpr uint32_t kWins = 4 * S;  // windows per row
+  constexpr uint32_t kWins = NW * S;  // windows per row
   const T16Loc loc = t16_locate(p, t);
   const GemvSeg& sg = p.seg[loc.seg];
-  const size_t win = static_cast<size_t>(loc.tile) * kWins + 4 * w + u;
+  const size_t win = static_cast<size_t>(loc.tile) * kWins + NW * w + u;
 #pragma unroll
   for (int mat = 0; mat < NMAT; ++mat) {
     const u32x4* wp = reinterpret_cast<const u32x4*>(sg.tw[mat]) + win * (kT16Steps * kWave) + lane;
@@ -90,9 +92,11 @@ __device__ inline float sum_c4(float v) {
   return a + b;
 }
 
-template <int M, int NMAT, int S, int EPI, int NORM>
+// NW windows (2 or 4) per wave: K = 256 NW S.
+template <int M, int NMAT, int S, int NW, int EPI, int NORM>
 __global__ __launch_bounds__(S * kWave) void q4_gemv_t16_kernel(const GemvParams p) {
-  constexpr uint32_t K = kT16WaveK * S;
+  static_assert(NW == 2 || NW == 4, "two or four windows per wave");
+  constexpr uint32_t K = kT16WinK * NW * S;
   constexpr uint32_t kThreads = S * kWave;
   constexpr uint32_t kUnits = K / 8;  // uint4 units of one activation row
   constexpr int XU = static_cast<int>(kUnits / kThreads);
@@ -113,19 +117,33 @@ __global__ __launch_bounds__(S * kWave) void q4_gemv_t16_kernel(const GemvParams
   uint32_t tile = blockIdx.x;
 
   // 1) activations (and norm weights) first so they return first, then this
-  // wave's first two windows of its first tile.
+  // wave's first window of its first tile; the second is issued once x is
+  // staged. Every wave's x loads queue behind the weight loads its CU has
+  // already issued, and the staging gates the first matrix instructions, so
+  // fewer bytes ahead of them (one window per wave instead of two) bring x in
+  // sooner.
   uint4 xv[M][XU];
-  uint4 nw[NORM == kNormRms ? XU : 1];
+  uint4 nw[NORM != kNormNone ? XU : 1];
+  float4 zv[NORM == kNormGated ? M : 1][NORM == kNormGated ? XU : 1][2];
 #pragma unroll
   for (int it = 0; it < XU; ++it) {
     const uint32_t gi = it * kThreads + tid;
 #pragma unroll
     for (int m = 0; m < M; ++m) xv[m][it] = reinterpret_cast<const uint4*>(p.x[m])[gi];
     if constexpr (NORM == kNormRms) nw[it] = reinterpret_cast<const uint4*>(p.norm_w)[gi];
+    if constexpr (NORM == kNormGated) {
+      // 8 values of head gi / 16: entries 8 (gi % 16) .. +8 of the [128] weight
+      nw[it] = reinterpret_cast<const uint4*>(p.norm_w)[gi % (kGdnDv / 8)];
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        const float4* zp = reinterpret_cast<const float4*>(p.gz[m]) + 2 * gi;
+        zv[m][it][0] = zp[0];
+        zv[m][it][1] = zp[1];
+      }
+    }
   }
   T16Win<NMAT> b0, b1;
-  t16_load<NMAT, S>(p, tile, w, 0, lane, b0);
-  t16_load<NMAT, S>(p, tile, w, 1, lane, b1);
+  t16_load<NMAT, S, NW>(p, tile, w, 0, lane, b0);
 
   // 2) normalise, stage x as the permuted pairs of the nibble unpack, and the
   // per-group sums of the staged values.
@@ -171,10 +189,24 @@ __global__ __launch_bounds__(S * kWave) void q4_gemv_t16_kernel(const GemvParams
     for (int it = 0; it < XU; ++it) {
       const uint32_t gi = it * kThreads + tid;
       uint4 v;
-      if constexpr (NORM == kNormRms)
+      if constexpr (NORM == kNormRms) {
         v = permute_pairs(rms_apply(xv[m][it], nw[it], scale[m]));
-      else
+      } else if constexpr (NORM == kNormGated) {
+        // The 16 lanes of a DPP row hold the 128 values of one head: the
+        // per-head RMSNorm of q4_gemv_kernel's gated prologue, same order.
+        float ss = 0.0f;
+        const uint32_t d[4] = {xv[m][it].x, xv[m][it].y, xv[m][it].z, xv[m][it].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float a = bf_lo(d[i]), b = bf_hi(d[i]);
+          ss = __fmaf_rn(a, a, ss);
+          ss = __fmaf_rn(b, b, ss);
+        }
+        const float hscale = rsqrtf(__fadd_rn(__fmul_rn(row16_sum(ss), 1.0f / kGdnDv), p.eps));
+        v = permute_pairs(gated_rms_apply(xv[m][it], nw[it], zv[m][it][0], zv[m][it][1], hscale));
+      } else {
         v = permute_pairs(xv[m][it]);
+      }
       reinterpret_cast<uint4*>(xs + m * (K / 2))[gi] = v;
       if (p.x_image[m] != nullptr && blockIdx.x == 0) reinterpret_cast<uint4*>(p.x_image[m])[gi] = v;
       float sm = dot2_bf16(v.x, kOnes, 0.0f);
@@ -194,6 +226,7 @@ __global__ __launch_bounds__(S * kWave) void q4_gemv_t16_kernel(const GemvParams
   __builtin_amdgcn_sched_barrier(0);
   __syncthreads();
   __builtin_amdgcn_sched_barrier(0);
+  t16_load<NMAT, S, NW>(p, tile, w, 1, lane, b1);
 
   // 3) A operand: lane (i = lane & 15, c) holds row i = 4 h + m, k-chunk c.
   // It carries x_m only when chunk c of step st lies in group slot h of the
@@ -204,15 +237,15 @@ __global__ __launch_bounds__(S * kWave) void q4_gemv_t16_kernel(const GemvParams
 #pragma unroll
   for (int st = 0; st < 2; ++st) {
     const bool data = ma < M && ha == 2 * st + (c >> 1);
-    aoff[st] = data ? static_cast<uint32_t>(ma) * (K / 2) + 512u * w + 64u * st + 16u * c : kZero;
+    aoff[st] = data ? static_cast<uint32_t>(ma) * (K / 2) + 128u * NW * w + 64u * st + 16u * c : kZero;
     ainc[st] = data ? 128u : 0u;
   }
   // Group sums of the lane's group slot c in each of the wave's windows.
-  float xsum[4][M];
+  float xsum[NW][M];
 #pragma unroll
-  for (int u = 0; u < 4; ++u)
+  for (int u = 0; u < NW; ++u)
 #pragma unroll
-    for (int m = 0; m < M; ++m) xsum[u][m] = xg[m * kGroups + 16 * w + 4 * u + c];
+    for (int m = 0; m < M; ++m) xsum[u][m] = xg[m * kGroups + 4 * NW * w + 4 * u + c];
 
   auto window = [&](const T16Win<NMAT>& b, int u, float (&acc)[NMAT][M]) {
     t16_f32x4 C[NMAT];
@@ -254,8 +287,8 @@ __global__ __launch_bounds__(S * kWave) void q4_gemv_t16_kernel(const GemvParams
   }
   int buf = 0;
 
-  // One tile: four windows, the next tile's first two windows prefetched
-  // (PF) while the last two are computed, then the row sums and epilogue.
+  // One tile: NW windows, the next tile's first two windows prefetched (PF)
+  // while the last two are computed, then the row sums and epilogue.
   auto tile_body = [&](uint32_t t, uint32_t nt, auto pf) {
     constexpr bool PF = decltype(pf)::value;
     float acc[NMAT][M];
@@ -263,14 +296,21 @@ __global__ __launch_bounds__(S * kWave) void q4_gemv_t16_kernel(const GemvParams
     for (int mat = 0; mat < NMAT; ++mat)
 #pragma unroll
       for (int m = 0; m < M; ++m) acc[mat][m] = 0.0f;
-    window(b0, 0, acc);
-    t16_load<NMAT, S>(p, t, w, 2, lane, b0);
-    window(b1, 1, acc);
-    t16_load<NMAT, S>(p, t, w, 3, lane, b1);
-    window(b0, 2, acc);
-    if constexpr (PF) t16_load<NMAT, S>(p, nt, w, 0, lane, b0);
-    window(b1, 3, acc);
-    if constexpr (PF) t16_load<NMAT, S>(p, nt, w, 1, lane, b1);
+    if constexpr (NW == 4) {
+      window(b0, 0, acc);
+      t16_load<NMAT, S, NW>(p, t, w, 2, lane, b0);
+      window(b1, 1, acc);
+      t16_load<NMAT, S, NW>(p, t, w, 3, lane, b1);
+      window(b0, 2, acc);
+      if constexpr (PF) t16_load<NMAT, S, NW>(p, nt, w, 0, lane, b0);
+      window(b1, 3, acc);
+      if constexpr (PF) t16_load<NMAT, S, NW>(p, nt, w, 1, lane, b1);
+    } else {
+      window(b0, 0, acc);
+      if constexpr (PF) t16_load<NMAT, S, NW>(p, nt, w, 0, lane, b0);
+      window(b1, 1, acc);
+      if constexpr (PF) t16_load<NMAT, S, NW>(p, nt, w, 1, lane, b1);
+    }
 #pragma unroll
     for (int mat = 0; mat < NMAT; ++mat)
 #pragma unroll
@@ -351,27 +391,33 @@ __global__ __launch_bounds__(S * kWave) void q4_gemv_t16_kernel(const GemvParams
   }
 }
 
-// Kernel variants: (NMAT, S, EPI, NORM) x M in {1, 2}.
-#define PRG_T16_VARIANTS(X)                 \
-  X(2, 4, kEpiSiluGate, kNormRms)           \
-  X(1, 4, kEpiPlain, kNormRms)              \
-  X(1, 4, kEpiPlain, kNormNone)             \
-  X(1, 8, kEpiPlain, kNormNone)             \
-  X(1, 12, kEpiPlain, kNormNone)            \
-  X(1, 12, kEpiResidual, kNormNone)         \
-  X(1, 4, kEpiArgmax, kNormRms)             \
-  X(1, 4, kEpiArgmax, kNormNone)
+// Kernel variants: (NMAT, S, NW, EPI, NORM) x M in {1, 2}; K = 256 NW S.
+#define PRG_T16_VARIANTS(X)                    \
+  X(2, 4, 4, kEpiSiluGate, kNormRms)           \
+  X(1, 8, 2, kEpiResidual, kNormGated)         \
+  X(1, 8, 2, kEpiResidual, kNormNone)          \
+  X(1, 4, 4, kEpiResidual, kNormGated)         \
+  X(1, 4, 4, kEpiResidual, kNormNone)          \
+  X(1, 4, 4, kEpiPlain, kNormRms)              \
+  X(1, 4, 4, kEpiPlain, kNormNone)             \
+  X(1, 8, 4, kEpiPlain, kNormNone)             \
+  X(1, 12, 4, kEpiPlain, kNormNone)            \
+  X(1, 12, 4, kEpiResidual, kNormNone)         \
+  X(1, 4, 4, kEpiArgmax, kNormRms)             \
+  X(1, 4, 4, kEpiArgmax, kNormNone)
 
 // Launches (or, with grid == 0, only looks up) the variant; -1 if none.
-int t16_dispatch(hipStream_t s, const GemvParams& p, int M, int nmat, uint32_t S, int epi, int norm, uint32_t grid) {
-#define PRG_T16_CASE(NM, SS, EP, NO)                                                                          \
-  if (nmat == NM && S == SS && epi == EP && norm == NO) {                                                   \
-    if (grid == 0) return 0;                                                                                \
-    if (M == 1)                                                                                             \
-      hipLaunchKernelGGL((q4_gemv_t16_kernel<1, NM, SS, EP, NO>), dim3(grid), dim3(SS * kWave), 0, s, p);   \
-    else                                                                                                    \
-      hipLaunchKernelGGL((q4_gemv_t16_kernel<2, NM, SS, EP, NO>), dim3(grid), dim3(SS * kWave), 0, s, p);   \
-    return 0;                                                                                               \
+// (S, NW) per launch: the variant with K = 256 NW S, preferring NW = 4.
+int t16_dispatch(hipStream_t s, const GemvParams& p, int M, int nmat, int epi, int norm, uint32_t grid, bool prefer_nw2) {
+  const uint32_t K = p.K;
+#define PRG_T16_CASE(NM, SS, NWW, EP, NO)                                                                          \
+  if (nmat == NM && K == kT16WinK * NWW * SS && epi == EP && norm == NO && (NWW == 2) == prefer_nw2) {          \
+    if (grid == 0) return 0;                                                                                     \
+    if (M == 1)                                                                                                  \
+      hipLaunchKernelGGL((q4_gemv_t16_kernel<1, NM, SS, NWW, EP, NO>), dim3(grid), dim3(SS * kWave), 0, s, p);   \
+    else                                                                                                         \
+      hipLaunchKernelGGL((q4_gemv_t16_kernel<2, NM, SS, NWW, EP, NO>), dim3(grid), dim3(SS * kWave), 0, s, p);   \
+    return 0;                                                                                                    \
   }
   PRG_T16_VARIANTS(PRG_T16_CASE)
 #undef PRG_T16_CASE
@@ -395,28 +441,51 @@ int launch_t16_repack(hipStream_t s, const uint32_t* w, const uint16_t* scales, 
   return PRG_OK;
 }
 
-bool t16_usable(const GemvParams& p, int M, int epi, int norm, bool size_gate) {
+// Launches of at most this many tiles take two windows per wave (8 waves per
+// 4096-deep tile): a 4096-row matrix has 256 tiles, one block per CU.
+constexpr uint32_t kT16FewTiles = 384;
+
+static uint32_t t16_tiles(const GemvParams& p) {
+  uint32_t tiles = 0;
+  for (uint32_t i = 0; i < p.nseg; ++i) tiles += p.seg[i].rows / kT16Rows;
+  return tiles;
+}
+
+// The variant a launch takes: NW = 2 for few tiles when one exists, else NW = 4.
+// Returns 0 with *nw2 set, or -1 when there is none.
+static int t16_pick(const GemvParams& p, int M, int nmat, int epi, int norm, bool* nw2) {
+  const bool few = t16_tiles(p) <= kT16FewTiles;
+  for (bool pref : {few, !few}) {
+    if (t16_dispatch(nullptr, p, M, nmat, epi, norm, 0, pref) == 0) {
+      *nw2 = pref;
+      return 0;
+    }
+  }
+  return -1;
+}
+
+bool t16_usable(const GemvParams& p, int M, int epi, int norm) {
   if (M < 1 || M > 2 || p.nseg < 1 || p.nseg > kGemvMaxSegs) return false;
-  if (p.K % kT16WaveK != 0) return false;
+  if (p.K % kT16WaveK != 0 && p.K % (2 * kT16WinK) != 0) return false;
   if (epi == kEpiArgmax && (p.nseg != 1 || p.argmax_waves == nullptr)) return false;
   const int nmat = epi == kEpiSiluGate ? 2 : 1;
-  uint64_t rows = 0;
   for (uint32_t i = 0; i < p.nseg; ++i) {
     const GemvSeg& sg = p.seg[i];
     if (sg.rows == 0 || sg.rows % kT16Rows != 0) return false;
     for (int mat = 0; mat < nmat; ++mat)
       if (!sg.tw[mat] || !sg.ts[mat] || !sg.tb[mat]) return false;
-    rows += sg.rows;
   }
-  if (size_gate && rows * p.K <= (1ull << 25)) return false;
-  return t16_dispatch(nullptr, p, M, nmat, p.K / kT16WaveK, epi, norm, 0) == 0;
+  bool nw2 = false;
+  return t16_pick(p, M, nmat, epi, norm, &nw2) == 0;
 }
 
 int launch_q4_gemv_t16(hipStream_t s, GemvParams& p, int M, int epi, int norm, const char* name) {
-  if (!t16_usable(p, M, epi, norm, false))
+  if (!t16_usable(p, M, epi, norm))
     return set_error(PRG_ERR_INVALID_ARG, "%s: no T16 GEMV for M=%d epilogue %d norm %d K=%u (%u segments)", name, M,
                      epi, norm, p.K, p.nseg);
   if (norm == kNormRms && p.norm_w == nullptr) return set_error(PRG_ERR_INVALID_ARG, "%s: RMSNorm weight", name);
+  if (norm == kNormGated && (p.norm_w == nullptr || p.gz[0] == nullptr || (M == 2 && p.gz[1] == nullptr)))
+    return set_error(PRG_ERR_INVALID_ARG, "%s: gated norm needs norm_w and gz", name);
   uint32_t tiles = 0;
   for (uint32_t i = 0; i < p.nseg; ++i) {
     p.seg[i].block_begin = tiles;
@@ -426,7 +495,8 @@ int launch_q4_gemv_t16(hipStream_t s, GemvParams& p, int M, int epi, int norm, c
   p.tail_lanes = 64;
   const uint32_t grid = epi == kEpiArgmax ? std::min<uint32_t>(tiles, kArgmaxMaxWaves) : tiles;
   const int nmat = epi == kEpiSiluGate ? 2 : 1;
-  if (t16_dispatch(s, p, M, nmat, p.K / kT16WaveK, epi, norm, grid) != 0)
+  bool nw2 = false;
+  if (t16_pick(p, M, nmat, epi, norm, &nw2) != 0 || t16_dispatch(s, p, M, nmat, epi, norm, grid, nw2) != 0)
     return set_error(PRG_ERR_INVALID_ARG, "%s: no T16 kernel", name);
   PRG_CHECK_LAUNCH(name);
   return PRG_OK;
@@ -481,7 +551,7 @@ int prg_q4_gemv_t16_bf16(void* stream, const uint16_t* x, const uint32_t* tw, co
       p.x[m] = x + static_cast<size_t>(t + m) * in_dim;
       p.seg[0].out[m] = y + static_cast<size_t>(t + m) * out_dim;
     }
-    if (!prg::t16_usable(p, M, prg::kEpiPlain, prg::kNormNone, false))
+    if (!prg::t16_usable(p, M, prg::kEpiPlain, prg::kNormNone))
       return prg::set_error(PRG_ERR_INVALID_ARG, "%s: in_dim %u (4096, 8192 or 12288)", name, in_dim);
     if (int rc = prg::launch_q4_gemv_t16(s, p, M, prg::kEpiPlain, prg::kNormNone, name)) return rc;
   }
@@ -503,7 +573,7 @@ int prg_q4_gemv_t16_silu_gate_norm_bf16(void* stream, const uint16_t* x, const u
   p.x[0] = x;
   p.norm_w = norm_weight;
   p.eps = eps;
-  if (!prg::t16_usable(p, 1, prg::kEpiSiluGate, prg::kNormRms, false))
+  if (!prg::t16_usable(p, 1, prg::kEpiSiluGate, prg::kNormRms))
     return prg::set_error(PRG_ERR_INVALID_ARG, "%s: in_dim %u (4096)", name, in_dim);
   return prg::launch_q4_gemv_t16(prg::as_stream(stream), p, 1, prg::kEpiSiluGate, prg::kNormRms, name);
 }
@@ -531,7 +601,7 @@ int prg_q4_gemv_t16_argmax_bf16(void* stream, const uint16_t* x, const uint32_t*
     p.seg[0].pidx[m] = rows[m];
   }
   p.argmax_waves = count;
-  if (!prg::t16_usable(p, M, prg::kEpiArgmax, prg::kNormNone, false))
+  if (!prg::t16_usable(p, M, prg::kEpiArgmax, prg::kNormNone))
     return prg::set_error(PRG_ERR_INVALID_ARG, "%s: in_dim %u (4096)", name, in_dim);
   hipStream_t s = prg::as_stream(stream);
   if (int rc = prg::launch_q4_gemv_t16(s, p, M, prg::kEpiArgmax, prg::kNormNone, name)) return rc;

@@ -12,8 +12,9 @@
 // of contiguous memory. Scales and biases follow the same order: entry
 // 64 (tile * windows + win) + l is group 4 win + c of row 16 tile + j.
 //
-// Kernel: a tile's K range is split over the S waves of a block (S = K / 1024,
-// four windows per wave). Each unpacked word (v_perm_b32 under the byte 0x43:
+// Kernel: a tile's K range is split over the S waves of a block, four
+// windows per wave (S = K / 1024), or two (S = K / 512) when the launch has
+// few tiles, so a 4096-row matrix still runs 8 waves per tile. Each unpacked word (v_perm_b32 under the byte 0x43:
 // bf16 128 + q) is the B operand of a v_mfma_f32_16x16x32_bf16 whose 16
 // columns are the tile's rows; the A operand is x from LDS with row i = 4 h + m
 // holding activation row m only for the k of group slot h of the window
@@ -43,10 +44,8 @@ int launch_t16_repack(hipStream_t s, const uint32_t* w, const uint16_t* scales, 
                       uint32_t* tw, uint16_t* ts, uint16_t* tb, uint32_t N, uint32_t K);
 
 // True when every segment of p carries decode-layout copies (GemvSeg::tw..)
-// and a T16 kernel exists for (M, epilogue, norm, K). With size_gate the
-// launch must also be large (rows x K > 2^25): smaller matrices stream
-// faster through q4_gemv_kernel's row-per-wave form.
-bool t16_usable(const GemvParams& p, int M, int epi, int norm, bool size_gate);
+// and a T16 kernel exists for (M, epilogue, norm, K).
+bool t16_usable(const GemvParams& p, int M, int epi, int norm);
 
 // Launch the T16 GEMV (segment tile ranges are filled in here). Argmax
 // launches write one entry per block (grid <= kArgmaxMaxWaves) to
