@@ -92,15 +92,18 @@ __device__ inline float sum_c4(float v) {
   return a + b;
 }
 
-// NW windows (2 or 4) per wave: K = 256 NW S.
+// NW windows (1 to 4) per wave: K = 256 NW S.
 template <int M, int NMAT, int S, int NW, int EPI, int NORM>
 __global__ __launch_bounds__(S * kWave) void q4_gemv_t16_kernel(const GemvParams p) {
-  static_assert(NW == 2 || NW == 4, "two or four windows per wave");
+  static_assert(NW >= 1 && NW <= 4, "one to four windows per wave");
   constexpr uint32_t K = kT16WinK * NW * S;
   constexpr uint32_t kThreads = S * kWave;
   constexpr uint32_t kUnits = K / 8;  // uint4 units of one activation row
-  constexpr int XU = static_cast<int>(kUnits / kThreads);
-  static_assert(kUnits % kThreads == 0, "whole units per thread");
+  // units per thread: when the row does not fill the last pass, the threads
+  // past it skip that pass (a wave-uniform test: kUnits % 64 == 0)
+  constexpr int XU = static_cast<int>((kUnits + kThreads - 1) / kThreads);
+  static_assert(kUnits % kWave == 0, "whole waves per pass");
+  auto staged_unit = [&](int it) { return kUnits % kThreads == 0 || it * kThreads + threadIdx.x < kUnits; };
   constexpr uint32_t kGroups = K / 64;
   constexpr uint32_t kZero = M * K / 2;  // dword offset of the 64-byte zero block
   // x as permuted bf16 pairs (M rows), then 16 zero dwords
@@ -127,7 +130,8 @@ __global__ __launch_bounds__(S * kWave) void q4_gemv_t16_kernel(const GemvParams
   float4 zv[NORM == kNormGated ? M : 1][NORM == kNormGated ? XU : 1][2];
 #pragma unroll
   for (int it = 0; it < XU; ++it) {
-    const uint32_t gi = it * kThreads + tid;
+    // threads past the row load unit 0 and never use it
+    const uint32_t gi = staged_unit(it) ? it * kThreads + tid : 0u;
 #pragma unroll
     for (int m = 0; m < M; ++m) xv[m][it] = reinterpret_cast<const uint4*>(p.x[m])[gi];
     if constexpr (NORM == kNormRms) nw[it] = reinterpret_cast<const uint4*>(p.norm_w)[gi];
@@ -157,6 +161,7 @@ __global__ __launch_bounds__(S * kWave) void q4_gemv_t16_kernel(const GemvParams
 #pragma unroll
       for (int it = 0; it < XU; ++it) {
         const uint32_t d[4] = {xv[m][it].x, xv[m][it].y, xv[m][it].z, xv[m][it].w};
+        if (!staged_unit(it)) continue;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const float a = bf_lo(d[i]), b = bf_hi(d[i]);
@@ -187,6 +192,7 @@ __global__ __launch_bounds__(S * kWave) void q4_gemv_t16_kernel(const GemvParams
   for (int m = 0; m < M; ++m) {
 #pragma unroll
     for (int it = 0; it < XU; ++it) {
+      if (!staged_unit(it)) continue;
       const uint32_t gi = it * kThreads + tid;
       uint4 v;
       if constexpr (NORM == kNormRms) {
@@ -226,7 +232,7 @@ __global__ __launch_bounds__(S * kWave) void q4_gemv_t16_kernel(const GemvParams
   __builtin_amdgcn_sched_barrier(0);
   __syncthreads();
   __builtin_amdgcn_sched_barrier(0);
-  t16_load<NMAT, S, NW>(p, tile, w, 1, lane, b1);
+  if constexpr (NW >= 2) t16_load<NMAT, S, NW>(p, tile, w, 1, lane, b1);
 
   // 3) A operand: lane (i = lane & 15, c) holds row i = 4 h + m, k-chunk c.
   // It carries x_m only when chunk c of step st lies in group slot h of the
@@ -305,11 +311,21 @@ __global__ __launch_bounds__(S * kWave) void q4_gemv_t16_kernel(const GemvParams
       if constexpr (PF) t16_load<NMAT, S, NW>(p, nt, w, 0, lane, b0);
       window(b1, 3, acc);
       if constexpr (PF) t16_load<NMAT, S, NW>(p, nt, w, 1, lane, b1);
-    } else {
+    } else if constexpr (NW == 3) {
+      window(b0, 0, acc);
+      t16_load<NMAT, S, NW>(p, t, w, 2, lane, b0);
+      window(b1, 1, acc);
+      if constexpr (PF) t16_load<NMAT, S, NW>(p, nt, w, 1, lane, b1);
+      window(b0, 2, acc);
+      if constexpr (PF) t16_load<NMAT, S, NW>(p, nt, w, 0, lane, b0);
+    } else if constexpr (NW == 2) {
       window(b0, 0, acc);
       if constexpr (PF) t16_load<NMAT, S, NW>(p, nt, w, 0, lane, b0);
       window(b1, 1, acc);
       if constexpr (PF) t16_load<NMAT, S, NW>(p, nt, w, 1, lane, b1);
+    } else {
+      window(b0, 0, acc);
+      if constexpr (PF) t16_load<NMAT, S, NW>(p, nt, w, 0, lane, b0);
     }
 #pragma unroll
     for (int mat = 0; mat < NMAT; ++mat)
@@ -394,6 +410,8 @@ __global__ __launch_bounds__(S * kWave) void q4_gemv_t16_kernel(const GemvParams
 // Kernel variants: (NMAT, S, NW, EPI, NORM) x M in {1, 2}; K = 256 NW S.
 #define PRG_T16_VARIANTS(X)                    \
   X(2, 4, 4, kEpiSiluGate, kNormRms)           \
+  X(1, 16, 1, kEpiResidual, kNormGated)        \
+  X(1, 16, 1, kEpiResidual, kNormNone)         \
   X(1, 8, 2, kEpiResidual, kNormGated)         \
   X(1, 8, 2, kEpiResidual, kNormNone)          \
   X(1, 4, 4, kEpiResidual, kNormGated)         \
@@ -402,16 +420,17 @@ __global__ __launch_bounds__(S * kWave) void q4_gemv_t16_kernel(const GemvParams
   X(1, 4, 4, kEpiPlain, kNormNone)             \
   X(1, 8, 4, kEpiPlain, kNormNone)             \
   X(1, 12, 4, kEpiPlain, kNormNone)            \
+  X(1, 16, 3, kEpiResidual, kNormNone)         \
   X(1, 12, 4, kEpiResidual, kNormNone)         \
   X(1, 4, 4, kEpiArgmax, kNormRms)             \
   X(1, 4, 4, kEpiArgmax, kNormNone)
 
-// Launches (or, with grid == 0, only looks up) the variant; -1 if none.
-// (S, NW) per launch: the variant with K = 256 NW S, preferring NW = 4.
-int t16_dispatch(hipStream_t s, const GemvParams& p, int M, int nmat, int epi, int norm, uint32_t grid, bool prefer_nw2) {
+// Launches (or, with grid == 0, only looks up) the variant with NW windows
+// per wave for the launch's K (S = K / (256 NW)); -1 if none.
+int t16_dispatch(hipStream_t s, const GemvParams& p, int M, int nmat, int epi, int norm, uint32_t grid, int nw) {
   const uint32_t K = p.K;
 #define PRG_T16_CASE(NM, SS, NWW, EP, NO)                                                                          \
-  if (nmat == NM && K == kT16WinK * NWW * SS && epi == EP && norm == NO && (NWW == 2) == prefer_nw2) {          \
+  if (nmat == NM && K == kT16WinK * NWW * SS && epi == EP && norm == NO && NWW == nw) {                        \
     if (grid == 0) return 0;                                                                                     \
     if (M == 1)                                                                                                  \
       hipLaunchKernelGGL((q4_gemv_t16_kernel<1, NM, SS, NWW, EP, NO>), dim3(grid), dim3(SS * kWave), 0, s, p);   \
@@ -441,9 +460,22 @@ int launch_t16_repack(hipStream_t s, const uint32_t* w, const uint16_t* scales, 
   return PRG_OK;
 }
 
-// Launches of at most this many tiles take two windows per wave (8 waves per
-// 4096-deep tile): a 4096-row matrix has 256 tiles, one block per CU.
-constexpr uint32_t kT16FewTiles = 384;
+// Launches of at most this many tiles (a 4096-row matrix has 256) take the
+// fewest windows per wave that have a kernel, i.e. the most waves per tile;
+// larger launches take four. PEREGRINE_T16_FEW overrides the threshold and
+// PEREGRINE_T16_NWSKIP (bit 1 << nw) excludes window counts (tuning).
+static uint32_t t16_env(const char* name, uint32_t dflt) {
+  const char* e = getenv(name);
+  return e ? static_cast<uint32_t>(atoi(e)) : dflt;
+}
+static uint32_t t16_few_tiles() {
+  static const uint32_t v = t16_env("PEREGRINE_T16_FEW", 384u);
+  return v;
+}
+static uint32_t t16_nw_skip() {
+  static const uint32_t v = t16_env("PEREGRINE_T16_NWSKIP", 0u);
+  return v;
+}
 
 static uint32_t t16_tiles(const GemvParams& p) {
   uint32_t tiles = 0;
@@ -451,13 +483,15 @@ static uint32_t t16_tiles(const GemvParams& p) {
   return tiles;
 }
 
-// The variant a launch takes: NW = 2 for few tiles when one exists, else NW = 4.
-// Returns 0 with *nw2 set, or -1 when there is none.
-static int t16_pick(const GemvParams& p, int M, int nmat, int epi, int norm, bool* nw2) {
-  const bool few = t16_tiles(p) <= kT16FewTiles;
-  for (bool pref : {few, !few}) {
-    if (t16_dispatch(nullptr, p, M, nmat, epi, norm, 0, pref) == 0) {
-      *nw2 = pref;
+// The variant a launch takes (*nw windows per wave); -1 when there is none.
+// Argmax launches loop over tiles and take four windows.
+static int t16_pick(const GemvParams& p, int M, int nmat, int epi, int norm, int* nw) {
+  const bool few = epi != kEpiArgmax && t16_tiles(p) <= t16_few_tiles();
+  static const int kFew[4] = {1, 2, 3, 4}, kMany[4] = {4, 3, 2, 1};
+  for (int c : few ? kFew : kMany) {
+    if (c != 4 && (t16_nw_skip() >> c & 1u)) continue;
+    if (t16_dispatch(nullptr, p, M, nmat, epi, norm, 0, c) == 0) {
+      *nw = c;
       return 0;
     }
   }
@@ -475,8 +509,8 @@ bool t16_usable(const GemvParams& p, int M, int epi, int norm) {
     for (int mat = 0; mat < nmat; ++mat)
       if (!sg.tw[mat] || !sg.ts[mat] || !sg.tb[mat]) return false;
   }
-  bool nw2 = false;
-  return t16_pick(p, M, nmat, epi, norm, &nw2) == 0;
+  int nw = 0;
+  return t16_pick(p, M, nmat, epi, norm, &nw) == 0;
 }
 
 int launch_q4_gemv_t16(hipStream_t s, GemvParams& p, int M, int epi, int norm, const char* name) {
@@ -495,8 +529,8 @@ int launch_q4_gemv_t16(hipStream_t s, GemvParams& p, int M, int epi, int norm, c
   p.tail_lanes = 64;
   const uint32_t grid = epi == kEpiArgmax ? std::min<uint32_t>(tiles, kArgmaxMaxWaves) : tiles;
   const int nmat = epi == kEpiSiluGate ? 2 : 1;
-  bool nw2 = false;
-  if (t16_pick(p, M, nmat, epi, norm, &nw2) != 0 || t16_dispatch(s, p, M, nmat, epi, norm, grid, nw2) != 0)
+  int nw = 0;
+  if (t16_pick(p, M, nmat, epi, norm, &nw) != 0 || t16_dispatch(s, p, M, nmat, epi, norm, grid, nw) != 0)
     return set_error(PRG_ERR_INVALID_ARG, "%s: no T16 kernel", name);
   PRG_CHECK_LAUNCH(name);
   return PRG_OK;
