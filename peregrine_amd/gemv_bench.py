@@ -1,4 +1,5 @@
-"""Q4 GEMV sweep on one GPU with MALL-defeating rotation.
+"""Q4 GEMV sweep on one GPU with MALL-defeating rotation,
+on the decode layout the model runs and on the MLX layout beside it.
 
 Each shape is timed over a ring of distinct weight copies totalling >= 512 MiB
 (MI355X's Infinity Cache is 256 MiB), so every launch streams its weights from
@@ -14,7 +15,7 @@ import numpy as np
 
 from .device import DeviceArray, Stream, synchronize
 from .op_bench import time_graph
-from .ops import Q4Linear, argmax_pairs, gate_up_silu
+from .ops import DecodeLayoutQ4, Q4Linear, argmax_pairs, gate_up_silu, t16_argmax_workspace_bytes
 from .synth import random_bf16, random_q4
 
 HBM_PEAK_GBS = 8000.0
@@ -46,14 +47,21 @@ def time_launches(fn, ring, reps: int = 10) -> float:
 
 
 def sweep(shapes=None, Ms=(1, 2), seed: int = 0, reps: int = 10) -> list[dict]:
+    """Each shape and M on the decode layout (DecodeLayoutQ4, the matrix-core
+    kernel the model runs) and, beside it, on the MLX layout (Q4Linear). The
+    lm_head rows time the decode-layout GEMV + final argmax to the token (two
+    launches) and the MLX-layout argmax partials alone."""
     rng = np.random.default_rng(seed)
     shapes = shapes or [(12288, 4096), (4096, 12288), (4096, 4096), (248320, 4096)]
     rows = []
     for N, K in shapes:
         lm_head = N == 248320
         ring = _ring(rng, N, K, zero_mean=lm_head)
+        tring = [DecodeLayoutQ4(lin) for lin in ring]
+        synchronize()
         for M in Ms:
             x = [DeviceArray.from_numpy(random_bf16(rng, (1, K))) for _ in range(M)]
+            xx = DeviceArray.from_numpy(random_bf16(rng, (M, K)))
             if lm_head:
                 P = N // 8
                 pv = [DeviceArray((P,), np.float32) for _ in range(M)]
@@ -63,22 +71,30 @@ def sweep(shapes=None, Ms=(1, 2), seed: int = 0, reps: int = 10) -> list[dict]:
                 else:
                     fn = lambda lin, s: lin.encode_bf16_argmax_partial2(x[0], x[1], pv[0], pi[0], pv[1], pi[1],
                                                                         stream=s)
-                out_bytes = M * P * 8
+                tok = DeviceArray((2,), np.uint32)
+                ws = DeviceArray((t16_argmax_workspace_bytes(),), np.uint8)
+                tfn = lambda lin, s: lin.encode_argmax(xx, tok, ws, token_count=M, stream=s)
+                out_bytes, t_out_bytes = M * P * 8, M * 4
+                names = ("lm_head_argmax_t16", "lm_head_argmax_partials")
             else:
                 y = DeviceArray((M, N), np.uint16)
-                xx = DeviceArray.from_numpy(random_bf16(rng, (M, K)))
                 fn = lambda lin, s: lin.encode_bf16_fast(xx, y, token_count=M, stream=s)
-                out_bytes = M * N * 2
-            ms = time_launches(fn, ring, reps=reps)
-            algo = q4_bytes(N, K) + M * K * 2 + out_bytes
-            gbs = algo / (ms * 1e-3) / 1e9
-            rows.append({"kernel": "lm_head_argmax" if lm_head else "q4_gemv", "N": N, "K": K, "M": M,
-                         "us": ms * 1e3, "algo_bytes": algo, "GBps": gbs, "frac_peak": gbs / HBM_PEAK_GBS,
-                         "ring": len(ring)})
+                tfn = fn
+                out_bytes = t_out_bytes = M * N * 2
+                names = ("q4_gemv_t16", "q4_gemv")
+            for name, f, items, ob in ((names[0], tfn, tring, t_out_bytes), (names[1], fn, ring, out_bytes)):
+                ms = time_launches(f, items, reps=reps)
+                algo = q4_bytes(N, K) + M * K * 2 + ob
+                gbs = algo / (ms * 1e-3) / 1e9
+                rows.append({"kernel": name, "layout": "decode" if items is tring else "mlx", "N": N, "K": K,
+                             "M": M, "us": ms * 1e3, "algo_bytes": algo, "GBps": gbs,
+                             "frac_peak": gbs / HBM_PEAK_GBS, "ring": len(ring)})
             if lm_head:
                 o = DeviceArray((1,), np.uint32)
                 argmax_pairs(pv[0], pi[0], o, N // 8)
                 synchronize()
+        for t in tring:
+            t.close()
         for lin in ring:
             for a in (lin.weight, lin.scales, lin.biases):
                 a.close()

@@ -79,6 +79,49 @@ class Q4Linear:
              token_count, self.out_dim, self.in_dim)
 
 
+class DecodeLayoutQ4:
+    """A Q4Linear's weight permuted into the decode layout (16-row tiles,
+    256-wide K windows; prg_q4_repack_t16), read by the matrix-core GEMV the
+    model runs for its decode projections. Same results as Q4Linear's
+    encode_bf16_fast (linear_q4.zig:77-95) within the bf16 rounding of a
+    different summation order; argmax as encode_bf16_argmax_partial +
+    argmax_pairs (linear_q4.zig:97-118, argmax.zig:14-35)."""
+
+    def __init__(self, lin: Q4Linear, stream=None) -> None:
+        self.out_dim, self.in_dim = lin.out_dim, lin.in_dim
+        self.weight = DeviceArray(lin.weight.shape, np.uint32)
+        self.scales = DeviceArray(lin.scales.shape, np.uint16)
+        self.biases = DeviceArray(lin.biases.shape, np.uint16)
+        call("prg_q4_repack_t16", _s(stream), *lin._wsb(), *self._wsb(), self.out_dim, self.in_dim)
+
+    @property
+    def nbytes(self) -> int:
+        return self.weight.nbytes + self.scales.nbytes + self.biases.nbytes
+
+    def _wsb(self):
+        return ptr(self.weight), ptr(self.scales), ptr(self.biases)
+
+    def encode_bf16_fast(self, x, y, token_count: int = 1, stream=None) -> None:
+        call("prg_q4_gemv_t16_bf16", _s(stream), ptr(x), *self._wsb(), ptr(y), token_count, self.out_dim,
+             self.in_dim)
+
+    def encode_argmax(self, x, out_index, workspace, token_count: int = 1, stream=None) -> None:
+        """out_index[t] = greedy token of row t; workspace holds
+        prg_q4_gemv_t16_argmax_workspace_bytes() bytes."""
+        call("prg_q4_gemv_t16_argmax_bf16", _s(stream), ptr(x), *self._wsb(), ptr(out_index), token_count,
+             self.out_dim, self.in_dim, ptr(workspace))
+
+    def close(self) -> None:
+        for a in (self.weight, self.scales, self.biases):
+            a.close()
+
+
+def t16_argmax_workspace_bytes() -> int:
+    from ._lib import lib
+
+    return int(lib.prg_q4_gemv_t16_argmax_workspace_bytes())
+
+
 # block_mlp.zig:313-345 / :347-383
 def gate_up_silu(gate: Q4Linear, up: Q4Linear, x, out, stream=None) -> None:
     call("prg_q4_gemv_silu_gate_bf16", _s(stream), ptr(x), *gate._wsb(), *up._wsb(), ptr(out),
