@@ -156,3 +156,25 @@ def test_t16_argmax_full_vocab(gpu, orc, M):
         ulp = float(np.abs(srt[-1])) * 2.0**-7
         if margin > 2 * ulp:
             assert got[m] == orc.argmax_pairs(rpv[m], rpi[m]), f"row {m}"
+
+
+@pytest.mark.parametrize("N", [12288, 10240, 1024])
+def test_t16_silu_gate_norm_parity(gpu, orc, N):
+    """The model's post-attention RMSNorm + gate/up SiLU launch on the decode
+    layout vs the oracle's rmsnorm then SiLU pair (block_mlp.zig:313-345).
+    12288 rows is the 9B MLP, 10240 the attention q/k/v row count, 1024 a
+    launch of few tiles."""
+    from peregrine_amd._lib import call
+    from peregrine_amd.device import DeviceArray, ptr
+
+    K = 4096
+    rng = np.random.default_rng(N + 11)
+    g, u = random_q4(rng, N, K), random_q4(rng, N, K)
+    x = random_bf16(rng, (1, K), std=3.0)
+    nw = random_bf16(rng, (K,), std=0.3, mean=1.0)
+    tg, tu = T16Weight(g), T16Weight(u)
+    dx, dnw = DeviceArray.from_numpy(x), DeviceArray.from_numpy(nw)
+    out = DeviceArray((1, N), np.uint16)
+    call("prg_q4_gemv_t16_silu_gate_norm_bf16", None, ptr(dx), ptr(dnw), 1e-6, *tg.ptrs(), *tu.ptrs(), ptr(out), N, K)
+    want = orc.q4_gemv_silu_gate(orc.rmsnorm(x, nw, 1e-6), g, u)
+    assert_bf16_close(out.numpy(), want, min_exact=0.9, what=f"t16 silu norm {N}x{K}")
