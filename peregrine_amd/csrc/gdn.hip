@@ -27,6 +27,7 @@
 //   * Fused gated norm: one 512-thread block per head (16 half-waves x 8 rows)
 //     holds all 128 outputs of its head and normalises them in place.
 #include "gdn.hpp"
+#include "norm.hpp"
 #include "q4_gemv.hpp"
 
 namespace {
@@ -395,6 +396,34 @@ __global__ void rmsnorm_gated_kernel(const uint16_t* __restrict__ x, const uint1
   }
 }
 
+// dim == 128: 16 lanes per row (8 values each, 16-byte loads), 16 rows per
+// 256-thread block; the sum of squares and the per-value formula are those of
+// the out_proj GEMV's gated-norm prologue (8 values per lane in order, then
+// the 16-lane DPP row sum), so a row gets the prologue's bits.
+__global__ __launch_bounds__(256) void rmsnorm_gated128_kernel(const uint16_t* __restrict__ x,
+                                                               const uint16_t* __restrict__ w,
+                                                               const uint16_t* __restrict__ gate,
+                                                               uint16_t* __restrict__ out, uint32_t rows, float eps) {
+  const uint32_t row = blockIdx.x * 16 + threadIdx.x / 16, j = threadIdx.x % 16;
+  if (row >= rows) return;  // a whole DPP row
+  const size_t off = static_cast<size_t>(row) * kGdnDv + 8 * j;
+  const uint4 v = *reinterpret_cast<const uint4*>(x + off);
+  const uint4 wv = *reinterpret_cast<const uint4*>(w + 8 * j);
+  const uint4 gv = *reinterpret_cast<const uint4*>(gate + off);
+  const uint32_t d[4] = {v.x, v.y, v.z, v.w};
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float a = bf_lo(d[i]), b = bf_hi(d[i]);
+    ss = __fmaf_rn(a, a, ss);
+    ss = __fmaf_rn(b, b, ss);
+  }
+  const float scale = rsqrtf(__fadd_rn(__fmul_rn(row16_sum(ss), 1.0f / kGdnDv), eps));
+  const float4 z0 = make_float4(silu(bf_lo(gv.x)), silu(bf_hi(gv.x)), silu(bf_lo(gv.y)), silu(bf_hi(gv.y)));
+  const float4 z1 = make_float4(silu(bf_lo(gv.z)), silu(bf_hi(gv.z)), silu(bf_lo(gv.w)), silu(bf_hi(gv.w)));
+  *reinterpret_cast<uint4*>(out + off) = gated_rms_apply(v, wv, z0, z1, scale);
+}
+
 }  // namespace
 
 namespace prg {
@@ -522,8 +551,12 @@ int prg_rmsnorm_gated_bf16(void* stream, const uint16_t* x, const uint16_t* weig
   PRG_CHECK_ARG(x && weight && gate && out, "prg_rmsnorm_gated_bf16: null pointer");
   PRG_CHECK_ARG(dim > 0 && dim <= prg::kGdnDv, "prg_rmsnorm_gated_bf16: dim %u must be in (0, 128]", dim);
   PRG_CHECK_ARG(rows > 0, "prg_rmsnorm_gated_bf16: rows == 0");
-  hipLaunchKernelGGL(rmsnorm_gated_kernel, dim3(rows), dim3(prg::kGdnDv), 0, prg::as_stream(stream), x, weight,
-                     gate, out, dim, eps);
+  if (dim == prg::kGdnDv)
+    hipLaunchKernelGGL(rmsnorm_gated128_kernel, dim3((rows + 15) / 16), dim3(256), 0, prg::as_stream(stream), x,
+                       weight, gate, out, rows, eps);
+  else
+    hipLaunchKernelGGL(rmsnorm_gated_kernel, dim3(rows), dim3(prg::kGdnDv), 0, prg::as_stream(stream), x, weight,
+                       gate, out, dim, eps);
   PRG_CHECK_LAUNCH("prg_rmsnorm_gated_bf16");
   return PRG_OK;
 }

@@ -26,38 +26,69 @@ using namespace prg;
 
 constexpr int kPrepThreads = 256;     // QWEN35_QK_PREPARE_THREADS (attention.metal:9)
 constexpr int kSoftmaxThreads = 256;  // PREFILL_SOFTMAX_THREADS (attention.metal:42)
-constexpr int kQkNormThreads = 128;   // QK_NORM_PREFILL_THREADS_PER_THREADGROUP (gated_norm.metal:55)
 constexpr float kLog2e = 1.4426950408889634f;
 
 // Halving tree over blockDim.x == N threads in the reference's order
-// (partial[t] += partial[t + stride], stride N/2 .. 1). Every thread gets the
-// root. `sh` holds N floats.
+// (partial[t] = op(partial[t], partial[t + stride]), stride N/2 .. 1). Every
+// thread gets the root. `sh` holds N floats. N == 256 combines the first two
+// levels from LDS in wave 0 and the rest inside that wave (v_permlane32_swap,
+// v_permlane16_swap, then DPP row shifts): the same pairs, so the same bits,
+// with two barriers instead of nine.
+template <bool MAX>
+__device__ inline float tree_op(float a, float b) {
+  return MAX ? fmaxf(a, b) : __fadd_rn(a, b);
+}
+template <bool MAX>
+__device__ inline float wave_tree_tail(float s) {  // strides 32 .. 1 within one wave; lane 0 holds the root
+  {
+    float x = s, y = s;
+    swap32(x, y);
+    s = tree_op<MAX>(x, y);
+  }
+  {
+    float x = s, y = s;
+    swap16(x, y);
+    s = tree_op<MAX>(x, y);
+  }
+  s = tree_op<MAX>(s, dpp_f<0x108>(s));  // row_shl:8 -- lane i with lane i + 8
+  s = tree_op<MAX>(s, dpp_f<0x104>(s));
+  s = tree_op<MAX>(s, dpp_f<0x102>(s));
+  s = tree_op<MAX>(s, dpp_f<0x101>(s));
+  return s;
+}
+template <int N, bool MAX>
+__device__ inline float tree_reduce(float v, float* sh) {
+  sh[threadIdx.x] = v;
+  __syncthreads();
+  if constexpr (N == 256) {
+    if (threadIdx.x < kWave) {
+      const int l = threadIdx.x;
+      const float s = tree_op<MAX>(tree_op<MAX>(sh[l], sh[l + 128]), tree_op<MAX>(sh[l + 64], sh[l + 192]));
+      const float r = wave_tree_tail<MAX>(s);
+      if (l == 0) sh[N] = r;
+    }
+    __syncthreads();
+    return sh[N];
+  } else {
+#pragma unroll
+    for (int stride = N / 2; stride > 0; stride >>= 1) {
+      if (static_cast<int>(threadIdx.x) < stride)
+        sh[threadIdx.x] = tree_op<MAX>(sh[threadIdx.x], sh[threadIdx.x + stride]);
+      __syncthreads();
+    }
+    const float r = sh[0];
+    __syncthreads();
+    return r;
+  }
+}
+// `sh` holds N + 1 floats.
 template <int N>
 __device__ inline float tree_sum(float v, float* sh) {
-  sh[threadIdx.x] = v;
-  __syncthreads();
-#pragma unroll
-  for (int stride = N / 2; stride > 0; stride >>= 1) {
-    if (static_cast<int>(threadIdx.x) < stride) sh[threadIdx.x] += sh[threadIdx.x + stride];
-    __syncthreads();
-  }
-  const float r = sh[0];
-  __syncthreads();
-  return r;
+  return tree_reduce<N, false>(v, sh);
 }
-
 template <int N>
 __device__ inline float tree_max(float v, float* sh) {
-  sh[threadIdx.x] = v;
-  __syncthreads();
-#pragma unroll
-  for (int stride = N / 2; stride > 0; stride >>= 1) {
-    if (static_cast<int>(threadIdx.x) < stride) sh[threadIdx.x] = fmaxf(sh[threadIdx.x], sh[threadIdx.x + stride]);
-    __syncthreads();
-  }
-  const float r = sh[0];
-  __syncthreads();
-  return r;
+  return tree_reduce<N, true>(v, sh);
 }
 
 // ------------------------------------------------------- attention ----------
@@ -72,7 +103,7 @@ __global__ __launch_bounds__(kPrepThreads) void attn_prefill_prepare_kernel(
     const uint16_t* __restrict__ k_w, const uint16_t* __restrict__ v_in, uint16_t* __restrict__ q_out,
     uint16_t* __restrict__ gate_out, uint16_t* __restrict__ cache_k, uint16_t* __restrict__ cache_v, uint32_t T,
     uint32_t start_rope, uint32_t start_cache, uint32_t stride) {
-  __shared__ float sh[kPrepThreads];
+  __shared__ float sh[kPrepThreads + 1];
   const uint32_t rg = blockIdx.x, d = threadIdx.x;
   const uint32_t q_rows = T * kAttnQHeads;
   const bool is_q = rg < q_rows;
@@ -110,20 +141,46 @@ __global__ __launch_bounds__(kPrepThreads) void attn_prefill_prepare_kernel(
 __global__ __launch_bounds__(kSoftmaxThreads) void attn_prefill_softmax_kernel(uint16_t* __restrict__ scores,
                                                                                uint32_t ld, uint32_t L, uint32_t T,
                                                                                uint32_t prefix, float scale) {
-  __shared__ float sh[kSoftmaxThreads];
+  __shared__ float sh[kSoftmaxThreads + 1];
   uint16_t* row = scores + static_cast<size_t>(blockIdx.x) * ld;
   const uint32_t t = (blockIdx.x % (kAttnGroup * T)) % T;
   const uint32_t vis = prefix + t;
+  // The thread's first kCache columns (c = tid + 256 i) stay in registers
+  // across the three passes (one read of the row); later columns are read
+  // again. The arithmetic and its order per thread are unchanged.
+  constexpr int kCache = 8;
+  float xs[kCache];
+#pragma unroll
+  for (int i = 0; i < kCache; ++i) {
+    const uint32_t c = threadIdx.x + kSoftmaxThreads * i;
+    xs[i] = c < L ? __fmul_rn(bf2f(row[c]), scale) : 0.0f;
+  }
   float m = -INFINITY;
-  for (uint32_t c = threadIdx.x; c < L; c += kSoftmaxThreads)
+#pragma unroll
+  for (int i = 0; i < kCache; ++i) {
+    const uint32_t c = threadIdx.x + kSoftmaxThreads * i;
+    if (c < L) m = fmaxf(m, c > vis ? -INFINITY : xs[i]);
+  }
+  for (uint32_t c = threadIdx.x + kSoftmaxThreads * kCache; c < L; c += kSoftmaxThreads)
     m = fmaxf(m, c > vis ? -INFINITY : __fmul_rn(bf2f(row[c]), scale));
   const float row_max = tree_max<kSoftmaxThreads>(m, sh);
   float sum = 0.0f;
-  for (uint32_t c = threadIdx.x; c < L; c += kSoftmaxThreads)
+#pragma unroll
+  for (int i = 0; i < kCache; ++i) {
+    const uint32_t c = threadIdx.x + kSoftmaxThreads * i;
+    xs[i] = exp2f(__fmul_rn(__fsub_rn(xs[i], row_max), kLog2e));
+    if (c < L && c <= vis) sum += xs[i];
+  }
+  for (uint32_t c = threadIdx.x + kSoftmaxThreads * kCache; c < L; c += kSoftmaxThreads)
     if (c <= vis) sum += exp2f(__fmul_rn(__fsub_rn(__fmul_rn(bf2f(row[c]), scale), row_max), kLog2e));
   const float total = tree_sum<kSoftmaxThreads>(sum, sh);
   const float denom = total == 0.0f ? 1.0f : total;
-  for (uint32_t c = threadIdx.x; c < ld; c += kSoftmaxThreads) {
+#pragma unroll
+  for (int i = 0; i < kCache; ++i) {
+    const uint32_t c = threadIdx.x + kSoftmaxThreads * i;
+    if (c < ld) row[c] = c < L && c <= vis ? f2bf(xs[i] / denom) : uint16_t{0};
+  }
+  for (uint32_t c = threadIdx.x + kSoftmaxThreads * kCache; c < ld; c += kSoftmaxThreads) {
     uint16_t p = 0;
     if (c < L && c <= vis) p = f2bf(exp2f(__fmul_rn(__fsub_rn(__fmul_rn(bf2f(row[c]), scale), row_max), kLog2e)) / denom);
     row[c] = p;
@@ -191,27 +248,60 @@ __global__ void conv1d_prefill_state_kernel(float* __restrict__ state, const uin
   }
 }
 
-// Block (t, hk), 128 threads: f32 l2-normed q (x rsqrt(Dk)) and k of k-head hk
-// and their dot product kq; threads 0, 1 also produce the gates of v-heads
-// 2hk, 2hk+1.
-__global__ __launch_bounds__(kQkNormThreads) void gdn_prefill_prepare_kernel(
+// Sum of 128 values in tree_sum<128>'s order (entry i += entry i + stride
+// for stride 64, 32, ..., 1) within one wave: lane i holds entries i and
+// i + 64; the 32- and 16-lane steps pair lanes with v_permlane32_swap /
+// v_permlane16_swap, the rest shift within a DPP row. Returns the total to
+// every lane. Each step adds the same two values as the LDS tree, so the
+// bits are the tree's.
+__device__ inline float tree128_wave(float lo, float hi) {
+  float s = __fadd_rn(lo, hi);
+  {
+    float x = s, y = s;
+    swap32(x, y);  // own value and lane i ^ 32's
+    s = __fadd_rn(x, y);
+  }
+  {
+    float x = s, y = s;
+    swap16(x, y);  // own value and the partner row's lane
+    s = __fadd_rn(x, y);
+  }
+  s = __fadd_rn(s, dpp_f<0x108>(s));  // row_shl:8 -- lane i += lane i + 8
+  s = __fadd_rn(s, dpp_f<0x104>(s));
+  s = __fadd_rn(s, dpp_f<0x102>(s));
+  s = __fadd_rn(s, dpp_f<0x101>(s));
+  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, s)));
+}
+
+// One wave per (t, hk): f32 l2-normed q (x rsqrt(Dk)) and k of k-head hk and
+// their dot product kq, with the 128-thread tree's sums
+// (QK_NORM_PREFILL_THREADS_PER_THREADGROUP, gated_norm.metal:55); lanes 0, 1
+// also produce the gates of v-heads 2hk, 2hk+1. Lane i holds dims i and
+// i + 64.
+constexpr int kPrepWaves = 4;  // (t, hk) pairs per 256-thread block
+__global__ __launch_bounds__(kPrepWaves * kWave) void gdn_prefill_prepare_kernel(
     const uint16_t* __restrict__ conv_out, const uint16_t* __restrict__ a, const uint16_t* __restrict__ b,
     const float* __restrict__ A_log, const uint16_t* __restrict__ dt_bias, float* __restrict__ qn,
-    float* __restrict__ kn, float* __restrict__ g, float* __restrict__ beta, float* __restrict__ kq) {
-  __shared__ float sh[kQkNormThreads];
-  const uint32_t t = blockIdx.x / kGdnHk, hk = blockIdx.x % kGdnHk, d = threadIdx.x;
+    float* __restrict__ kn, float* __restrict__ g, float* __restrict__ beta, float* __restrict__ kq, uint32_t T) {
+  const uint32_t pair = blockIdx.x * kPrepWaves + (threadIdx.x / kWave);
+  if (pair >= T * kGdnHk) return;  // a whole wave
+  const uint32_t t = pair / kGdnHk, hk = pair % kGdnHk, d = threadIdx.x % kWave;
   const uint16_t* row = conv_out + static_cast<size_t>(t) * kGdnConvDim;
-  const float qv = bf2f(row[hk * kGdnDk + d]), kv = bf2f(row[kGdnKeyDim + hk * kGdnDk + d]);
-  const float qs = tree_sum<kQkNormThreads>(__fmul_rn(qv, qv), sh);
-  const float ks = tree_sum<kQkNormThreads>(__fmul_rn(kv, kv), sh);
+  const float q0 = bf2f(row[hk * kGdnDk + d]), q1 = bf2f(row[hk * kGdnDk + 64 + d]);
+  const float k0 = bf2f(row[kGdnKeyDim + hk * kGdnDk + d]), k1 = bf2f(row[kGdnKeyDim + hk * kGdnDk + 64 + d]);
+  const float qs = tree128_wave(__fmul_rn(q0, q0), __fmul_rn(q1, q1));
+  const float ks = tree128_wave(__fmul_rn(k0, k0), __fmul_rn(k1, k1));
   const float q_inv = 1.0f / sqrtf(qs + 1.0e-6f), k_inv = 1.0f / sqrtf(ks + 1.0e-6f);
   const float q_scale = 1.0f / sqrtf(static_cast<float>(kGdnDk));
   const size_t o = (static_cast<size_t>(t) * kGdnHk + hk) * kGdnDk + d;
-  const float qo = __fmul_rn(__fmul_rn(qv, q_inv), q_scale), ko = __fmul_rn(kv, k_inv);
-  qn[o] = qo;
-  kn[o] = ko;
+  const float qo0 = __fmul_rn(__fmul_rn(q0, q_inv), q_scale), qo1 = __fmul_rn(__fmul_rn(q1, q_inv), q_scale);
+  const float ko0 = __fmul_rn(k0, k_inv), ko1 = __fmul_rn(k1, k_inv);
+  qn[o] = qo0;
+  qn[o + 64] = qo1;
+  kn[o] = ko0;
+  kn[o + 64] = ko1;
   // k.q of the normalised pair: shared by every state row of the two v-heads.
-  const float kqs = tree_sum<kQkNormThreads>(__fmul_rn(ko, qo), sh);
+  const float kqs = tree128_wave(__fmul_rn(ko0, qo0), __fmul_rn(ko1, qo1));
   if (kq && d == 0) kq[static_cast<size_t>(t) * kGdnHk + hk] = kqs;
   if (d < kGdnHv / kGdnHk) {
     const uint32_t hv = hk * (kGdnHv / kGdnHk) + d;
@@ -492,8 +582,8 @@ int launch_conv1d_prefill(hipStream_t s, float* state, const uint16_t* qkv, cons
 int launch_gdn_prefill_prepare(hipStream_t s, const uint16_t* conv_out, const uint16_t* a, const uint16_t* b,
                                const float* A_log, const uint16_t* dt_bias, float* qn, float* kn, float* g,
                                float* beta, float* kq, uint32_t T) {
-  hipLaunchKernelGGL(gdn_prefill_prepare_kernel, dim3(T * kGdnHk), dim3(kQkNormThreads), 0, s, conv_out, a, b, A_log,
-                     dt_bias, qn, kn, g, beta, kq);
+  hipLaunchKernelGGL(gdn_prefill_prepare_kernel, dim3((T * kGdnHk + kPrepWaves - 1) / kPrepWaves),
+                     dim3(kPrepWaves * kWave), 0, s, conv_out, a, b, A_log, dt_bias, qn, kn, g, beta, kq, T);
   PRG_CHECK_LAUNCH("gdn_prefill_prepare");
   return PRG_OK;
 }
