@@ -36,42 +36,38 @@ def repack_ref(wt):
 
 
 class T16Weight:
-    """A device copy of wt in the decode layout (prg_q4_repack_t16)."""
+    """A device copy of wt in the decode layout, through the op layer's
+    DecodeLayoutQ4 (prg_q4_repack_t16 and the decode-layout entry points)."""
 
     def __init__(self, wt):
-        from peregrine_amd._lib import call
-        from peregrine_amd.device import DeviceArray, ptr
+        from peregrine_amd.ops import DecodeLayoutQ4, Q4Linear
 
         self.N, self.K = wt.shape
-        src = [DeviceArray.from_numpy(np.ascontiguousarray(a)) for a in (wt.w, wt.s, wt.b)]
-        self.dst = [DeviceArray(a.shape, a.dtype) for a in (wt.w, wt.s, wt.b)]
-        call("prg_q4_repack_t16", None, *[ptr(a) for a in src], *[ptr(a) for a in self.dst], self.N, self.K)
-        self._src = src
+        self._src = Q4Linear.upload(wt)
+        self.lin = DecodeLayoutQ4(self._src)
+        self.dst = [self.lin.weight, self.lin.scales, self.lin.biases]
 
     def ptrs(self):
-        from peregrine_amd.device import ptr
-
-        return [ptr(a) for a in self.dst]
+        return list(self.lin._wsb())
 
     def gemv(self, x):
-        from peregrine_amd._lib import call
-        from peregrine_amd.device import DeviceArray, ptr
+        from peregrine_amd.device import DeviceArray
 
         M = x.shape[0]
         dx = DeviceArray.from_numpy(np.ascontiguousarray(x))
         dy = DeviceArray((M, self.N), np.uint16)
-        call("prg_q4_gemv_t16_bf16", None, ptr(dx), *self.ptrs(), ptr(dy), M, self.N, self.K)
+        self.lin.encode_bf16_fast(dx, dy, token_count=M)
         return dy.numpy()
 
     def argmax(self, x):
-        from peregrine_amd._lib import call, lib
-        from peregrine_amd.device import DeviceArray, ptr
+        from peregrine_amd.device import DeviceArray
+        from peregrine_amd.ops import t16_argmax_workspace_bytes
 
         M = x.shape[0]
         dx = DeviceArray.from_numpy(np.ascontiguousarray(x))
         out = DeviceArray((2,), np.uint32)
-        ws = DeviceArray((int(lib.prg_q4_gemv_t16_argmax_workspace_bytes()),), np.uint8)
-        call("prg_q4_gemv_t16_argmax_bf16", None, ptr(dx), *self.ptrs(), ptr(out), M, self.N, self.K, ptr(ws))
+        ws = DeviceArray((t16_argmax_workspace_bytes(),), np.uint8)
+        self.lin.encode_argmax(dx, out, ws, token_count=M)
         return [int(v) for v in out.numpy()[:M]]
 
 
