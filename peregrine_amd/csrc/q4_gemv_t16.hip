@@ -557,6 +557,10 @@ int t16_check(const char* name, const void* x, const void* tw, const void* ts, c
   PRG_CHECK_ARG(x && tw && ts && tb, "%s: null pointer", name);
   PRG_CHECK_ARG(prg::t16_shape_ok(out_dim, in_dim), "%s: shape %u x %u (out_dim %% 16, in_dim %% 1024)", name, out_dim,
                 in_dim);
+  // the kernels read x and the packed words 16 bytes at a time
+  PRG_CHECK_ARG(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(tw) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(ts) % 2 == 0 && reinterpret_cast<uintptr_t>(tb) % 2 == 0,
+                "%s: x and the packed words must be 16-byte aligned", name);
   return PRG_OK;
 }
 

@@ -48,3 +48,16 @@ def test_gemv_contract_rejected_on_host(in_dim, out_dim, tokens, code):
 def test_null_pointer_rejected():
     rc = lib.prg_q4_gemv_bf16(None, None, None, None, None, None, 1, 8, 512)
     assert rc == 1
+
+
+@pytest.mark.parametrize("x,out_dim,in_dim,tokens,code", [
+    (0x1000, 40, 4096, 1, 1),    # out_dim % 16 != 0
+    (0x1000, 64, 2048, 1, 1),    # in_dim % 1024 != 0
+    (0x1002, 64, 4096, 1, 1),    # x not 16-byte aligned
+    (0x1000, 64, 4096, 0, 7),    # token_count == 0 -> EmptyInput (linear_q4.zig:85)
+])
+def test_decode_layout_gemv_contract_rejected_on_host(x, out_dim, in_dim, tokens, code):
+    dummy = C.c_void_p(0x1000)  # never dereferenced: validation fails first
+    rc = lib.prg_q4_gemv_t16_bf16(None, C.c_void_p(x), dummy, dummy, dummy, dummy, tokens, out_dim, in_dim)
+    assert rc == code
+    assert lib.prg_last_error()
