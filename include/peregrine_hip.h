@@ -314,7 +314,10 @@ int prg_gated_delta_decode_norm_bf16(void *stream, float *state, const uint16_t 
                                      uint32_t has_previous_state);
 
 /* Gated RMSNorm per row of `dim` (<= 128) values. Replaces rmsnorm_gated_bf16
- * (shaders/gated_norm.metal:163-189), host block_linear.zig:471-489. */
+ * (shaders/gated_norm.metal:163-189), host block_linear.zig:471-489.
+ * dim == 128 with x, weight, gate and out 16-byte aligned: 16 lanes per row,
+ * the same bits as the out_proj GEMV's gated-norm prologue; any other dim or
+ * alignment: one 128-thread block per row (a different summation order). */
 int prg_rmsnorm_gated_bf16(void *stream, const uint16_t *x, const uint16_t *weight,
                            const uint16_t *gate, uint16_t *out, uint32_t dim, float eps,
                            uint32_t rows);

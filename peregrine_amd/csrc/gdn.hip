@@ -551,7 +551,10 @@ int prg_rmsnorm_gated_bf16(void* stream, const uint16_t* x, const uint16_t* weig
   PRG_CHECK_ARG(x && weight && gate && out, "prg_rmsnorm_gated_bf16: null pointer");
   PRG_CHECK_ARG(dim > 0 && dim <= prg::kGdnDv, "prg_rmsnorm_gated_bf16: dim %u must be in (0, 128]", dim);
   PRG_CHECK_ARG(rows > 0, "prg_rmsnorm_gated_bf16: rows == 0");
-  if (dim == prg::kGdnDv)
+  // 16 lanes per row with 16-byte accesses when every pointer allows them
+  const bool aligned16 = ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(weight) |
+                           reinterpret_cast<uintptr_t>(gate) | reinterpret_cast<uintptr_t>(out)) & 15u) == 0;
+  if (dim == prg::kGdnDv && aligned16)
     hipLaunchKernelGGL(rmsnorm_gated128_kernel, dim3((rows + 15) / 16), dim3(256), 0, prg::as_stream(stream), x,
                        weight, gate, out, rows, eps);
   else

@@ -141,15 +141,27 @@ def test_gated_delta_fused_norm(gpu, orc):
     assert_bf16_close(out.numpy(), ref, min_exact=0.9, what="gdn+norm")
 
 
-def test_rmsnorm_gated(gpu, orc):
-    from peregrine_amd import ops
+@pytest.mark.parametrize("shift", [0, 1])
+def test_rmsnorm_gated(gpu, orc, shift):
+    """shift 0: 16-byte aligned rows (16 lanes per row); shift 1: x, gate and
+    out one bf16 element past alignment, which takes the one-block-per-row
+    kernel. Both against the oracle (gated_norm.metal:163-189)."""
+    from peregrine_amd._lib import call
+    from peregrine_amd.device import ptr
 
     rng = np.random.default_rng(8)
     x, z = random_bf16(rng, (4096,)), random_bf16(rng, (4096,))
     w = random_bf16(rng, (128,), std=0.1, mean=1.0)
-    out = _e((4096,))
-    ops.rmsnorm_gated(_d(x), _d(w), _d(z), out)
-    assert_bf16_close(out.numpy(), orc.rmsnorm_gated(x, w, z, 128), min_exact=0.97, what="gated norm")
+    pad = np.zeros(shift, np.uint16)
+    dx, dz, dw = _d(np.concatenate([pad, x])), _d(np.concatenate([pad, z])), _d(w)
+    out = _e((4096 + shift,))
+
+    def at(a):
+        return ptr(a).value + 2 * shift
+
+    call("prg_rmsnorm_gated_bf16", None, at(dx), ptr(dw), at(dz), at(out), 128, 1e-6, 32)
+    got = out.numpy()[shift:]
+    assert_bf16_close(got, orc.rmsnorm_gated(x, w, z, 128), min_exact=0.97, what=f"gated norm shift {shift}")
 
 
 @pytest.mark.parametrize("pos", [0, 7, 4096, 65535])
