@@ -310,11 +310,14 @@ __global__ __launch_bounds__(kQ4Threads) void gemm_q4_kernel(const GemmArgs g) {
   const uint32_t K = g.K, steps = K / kBK;
 
   // A: thread t stages rows (t >> 3) + 64 i (i < BM / 64), chunk t & 7; rows >= M
-  // read as zero.
+  // read as zero. Each row's offset is in the per-lane (VGPR) offset, which
+  // the buffer range check covers; only the step's k offset, always inside a
+  // row, goes in the scalar offset.
   const __amdgpu_buffer_rsrc_t a_rsrc = buffer_rsrc(g.a, static_cast<uint32_t>(static_cast<uint64_t>(g.M) * g.lda * 2));
   const uint32_t ar = tid >> 3, ac = tid & 7;
-  const uint32_t a_voff = static_cast<uint32_t>(((m0 + ar) * g.lda + ac * 8) * 2);
-  const uint32_t a_row64 = static_cast<uint32_t>(64 * g.lda * 2);
+  uint32_t a_voff[BM / 64];
+#pragma unroll
+  for (int i = 0; i < BM / 64; ++i) a_voff[i] = static_cast<uint32_t>(((m0 + ar + 64 * i) * g.lda + ac * 8) * 2);
   const uint32_t a_lds = ar * 128 + ((ac ^ (ar & 7)) << 4);
   // B: thread t dequantises word t & 7 (columns 8 (t&7) .. +8 of the step) of
   // tile rows (t >> 3) + 64 j. Pair: j = 0 gate, j = 1 up (same output columns).
@@ -348,7 +351,7 @@ __global__ __launch_bounds__(kQ4Threads) void gemm_q4_kernel(const GemmArgs g) {
   u32x4 rd[DENSE ? 2 : 1][2];
   auto gload = [&](int set, uint32_t ks) {
 #pragma unroll
-    for (int i = 0; i < BM / 64; ++i) ra[set][i] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, a_voff, ks * 128 + i * a_row64, 0);
+    for (int i = 0; i < BM / 64; ++i) ra[set][i] = __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, a_voff[i], ks * 128, 0);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       if constexpr (DENSE) {
