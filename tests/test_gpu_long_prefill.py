@@ -125,3 +125,26 @@ def test_prepared_dense_prefill_is_identical(m9b, monkeypatch):
     np.testing.assert_array_equal(a.decode(4)[0], b.decode(4)[0])
     a.close()
     b.close()
+
+
+@pytest.mark.parametrize("T", [100, 700, 1600])
+def test_pair256_gate_up_matches_the_q4_kernel(m9b, monkeypatch, T):
+    """The 256 x 256 SiLU-pair kernel (gemm_pair256_kernel, taken for the dense
+    gate / up GEMM when it costs less) issues, per output element, the matrix
+    instructions of gemm_q4_kernel in the same k order. Forced off and on
+    (PEREGRINE_GEMM_PAIR256, read per launch), prompts of 100 / 700 / 1600
+    tokens (one partial row tile; several with a partial last one) leave the
+    same next token, GDN states and KV caches bit for bit."""
+    m9b.prepare_dense()
+    prompt = np.random.default_rng(11 + T).integers(0, 248320, size=T).astype(np.uint32)
+    a = _state(m9b, 2048, None, monkeypatch)
+    b = _state(m9b, 2048, None, monkeypatch)
+    monkeypatch.setenv("PEREGRINE_GEMM_PAIR256", "0")
+    fa = a.prefill(prompt)
+    monkeypatch.setenv("PEREGRINE_GEMM_PAIR256", "1")
+    fb = b.prefill(prompt)
+    monkeypatch.delenv("PEREGRINE_GEMM_PAIR256")
+    assert fa == fb
+    _same_states(a, b, m9b, T)
+    a.close()
+    b.close()
