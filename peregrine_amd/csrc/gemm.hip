@@ -510,25 +510,28 @@ __global__ __launch_bounds__(kQ4Threads) void gemm_q4_kernel(const GemmArgs g) {
   }
 }
 
-// SiLU pair over the prepared dense copies, 256 prompt rows x 128 output
-// columns per block (the gate and up rows of those columns: 256 weight rows).
-// 8 waves as 2 along M x 4 along N; wave (wm, wn) owns rows 128 wm .. +128 and
-// output columns 32 wn .. +32, i.e. fragment blocks j = 0, 1 of gate and
-// j = 2, 3 of up for the same columns, so the epilogue pairs acc[i][j] with
-// acc[i][j + 2] in registers. Per output element the matrix instructions are
-// those of gemm_q4_kernel in the same k order (16x16x32 blocks of k 32 s ..
-// 32 s + 31 with the same lane -> k map), so both kernels give the same bits.
+// SiLU pair over the prepared dense copies, BM prompt rows (256 or 320) x 128
+// output columns per block (the gate and up rows of those columns: 256
+// weight rows). 8 waves as 2 along M x 4 along N; wave (wm, wn) owns rows
+// BM/2 wm .. +BM/2 and output columns 32 wn .. +32, i.e. fragment blocks
+// j = 0, 1 of gate and j = 2, 3 of up for the same columns, so the epilogue
+// pairs acc[i][j] with acc[i][j + 2] in registers. Per output element the
+// matrix instructions are those of gemm_q4_kernel in the same k order
+// (16x16x32 blocks of k 32 s .. 32 s + 31 with the same lane -> k map), so
+// every row tile and both kernels give the same bits.
 //
-// Pipeline per 32-k step s (one barrier per step), five LDS stages of 32 KB
-// (the whole 160 KB): every thread issues the step s + 4 loads straight into
-// LDS (buffer_load_dwordx4 ... lds: 64 lanes x 16 B = 1 KB of 64-byte rows
-// per instruction, four per thread per step), reads the fragments of step s
-// and runs its 32 matrix instructions, then waits until its step s + 1 loads
-// have landed (the 12 newer loads may still be in flight) before the barrier.
-// Rows of A past M and weight rows past N fall outside the buffer range and
-// read as zero (their row offset is in the range-checked per-lane offset).
-constexpr int kP256Threads = 512, kP256Stages = 5, kP256BK = 32;
-constexpr uint32_t kP256Stage = 512 * kP256BK * 2;  // 256 A rows + 256 weight rows of 64 bytes
+// Pipeline per 32-k step s (one barrier per step), LDS stages of
+// (BM + 256) x 64 bytes, as many as fit in 160 KB (5 at BM = 256, 4 at 320):
+// the step s + NS - 1 loads go straight into LDS (buffer_load_dwordx4 ...
+// lds: 64 lanes x 16 B = 1 KB of 64-byte rows per instruction; 4 per wave
+// per step, 5 for the waves that also take the rows past 256), the step's
+// fragments are read and its matrix instructions run, then each wave waits
+// until its step s + 1 loads have landed (the newer ones may still be in
+// flight) before the barrier. Rows of A past M and weight rows past N fall
+// outside the buffer range and read as zero (their row offset is in the
+// range-checked per-lane offset).
+constexpr int kPairThreads = 512, kPairBK = 32;
+constexpr uint32_t kLdsBytes = 160 * 1024;
 
 // One direct-to-LDS load: 16 bytes per lane at LDS address m0 + 16 * lane.
 // m0 is written only here; nothing else in the kernel reads it (no indirect
@@ -544,15 +547,22 @@ __device__ inline void lds_load16(__amdgpu_buffer_rsrc_t r, uint32_t lds_addr, u
 #define PRG_WAIT_VMCNT(n) \
   __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8) | ((((n) >> 4) & 3) << 14))
 
-__global__ __launch_bounds__(kP256Threads) void gemm_pair256_kernel(const GemmArgs g) {
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[kP256Stages * kP256Stage];
+template <int BM>
+__global__ __launch_bounds__(kPairThreads) void gemm_pair_dma_kernel(const GemmArgs g) {
+  static_assert(BM == 256 || BM == 320, "row tile");
+  constexpr uint32_t kStage = (BM + 256) * kPairBK * 2;
+  constexpr int NS = static_cast<int>(kLdsBytes / kStage);  // 5 or 4
+  constexpr int IM = BM / 32;                               // 16-row blocks per wave
+  constexpr int kExtra = BM / 16 - 16;                      // waves that load a third A group
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * kStage];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 2, wn = wave & 3;
-  const uint32_t N = g.q[0].n, K = g.K, steps = K / kP256BK;
+  const bool extra = wave < kExtra;
+  const uint32_t N = g.q[0].n, K = g.K, steps = K / kPairBK;
   // Block -> tile as in gemm_q4_kernel: each XCD walks a contiguous range,
   // tm-fastest within groups of 4 tile rows.
-  const uint32_t tiles_m = (g.M + 255) / 256;
+  const uint32_t tiles_m = (g.M + BM - 1) / BM;
   uint32_t tm, tn;
   {
     const uint32_t T = gridDim.x, b = blockIdx.x, x = b % 8, q = T / 8, r = T % 8;
@@ -563,56 +573,65 @@ __global__ __launch_bounds__(kP256Threads) void gemm_pair256_kernel(const GemmAr
     tm = first + (L % width) % gs;
     tn = (L % width) / gs;
   }
-  const uint32_t m0 = tm * 256, n0 = tn * 128;
+  const uint32_t m0 = tm * BM, n0 = tn * 128;
   const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(g.a, static_cast<uint32_t>(static_cast<uint64_t>(g.M) * g.lda * 2));
   const __amdgpu_buffer_rsrc_t rg = buffer_rsrc(g.q[0].dense, static_cast<uint32_t>(static_cast<uint64_t>(N) * K * 2));
   const __amdgpu_buffer_rsrc_t ru = buffer_rsrc(g.q[1].dense, static_cast<uint32_t>(static_cast<uint64_t>(N) * K * 2));
-  // Wave w, load h: 16 rows 16 (w + 8 h) .. +15 of the A tile, and 16 rows
-  // 16 w .. +15 of gate (h = 0) or up (h = 1); lane l: row + l / 4, chunk l % 4.
+  // Wave w loads A rows 16 (w + 8 h) .. +15 for h = 0, 1 (and 256 + 16 w when
+  // it is one of the kExtra), and weight rows 16 w .. +15 of gate and of up;
+  // lane l: row + l / 4, chunk l % 4.
   const uint32_t lrow = 16 * wave + (lane >> 2), lch = 8 * (lane & 3);
-  uint32_t va[2];
+  uint32_t va[3];
 #pragma unroll
-  for (int h = 0; h < 2; ++h) va[h] = static_cast<uint32_t>(((m0 + lrow + 128 * h) * g.lda + lch) * 2);
+  for (int h = 0; h < 3; ++h) va[h] = static_cast<uint32_t>(((m0 + lrow + 128 * h) * g.lda + lch) * 2);
   const uint32_t vw = ((n0 + lrow) * K + lch) * 2;
   // LDS byte address of the ring (the address-space cast is a C-style cast)
   const uint32_t lbase = static_cast<uint32_t>(
       reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint8_t*)lds));
   auto issue = [&](uint32_t ks, uint32_t stage) {
-    const uint32_t sb = lbase + stage * kP256Stage + 1024 * wave;
+    const uint32_t sb = lbase + stage * kStage + 1024 * wave;
     lds_load16(ra, sb, va[0], ks * 64);
     lds_load16(ra, sb + 128 * 64, va[1], ks * 64);
-    lds_load16(rg, sb + 256 * 64, vw, ks * 64);
-    lds_load16(ru, sb + 384 * 64, vw, ks * 64);
+    if (kExtra > 0 && extra) lds_load16(ra, sb + 256 * 64, va[2], ks * 64);
+    lds_load16(rg, sb + BM * 64, vw, ks * 64);
+    lds_load16(ru, sb + (BM + 128) * 64, vw, ks * 64);
+  };
+  // this wave's loads newer than the ones of the step it needs next
+  auto wait_next = [&]() {
+    if (kExtra > 0 && extra)
+      PRG_WAIT_VMCNT(5 * (NS - 2));
+    else
+      PRG_WAIT_VMCNT(4 * (NS - 2));
   };
   // fragments: lane -> row (lane & 15) of a 16-row block, 16-byte chunk lane >> 4
-  const uint32_t fa = (wm * 128 + (lane & 15)) * 64 + (lane >> 4) * 16;
+  const uint32_t fa = (wm * (BM / 2) + (lane & 15)) * 64 + (lane >> 4) * 16;
   uint32_t fb[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) fb[j] = (256 + (j < 2 ? 0 : 128) + wn * 32 + 16 * (j & 1) + (lane & 15)) * 64 + (lane >> 4) * 16;
-  f32x4 acc[8][4];
+  for (int j = 0; j < 4; ++j) fb[j] = (BM + (j < 2 ? 0 : 128) + wn * 32 + 16 * (j & 1) + (lane & 15)) * 64 + (lane >> 4) * 16;
+  f32x4 acc[IM][4];
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < IM; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   // Steps past the end reload the last one (in bounds, never consumed).
   auto clampk = [&](uint32_t k) { return k < steps ? k : steps - 1; };
 
 #pragma unroll
-  for (int i = 0; i < kP256Stages - 1; ++i) issue(clampk(i), i);
-  PRG_WAIT_VMCNT(4 * (kP256Stages - 2));
+  for (int i = 0; i < NS - 1; ++i) issue(clampk(i), i);
+  wait_next();
   __syncthreads();
   uint32_t st = 0;
   for (uint32_t s = 0; s < steps; ++s) {
-    // stage of step s + 4: the one step s - 1 read, released by the last barrier
-    issue(clampk(s + kP256Stages - 1), st == 0 ? kP256Stages - 1 : st - 1);
-    const uint8_t* base = lds + st * kP256Stage;
-    bf16x8 fav[8], fbv[4];
+    // stage of step s + NS - 1: the one step s - 1 read, released by the last barrier
+    issue(clampk(s + NS - 1), st == 0 ? NS - 1 : st - 1);
+    const uint8_t* base = lds + st * kStage;
+    bf16x8 fav[IM], fbv[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) fbv[j] = *reinterpret_cast<const bf16x8*>(base + fb[j]);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) fav[i] = *reinterpret_cast<const bf16x8*>(base + fa + i * 1024);
+    for (int i = 0; i < IM; ++i) fav[i] = *reinterpret_cast<const bf16x8*>(base + fa + i * 1024);
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < IM; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fav[i], fbv[j], acc[i][j], 0, 0, 0);
     // the first matrix instructions start as soon as their fragments arrive
@@ -621,10 +640,11 @@ __global__ __launch_bounds__(kP256Threads) void gemm_pair256_kernel(const GemmAr
       __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);  // DS read
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 28, 0);
-    PRG_WAIT_VMCNT(4 * (kP256Stages - 2));  // this thread's step s + 1 loads have landed
+    if constexpr (IM > 8) __builtin_amdgcn_sched_group_barrier(0x100, IM - 8, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, 4 * IM - 4, 0);
+    wait_next();  // this wave's step s + 1 loads have landed
     __syncthreads();
-    st = st + 1 == kP256Stages ? 0 : st + 1;
+    st = st + 1 == NS ? 0 : st + 1;
   }
   PRG_WAIT_VMCNT(0);
 
@@ -632,10 +652,10 @@ __global__ __launch_bounds__(kP256Threads) void gemm_pair256_kernel(const GemmAr
   const int crow = 4 * (lane >> 4), ccol = lane & 15;
   uint16_t* C = g.q[0].c;
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < IM; ++i)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const uint32_t m = m0 + wm * 128 + 16 * i + crow + r;
+      const uint32_t m = m0 + wm * (BM / 2) + 16 * i + crow + r;
       if (m >= g.M) continue;
       uint16_t* out = C + static_cast<uint64_t>(m) * N;
 #pragma unroll
@@ -675,16 +695,28 @@ int launch_q4_bm(hipStream_t s, const GemmArgs& g, uint32_t tiles_n, const char*
   return PRG_OK;
 }
 
-// The 256 x 256 SiLU-pair kernel's round of blocks costs about as long as
-// 396 rows of gemm_q4_kernel rounds (one round measured at 2.06 rounds of
-// 192-row tiles, for 2.67 times their work). PEREGRINE_GEMM_PAIR256 = 0 / 1
-// turns it off / on whatever the estimate (both kernels give the same bits).
-constexpr uint64_t kPair256RoundCost = 396;
+// A round of gemm_pair_dma_kernel<256> blocks costs about as long as 396 rows
+// of gemm_q4_kernel rounds (one round measured at 2.06 rounds of 192-row
+// tiles, for 2.67 times their work); a 320-row round about 1.25 times that.
+// PEREGRINE_GEMM_PAIR_DMA = 0 / 256 / 320 forces the 192 / 256-row kernel or
+// that row tile of this one, whatever the estimate (all give the same bits).
+constexpr uint64_t kPairDmaRoundCost256 = 396, kPairDmaRoundCost320 = 495;
 
-inline int pair256_override() {
-  const char* e = getenv("PEREGRINE_GEMM_PAIR256");
+inline int pair_dma_override() {
+  const char* e = getenv("PEREGRINE_GEMM_PAIR_DMA");
   if (e == nullptr || e[0] == '\0') return -1;
-  return e[0] == '0' ? 0 : 1;
+  return atoi(e);
+}
+
+template <int BM>
+int launch_pair_dma(hipStream_t s, const GemmArgs& g, const char* name) {
+  PRG_CHECK_ARG(static_cast<uint64_t>(g.q[0].n + 128) * g.K * 2 < (1ull << 32) &&
+                    static_cast<uint64_t>(g.M + BM) * g.lda * 2 < (1ull << 32),
+                "%s: operands too large for 32-bit offsets", name);
+  const uint32_t tiles = ((g.M + BM - 1) / BM) * ((g.q[0].n + 127) / 128);
+  hipLaunchKernelGGL((gemm_pair_dma_kernel<BM>), dim3(tiles), dim3(kPairThreads), 0, s, g);
+  PRG_CHECK_LAUNCH(name);
+  return PRG_OK;
 }
 
 template <int EPI>
@@ -697,16 +729,18 @@ int launch_q4_t(hipStream_t s, const GemmArgs& g, const char* name) {
     return static_cast<uint64_t>((blocks + cus - 1) / cus) * bm;
   };
   if constexpr (EPI == kGemmSiluPair) {
-    const bool dense = g.q[0].dense != nullptr && g.q[1].dense != nullptr;
-    const uint32_t tiles256 = ((g.M + 255) / 256) * ((g.q[0].n + 127) / 128);
-    const uint64_t cost256 = static_cast<uint64_t>((tiles256 + cus - 1) / cus) * kPair256RoundCost;
-    const int force = pair256_override();
-    if (dense && (force == 1 || (force == -1 && cost256 < std::min(cost(192), cost(256))))) {
-      PRG_CHECK_ARG(static_cast<uint64_t>(g.q[0].n + 128) * g.K * 2 < (1ull << 32),
-                    "%s: weight rows too large for 32-bit offsets", name);
-      hipLaunchKernelGGL(gemm_pair256_kernel, dim3(tiles256), dim3(kP256Threads), 0, s, g);
-      PRG_CHECK_LAUNCH(name);
-      return PRG_OK;
+    if (g.q[0].dense != nullptr && g.q[1].dense != nullptr) {
+      const uint32_t tiles_nd = (g.q[0].n + 127) / 128;
+      auto cost_dma = [&](uint32_t bm, uint64_t round) -> uint64_t {
+        const uint32_t blocks = ((g.M + bm - 1) / bm) * tiles_nd;
+        return static_cast<uint64_t>((blocks + cus - 1) / cus) * round;
+      };
+      const uint64_t c256 = cost_dma(256, kPairDmaRoundCost256), c320 = cost_dma(320, kPairDmaRoundCost320);
+      const uint64_t cold = std::min(cost(192), cost(256));
+      int pick = pair_dma_override();
+      if (pick < 0) pick = std::min(c256, c320) < cold ? (c320 < c256 ? 320 : 256) : 0;
+      if (pick == 320) return launch_pair_dma<320>(s, g, name);
+      if (pick == 256) return launch_pair_dma<256>(s, g, name);
     }
   }
   if (cost(192) < cost(256)) return launch_q4_bm<EPI, 192>(s, g, tiles_n, name);
