@@ -510,15 +510,18 @@ __global__ __launch_bounds__(kQ4Threads) void gemm_q4_kernel(const GemmArgs g) {
   }
 }
 
-// SiLU pair over the prepared dense copies, BM prompt rows (256 or 320) x 128
-// output columns per block (the gate and up rows of those columns: 256
-// weight rows). 8 waves as 2 along M x 4 along N; wave (wm, wn) owns rows
-// BM/2 wm .. +BM/2 and output columns 32 wn .. +32, i.e. fragment blocks
-// j = 0, 1 of gate and j = 2, 3 of up for the same columns, so the epilogue
-// pairs acc[i][j] with acc[i][j + 2] in registers. Per output element the
-// matrix instructions are those of gemm_q4_kernel in the same k order
-// (16x16x32 blocks of k 32 s .. 32 s + 31 with the same lane -> k map), so
-// every row tile and both kernels give the same bits.
+// MFMA GEMM over the prepared dense copies with 256 weight rows per block and
+// BM prompt rows (256 or 320), epilogues SiLU pair (the 128 gate and 128 up
+// rows of 128 output columns) or store (256 output columns of one weight
+// segment; segments start at multiples of 256 tiles' columns, tile0 counted in
+// 256-column tiles). 8 waves as 2 along M x 4 along N; wave (wm, wn) owns rows
+// BM/2 wm .. +BM/2 and four 16-column fragment blocks: for the pair, blocks
+// 0, 1 of gate and 2, 3 of up for the same output columns 32 wn .. +32, so the
+// epilogue pairs acc[i][j] with acc[i][j + 2] in registers; for the store,
+// output columns 64 wn .. +64. Per output element the matrix instructions
+// are those of gemm_q4_kernel in the same k order (16x16x32 blocks of k 32 s
+// .. 32 s + 31 with the same lane -> k map), so every row tile and both
+// kernels give the same bits.
 //
 // Pipeline per 32-k step s (one barrier per step), LDS stages of
 // (BM + 256) x 64 bytes, as many as fit in 160 KB (5 at BM = 256, 4 at 320):
@@ -530,7 +533,7 @@ __global__ __launch_bounds__(kQ4Threads) void gemm_q4_kernel(const GemmArgs g) {
 // flight) before the barrier. Rows of A past M and weight rows past N fall
 // outside the buffer range and read as zero (their row offset is in the
 // range-checked per-lane offset).
-constexpr int kPairThreads = 512, kPairBK = 32;
+constexpr int kDmaThreads = 512, kDmaBK = 32;
 constexpr uint32_t kLdsBytes = 160 * 1024;
 
 // One direct-to-LDS load: 16 bytes per lane at LDS address m0 + 16 * lane.
@@ -547,10 +550,12 @@ __device__ inline void lds_load16(__amdgpu_buffer_rsrc_t r, uint32_t lds_addr, u
 #define PRG_WAIT_VMCNT(n) \
   __builtin_amdgcn_s_waitcnt(((n) & 15) | (7 << 4) | (15 << 8) | ((((n) >> 4) & 3) << 14))
 
-template <int BM>
-__global__ __launch_bounds__(kPairThreads) void gemm_pair_dma_kernel(const GemmArgs g) {
+template <int EPI, int BM>
+__global__ __launch_bounds__(kDmaThreads) void gemm_dma_kernel(const GemmArgs g) {
   static_assert(BM == 256 || BM == 320, "row tile");
-  constexpr uint32_t kStage = (BM + 256) * kPairBK * 2;
+  static_assert(EPI == kGemmSiluPair || EPI == kGemmStore, "epilogue");
+  constexpr bool kPair = EPI == kGemmSiluPair;
+  constexpr uint32_t kStage = (BM + 256) * kDmaBK * 2;
   constexpr int NS = static_cast<int>(kLdsBytes / kStage);  // 5 or 4
   constexpr int IM = BM / 32;                               // 16-row blocks per wave
   constexpr int kExtra = BM / 16 - 16;                      // waves that load a third A group
@@ -559,7 +564,7 @@ __global__ __launch_bounds__(kPairThreads) void gemm_pair_dma_kernel(const GemmA
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 2, wn = wave & 3;
   const bool extra = wave < kExtra;
-  const uint32_t N = g.q[0].n, K = g.K, steps = K / kPairBK;
+  const uint32_t K = g.K, steps = K / kDmaBK;
   // Block -> tile as in gemm_q4_kernel: each XCD walks a contiguous range,
   // tm-fastest within groups of 4 tile rows.
   const uint32_t tiles_m = (g.M + BM - 1) / BM;
@@ -573,18 +578,29 @@ __global__ __launch_bounds__(kPairThreads) void gemm_pair_dma_kernel(const GemmA
     tm = first + (L % width) % gs;
     tn = (L % width) / gs;
   }
-  const uint32_t m0 = tm * BM, n0 = tn * 128;
+  uint32_t seg = 0;
+  if constexpr (!kPair) {
+#pragma unroll
+    for (int i = 1; i < kGemmMaxSegs; ++i)
+      if (i < static_cast<int>(g.nq) && tn >= g.q[i].tile0) seg = i;
+  }
+  const GemmQ4& q0 = g.q[seg];
+  const uint32_t N = q0.n;
+  const uint32_t m0 = tm * BM, n0 = kPair ? tn * 128 : (tn - q0.tile0) * 256;
   const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(g.a, static_cast<uint32_t>(static_cast<uint64_t>(g.M) * g.lda * 2));
-  const __amdgpu_buffer_rsrc_t rg = buffer_rsrc(g.q[0].dense, static_cast<uint32_t>(static_cast<uint64_t>(N) * K * 2));
-  const __amdgpu_buffer_rsrc_t ru = buffer_rsrc(g.q[1].dense, static_cast<uint32_t>(static_cast<uint64_t>(N) * K * 2));
+  const __amdgpu_buffer_rsrc_t rw0 = buffer_rsrc(q0.dense, static_cast<uint32_t>(static_cast<uint64_t>(N) * K * 2));
+  const __amdgpu_buffer_rsrc_t rw1 =
+      kPair ? buffer_rsrc(g.q[1].dense, static_cast<uint32_t>(static_cast<uint64_t>(N) * K * 2)) : rw0;
   // Wave w loads A rows 16 (w + 8 h) .. +15 for h = 0, 1 (and 256 + 16 w when
-  // it is one of the kExtra), and weight rows 16 w .. +15 of gate and of up;
-  // lane l: row + l / 4, chunk l % 4.
+  // it is one of the kExtra), and 16 weight rows into LDS rows BM + 16 w and
+  // BM + 128 + 16 w: gate and up row n0 + 16 w (pair), or rows n0 + 16 w and
+  // n0 + 128 + 16 w of the segment (store); lane l: row + l / 4, chunk l % 4.
   const uint32_t lrow = 16 * wave + (lane >> 2), lch = 8 * (lane & 3);
   uint32_t va[3];
 #pragma unroll
   for (int h = 0; h < 3; ++h) va[h] = static_cast<uint32_t>(((m0 + lrow + 128 * h) * g.lda + lch) * 2);
-  const uint32_t vw = ((n0 + lrow) * K + lch) * 2;
+  const uint32_t vw0 = ((n0 + lrow) * K + lch) * 2;
+  const uint32_t vw1 = kPair ? vw0 : ((n0 + 128 + lrow) * K + lch) * 2;
   // LDS byte address of the ring (the address-space cast is a C-style cast)
   const uint32_t lbase = static_cast<uint32_t>(
       reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint8_t*)lds));
@@ -593,8 +609,8 @@ __global__ __launch_bounds__(kPairThreads) void gemm_pair_dma_kernel(const GemmA
     lds_load16(ra, sb, va[0], ks * 64);
     lds_load16(ra, sb + 128 * 64, va[1], ks * 64);
     if (kExtra > 0 && extra) lds_load16(ra, sb + 256 * 64, va[2], ks * 64);
-    lds_load16(rg, sb + BM * 64, vw, ks * 64);
-    lds_load16(ru, sb + (BM + 128) * 64, vw, ks * 64);
+    lds_load16(rw0, sb + BM * 64, vw0, ks * 64);
+    lds_load16(rw1, sb + (BM + 128) * 64, vw1, ks * 64);
   };
   // this wave's loads newer than the ones of the step it needs next
   auto wait_next = [&]() {
@@ -607,7 +623,10 @@ __global__ __launch_bounds__(kPairThreads) void gemm_pair_dma_kernel(const GemmA
   const uint32_t fa = (wm * (BM / 2) + (lane & 15)) * 64 + (lane >> 4) * 16;
   uint32_t fb[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) fb[j] = (BM + (j < 2 ? 0 : 128) + wn * 32 + 16 * (j & 1) + (lane & 15)) * 64 + (lane >> 4) * 16;
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t brow = kPair ? (j < 2 ? 0 : 128) + wn * 32 + 16 * (j & 1) : wn * 64 + 16 * j;
+    fb[j] = (BM + brow + (lane & 15)) * 64 + (lane >> 4) * 16;
+  }
   f32x4 acc[IM][4];
 #pragma unroll
   for (int i = 0; i < IM; ++i)
@@ -650,7 +669,7 @@ __global__ __launch_bounds__(kPairThreads) void gemm_pair_dma_kernel(const GemmA
 
   // Epilogue: lane holds rows 4 (lane / 16) + r, column lane % 16 of each block.
   const int crow = 4 * (lane >> 4), ccol = lane & 15;
-  uint16_t* C = g.q[0].c;
+  uint16_t* C = q0.c;
 #pragma unroll
   for (int i = 0; i < IM; ++i)
 #pragma unroll
@@ -658,12 +677,21 @@ __global__ __launch_bounds__(kPairThreads) void gemm_pair_dma_kernel(const GemmA
       const uint32_t m = m0 + wm * (BM / 2) + 16 * i + crow + r;
       if (m >= g.M) continue;
       uint16_t* out = C + static_cast<uint64_t>(m) * N;
+      if constexpr (kPair) {
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const uint32_t n = n0 + wn * 32 + 16 * j + ccol;
-        if (n >= N) continue;
-        const float gate = round_bf(acc[i][j][r]), up = round_bf(acc[i][j + 2][r]);
-        out[n] = f2bf(silu(gate) * up);
+        for (int j = 0; j < 2; ++j) {
+          const uint32_t n = n0 + wn * 32 + 16 * j + ccol;
+          if (n >= N) continue;
+          const float gate = round_bf(acc[i][j][r]), up = round_bf(acc[i][j + 2][r]);
+          out[n] = f2bf(silu(gate) * up);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t n = n0 + wn * 64 + 16 * j + ccol;
+          if (n >= N) continue;
+          out[n] = f2bf(acc[i][j][r]);
+        }
       }
     }
 }
@@ -695,26 +723,36 @@ int launch_q4_bm(hipStream_t s, const GemmArgs& g, uint32_t tiles_n, const char*
   return PRG_OK;
 }
 
-// A round of gemm_pair_dma_kernel<256> blocks costs about as long as 396 rows
-// of gemm_q4_kernel rounds (one round measured at 2.06 rounds of 192-row
-// tiles, for 2.67 times their work); a 320-row round about 1.25 times that.
-// PEREGRINE_GEMM_PAIR_DMA = 0 / 256 / 320 forces the 192 / 256-row kernel or
-// that row tile of this one, whatever the estimate (all give the same bits).
-constexpr uint64_t kPairDmaRoundCost256 = 396, kPairDmaRoundCost320 = 495;
+// Rounds of gemm_dma_kernel blocks in units of gemm_q4_kernel rows (its cost
+// model: a round of BM-row tiles costs BM), from the 1600-token ingest trace:
+// 192-row gate/up rounds 48.9 us, 256-row direct-to-LDS rounds 113 us, 320-row
+// rounds 149 us. PEREGRINE_GEMM_DMA = 0 / 256 / 320 forces the 192 / 256-row
+// kernel or that row tile of this one, whatever the estimate (all give the
+// same bits).
+constexpr uint64_t kDmaRoundCost256 = 445, kDmaRoundCost320 = 585;
 
-inline int pair_dma_override() {
-  const char* e = getenv("PEREGRINE_GEMM_PAIR_DMA");
+inline int dma_override() {
+  const char* e = getenv("PEREGRINE_GEMM_DMA");
   if (e == nullptr || e[0] == '\0') return -1;
   return atoi(e);
 }
 
-template <int BM>
-int launch_pair_dma(hipStream_t s, const GemmArgs& g, const char* name) {
-  PRG_CHECK_ARG(static_cast<uint64_t>(g.q[0].n + 128) * g.K * 2 < (1ull << 32) &&
-                    static_cast<uint64_t>(g.M + BM) * g.lda * 2 < (1ull << 32),
+// g: as launch_gemm_q4 leaves it (segments' tile0 in 128-column tiles).
+template <int EPI, int BM>
+int launch_dma(hipStream_t s, GemmArgs g, uint32_t tiles_n, const char* name) {
+  uint64_t rows = 0;
+  for (uint32_t i = 0; i < g.nq; ++i) rows = std::max<uint64_t>(rows, g.q[i].n);
+  PRG_CHECK_ARG((rows + 256) * g.K * 2 < (1ull << 32) && static_cast<uint64_t>(g.M + BM) * g.lda * 2 < (1ull << 32),
                 "%s: operands too large for 32-bit offsets", name);
-  const uint32_t tiles = ((g.M + BM - 1) / BM) * ((g.q[0].n + 127) / 128);
-  hipLaunchKernelGGL((gemm_pair_dma_kernel<BM>), dim3(tiles), dim3(kPairThreads), 0, s, g);
+  if constexpr (EPI == kGemmStore) {
+    uint32_t tile = 0;
+    for (uint32_t i = 0; i < g.nq; ++i) {
+      g.q[i].tile0 = tile;
+      tile += (g.q[i].n + 255) / 256;
+    }
+  }
+  const uint32_t tiles = ((g.M + BM - 1) / BM) * tiles_n;
+  hipLaunchKernelGGL((gemm_dma_kernel<EPI, BM>), dim3(tiles), dim3(kDmaThreads), 0, s, g);
   PRG_CHECK_LAUNCH(name);
   return PRG_OK;
 }
@@ -728,19 +766,27 @@ int launch_q4_t(hipStream_t s, const GemmArgs& g, const char* name) {
     const uint32_t blocks = ((g.M + bm - 1) / bm) * tiles_n;
     return static_cast<uint64_t>((blocks + cus - 1) / cus) * bm;
   };
-  if constexpr (EPI == kGemmSiluPair) {
-    if (g.q[0].dense != nullptr && g.q[1].dense != nullptr) {
-      const uint32_t tiles_nd = (g.q[0].n + 127) / 128;
+  if constexpr (EPI == kGemmSiluPair || EPI == kGemmStore) {
+    bool dense = true;
+    for (uint32_t i = 0; i < g.nq; ++i) dense = dense && g.q[i].dense != nullptr;
+    if (dense) {
+      // columns per block: 128 outputs of the pair, 256 of a store segment
+      uint32_t tiles_nd = 0;
+      if constexpr (EPI == kGemmSiluPair) {
+        tiles_nd = (g.q[0].n + 127) / 128;
+      } else {
+        for (uint32_t i = 0; i < g.nq; ++i) tiles_nd += (g.q[i].n + 255) / 256;
+      }
       auto cost_dma = [&](uint32_t bm, uint64_t round) -> uint64_t {
         const uint32_t blocks = ((g.M + bm - 1) / bm) * tiles_nd;
         return static_cast<uint64_t>((blocks + cus - 1) / cus) * round;
       };
-      const uint64_t c256 = cost_dma(256, kPairDmaRoundCost256), c320 = cost_dma(320, kPairDmaRoundCost320);
+      const uint64_t c256 = cost_dma(256, kDmaRoundCost256), c320 = cost_dma(320, kDmaRoundCost320);
       const uint64_t cold = std::min(cost(192), cost(256));
-      int pick = pair_dma_override();
+      int pick = dma_override();
       if (pick < 0) pick = std::min(c256, c320) < cold ? (c320 < c256 ? 320 : 256) : 0;
-      if (pick == 320) return launch_pair_dma<320>(s, g, name);
-      if (pick == 256) return launch_pair_dma<256>(s, g, name);
+      if (pick == 320) return launch_dma<EPI, 320>(s, g, tiles_nd, name);
+      if (pick == 256) return launch_dma<EPI, 256>(s, g, tiles_nd, name);
     }
   }
   if (cost(192) < cost(256)) return launch_q4_bm<EPI, 192>(s, g, tiles_n, name);

@@ -128,24 +128,25 @@ def test_prepared_dense_prefill_is_identical(m9b, monkeypatch):
 
 
 @pytest.mark.parametrize("T", [100, 700, 1600])
-def test_pair_dma_gate_up_matches_the_q4_kernel(m9b, monkeypatch, T):
-    """The SiLU-pair GEMM with direct-to-LDS copies (gemm_pair_dma_kernel,
-    256- or 320-row tiles, taken for the dense gate / up GEMM when it costs
+def test_dma_gemms_match_the_q4_kernel(m9b, monkeypatch, T):
+    """The prompt GEMM with direct-to-LDS copies (gemm_dma_kernel: 256- or
+    320-row tiles, SiLU-pair and multi-segment store epilogues, taken for the
+    dense gate / up, GDN in_proj and attention q / k / v GEMMs when it costs
     fewer rounds) issues, per output element, the matrix instructions of
     gemm_q4_kernel in the same k order. Forced to each kernel in turn
-    (PEREGRINE_GEMM_PAIR_DMA = 0 / 256 / 320, read per launch), prompts of
-    100 / 700 / 1600 tokens (one partial row tile; several with a partial last
-    one; 1600 = 5 x 320) leave the same next token, GDN states and KV caches
-    bit for bit."""
+    (PEREGRINE_GEMM_DMA = 0 / 256 / 320, read per launch), prompts of 100 /
+    700 / 1600 tokens (one partial row tile; several with a partial last one;
+    1600 = 5 x 320) leave the same next token, GDN states and KV caches bit
+    for bit."""
     m9b.prepare_dense()
     prompt = np.random.default_rng(11 + T).integers(0, 248320, size=T).astype(np.uint32)
     states, firsts = [], []
     for pick in ("0", "256", "320"):
         st = _state(m9b, 2048, None, monkeypatch)
-        monkeypatch.setenv("PEREGRINE_GEMM_PAIR_DMA", pick)
+        monkeypatch.setenv("PEREGRINE_GEMM_DMA", pick)
         firsts.append(st.prefill(prompt))
         states.append(st)
-    monkeypatch.delenv("PEREGRINE_GEMM_PAIR_DMA")
+    monkeypatch.delenv("PEREGRINE_GEMM_DMA")
     assert len(set(firsts)) == 1, firsts
     for st in states[1:]:
         _same_states(states[0], st, m9b, T)
