@@ -724,12 +724,14 @@ int launch_q4_bm(hipStream_t s, const GemmArgs& g, uint32_t tiles_n, const char*
 }
 
 // Rounds of gemm_dma_kernel blocks in units of gemm_q4_kernel rows (its cost
-// model: a round of BM-row tiles costs BM), from the 1600-token ingest trace:
-// 192-row gate/up rounds 48.9 us, 256-row direct-to-LDS rounds 113 us, 320-row
-// rounds 149 us. PEREGRINE_GEMM_DMA = 0 / 256 / 320 forces the 192 / 256-row
-// kernel or that row tile of this one, whatever the estimate (all give the
-// same bits).
-constexpr uint64_t kDmaRoundCost256 = 445, kDmaRoundCost320 = 585;
+// model: a round of BM-row tiles costs BM; one unit ~ 0.255 us at K = 4096),
+// from 1600-token ingest traces: 256-row direct-to-LDS rounds 113 us (445); a
+// 320-row round takes 123 / 131 / 139 / 147 us with 80 / 200 / 250 / 240 x 2
+// blocks, i.e. mostly the per-block time, so 530 stands for it (q / k / v and
+// in_proj take it; the 80-block N = 4096 launches stay on gemm_q4_kernel).
+// PEREGRINE_GEMM_DMA = 0 / 256 / 320 forces the 192 / 256-row kernel or that
+// row tile of this one, whatever the estimate (all give the same bits).
+constexpr uint64_t kDmaRoundCost256 = 445, kDmaRoundCost320 = 530;
 
 inline int dma_override() {
   const char* e = getenv("PEREGRINE_GEMM_DMA");
