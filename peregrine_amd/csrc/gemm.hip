@@ -20,6 +20,7 @@ namespace {
 using namespace prg;
 
 constexpr int kBM = 128, kBN = 128, kBK = 64, kGemmThreads = 256;
+static_assert(kBM == kGemmBf16RowTile && kBK == kGemmBf16KStep, "causal_pv_columns follows this tiling");
 constexpr int kLdsRow = kBK + 8;  // bf16 per LDS row (144 bytes)
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -90,6 +91,14 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const GemmArgs g) {
   const uint32_t N = Q4 ? g.q[seg].n : g.N;
   const uint64_t z = blockIdx.z;
   const uint32_t K = g.K;
+  // Causal attention: the last column any row of this tile sees (rows of one
+  // tile may span two q heads; then the tile holds token T - 1).
+  uint32_t k_end = K;
+  if (!Q4 && g.causal_T != 0) {
+    const uint32_t last = g.causal_prefix + min(g.causal_T - 1, m0 % g.causal_T + (kBM - 1));
+    if (EPI == kGemmStore && n0 > last) return;  // scores: every column masked
+    if (EPI == kGemmSigmoidGate) k_end = causal_pv_columns(m0, g.causal_T, g.causal_prefix, K);  // P.V: zeros past it
+  }
 
   // Global -> register staging. A (and bf16 B): 16-byte chunk i of this
   // thread is row (tid/8 + 32 i), columns k0 + 8*(tid%8) .. +8.
@@ -174,13 +183,13 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(const GemmArgs g) {
   // barrier then both publishes stage k+1 and retires the reads of stage k.
   load(0);
   store_stage(0);
-  if (kBK < K) load(kBK);
+  if (kBK < k_end) load(kBK);
   __syncthreads();
   int st = 0;
-  for (uint32_t k0 = 0; k0 < K; k0 += kBK, st ^= 1) {
-    if (k0 + kBK < K) {
+  for (uint32_t k0 = 0; k0 < k_end; k0 += kBK, st ^= 1) {
+    if (k0 + kBK < k_end) {
       store_stage(st ^ 1);
-      if (k0 + 2 * kBK < K) load(k0 + 2 * kBK);
+      if (k0 + 2 * kBK < k_end) load(k0 + 2 * kBK);
     }
     const uint16_t* A = sA[st];
     const uint16_t* B = sB[st];

@@ -34,6 +34,18 @@ enum GemmEpi : int {
 };
 
 constexpr int kGemmMaxSegs = 4;
+// Row tile and K step of the bf16 GEMM (attention scores and P.V). The P.V
+// GEMM of a causal prefill reads a tile's probabilities up to its last visible
+// column rounded up to the K step; the softmax writes its zeros that far.
+constexpr uint32_t kGemmBf16RowTile = 128, kGemmBf16KStep = 64;
+// Columns [0, result) of the probability rows that the P.V tile holding row
+// `row` (of rows = 4 x T per kv head) reads.
+__host__ __device__ inline uint32_t causal_pv_columns(uint32_t row, uint32_t T, uint32_t prefix, uint32_t L) {
+  const uint32_t m0 = row / kGemmBf16RowTile * kGemmBf16RowTile;
+  const uint32_t t_last = m0 % T + (kGemmBf16RowTile - 1) < T ? m0 % T + (kGemmBf16RowTile - 1) : T - 1;
+  const uint32_t end = (prefix + t_last + kGemmBf16KStep) / kGemmBf16KStep * kGemmBf16KStep;
+  return end < L ? end : L;
+}
 
 struct GemmQ4 {
   const uint32_t* w = nullptr;  // u32 [n, K/8]
@@ -68,6 +80,11 @@ struct GemmArgs {
   uint64_t ldc = 0, ldc_hi = 0, c_z = 0;
   uint32_t c_group = 0;
   uint32_t M = 0, N = 0, K = 0;
+  // Causal attention (bf16 mode; 0 = off): row m is token m % causal_T of the
+  // chunk and sees columns [0, causal_prefix + token]. The scores GEMM skips
+  // tiles past every row's last visible column (the softmax masks them); the
+  // P.V GEMM stops K there (the probabilities past it are exact zeros).
+  uint32_t causal_T = 0, causal_prefix = 0;
 };
 
 // Q4 weights in g.q[0..nq). K % 64 == 0; A rows 16-byte aligned (lda % 8 == 0).

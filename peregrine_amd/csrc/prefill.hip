@@ -145,15 +145,19 @@ __global__ __launch_bounds__(kSoftmaxThreads) void attn_prefill_softmax_kernel(u
   uint16_t* row = scores + static_cast<size_t>(blockIdx.x) * ld;
   const uint32_t t = (blockIdx.x % (kAttnGroup * T)) % T;
   const uint32_t vis = prefix + t;
+  // the P.V GEMM reads this row up to wend (zeros between vis and wend)
+  const uint32_t wend = causal_pv_columns(blockIdx.x % (kAttnGroup * T), T, prefix, L);
   // The thread's first kCache columns (c = tid + 256 i) stay in registers
   // across the three passes (one read of the row); later columns are read
-  // again. The arithmetic and its order per thread are unchanged.
+  // again. The arithmetic and its order per thread are unchanged. Masked
+  // columns (c > vis) are never read: the scores GEMM skips tiles that hold
+  // only masked columns, so they may hold anything.
   constexpr int kCache = 8;
   float xs[kCache];
 #pragma unroll
   for (int i = 0; i < kCache; ++i) {
     const uint32_t c = threadIdx.x + kSoftmaxThreads * i;
-    xs[i] = c < L ? __fmul_rn(bf2f(row[c]), scale) : 0.0f;
+    xs[i] = c <= vis ? __fmul_rn(bf2f(row[c]), scale) : 0.0f;
   }
   float m = -INFINITY;
 #pragma unroll
@@ -161,8 +165,8 @@ __global__ __launch_bounds__(kSoftmaxThreads) void attn_prefill_softmax_kernel(u
     const uint32_t c = threadIdx.x + kSoftmaxThreads * i;
     if (c < L) m = fmaxf(m, c > vis ? -INFINITY : xs[i]);
   }
-  for (uint32_t c = threadIdx.x + kSoftmaxThreads * kCache; c < L; c += kSoftmaxThreads)
-    m = fmaxf(m, c > vis ? -INFINITY : __fmul_rn(bf2f(row[c]), scale));
+  for (uint32_t c = threadIdx.x + kSoftmaxThreads * kCache; c <= vis; c += kSoftmaxThreads)
+    m = fmaxf(m, __fmul_rn(bf2f(row[c]), scale));
   const float row_max = tree_max<kSoftmaxThreads>(m, sh);
   float sum = 0.0f;
 #pragma unroll
@@ -171,18 +175,18 @@ __global__ __launch_bounds__(kSoftmaxThreads) void attn_prefill_softmax_kernel(u
     xs[i] = exp2f(__fmul_rn(__fsub_rn(xs[i], row_max), kLog2e));
     if (c < L && c <= vis) sum += xs[i];
   }
-  for (uint32_t c = threadIdx.x + kSoftmaxThreads * kCache; c < L; c += kSoftmaxThreads)
-    if (c <= vis) sum += exp2f(__fmul_rn(__fsub_rn(__fmul_rn(bf2f(row[c]), scale), row_max), kLog2e));
+  for (uint32_t c = threadIdx.x + kSoftmaxThreads * kCache; c <= vis; c += kSoftmaxThreads)
+    sum += exp2f(__fmul_rn(__fsub_rn(__fmul_rn(bf2f(row[c]), scale), row_max), kLog2e));
   const float total = tree_sum<kSoftmaxThreads>(sum, sh);
   const float denom = total == 0.0f ? 1.0f : total;
 #pragma unroll
   for (int i = 0; i < kCache; ++i) {
     const uint32_t c = threadIdx.x + kSoftmaxThreads * i;
-    if (c < ld) row[c] = c < L && c <= vis ? f2bf(xs[i] / denom) : uint16_t{0};
+    if (c < wend) row[c] = c <= vis ? f2bf(xs[i] / denom) : uint16_t{0};
   }
-  for (uint32_t c = threadIdx.x + kSoftmaxThreads * kCache; c < ld; c += kSoftmaxThreads) {
+  for (uint32_t c = threadIdx.x + kSoftmaxThreads * kCache; c < wend; c += kSoftmaxThreads) {
     uint16_t p = 0;
-    if (c < L && c <= vis) p = f2bf(exp2f(__fmul_rn(__fsub_rn(__fmul_rn(bf2f(row[c]), scale), row_max), kLog2e)) / denom);
+    if (c <= vis) p = f2bf(exp2f(__fmul_rn(__fsub_rn(__fmul_rn(bf2f(row[c]), scale), row_max), kLog2e)) / denom);
     row[c] = p;
   }
 }
@@ -545,6 +549,8 @@ int launch_attn_prefill(hipStream_t s, const uint16_t* q, const uint16_t* cache_
   sc.M = rows;
   sc.N = L;
   sc.K = kAttnHeadDim;
+  sc.causal_T = T;
+  sc.causal_prefix = prefix;
   if (int rc = launch_gemm_bf16(s, sc, kGemmStore, kAttnKvHeads, "attn_prefill.scores")) return rc;
   hipLaunchKernelGGL(attn_prefill_softmax_kernel, dim3(kAttnKvHeads * rows), dim3(kSoftmaxThreads), 0, s, scores, ld,
                      L, T, prefix, scale);
@@ -565,6 +571,8 @@ int launch_attn_prefill(hipStream_t s, const uint16_t* q, const uint16_t* cache_
   pv.M = rows;
   pv.N = kAttnHeadDim;
   pv.K = L;
+  pv.causal_T = T;
+  pv.causal_prefix = prefix;
   return launch_gemm_bf16(s, pv, kGemmSigmoidGate, kAttnKvHeads, "attn_prefill.values");
 }
 
