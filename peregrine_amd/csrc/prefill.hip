@@ -92,44 +92,64 @@ __device__ inline float tree_max(float v, float* sh) {
 }
 
 // ------------------------------------------------------- attention ----------
-// One block per row: rows [0, 16T) are query heads (t = row/16, h = row%16),
-// rows [16T, 20T) key heads (t = r/4, h = r%4). Thread d owns dimension d.
-// Queries: split from the packed q ‖ gate projection, RMS-normed, partial
-// NeoX RoPE on dims [0, 64), written to q_out; gate copied to gate_out. Keys:
-// same norm/RoPE into cache_k[h, stride, 256] at start_cache + t; values copied
-// to cache_v[h, 256, stride]. The normed value stays f32 through RoPE.
+// Rows [0, 16T) are query heads (t = row/16, h = row%16), rows [16T, 20T)
+// key heads (t = r/4, h = r%4). Queries: split from the packed q ‖ gate
+// projection, RMS-normed, partial NeoX RoPE on dims [0, 64), written to q_out;
+// gate copied to gate_out. Keys: same norm/RoPE into cache_k[h, stride, 256]
+// at start_cache + t; values copied to cache_v[h, 256, stride]. The normed
+// value stays f32 through RoPE.
+// One wave per row, four rows per block: lane l holds elements l, l + 64,
+// l + 128 and l + 192. The sum of squares combines them in the 256-thread
+// halving tree's pairs ((l, l + 128) and (l + 64, l + 192), then l with
+// l + 64) and finishes inside the wave, so the bits are the tree's; RoPE pairs
+// element d < 32 with d + 32, i.e. lane l with lane l ^ 32.
+constexpr int kPrepRows = kPrepThreads / kWave;
 __global__ __launch_bounds__(kPrepThreads) void attn_prefill_prepare_kernel(
     const uint16_t* __restrict__ qp, const uint16_t* __restrict__ q_w, const uint16_t* __restrict__ k_in,
     const uint16_t* __restrict__ k_w, const uint16_t* __restrict__ v_in, uint16_t* __restrict__ q_out,
     uint16_t* __restrict__ gate_out, uint16_t* __restrict__ cache_k, uint16_t* __restrict__ cache_v, uint32_t T,
     uint32_t start_rope, uint32_t start_cache, uint32_t stride) {
-  __shared__ float sh[kPrepThreads + 1];
-  const uint32_t rg = blockIdx.x, d = threadIdx.x;
+  static_assert(kAttnHeadDim == 4 * kWave && kAttnRotary == kWave, "lane layout");
+  const uint32_t rg = blockIdx.x * kPrepRows + (threadIdx.x / kWave), l = threadIdx.x % kWave;
   const uint32_t q_rows = T * kAttnQHeads;
+  if (rg >= T * (kAttnQHeads + kAttnKvHeads)) return;  // whole wave: no barrier below
   const bool is_q = rg < q_rows;
   const uint32_t lr = is_q ? rg : rg - q_rows;
   const uint32_t heads = is_q ? kAttnQHeads : kAttnKvHeads;
   const uint32_t t = lr / heads, h = lr - t * heads;
   const uint16_t* src = is_q ? qp + static_cast<size_t>(lr) * 2 * kAttnHeadDim : k_in + static_cast<size_t>(lr) * kAttnHeadDim;
   const uint16_t* w = is_q ? q_w : k_w;
-  const float x = bf2f(src[d]);
-  if (is_q) gate_out[static_cast<size_t>(lr) * kAttnHeadDim + d] = src[kAttnHeadDim + d];
-  else cache_v[(static_cast<size_t>(h) * kAttnHeadDim + d) * stride + start_cache + t] = v_in[static_cast<size_t>(lr) * kAttnHeadDim + d];
-  const float ss = tree_sum<kPrepThreads>(__fmul_rn(x, x), sh);
+  float x[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) x[i] = bf2f(src[l + kWave * i]);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t d = l + kWave * i;
+    if (is_q) gate_out[static_cast<size_t>(lr) * kAttnHeadDim + d] = src[kAttnHeadDim + d];
+    else cache_v[(static_cast<size_t>(h) * kAttnHeadDim + d) * stride + start_cache + t] = v_in[static_cast<size_t>(lr) * kAttnHeadDim + d];
+  }
+  const float sq0 = __fmul_rn(x[0], x[0]), sq1 = __fmul_rn(x[1], x[1]);
+  const float sq2 = __fmul_rn(x[2], x[2]), sq3 = __fmul_rn(x[3], x[3]);
+  const float root = wave_tree_tail<false>(__fadd_rn(__fadd_rn(sq0, sq2), __fadd_rn(sq1, sq3)));
+  const float ss = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, root), 0));
   const float scale = 1.0f / sqrtf(ss / static_cast<float>(kAttnHeadDim) + kAttnEps);
   uint16_t* dst = is_q ? q_out + static_cast<size_t>(lr) * kAttnHeadDim
                        : cache_k + (static_cast<size_t>(h) * stride + start_cache + t) * kAttnHeadDim;
-  constexpr uint32_t half = kAttnRotary / 2;
-  if (d < half) {
-    const float a = __fmul_rn(__fmul_rn(x, scale), bf2f(w[d]));
-    const float b = __fmul_rn(__fmul_rn(bf2f(src[d + half]), scale), bf2f(w[d + half]));
+  // rotary dims: after the swap every lane holds a = element d and b = element d + 32 (d = l % 32)
+  {
+    constexpr uint32_t half = kAttnRotary / 2;
+    const uint32_t d = l % half;
+    float a = __fmul_rn(__fmul_rn(x[0], scale), bf2f(w[l])), b = a;
+    swap32(a, b);
     const float inv_freq = powf(kAttnTheta, -(2.0f * static_cast<float>(d)) / static_cast<float>(kAttnRotary));
     const float th = static_cast<float>(start_rope + t) * inv_freq;
-    const float c = cosf(th), s = sinf(th);
-    dst[d] = f2bf(__fsub_rn(__fmul_rn(a, c), __fmul_rn(b, s)));
-    dst[d + half] = f2bf(__fadd_rn(__fmul_rn(b, c), __fmul_rn(a, s)));
-  } else if (d >= kAttnRotary) {
-    dst[d] = f2bf(__fmul_rn(__fmul_rn(x, scale), bf2f(w[d])));
+    const float c = cosf(th), sn = sinf(th);
+    dst[l] = l < half ? f2bf(__fsub_rn(__fmul_rn(a, c), __fmul_rn(b, sn))) : f2bf(__fadd_rn(__fmul_rn(b, c), __fmul_rn(a, sn)));
+  }
+#pragma unroll
+  for (int i = 1; i < 4; ++i) {
+    const uint32_t d = l + kWave * i;
+    dst[d] = f2bf(__fmul_rn(__fmul_rn(x[i], scale), bf2f(w[d])));
   }
 }
 
@@ -519,7 +539,8 @@ int launch_attn_prefill_prepare(hipStream_t s, const uint16_t* qp, const uint16_
                                 const uint16_t* k_w, const uint16_t* v_in, uint16_t* q_out, uint16_t* gate_out,
                                 uint16_t* cache_k, uint16_t* cache_v, uint32_t T, uint32_t start_rope,
                                 uint32_t start_cache, uint32_t stride) {
-  hipLaunchKernelGGL(attn_prefill_prepare_kernel, dim3(T * (kAttnQHeads + kAttnKvHeads)), dim3(kPrepThreads), 0, s,
+  hipLaunchKernelGGL(attn_prefill_prepare_kernel, dim3((T * (kAttnQHeads + kAttnKvHeads) + kPrepRows - 1) / kPrepRows),
+                     dim3(kPrepThreads), 0, s,
                      qp, q_w, k_in, k_w, v_in, q_out, gate_out, cache_k, cache_v, T, start_rope, start_cache, stride);
   PRG_CHECK_LAUNCH("attn_prefill_prepare");
   return PRG_OK;
