@@ -475,10 +475,15 @@ __global__ __launch_bounds__(256) void gdn_prefill_kernel(float* __restrict__ st
       // full chunk: unrolled, every LDS operand at a constant offset
 #pragma unroll
       for (uint32_t tt = 0; tt < kGdnChunk; tt += 2) {
+        // each fetch is issued before the other token's arithmetic
         fetch(tb, buf, tt + 1);
+        __builtin_amdgcn_sched_barrier(0);
         token(ta, buf, tt);
+        __builtin_amdgcn_sched_barrier(0);
         if (tt + 2 < kGdnChunk) fetch(ta, buf, tt + 2);
+        __builtin_amdgcn_sched_barrier(0);
         token(tb, buf, tt + 1);
+        __builtin_amdgcn_sched_barrier(0);
       }
     } else {
       uint32_t tt = 0;
