@@ -27,6 +27,53 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(
   const uint4* src = reinterpret_cast<const uint4*>(a + row_off);
   const uint32_t n8 = hidden / 8;
   if constexpr (ADD) {
+    constexpr int kRegUnits = 4;  // rows up to 8192 wide keep the rounded sum in registers
+    if (n8 <= kRegUnits * kNormThreads) {
+      // Every load first; the sum is stored and normalised from registers
+      // (no read-back of residual_out). The sum of squares visits the units
+      // in rms_scale's order, so the bits are those of the read-back form.
+      const uint4* srcb = reinterpret_cast<const uint4*>(b + row_off);
+      const uint4* ws = reinterpret_cast<const uint4*>(w);
+      uint4 xv[kRegUnits], yv[kRegUnits], wv[kRegUnits];
+#pragma unroll
+      for (int k = 0; k < kRegUnits; ++k) {
+        const uint32_t g = threadIdx.x + k * kNormThreads;
+        if (g < n8) {
+          xv[k] = src[g];
+          yv[k] = srcb[g];
+          wv[k] = ws[g];
+        }
+      }
+      uint4* r = reinterpret_cast<uint4*>(residual_out + row_off);
+      float ss = 0.0f;
+#pragma unroll
+      for (int k = 0; k < kRegUnits; ++k) {
+        const uint32_t g = threadIdx.x + k * kNormThreads;
+        if (g >= n8) continue;
+        const uint32_t xd[4] = {xv[k].x, xv[k].y, xv[k].z, xv[k].w}, yd[4] = {yv[k].x, yv[k].y, yv[k].z, yv[k].w};
+        uint32_t o[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t lo = f2bf(bf_lo(xd[i]) + bf_lo(yd[i]));
+          const uint32_t hi = f2bf(bf_hi(xd[i]) + bf_hi(yd[i]));
+          o[i] = lo | (hi << 16);
+          const float fa = bf_lo(o[i]), fb = bf_hi(o[i]);
+          ss = __fmaf_rn(fa, fa, ss);
+          ss = __fmaf_rn(fb, fb, ss);
+        }
+        xv[k] = make_uint4(o[0], o[1], o[2], o[3]);
+        r[g] = xv[k];
+      }
+      const float total = block_sum256_dpp(ss, red);
+      const float scale = 1.0f / sqrtf(__fadd_rn(total / static_cast<float>(hidden), eps));
+      uint4* dst = reinterpret_cast<uint4*>(out + row_off);
+#pragma unroll
+      for (int k = 0; k < kRegUnits; ++k) {
+        const uint32_t g = threadIdx.x + k * kNormThreads;
+        if (g < n8) dst[g] = rms_apply(xv[k], wv[k], scale);
+      }
+      return;
+    }
     // r = bf16(float(lhs) + float(rhs)), stored, then normalised.
     const uint4* srcb = reinterpret_cast<const uint4*>(b + row_off);
     uint4* r = reinterpret_cast<uint4*>(residual_out + row_off);

@@ -38,16 +38,24 @@ def test_rmsnorm(gpu, orc):
     assert_bf16_close(out.numpy(), orc.rmsnorm(x, w), min_exact=0.98, what="rmsnorm")
 
 
-def test_add_rmsnorm(gpu, orc):
+@pytest.mark.parametrize("hidden", [4096, 4104, 8192, 12288])
+def test_add_rmsnorm(gpu, orc, hidden):
+    """Rows up to 8192 wide normalise the rounded sum from registers, wider
+    ones read it back (4104: one thread holds a third unit). Either way the
+    normalised row equals the standalone RMSNorm of the stored sum bit for
+    bit, and the sum equals the oracle's."""
     from peregrine_amd import ops
 
-    rng = np.random.default_rng(1)
-    a, b = random_bf16(rng, (2, 4096), std=3.0), random_bf16(rng, (2, 4096), std=3.0)
-    w = random_bf16(rng, (4096,), std=0.1, mean=1.0)
-    r, n = _e((2, 4096)), _e((2, 4096))
-    ops.add_rmsnorm(_d(a), _d(b), _d(w), r, n, 4096, 2)
+    rng = np.random.default_rng(1 + hidden)
+    a, b = random_bf16(rng, (2, hidden), std=3.0), random_bf16(rng, (2, hidden), std=3.0)
+    w = random_bf16(rng, (hidden,), std=0.1, mean=1.0)
+    r, n, n2 = _e((2, hidden)), _e((2, hidden)), _e((2, hidden))
+    wd = _d(w)
+    ops.add_rmsnorm(_d(a), _d(b), wd, r, n, hidden, 2)
+    ops.rmsnorm(r, wd, n2, hidden, 2)
     rr, rn = orc.add_rmsnorm(a, b, w)
     np.testing.assert_array_equal(r.numpy(), rr)
+    np.testing.assert_array_equal(n.numpy(), n2.numpy())
     assert_bf16_close(n.numpy(), rn, min_exact=0.98, what="add_rmsnorm")
 
 
