@@ -240,9 +240,26 @@ __global__ __launch_bounds__(256) void conv1d_prefill_kernel(const float* __rest
   const float w0[4] = {bf_lo(wv.x), bf_hi(wv.x), bf_lo(wv.y), bf_hi(wv.y)};
   const float w1[4] = {bf_lo(wv.z), bf_hi(wv.z), bf_lo(wv.w), bf_hi(wv.w)};
   const bool hs = has_state != 0;
+  const uint32_t t1 = min(t0 + kConvChunk, T);
+  if (t1 - t0 == kConvChunk) {
+    // A full chunk issues all of its kConvChunk + 3 loads before the first
+    // tap (the same arithmetic per output as the loop below).
+    float2 h[kConvChunk + kGdnConvK - 1];
+#pragma unroll
+    for (uint32_t i = 0; i < kConvChunk + kGdnConvK - 1; ++i) h[i] = conv_src(state, qkv, t0 + i, c, hs);
+#pragma unroll
+    for (uint32_t i = 0; i < kConvChunk; ++i) {
+      float a0 = 0.0f, a1 = 0.0f;
+      a0 = conv_tap(a0, w0[0], h[i].x); a0 = conv_tap(a0, w0[1], h[i + 1].x); a0 = conv_tap(a0, w0[2], h[i + 2].x); a0 = conv_tap(a0, w0[3], h[i + 3].x);
+      a1 = conv_tap(a1, w1[0], h[i].y); a1 = conv_tap(a1, w1[1], h[i + 1].y); a1 = conv_tap(a1, w1[2], h[i + 2].y); a1 = conv_tap(a1, w1[3], h[i + 3].y);
+      const uint32_t o = static_cast<uint32_t>(f2bf(a0 / (1.0f + expf(-a0)))) |
+                         (static_cast<uint32_t>(f2bf(a1 / (1.0f + expf(-a1)))) << 16);
+      *reinterpret_cast<uint32_t*>(out + static_cast<size_t>(t0 + i) * kGdnConvDim + c) = o;
+    }
+    return;
+  }
   float2 h0 = conv_src(state, qkv, t0, c, hs), h1 = conv_src(state, qkv, t0 + 1, c, hs),
          h2 = conv_src(state, qkv, t0 + 2, c, hs);
-  const uint32_t t1 = min(t0 + kConvChunk, T);
   for (uint32_t t = t0; t < t1; ++t) {
     const float2 h3 = conv_src(state, qkv, t + 3, c, hs);
     float a0 = 0.0f, a1 = 0.0f;
